@@ -1,0 +1,293 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Headline workload: the matmuls of one Llama-3.2-1B
+decode step in the Q4_K_M layout -- 16 layers x {q, k, v, o, gate, up, down}
+(Q4_K, with attn_v and ffn_down in Q6_K) plus the 128256-row output projection
+-- batch 1, fp32 activations.  One "step" = those 113 GEMVs over weights that
+are resident in HBM (raw GGUF blocks, never re-quantized).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--graph] [--no-extra]
+
+Prints one JSON line.  `value` is HBM GB/s over the algorithmic bytes of the
+step (raw weight bytes + fp32 activation-in + fp32 output bytes).  Extra keys:
+  roofline      the GEMV kernel's per-launch time measured with HIP events on
+                the launch stream, vs the 8 TB/s HBM peak
+  cpu_baseline  the single-core CPU restatement of the reference's
+                CpuRefBackend::mul_mat_q on layer 0 of the same workload
+  extra         config 1 (single Q4_K GEMV, weights rotated over 32 copies to
+                defeat the 256 MB MALL) and config 3 (Qwen2.5-1.5B 512-token
+                Q8_0 prefill, int8 TOPS on MFMA)
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import ggnpu_amd.lib as gl  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+Q4K, Q6K, Q8_0 = int(gl.GgmlType.Q4_K), int(gl.GgmlType.Q6_K), int(gl.GgmlType.Q8_0)
+
+# (name, type, N, K) per layer -- configs[1]
+LLAMA_LAYER = [("q", Q4K, 2048, 2048), ("k", Q4K, 512, 2048), ("v", Q6K, 512, 2048),
+               ("o", Q4K, 2048, 2048), ("gate", Q4K, 8192, 2048), ("up", Q4K, 8192, 2048),
+               ("down", Q6K, 2048, 8192)]
+LLAMA_LAYERS = 16
+LLAMA_OUTPUT = ("output", Q4K, 128256, 2048)
+# Qwen2.5-1.5B, hidden 1536, FFN 8960, 12 q / 2 kv heads of 128
+QWEN_LAYER = [("q", Q8_0, 1536, 1536), ("k", Q8_0, 256, 1536), ("v", Q8_0, 256, 1536),
+              ("o", Q8_0, 1536, 1536), ("gate", Q8_0, 8960, 1536), ("up", Q8_0, 8960, 1536),
+              ("down", Q8_0, 1536, 8960)]
+QWEN_LAYERS = 28
+PREFILL_TOKENS = 512
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Mat:
+    """One resident weight matrix plus its activation / output buffers."""
+
+    def __init__(self, torch, name, t, N, K, raw_dev, M=1, x=None):
+        self.name, self.t, self.N, self.K, self.M = name, t, N, K, M
+        self.w = raw_dev
+        self.x = x if x is not None else torch.randn((M, K), device="cuda", dtype=torch.float32)
+        self.y = torch.empty((M, N), device="cuda", dtype=torch.float32)
+
+    def bytes(self):
+        return gl.row_bytes(self.t, self.K) * self.N + 4 * self.M * (self.K + self.N)
+
+
+def make_weight(torch, gen, t, N, K):
+    """Seeded N(0, 0.02) fp32 values -> GGUF blocks (host encoder) -> HBM."""
+    x = (torch.randn((N, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02).cpu().numpy()
+    raw = gl.encode(t, x)
+    dev = torch.zeros(raw.size + 256, dtype=torch.uint8, device="cuda")
+    dev[: raw.size].copy_(torch.from_numpy(raw))
+    return dev, raw
+
+
+def launch(ctx, m, act_mode, stream):
+    st = ctx.lib.ggq_mul_mat_dev(ctx.h, ctypes.c_void_p(m.w.data_ptr()), m.t, m.N, m.K,
+                                 ctypes.c_void_p(m.x.data_ptr()), m.K, ctypes.c_void_p(m.y.data_ptr()), m.N,
+                                 m.M, act_mode, stream)
+    if st != 0:
+        ctx.check(st, f"mul_mat_dev {m.name}")
+
+
+def time_steps(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def per_launch_times(torch, ctx, mats, act_mode, stream, reps):
+    """HIP events around every launch, on the launch stream; returns the
+    mean duration (s) of each matrix's kernel(s) over `reps` steps."""
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in mats]
+          for _ in range(reps)]
+    for r in range(reps):
+        for i, m in enumerate(mats):
+            ev[r][i][0].record()
+            launch(ctx, m, act_mode, stream)
+            ev[r][i][1].record()
+    torch.cuda.synchronize()
+    return [sum(ev[r][i][0].elapsed_time(ev[r][i][1]) for r in range(reps)) / reps / 1e3 for i in range(len(mats))]
+
+
+def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream):
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+    mats, host_layer0 = [], []
+    t0 = time.time()
+    for layer in range(LLAMA_LAYERS):
+        for name, t, N, K in LLAMA_LAYER:
+            dev, raw = make_weight(torch, gen, t, N, K)
+            m = Mat(torch, f"blk{layer}.{name}", t, N, K, dev)
+            mats.append(m)
+            if layer == 0:
+                host_layer0.append((m, raw))
+    name, t, N, K = LLAMA_OUTPUT
+    dev, _ = make_weight(torch, gen, t, N, K)
+    mats.append(Mat(torch, name, t, N, K, dev))
+    torch.cuda.synchronize()
+    log(f"decode step: {len(mats)} matrices resident ({sum(m.bytes() for m in mats) / 1e6:.1f} MB) "
+        f"in {time.time() - t0:.1f}s")
+
+    def step():
+        for m in mats:
+            launch(ctx, m, 0, stream)
+
+    fn = step
+    if use_graph:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step_stream = ctypes.c_void_p(s.cuda_stream)
+            for m in mats:  # warm the kernels outside capture
+                launch(ctx, m, 0, step_stream)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                for m in mats:
+                    launch(ctx, m, 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        fn = g.replay
+    sec = time_steps(torch, fn, steps, warmup)
+    step_bytes = sum(m.bytes() for m in mats)
+    kt = per_launch_times(torch, ctx, mats, 0, stream, reps=3)
+    return mats, host_layer0, sec, step_bytes, kt
+
+
+def bench_config1(torch, ctx, stream, reps=200):
+    """Single Q4_K GEMV 8192x2048; 32 distinct HBM copies rotated."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1)
+    dev, _ = make_weight(torch, gen, Q4K, 8192, 2048)
+    copies = [dev.clone() for _ in range(32)]
+    x = torch.randn((1, 2048), device="cuda")
+    mats = [Mat(torch, f"c1.{i}", Q4K, 8192, 2048, c, x=x) for i, c in enumerate(copies)]
+
+    def run():
+        for m in mats:
+            launch(ctx, m, 0, stream)
+
+    sec = time_steps(torch, run, max(1, reps // 32), 2) / len(mats)
+    kt = per_launch_times(torch, ctx, mats, 0, stream, reps=2)
+    kmean = sum(kt) / len(kt)
+    b = mats[0].bytes()
+    return {"workload": "Q4_K GEMV 8192x2048 batch 1 fp32 (32 rotated copies)", "bytes_per_call": b,
+            "us_per_call_wall": sec * 1e6, "us_per_kernel_event": kmean * 1e6,
+            "GBps": b / kmean / 1e9, "frac_hbm_peak": b / kmean / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_prefill(torch, ctx, stream, steps=3):
+    """28 layers of Q8_0 matmuls on 512 tokens, per-row int8
+    activations (reference XDNA semantics) -> int8 MFMA GEMM."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2)
+    layer = []
+    for name, t, N, K in QWEN_LAYER:
+        dev, _ = make_weight(torch, gen, t, N, K)
+        layer.append((name, t, N, K, dev))
+    xs = {K: torch.randn((PREFILL_TOKENS, K), device="cuda") for K in (1536, 8960)}
+    mats = []
+    for li in range(QWEN_LAYERS):
+        for name, t, N, K, dev in layer:
+            w = dev if li == 0 else dev.clone()
+            mats.append(Mat(torch, f"blk{li}.{name}", t, N, K, w, M=PREFILL_TOKENS, x=xs[K]))
+
+    def run():
+        for m in mats:
+            launch(ctx, m, 1, stream)
+
+    sec = time_steps(torch, run, steps, 1)
+    ops = sum(2 * m.M * m.N * m.K for m in mats)
+    return {"workload": "Qwen2.5-1.5B Q8_0 prefill, 512 tokens x 28 layers, per-row int8 activations",
+            "int8_ops": ops, "ms_per_step": sec * 1e3, "TOPS": ops / sec / 1e12,
+            "frac_int8_peak": ops / sec / 1e12 / INT8_PEAK_TOPS}
+
+
+def cpu_baseline(host_layer0, budget_s=8.0):
+    """Single-core fp32 CpuRefBackend::mul_mat_q restatement (oracle, bit-exact
+    with the reference's output) on layer 0 of the decode step."""
+    from oracle import oracle as orc
+    rng = np.random.default_rng(0)
+    work = [(m.t, raw, m.N, m.K, rng.standard_normal((1, m.K)).astype(np.float32)) for m, raw in host_layer0]
+    nbytes, t0, reps = 0, time.perf_counter(), 0
+    while True:
+        for t, raw, N, K, A in work:
+            orc.mul_mat_cpuref_f32(t, raw, N, K, A)
+            nbytes += gl.row_bytes(t, K) * N + 4 * (K + N)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    el = time.perf_counter() - t0
+    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"Llama-3.2-1B layer 0 (q,k,v,o,gate,up,down; 38.8 MB Q4_K/Q6_K), batch 1, "
+                      f"{reps} passes in {el:.1f}s, oracle/ggq_oracle.c orc_mul_mat_cpuref_f32"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
+    ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the backend is a single-device hot path "
+              "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    ctx = gl.Context(0)
+    # All work runs on one non-default stream: kernels are launched on it and
+    # the HIP events are recorded on it (a null handle would select the
+    # library's own stream, which the events would not see).
+    side = torch.cuda.Stream()
+    torch.cuda.set_stream(side)
+    stream = ctypes.c_void_p(side.cuda_stream)
+    assert stream.value, "expected a non-null stream handle"
+
+    mats, host_layer0, sec, step_bytes, kt = bench_decode_step(torch, ctx, args.steps, args.warmup,
+                                                               args.graph, stream)
+    value = step_bytes / sec / 1e9
+    ktot = sum(kt)
+    achieved = step_bytes / ktot / 1e9
+    out = {
+        "metric": "Q4_K GEMV HBM GB/s (% of peak); prefill int8 GEMM TOPS (% MFMA peak)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 activations x Q4_K/Q6_K raw blocks (fp32 accumulate)",
+        "data": "synthetic: seeded N(0,0.02) weights encoded to GGUF blocks, N(0,1) activations",
+        "config": {"workload": "Llama-3.2-1B decode step matmuls (configs[1]): 16 layers q/k/v/o/gate/up/down "
+                               "Q4_K (v, down Q6_K) + 128256x2048 Q4_K output, batch 1",
+                   "matmuls_per_step": len(mats), "bytes_per_step": step_bytes,
+                   "graph": bool(args.graph)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_kernel (sum of per-launch HIP-event durations over one step)",
+                     "kernel_us_per_step": round(ktot * 1e6, 1)},
+    }
+    if not args.no_extra:
+        out["extra"] = {"config1": bench_config1(torch, ctx, stream)}
+        try:
+            out["extra"]["config3_prefill"] = bench_prefill(torch, ctx, stream)
+        except Exception as e:  # reported, never silently replaced
+            out["extra"]["config3_prefill"] = {"error": str(e)}
+        out["cpu_baseline"] = cpu_baseline(host_layer0)
+    per = {}
+    for m, d in zip(mats[:7], kt[:7]):
+        per[m.name.split(".")[1]] = {"us": round(d * 1e6, 2), "GBps": round(m.bytes() / d / 1e9, 1)}
+    per["output"] = {"us": round(kt[-1] * 1e6, 2), "GBps": round(mats[-1].bytes() / kt[-1] / 1e9, 1)}
+    out["per_matmul_layer0"] = per
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,450 @@
+// ggq_api.cpp -- implementation of the C ABI in include/ggq.h.
+//
+// Control plane of the backend: validates shapes, owns HBM-resident raw
+// weights and a growable workspace, and queues the kernels of
+// ggq_kernels.hip on a HIP stream.  Replaces the host tile loop of the XDNA
+// backend (src/backends/amd_xdna/amd_xdna.cpp:491-952): there is no host
+// re-quantization, no tiling on the host and no per-tile readback; one
+// launch covers a whole matmul.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <new>
+#include <set>
+#include <string>
+#include <tuple>
+
+#include "../../include/ggq.h"
+#include "ggq_formats.h"
+#include "ggq_launch.h"
+
+struct ggq_weight {
+    void* dev = nullptr;
+    uint32_t type = 0;
+    int64_t N = 0, K = 0;
+    size_t bytes = 0;
+};
+
+namespace {
+
+struct Buffer {
+    void* ptr = nullptr;
+    size_t size = 0;
+};
+
+}  // namespace
+
+struct ggq_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::recursive_mutex mu;
+    int last = GGQ_OK;
+    std::string msg;
+    std::map<std::tuple<const void*, uint32_t, int64_t, int64_t>, ggq_weight*> cache;
+    std::set<ggq_weight*> weights;
+    Buffer ws;  // kernel workspace (activation quant, MoE intermediates)
+    Buffer io;  // staging of host A / C for the synchronous entry points
+};
+
+namespace {
+
+using ggq::block_bytes;
+using ggq::block_elems;
+
+int set_status(ggq_ctx* c, int st, const char* fmt = nullptr, ...) {
+    c->last = st;
+    c->msg.clear();
+    if (fmt) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        c->msg = buf;
+    }
+    return st;
+}
+
+int hip_status(ggq_ctx* c, hipError_t e, const char* what) {
+    if (e == hipSuccess) return set_status(c, GGQ_OK);
+    const int st = e == hipErrorOutOfMemory ? GGQ_OUT_OF_MEMORY : GGQ_ERROR;
+    return set_status(c, st, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Grows `b` to at least `need` bytes.  Work queued earlier may still use the
+// old allocation, so the device is drained before it is released.
+hipError_t ensure(Buffer& b, size_t need) {
+    if (b.size >= need) return hipSuccess;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    if (b.ptr) hipFree(b.ptr);
+    b.ptr = nullptr;
+    b.size = 0;
+    size_t sz = need + need / 4 + 4096;
+    e = hipMalloc(&b.ptr, sz);
+    if (e != hipSuccess) return e;
+    b.size = sz;
+    return hipSuccess;
+}
+
+inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+hipStream_t pick_stream(ggq_ctx* c, void* s) { return s ? (hipStream_t)s : c->stream; }
+
+int check_matmul_shape(ggq_ctx* c, uint32_t type, int64_t N, int64_t K, int M, int lda, int ldc,
+                       int act_mode) {
+    if (!ggq::supported(type)) return set_status(c, GGQ_INVALID_PARAM, "unsupported weight type %u", type);
+    if (N <= 0 || K <= 0 || M < 0) return set_status(c, GGQ_INVALID_PARAM, "bad shape N=%lld K=%lld M=%d", (long long)N, (long long)K, M);
+    if (K % block_elems(type)) return set_status(c, GGQ_INVALID_PARAM, "K=%lld not a multiple of the block size %d", (long long)K, block_elems(type));
+    if (N > INT32_MAX || K > ggq::kGemvMaxK) return set_status(c, GGQ_INVALID_PARAM, "K=%lld exceeds the supported maximum %d", (long long)K, ggq::kGemvMaxK);
+    if (lda < K || ldc < N) return set_status(c, GGQ_INVALID_PARAM, "lda/ldc smaller than K/N");
+    if (act_mode < GGQ_ACT_F32 || act_mode > GGQ_ACT_Q8_BLOCK32) return set_status(c, GGQ_INVALID_PARAM, "bad act_mode %d", act_mode);
+    return GGQ_OK;
+}
+
+// Queues C = A . W^T with the requested activation treatment.
+int mul_mat_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const float* A,
+                  int lda, float* C, int ldc, int M, int act_mode, hipStream_t s) {
+    if (M == 0) return set_status(c, GGQ_OK);
+    hipError_t e;
+    ggq::GemvProblem g{};
+    g.type = type;
+    g.W = W;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.Y = C;
+    g.ldy = ldc;
+    g.M = M;
+    g.groups = 1;
+    if (act_mode == GGQ_ACT_F32) {
+        g.X = A;
+        g.ldx = lda;
+        return hip_status(c, ggq::launch_gemv(g, s), "gemv");
+    }
+    const size_t q_off = 0;
+    const size_t s_off = align256(q_off + (size_t)M * K);
+    const size_t x_off = align256(s_off + sizeof(float) * (size_t)M * (K / 32));
+    const bool use_gemm = act_mode == GGQ_ACT_Q8_ROW && M > 8;
+    const size_t need = use_gemm ? x_off : align256(x_off + sizeof(float) * (size_t)M * K);
+    if ((e = ensure(c->ws, need)) != hipSuccess) return hip_status(c, e, "workspace");
+    int8_t* q = (int8_t*)c->ws.ptr + q_off;
+    float* sc = (float*)((char*)c->ws.ptr + s_off);
+    float* xe = (float*)((char*)c->ws.ptr + x_off);
+    if (use_gemm) {
+        if ((e = ggq::launch_quant_act(A, lda, M, (int)K, act_mode, q, sc, nullptr, s)) != hipSuccess)
+            return hip_status(c, e, "quant_act");
+        return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, q, sc, M, C, ldc, s), "gemm_i8");
+    }
+    if ((e = ggq::launch_quant_act(A, lda, M, (int)K, act_mode, nullptr, nullptr, xe, s)) != hipSuccess)
+        return hip_status(c, e, "quant_act");
+    g.X = xe;
+    g.ldx = (int)K;
+    return hip_status(c, ggq::launch_gemv(g, s), "gemv");
+}
+
+ggq_weight* upload(ggq_ctx* c, const void* raw, uint32_t type, int64_t N, int64_t K, int* st) {
+    const size_t bytes = (size_t)N * (size_t)ggq::row_bytes(type, K);
+    ggq_weight* w = new (std::nothrow) ggq_weight;
+    if (!w) { *st = set_status(c, GGQ_OUT_OF_MEMORY, "host allocation"); return nullptr; }
+    hipError_t e = hipMalloc(&w->dev, bytes + ggq::kWeightPad);
+    if (e == hipSuccess) e = hipMemsetAsync((char*)w->dev + bytes, 0, ggq::kWeightPad, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(w->dev, raw, bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        if (w->dev) hipFree(w->dev);
+        delete w;
+        *st = hip_status(c, e, "weight upload");
+        return nullptr;
+    }
+    w->type = type;
+    w->N = N;
+    w->K = K;
+    w->bytes = bytes;
+    c->weights.insert(w);
+    *st = set_status(c, GGQ_OK);
+    return w;
+}
+
+// Synchronous host-pointer matmul against a resident weight.
+int mul_mat_host(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float* C, int ldc, int M,
+                 int act_mode) {
+    int st = check_matmul_shape(c, w->type, w->N, w->K, M, lda, ldc, act_mode);
+    if (st != GGQ_OK) return st;
+    if (M == 0) return set_status(c, GGQ_OK);
+    const size_t a_bytes = sizeof(float) * (size_t)M * w->K;
+    const size_t c_bytes = sizeof(float) * (size_t)M * w->N;
+    hipError_t e = ensure(c->io, align256(a_bytes) + c_bytes);
+    if (e != hipSuccess) return hip_status(c, e, "io buffer");
+    float* dA = (float*)c->io.ptr;
+    float* dC = (float*)((char*)c->io.ptr + align256(a_bytes));
+    e = hipMemcpy2DAsync(dA, sizeof(float) * w->K, A, sizeof(float) * (size_t)lda, sizeof(float) * w->K, M,
+                         hipMemcpyHostToDevice, c->stream);
+    if (e != hipSuccess) return hip_status(c, e, "copy A");
+    st = mul_mat_queue(c, w->dev, w->type, w->N, w->K, dA, (int)w->K, dC, (int)w->N, M, act_mode, c->stream);
+    if (st != GGQ_OK) return st;
+    e = hipMemcpy2DAsync(C, sizeof(float) * (size_t)ldc, dC, sizeof(float) * w->N, sizeof(float) * w->N, M,
+                         hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return hip_status(c, e, "copy C");
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+#define GGQ_GUARD(ctx)                                   \
+    if (!(ctx)) return GGQ_INVALID_PARAM;                \
+    std::lock_guard<std::recursive_mutex> lock_((ctx)->mu); \
+    hipSetDevice((ctx)->device);                         \
+    try {
+#define GGQ_END(ctx)                                                             \
+    }                                                                           \
+    catch (const std::bad_alloc&) {                                             \
+        return set_status(ctx, GGQ_OUT_OF_MEMORY, "host allocation failed");   \
+    }                                                                           \
+    catch (...) {                                                               \
+        return set_status(ctx, GGQ_ERROR, "internal error");                   \
+    }                                                                           \
+    return set_status(ctx, GGQ_ERROR, "unreachable");
+
+extern "C" {
+
+int ggq_create(int device, ggq_ctx** out) {
+    if (!out) return GGQ_INVALID_PARAM;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return GGQ_DEVICE_UNAVAILABLE;
+    ggq_ctx* c = new (std::nothrow) ggq_ctx;
+    if (!c) return GGQ_OUT_OF_MEMORY;
+    c->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return GGQ_DEVICE_UNAVAILABLE;
+    }
+    *out = c;
+    return GGQ_OK;
+}
+
+void ggq_destroy(ggq_ctx* c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipDeviceSynchronize();
+    for (ggq_weight* w : c->weights) {
+        hipFree(w->dev);
+        delete w;
+    }
+    if (c->ws.ptr) hipFree(c->ws.ptr);
+    if (c->io.ptr) hipFree(c->io.ptr);
+    hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int ggq_last_error(const ggq_ctx* c) { return c ? c->last : GGQ_INVALID_PARAM; }
+const char* ggq_last_error_message(const ggq_ctx* c) { return c ? c->msg.c_str() : "null context"; }
+const char* ggq_name(const ggq_ctx*) { return "hip_gfx950"; }
+int ggq_is_available(const ggq_ctx* c) { return c != nullptr; }
+
+int ggq_sync(ggq_ctx* c) {
+    GGQ_GUARD(c)
+    return hip_status(c, hipStreamSynchronize(c->stream), "sync");
+    GGQ_END(c)
+}
+
+int64_t ggq_row_bytes(uint32_t type, int64_t K) {
+    if (!ggq::supported(type) || K <= 0 || K % block_elems(type)) return 0;
+    return ggq::row_bytes(type, K);
+}
+
+int ggq_weight_upload(ggq_ctx* c, const void* raw, uint32_t type, int64_t N, int64_t K, ggq_weight** out) {
+    GGQ_GUARD(c)
+    if (!raw || !out) return set_status(c, GGQ_INVALID_PARAM, "null pointer");
+    *out = nullptr;
+    int st = check_matmul_shape(c, type, N, K, 0, (int)K, (int)N, GGQ_ACT_F32);
+    if (st != GGQ_OK) return st;
+    *out = upload(c, raw, type, N, K, &st);
+    return st;
+    GGQ_END(c)
+}
+
+int ggq_weight_free(ggq_ctx* c, ggq_weight* w) {
+    GGQ_GUARD(c)
+    if (!w || !c->weights.count(w)) return set_status(c, GGQ_INVALID_PARAM, "unknown weight");
+    hipError_t e = hipStreamSynchronize(c->stream);
+    for (auto it = c->cache.begin(); it != c->cache.end();)
+        it = it->second == w ? c->cache.erase(it) : std::next(it);
+    c->weights.erase(w);
+    hipFree(w->dev);
+    delete w;
+    return hip_status(c, e, "weight free");
+    GGQ_END(c)
+}
+
+const void* ggq_weight_device_ptr(const ggq_weight* w) { return w ? w->dev : nullptr; }
+
+int ggq_mul_mat(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float* C, int ldc, int M,
+                int act_mode) {
+    GGQ_GUARD(c)
+    if (!w || !c->weights.count(const_cast<ggq_weight*>(w))) return set_status(c, GGQ_INVALID_PARAM, "unknown weight");
+    if (!A || !C) return set_status(c, GGQ_INVALID_PARAM, "null A/C");
+    return mul_mat_host(c, w, A, lda ? lda : (int)w->K, C, ldc ? ldc : (int)w->N, M, act_mode);
+    GGQ_END(c)
+}
+
+int ggq_mul_mat_q(ggq_ctx* c, const ggq_mul_mat_params* p, int act_mode) {
+    GGQ_GUARD(c)
+    // Null A/B/C -> INVALID_PARAM, as cpu_ref.cpp:26 and amd_xdna.cpp:492-495.
+    if (!p || !p->A || !p->B || !p->C) return set_status(c, GGQ_INVALID_PARAM, "null A/B/C");
+    if (p->scales || p->n_weight_scales)
+        return set_status(c, GGQ_INVALID_PARAM, "re-quantized weight scales are not used by this backend");
+    const int lda = p->lda ? p->lda : p->K, ldc = p->ldc ? p->ldc : p->N;
+    int st = check_matmul_shape(c, p->B_type, p->N, p->K, p->M, lda, ldc, act_mode);
+    if (st != GGQ_OK) return st;
+    const auto key = std::make_tuple(p->B, p->B_type, (int64_t)p->N, (int64_t)p->K);
+    auto it = c->cache.find(key);
+    ggq_weight* w;
+    if (it != c->cache.end()) {
+        w = it->second;
+    } else {
+        w = upload(c, p->B, p->B_type, p->N, p->K, &st);
+        if (!w) return st;
+        c->cache[key] = w;
+    }
+    return mul_mat_host(c, w, (const float*)p->A, lda, (float*)p->C, ldc, p->M, act_mode);
+    GGQ_END(c)
+}
+
+int ggq_mul_mat_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const float* A, int lda,
+                    float* C, int ldc, int M, int act_mode, void* stream) {
+    GGQ_GUARD(c)
+    if (!W || !A || !C) return set_status(c, GGQ_INVALID_PARAM, "null W/A/C");
+    if (!aligned16(W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
+    int st = check_matmul_shape(c, type, N, K, M, lda, ldc, act_mode);
+    if (st != GGQ_OK) return st;
+    return mul_mat_queue(c, W, type, N, K, A, lda, C, ldc, M, act_mode, pick_stream(c, stream));
+    GGQ_END(c)
+}
+
+int ggq_dequant_dev(ggq_ctx* c, const void* raw, uint32_t type, int64_t n_blocks, float* out, void* stream) {
+    GGQ_GUARD(c)
+    if (!raw || !out || n_blocks < 0) return set_status(c, GGQ_INVALID_PARAM, "bad arguments");
+    if (!ggq::supported(type)) return set_status(c, GGQ_INVALID_PARAM, "unsupported weight type %u", type);
+    if (!aligned16(raw) || !aligned16(out)) return set_status(c, GGQ_INVALID_PARAM, "raw/out must be 16-byte aligned");
+    return hip_status(c, ggq::launch_dequant(type, raw, n_blocks, out, pick_stream(c, stream)), "dequant");
+    GGQ_END(c)
+}
+
+int ggq_quantize_act_dev(ggq_ctx* c, const float* A, int lda, int M, int K, int act_mode, int8_t* q,
+                         float* scales, void* stream) {
+    GGQ_GUARD(c)
+    if (!A || !q || !scales || M < 0 || K <= 0 || lda < K) return set_status(c, GGQ_INVALID_PARAM, "bad arguments");
+    if (act_mode != GGQ_ACT_Q8_ROW && act_mode != GGQ_ACT_Q8_BLOCK32)
+        return set_status(c, GGQ_INVALID_PARAM, "act_mode must be Q8_ROW or Q8_BLOCK32");
+    if (act_mode == GGQ_ACT_Q8_BLOCK32 && K % 32) return set_status(c, GGQ_INVALID_PARAM, "K must be a multiple of 32");
+    return hip_status(c, ggq::launch_quant_act(A, lda, M, K, act_mode, q, scales, nullptr, pick_stream(c, stream)),
+                      "quant_act");
+    GGQ_END(c)
+}
+
+int ggq_block_dot_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const int8_t* qa, int M,
+                      int32_t* out, void* stream) {
+    GGQ_GUARD(c)
+    if (!W || !qa || !out) return set_status(c, GGQ_INVALID_PARAM, "null pointer");
+    if (!aligned16(W) || ((uintptr_t)qa & 15u) || (K % 16)) return set_status(c, GGQ_INVALID_PARAM, "alignment");
+    int st = check_matmul_shape(c, type, N, K, M, (int)K, (int)N, GGQ_ACT_F32);
+    if (st != GGQ_OK) return st;
+    return hip_status(c, ggq::launch_block_dot(type, W, (int)N, (int)K, qa, M, out, pick_stream(c, stream)), "block_dot");
+    GGQ_END(c)
+}
+
+int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
+    GGQ_GUARD(c)
+    if (!p || !p->x || !p->router_logits || !p->gate_exps || !p->up_exps || !p->down_exps || !p->out)
+        return set_status(c, GGQ_INVALID_PARAM, "null pointer");
+    const int T = p->T, H = p->H, F = p->F, E = p->E, k = p->top_k;
+    if (T < 0 || H <= 0 || F <= 0 || E <= 0 || E > 1024 || k <= 0 || k > 64 || k > E || (int64_t)T * k > 65536)
+        return set_status(c, GGQ_INVALID_PARAM, "bad MoE shape");
+    int st;
+    if ((st = check_matmul_shape(c, p->gate_type, F, H, T, H, F, 0)) != GGQ_OK) return st;
+    if ((st = check_matmul_shape(c, p->up_type, F, H, T, H, F, 0)) != GGQ_OK) return st;
+    if ((st = check_matmul_shape(c, p->down_type, H, F, T, F, H, 0)) != GGQ_OK) return st;
+    const bool shared = p->gate_shexp != nullptr;
+    if (shared && (!p->up_shexp || !p->down_shexp)) return set_status(c, GGQ_INVALID_PARAM, "partial shared expert");
+    for (const void* w : {p->gate_exps, p->up_exps, p->down_exps, p->gate_shexp, p->up_shexp, p->down_shexp})
+        if (w && !aligned16(w)) return set_status(c, GGQ_INVALID_PARAM, "weights must be 16-byte aligned");
+    if (T == 0) return set_status(c, GGQ_OK);
+    hipStream_t s = pick_stream(c, stream);
+
+    const size_t nk = (size_t)T * k;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off = align256(off + bytes); return o; };
+    const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 1)),
+                 o_tok = take(4 * nk), o_pos = take(4 * nk), o_g = take(4 * nk * F), o_u = take(4 * nk * F),
+                 o_h = take(4 * nk * F), o_d = take(4 * nk * H);
+    size_t o_sg = 0, o_su = 0, o_sh = 0, o_sd = 0;
+    if (shared) {
+        o_sg = take(4 * (size_t)T * F);
+        o_su = take(4 * (size_t)T * F);
+        o_sh = take(4 * (size_t)T * F);
+        o_sd = take(4 * (size_t)T * H);
+    }
+    hipError_t e = ensure(c->ws, off);
+    if (e != hipSuccess) return hip_status(c, e, "workspace");
+    char* base = (char*)c->ws.ptr;
+    int32_t* sel = (int32_t*)(base + o_sel);
+    float* wsel = (float*)(base + o_w);
+    int32_t* grp = (int32_t*)(base + o_go);
+    int32_t* tok = (int32_t*)(base + o_tok);
+    int32_t* pos = (int32_t*)(base + o_pos);
+    float *G = (float*)(base + o_g), *U = (float*)(base + o_u), *Hh = (float*)(base + o_h), *D = (float*)(base + o_d);
+
+    if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s)) != hipSuccess) return hip_status(c, e, "moe_group");
+
+    ggq::GemvProblem g{};
+    g.groups = E;
+    g.grp_off = grp;
+    g.M = (int)nk;
+    g.max_group_rows = T;
+    // gate / up: rows F, K = H, activations gathered by token.
+    g.N = F; g.K = H; g.X = p->x; g.ldx = H; g.x_idx = tok; g.ldy = F;
+    g.type = p->gate_type; g.W = p->gate_exps; g.w_group_stride = (int64_t)F * ggq::row_bytes(p->gate_type, H); g.Y = G;
+    if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe gate");
+    g.type = p->up_type; g.W = p->up_exps; g.w_group_stride = (int64_t)F * ggq::row_bytes(p->up_type, H); g.Y = U;
+    if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe up");
+    if ((e = ggq::launch_swiglu(G, U, Hh, (int64_t)nk * F, s)) != hipSuccess) return hip_status(c, e, "swiglu");
+    // down: rows H, K = F, activations are the sorted pair rows themselves.
+    g.N = H; g.K = F; g.X = Hh; g.ldx = F; g.x_idx = nullptr; g.ldy = H; g.Y = D;
+    g.type = p->down_type; g.W = p->down_exps; g.w_group_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
+    if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe down");
+
+    float* Dsh = nullptr;
+    if (shared) {
+        float *SG = (float*)(base + o_sg), *SU = (float*)(base + o_su), *SH = (float*)(base + o_sh);
+        Dsh = (float*)(base + o_sd);
+        ggq::GemvProblem q{};
+        q.groups = 1;
+        q.M = T;
+        q.N = F; q.K = H; q.X = p->x; q.ldx = H; q.ldy = F;
+        q.type = p->gate_type; q.W = p->gate_shexp; q.Y = SG;
+        if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared gate");
+        q.type = p->up_type; q.W = p->up_shexp; q.Y = SU;
+        if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared up");
+        if ((e = ggq::launch_swiglu(SG, SU, SH, (int64_t)T * F, s)) != hipSuccess) return hip_status(c, e, "shared swiglu");
+        q.N = H; q.K = F; q.X = SH; q.ldx = F; q.ldy = H; q.type = p->down_type; q.W = p->down_shexp; q.Y = Dsh;
+        if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared down");
+    }
+    if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, Dsh, p->shared_w, p->out, s)) != hipSuccess)
+        return hip_status(c, e, "moe combine");
+    if (p->sel_experts && (e = hipMemcpyAsync(p->sel_experts, sel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_status(c, e, "copy selection");
+    if (p->sel_weights && (e = hipMemcpyAsync(p->sel_weights, wsel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_status(c, e, "copy weights");
+    return set_status(c, GGQ_OK);
+    GGQ_END(c)
+}
+
+}  // extern "C"

@@ -1,0 +1,469 @@
+// ggq_device.h -- device-side decoding of raw GGUF blocks for CDNA4 (gfx950).
+//
+// Three views of the same block formats live here:
+//   * codes16<T>(row, k): 16 signed int8 "codes" for values k..k+15 of a row,
+//     packed 4 per dword in natural k order.  Codes are the integers the
+//     format scales: Q4_K nibble, Q5_K 5-bit value, Q6_K (6-bit - 32), Q8_0
+//     int8, IQ4_NL/IQ4_XS codebook entry.  Used by the bit-exact dequant
+//     kernel, the int32 block-dot kernel and the int8-MFMA GEMM.
+//   * group scales (dl, ml) per scale group, computed exactly as the
+//     reference does (fp16 -> fp32, then one rounded fp32 multiply).
+//   * Piece<T>: the decode-GEMV view.  A piece is 32 values of one row laid
+//     out as two runs of 16 consecutive k; it is decoded to unsigned byte codes
+//     u plus four coefficients so that
+//        sum_k x_k w_k = a0*sum(x_run0*u0) + b0*sum(x_run0)
+//                      + a1*sum(x_run1*u1) + b1*sum(x_run1).
+//     Signed codes are biased to unsigned bytes (v_cvt_f32_ubyteN converts
+//     them in one instruction) and the bias is removed through b*sum(x).
+//
+// Format references (ggnpu): include/ggnpu/quant/kquant.h:9-20 (K-quant
+// layouts), :56-64 (6-bit scale/min packing), :133-202 (dequant order),
+// src/quant/q8_0.cpp:19-25, src/quant/iq4_nl.cpp:16-31,
+// src/quant/iq4_xs.cpp:21-38.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "ggq_formats.h"
+
+namespace ggq {
+
+// ---------------------------------------------------------------- loads --
+
+// Unaligned 16-byte load: reads the dword-aligned window that covers
+// [p, p+16) (5 dwords, at most 4 bytes past p+16) and realigns it with
+// v_alignbyte.  Pointer arithmetic (not integer casts) keeps the global
+// address space, so these are global_load_dword* instructions.
+__device__ __forceinline__ uint4 ld16_u(const uint8_t* p) {
+    const uint32_t s = (uint32_t)(uintptr_t)p & 3u;
+    const uint32_t* q = (const uint32_t*)(p - s);
+    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2], d3 = q[3], d4 = q[4];
+    uint4 r;
+    r.x = __builtin_amdgcn_alignbyte(d1, d0, s);
+    r.y = __builtin_amdgcn_alignbyte(d2, d1, s);
+    r.z = __builtin_amdgcn_alignbyte(d3, d2, s);
+    r.w = __builtin_amdgcn_alignbyte(d4, d3, s);
+    return r;
+}
+
+// Unaligned 8-byte load (3 dwords window).
+__device__ __forceinline__ uint2 ld8_u(const uint8_t* p) {
+    const uint32_t s = (uint32_t)(uintptr_t)p & 3u;
+    const uint32_t* q = (const uint32_t*)(p - s);
+    const uint32_t d0 = q[0], d1 = q[1], d2 = q[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, s), __builtin_amdgcn_alignbyte(d2, d1, s));
+}
+
+// 16-bit little-endian load from an even address.
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *(const uint16_t*)p; }
+
+__device__ __forceinline__ uint4 ld16_a(const uint8_t* p) { return *(const uint4*)p; }
+
+// Exact IEEE half -> float (v_cvt_f32_f16; fp16 subnormals are preserved).
+__device__ __forceinline__ float h2f(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+__device__ __forceinline__ uint32_t byte_at(uint32_t w0, uint32_t w1, uint32_t w2, int i) {
+    const uint32_t w = i < 4 ? w0 : (i < 8 ? w1 : w2);
+    return (w >> (8 * (i & 3))) & 0xFFu;
+}
+
+// 6-bit scale and min of sub-block j (0..7) from the 12 packed bytes held in
+// w0..w2 (Q4_K/Q5_K header bytes 4..15).  j<4: low 6 bits of bytes j and
+// j+4.  j>=4: low nibble / high nibble of byte j+4, plus the top two bits of
+// bytes j-4 (scale) and j (min).
+__device__ __forceinline__ void kq_scale_min(uint32_t w0, uint32_t w1, uint32_t w2, int j,
+                                             uint32_t& sc, uint32_t& m) {
+    if (j < 4) {
+        sc = byte_at(w0, w1, w2, j) & 63u;
+        m = byte_at(w0, w1, w2, j + 4) & 63u;
+    } else {
+        const uint32_t c = byte_at(w0, w1, w2, j + 4);
+        sc = (c & 15u) | ((byte_at(w0, w1, w2, j - 4) >> 6) << 4);
+        m = (c >> 4) | ((byte_at(w0, w1, w2, j) >> 6) << 4);
+    }
+}
+
+// ---------------------------------------------------- IQ4 codebook lookup --
+// Codebook of IQ4_NL/IQ4_XS (src/quant/iq4_nl.cpp:16-18), packed 4 per dword
+// little-endian.  kIq4S: signed entries.  kIq4U: entries + 128 (unsigned).
+#define GGQ_IQ4S0 0xBFAD9881u  // -127 -104 -83 -65
+#define GGQ_IQ4S1 0xF6EADDCFu  //  -49  -35 -22 -10
+#define GGQ_IQ4S2 0x26190D01u  //    1   13  25  38
+#define GGQ_IQ4S3 0x71594535u  //   53   69  89 113
+#define GGQ_IQ4U0 0x3F2D1801u
+#define GGQ_IQ4U1 0x766A5D4Fu
+#define GGQ_IQ4U2 0xA6998D81u
+#define GGQ_IQ4U3 0xF1D9C5B5u
+
+// Per-byte table lookup of 4 nibbles (one per byte, values 0..15): v_perm
+// picks from the 8-byte half tables, v_bfi merges on bit 3.
+__device__ __forceinline__ uint32_t lut16(uint32_t nib, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
+    const uint32_t msk = ((nib >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & msk) | (lo & ~msk);
+}
+
+__device__ __forceinline__ uint4 lut16x4(uint4 n, bool biased) {
+    uint4 r;
+    if (biased) {
+        r.x = lut16(n.x, GGQ_IQ4U0, GGQ_IQ4U1, GGQ_IQ4U2, GGQ_IQ4U3);
+        r.y = lut16(n.y, GGQ_IQ4U0, GGQ_IQ4U1, GGQ_IQ4U2, GGQ_IQ4U3);
+        r.z = lut16(n.z, GGQ_IQ4U0, GGQ_IQ4U1, GGQ_IQ4U2, GGQ_IQ4U3);
+        r.w = lut16(n.w, GGQ_IQ4U0, GGQ_IQ4U1, GGQ_IQ4U2, GGQ_IQ4U3);
+    } else {
+        r.x = lut16(n.x, GGQ_IQ4S0, GGQ_IQ4S1, GGQ_IQ4S2, GGQ_IQ4S3);
+        r.y = lut16(n.y, GGQ_IQ4S0, GGQ_IQ4S1, GGQ_IQ4S2, GGQ_IQ4S3);
+        r.z = lut16(n.z, GGQ_IQ4S0, GGQ_IQ4S1, GGQ_IQ4S2, GGQ_IQ4S3);
+        r.w = lut16(n.w, GGQ_IQ4S0, GGQ_IQ4S1, GGQ_IQ4S2, GGQ_IQ4S3);
+    }
+    return r;
+}
+
+__device__ __forceinline__ uint4 and4(uint4 v, uint32_t m) { return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m); }
+__device__ __forceinline__ uint4 shr4(uint4 v, uint32_t s) { return make_uint4(v.x >> s, v.y >> s, v.z >> s, v.w >> s); }
+__device__ __forceinline__ uint4 or4(uint4 a, uint4 b) { return make_uint4(a.x | b.x, a.y | b.y, a.z | b.z, a.w | b.w); }
+__device__ __forceinline__ uint4 xor4(uint4 v, uint32_t m) { return make_uint4(v.x ^ m, v.y ^ m, v.z ^ m, v.w ^ m); }
+__device__ __forceinline__ uint4 shl4(uint4 v, uint32_t s) { return make_uint4(v.x << s, v.y << s, v.z << s, v.w << s); }
+
+// 6-bit offset-binary bytes (0..63) -> signed bytes (u - 32): flip bit 5,
+// then copy bit 5 into bits 6-7 (0x20*6 = 0xC0, no carry between bytes).
+__device__ __forceinline__ uint32_t six_to_s8(uint32_t u) {
+    const uint32_t t = u ^ 0x20202020u;
+    return t | ((t & 0x20202020u) * 6u);
+}
+
+// ------------------------------------------------------- codes16<T> ------
+// 16 signed codes for values k..k+15 of the row starting at `row`
+// (k a multiple of 16).
+template <int T> __device__ __forceinline__ uint4 codes16(const uint8_t* row, int k);
+
+template <> __device__ __forceinline__ uint4 codes16<T_Q4_K>(const uint8_t* row, int k) {
+    const uint8_t* b = row + (k >> 8) * 144;
+    const int kk = k & 255, c = kk >> 6, hi = (kk >> 5) & 1, off = kk & 16;
+    const uint4 q = ld16_a(b + 16 + 32 * c + off);
+    return and4(shr4(q, 4 * hi), 0x0F0F0F0Fu);
+}
+
+template <> __device__ __forceinline__ uint4 codes16<T_Q5_K>(const uint8_t* row, int k) {
+    const uint8_t* b = row + (k >> 8) * 176;
+    const int kk = k & 255, c = kk >> 6, hi = (kk >> 5) & 1, off = kk & 16;
+    const uint4 q = ld16_a(b + 48 + 32 * c + off);
+    const uint4 h = ld16_a(b + 16 + off);
+    return or4(and4(shr4(q, 4 * hi), 0x0F0F0F0Fu), shl4(and4(shr4(h, 2 * c + hi), 0x01010101u), 4));
+}
+
+template <> __device__ __forceinline__ uint4 codes16<T_Q6_K>(const uint8_t* row, int k) {
+    const uint8_t* b = row + (k >> 8) * 210;
+    const int kk = k & 255, h = kk >> 7, r = kk & 127, qd = r >> 5, l0 = r & 16;
+    const uint4 ql = ld16_u(b + 64 * h + 32 * (qd & 1) + l0);
+    const uint4 qh = ld16_u(b + 128 + 32 * h + l0);
+    const uint4 u = or4(and4(shr4(ql, 4 * (qd >> 1)), 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * qd), 0x03030303u), 4));
+    return make_uint4(six_to_s8(u.x), six_to_s8(u.y), six_to_s8(u.z), six_to_s8(u.w));
+}
+
+template <> __device__ __forceinline__ uint4 codes16<T_Q8_0>(const uint8_t* row, int k) {
+    return ld16_u(row + (k >> 5) * 34 + 2 + (k & 16));
+}
+
+template <> __device__ __forceinline__ uint4 codes16<T_IQ4_NL>(const uint8_t* row, int k) {
+    const uint4 q = ld16_u(row + (k >> 5) * 18 + 2);
+    return lut16x4(and4(shr4(q, (k & 16) >> 2), 0x0F0F0F0Fu), false);
+}
+
+template <> __device__ __forceinline__ uint4 codes16<T_IQ4_XS>(const uint8_t* row, int k) {
+    const uint8_t* b = row + (k >> 8) * 136;
+    const int ib = (k & 255) >> 5;
+    const uint2 lo = *(const uint2*)(b + 8 + 16 * ib);
+    const uint2 hi = *(const uint2*)(b + 16 + 16 * ib);
+    const uint4 q = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    return lut16x4(and4(shr4(q, (k & 16) >> 2), 0x0F0F0F0Fu), false);
+}
+
+// ------------------------------------------------------ group scales -----
+// Scale (dl) and offset (ml) of the group containing value k, computed with
+// the reference's rounding: dl = d*sc, ml = dmin*m (one fp32 multiply each).
+// Value = dl*code - ml (ml = 0 for formats without a min).
+struct GroupScale { float dl, ml; };
+
+template <int T> __device__ __forceinline__ GroupScale group_scale(const uint8_t* row, int k);
+
+template <> __device__ __forceinline__ GroupScale group_scale<T_Q4_K>(const uint8_t* row, int k) {
+    const uint4 hd = ld16_a(row + (k >> 8) * 144);
+    uint32_t sc, m;
+    kq_scale_min(hd.y, hd.z, hd.w, (k & 255) >> 5, sc, m);
+    return {__fmul_rn(h2f(hd.x & 0xFFFFu), (float)sc), __fmul_rn(h2f(hd.x >> 16), (float)m)};
+}
+
+template <> __device__ __forceinline__ GroupScale group_scale<T_Q5_K>(const uint8_t* row, int k) {
+    const uint4 hd = ld16_a(row + (k >> 8) * 176);
+    uint32_t sc, m;
+    kq_scale_min(hd.y, hd.z, hd.w, (k & 255) >> 5, sc, m);
+    return {__fmul_rn(h2f(hd.x & 0xFFFFu), (float)sc), __fmul_rn(h2f(hd.x >> 16), (float)m)};
+}
+
+template <> __device__ __forceinline__ GroupScale group_scale<T_Q6_K>(const uint8_t* row, int k) {
+    const uint8_t* b = row + (k >> 8) * 210;
+    const int sc = (int)(int8_t)b[192 + ((k & 255) >> 4)];
+    return {__fmul_rn(h2f(ld_u16(b + 208)), (float)sc), 0.0f};
+}
+
+template <> __device__ __forceinline__ GroupScale group_scale<T_Q8_0>(const uint8_t* row, int k) {
+    return {h2f(ld_u16(row + (k >> 5) * 34)), 0.0f};
+}
+
+template <> __device__ __forceinline__ GroupScale group_scale<T_IQ4_NL>(const uint8_t* row, int k) {
+    return {h2f(ld_u16(row + (k >> 5) * 18)), 0.0f};
+}
+
+template <> __device__ __forceinline__ GroupScale group_scale<T_IQ4_XS>(const uint8_t* row, int k) {
+    const uint8_t* b = row + (k >> 8) * 136;
+    const uint2 hd = *(const uint2*)b;
+    const int ib = (k & 255) >> 5;
+    const int ls = (int)(((hd.y >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15u) | (((hd.x >> (16 + 2 * ib)) & 3u) << 4));
+    return {__fmul_rn(h2f(hd.x & 0xFFFFu), (float)(ls - 32)), 0.0f};
+}
+
+// Dequantized value with the reference's operation order (no contraction):
+//   Q4_K/Q5_K: (d*sc)*q - (dmin*m); Q6_K, IQ4_XS: (d*sc)*q;
+//   Q8_0: q*d; IQ4_NL: d*kv.
+__device__ __forceinline__ float dequant_value(GroupScale g, int code) {
+    return __fsub_rn(__fmul_rn(g.dl, (float)code), g.ml);
+}
+
+// ------------------------------------------------------------ pieces -----
+// Decode-GEMV piece: 32 values = two runs of 16 consecutive k.  Pieces of a
+// row are numbered p = 0..K/32-1.  Each format provides
+//   fetch(row, p)  -> Raw: the dwords covering the piece, loaded with plain
+//                     dword-aligned loads and not yet inspected, so a caller
+//                     can keep loads of later rows in flight;
+//   decode(raw, row, p) -> PieceCodes (realignment, unpacking, scales).
+struct PieceCodes {
+    uint4 u0, u1;        // unsigned byte codes of run 0 / run 1
+    float a0, b0, a1, b1;
+};
+
+template <int NW> struct RawW { uint32_t w[NW]; };
+
+__device__ __forceinline__ const uint32_t* align_down4(const uint8_t* p) {
+    return (const uint32_t*)(p - ((uint32_t)(uintptr_t)p & 3u));
+}
+
+template <int N> __device__ __forceinline__ void ld_dw(const uint32_t* q, uint32_t* w) {
+#pragma unroll
+    for (int i = 0; i < N; i++) w[i] = q[i];
+}
+
+__device__ __forceinline__ uint32_t align2(uint32_t hi, uint32_t lo, uint32_t s) {
+    return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+
+template <int T> struct Piece;
+
+// Q4_K: piece j of block b covers qs bytes [32c+16h, +16) (c=j/2, h=j%2):
+// low nibbles are values 64c+16h+i (sub-block 2c), high nibbles values
+// 64c+32+16h+i (sub-block 2c+1).
+template <> struct Piece<T_Q4_K> {
+    typedef RawW<8> Raw;
+    static __device__ __forceinline__ int run0(int p) { return (p >> 3) * 256 + ((p >> 1) & 3) * 64 + (p & 1) * 16; }
+    static constexpr int kRun1 = 32;
+    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
+        const uint8_t* b = row + (p >> 3) * 144;
+        const int c = (p >> 1) & 3, h = p & 1;
+        Raw r;
+        const uint4 hd = ld16_a(b), q = ld16_a(b + 16 + 32 * c + 16 * h);
+        r.w[0] = hd.x; r.w[1] = hd.y; r.w[2] = hd.z; r.w[3] = hd.w;
+        r.w[4] = q.x; r.w[5] = q.y; r.w[6] = q.z; r.w[7] = q.w;
+        return r;
+    }
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t*, int p) {
+        const int c = (p >> 1) & 3;
+        uint32_t sc0, m0, sc1, m1;
+        kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c, sc0, m0);
+        kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c + 1, sc1, m1);
+        const float d = h2f(r.w[0] & 0xFFFFu), dm = h2f(r.w[0] >> 16);
+        const uint4 q = make_uint4(r.w[4], r.w[5], r.w[6], r.w[7]);
+        PieceCodes o;
+        o.u0 = and4(q, 0x0F0F0F0Fu);
+        o.u1 = and4(shr4(q, 4), 0x0F0F0F0Fu);
+        o.a0 = d * (float)sc0; o.b0 = -(dm * (float)m0);
+        o.a1 = d * (float)sc1; o.b1 = -(dm * (float)m1);
+        return o;
+    }
+};
+
+// Q5_K: as Q4_K, plus bits 2c (run 0) and 2c+1 (run 1) of qh[16h+i].
+template <> struct Piece<T_Q5_K> {
+    typedef RawW<12> Raw;
+    static __device__ __forceinline__ int run0(int p) { return Piece<T_Q4_K>::run0(p); }
+    static constexpr int kRun1 = 32;
+    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
+        const uint8_t* b = row + (p >> 3) * 176;
+        const int c = (p >> 1) & 3, h = p & 1;
+        Raw r;
+        const uint4 hd = ld16_a(b), qh = ld16_a(b + 16 + 16 * h), q = ld16_a(b + 48 + 32 * c + 16 * h);
+        r.w[0] = hd.x; r.w[1] = hd.y; r.w[2] = hd.z; r.w[3] = hd.w;
+        r.w[4] = qh.x; r.w[5] = qh.y; r.w[6] = qh.z; r.w[7] = qh.w;
+        r.w[8] = q.x; r.w[9] = q.y; r.w[10] = q.z; r.w[11] = q.w;
+        return r;
+    }
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t*, int p) {
+        const int c = (p >> 1) & 3;
+        uint32_t sc0, m0, sc1, m1;
+        kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c, sc0, m0);
+        kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c + 1, sc1, m1);
+        const float d = h2f(r.w[0] & 0xFFFFu), dm = h2f(r.w[0] >> 16);
+        const uint4 qh = make_uint4(r.w[4], r.w[5], r.w[6], r.w[7]);
+        const uint4 q = make_uint4(r.w[8], r.w[9], r.w[10], r.w[11]);
+        PieceCodes o;
+        o.u0 = or4(and4(q, 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * c), 0x01010101u), 4));
+        o.u1 = or4(and4(shr4(q, 4), 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * c + 1), 0x01010101u), 4));
+        o.a0 = d * (float)sc0; o.b0 = -(dm * (float)m0);
+        o.a1 = d * (float)sc1; o.b1 = -(dm * (float)m1);
+        return o;
+    }
+};
+
+// Q6_K: piece j of block b: half n=j/4, l0=16*((j/2)%2), s=j%2.  ql bytes
+// [64n+32s+l0, +16) low nibbles + qh[32n+l0+i] bits 2s..2s+1 -> values
+// 128n+32s+l0+i (scale sc[8n+l0/16+2s]); the high nibbles + qh bits 4+2s..
+// -> values 128n+64+32s+l0+i (scale index +4).  Codes are 6-bit offset 32.
+// Blocks are 210 bytes, so fields are only 2-byte aligned: each field is
+// fetched as the dword window covering it and realigned in decode.
+template <> struct Piece<T_Q6_K> {
+    typedef RawW<14> Raw;
+    static __device__ __forceinline__ int run0(int p) {
+        return (p >> 3) * 256 + ((p >> 2) & 1) * 128 + (p & 1) * 32 + ((p >> 1) & 1) * 16;
+    }
+    static constexpr int kRun1 = 64;
+    static __device__ __forceinline__ int sc_index(int p) { return 8 * ((p >> 2) & 1) + ((p >> 1) & 1) + 2 * (p & 1); }
+    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
+        const uint8_t* b = row + (p >> 3) * 210;
+        const int n = (p >> 2) & 1, l0 = ((p >> 1) & 1) * 16, s = p & 1;
+        Raw r;
+        ld_dw<5>(align_down4(b + 64 * n + 32 * s + l0), r.w);
+        ld_dw<5>(align_down4(b + 128 + 32 * n + l0), r.w + 5);
+        ld_dw<3>(align_down4(b + 192 + sc_index(p)), r.w + 10);
+        r.w[13] = ld_u16(b + 208);
+        return r;
+    }
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
+        const uint8_t* b = row + (p >> 3) * 210;
+        const uint32_t sh = (uint32_t)(uintptr_t)b & 3u;                 // ql / qh windows
+        const uint32_t ss = (uint32_t)(uintptr_t)(b + 192 + sc_index(p)) & 3u;
+        const int s = p & 1;
+        const uint4 ql = make_uint4(align2(r.w[1], r.w[0], sh), align2(r.w[2], r.w[1], sh),
+                                    align2(r.w[3], r.w[2], sh), align2(r.w[4], r.w[3], sh));
+        const uint4 qh = make_uint4(align2(r.w[6], r.w[5], sh), align2(r.w[7], r.w[6], sh),
+                                    align2(r.w[8], r.w[7], sh), align2(r.w[9], r.w[8], sh));
+        const uint32_t sc0 = align2(r.w[11], r.w[10], ss), sc1 = align2(r.w[12], r.w[11], ss);
+        const float d = h2f(r.w[13]);
+        PieceCodes o;
+        o.u0 = or4(and4(ql, 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * s), 0x03030303u), 4));
+        o.u1 = or4(and4(shr4(ql, 4), 0x0F0F0F0Fu), shl4(and4(shr4(qh, 4 + 2 * s), 0x03030303u), 4));
+        o.a0 = d * (float)(int8_t)(sc0 & 0xFFu);
+        o.a1 = d * (float)(int8_t)(sc1 & 0xFFu);
+        o.b0 = -32.0f * o.a0;
+        o.b1 = -32.0f * o.a1;
+        return o;
+    }
+};
+
+// Q8_0: one piece per 34-byte block; run 0 = qs[0..15], run 1 = qs[16..31].
+// Signed bytes are biased by 128 (xor 0x80).  Block bases are even, so the
+// 9-dword window from the aligned-down base covers d and qs.
+template <> struct Piece<T_Q8_0> {
+    typedef RawW<9> Raw;
+    static __device__ __forceinline__ int run0(int p) { return p * 32; }
+    static constexpr int kRun1 = 16;
+    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
+        Raw r;
+        ld_dw<9>(align_down4(row + p * 34), r.w);
+        return r;
+    }
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
+        const bool odd = ((uint32_t)(uintptr_t)(row + p * 34) & 2u) != 0;
+        const float d = h2f(odd ? (r.w[0] >> 16) : (r.w[0] & 0xFFFFu));
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = (odd ? r.w[i + 1] : align2(r.w[i + 1], r.w[i], 2)) ^ 0x80808080u;
+        PieceCodes o;
+        o.u0 = make_uint4(q[0], q[1], q[2], q[3]);
+        o.u1 = make_uint4(q[4], q[5], q[6], q[7]);
+        o.a0 = o.a1 = d;
+        o.b0 = o.b1 = -128.0f * d;
+        return o;
+    }
+};
+
+// IQ4_NL: one piece per 18-byte block; low nibbles -> values 0..15, high ->
+// 16..31.  5-dword window from the aligned-down (even) base.
+template <> struct Piece<T_IQ4_NL> {
+    typedef RawW<5> Raw;
+    static __device__ __forceinline__ int run0(int p) { return p * 32; }
+    static constexpr int kRun1 = 16;
+    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
+        Raw r;
+        ld_dw<5>(align_down4(row + p * 18), r.w);
+        return r;
+    }
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
+        const bool odd = ((uint32_t)(uintptr_t)(row + p * 18) & 2u) != 0;
+        const float d = h2f(odd ? (r.w[0] >> 16) : (r.w[0] & 0xFFFFu));
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = odd ? r.w[i + 1] : align2(r.w[i + 1], r.w[i], 2);
+        const uint4 qq = make_uint4(q[0], q[1], q[2], q[3]);
+        PieceCodes o;
+        o.u0 = lut16x4(and4(qq, 0x0F0F0F0Fu), true);
+        o.u1 = lut16x4(and4(shr4(qq, 4), 0x0F0F0F0Fu), true);
+        o.a0 = o.a1 = d;
+        o.b0 = o.b1 = -128.0f * d;
+        return o;
+    }
+};
+
+// IQ4_XS: piece = sub-block ib of block b (32 values, scale d*(ls-32)).
+template <> struct Piece<T_IQ4_XS> {
+    typedef RawW<6> Raw;
+    static __device__ __forceinline__ int run0(int p) { return p * 32; }
+    static constexpr int kRun1 = 16;
+    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
+        const uint8_t* b = row + (p >> 3) * 136;
+        const int ib = p & 7;
+        Raw r;
+        const uint2 hd = *(const uint2*)b;
+        const uint2 lo = *(const uint2*)(b + 8 + 16 * ib);
+        const uint2 hi = *(const uint2*)(b + 16 + 16 * ib);
+        r.w[0] = hd.x; r.w[1] = hd.y; r.w[2] = lo.x; r.w[3] = lo.y; r.w[4] = hi.x; r.w[5] = hi.y;
+        return r;
+    }
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t*, int p) {
+        const int ib = p & 7;
+        const int ls = (int)(((r.w[1] >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15u) | (((r.w[0] >> (16 + 2 * ib)) & 3u) << 4));
+        const float dl = h2f(r.w[0] & 0xFFFFu) * (float)(ls - 32);
+        const uint4 q = make_uint4(r.w[2], r.w[3], r.w[4], r.w[5]);
+        PieceCodes o;
+        o.u0 = lut16x4(and4(q, 0x0F0F0F0Fu), true);
+        o.u1 = lut16x4(and4(shr4(q, 4), 0x0F0F0F0Fu), true);
+        o.a0 = o.a1 = dl;
+        o.b0 = o.b1 = -128.0f * dl;
+        return o;
+    }
+};
+
+// Unsigned byte codes -> floats (v_cvt_f32_ubyte0..3).
+__device__ __forceinline__ void ubytes_to_f32(uint4 u, float* f) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[4 * i + 0] = (float)(w[i] & 0xFFu);
+        f[4 * i + 1] = (float)((w[i] >> 8) & 0xFFu);
+        f[4 * i + 2] = (float)((w[i] >> 16) & 0xFFu);
+        f[4 * i + 3] = (float)(w[i] >> 24);
+    }
+}
+
+}  // namespace ggq

@@ -1,0 +1,702 @@
+// ggq_kernels.hip -- CDNA4 (gfx950) kernels of the quantized-matmul backend.
+//
+// Raw GGUF weight blocks are read straight from HBM (no re-quantization);
+// block decode is fused into every kernel through ggq_device.h.
+//
+//   dequant_kernel     bit-exact fp32 dequant (parity probe for the decoders)
+//   block_dot_kernel   int32 per-group dot products of codes x int8 activations
+//   quant_act_*        per-row / per-32-block int8 activation quantization
+//   gemv_kernel        decode GEMV (batch 1..8, also expert-grouped for MoE)
+//   gemm_i8_kernel     prefill GEMM on int8 MFMA (v_mfma_i32_32x32x32_i8)
+//   moe_*              top-k routing, expert grouping, SwiGLU, weighted combine
+//
+// The reference path these replace: CpuRefBackend::mul_mat_q
+// (src/backends/cpu_ref/cpu_ref.cpp:25-137) and the XDNA int8 tile loop
+// (src/backends/amd_xdna/amd_xdna.cpp:491-952).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "ggq_device.h"
+#include "ggq_launch.h"
+
+namespace ggq {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+#define GGQ_DISPATCH_TYPE(t, F)                 \
+    switch (t) {                                \
+    case T_Q4_K: F(T_Q4_K); break;              \
+    case T_Q5_K: F(T_Q5_K); break;              \
+    case T_Q6_K: F(T_Q6_K); break;              \
+    case T_Q8_0: F(T_Q8_0); break;              \
+    case T_IQ4_NL: F(T_IQ4_NL); break;          \
+    case T_IQ4_XS: F(T_IQ4_XS); break;          \
+    default: return hipErrorInvalidValue;       \
+    }
+
+// =================================================================== dequant
+// One thread per 16 values: codes16 + group_scale, then the reference's
+// rounding order (dequant_value).
+template <int T>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ raw, int64_t n16,
+                                                      float* __restrict__ out) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n16) return;
+    constexpr int be = T == T_Q8_0 || T == T_IQ4_NL ? 32 : 256;
+    constexpr int bb = T == T_Q8_0 ? 34 : T == T_IQ4_NL ? 18 : T == T_Q4_K ? 144
+                     : T == T_Q5_K ? 176 : T == T_Q6_K ? 210 : 136;
+    const int64_t b = g / (be / 16);
+    const int k = (int)(g % (be / 16)) * 16;
+    const uint8_t* blk = raw + b * bb;
+    const uint4 c = codes16<T>(blk, k);
+    const GroupScale gs = group_scale<T>(blk, k);
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    float4* o = (float4*)(out + b * be + k);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float4 v;
+        v.x = dequant_value(gs, (int)(int8_t)(w[i] & 0xFFu));
+        v.y = dequant_value(gs, (int)(int8_t)((w[i] >> 8) & 0xFFu));
+        v.z = dequant_value(gs, (int)(int8_t)((w[i] >> 16) & 0xFFu));
+        v.w = dequant_value(gs, (int)(int8_t)(w[i] >> 24));
+        o[i] = v;
+    }
+}
+
+hipError_t launch_dequant(uint32_t type, const void* raw, int64_t n_blocks, float* out, hipStream_t s) {
+    const int64_t n16 = n_blocks * (block_elems(type) / 16);
+    if (n16 == 0) return hipSuccess;
+    const dim3 grid((unsigned)((n16 + 255) / 256));
+#define L(TT) dequant_kernel<TT><<<grid, 256, 0, s>>>((const uint8_t*)raw, n16, out)
+    GGQ_DISPATCH_TYPE(type, L)
+#undef L
+    return hipGetLastError();
+}
+
+// ================================================================= block dot
+template <int T>
+__global__ __launch_bounds__(256) void block_dot_kernel(const uint8_t* __restrict__ W, int N, int K,
+                                                        const int8_t* __restrict__ qa, int M,
+                                                        int32_t* __restrict__ out) {
+    constexpr int ge = T == T_Q6_K ? 16 : 32;
+    const int G = K / ge;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)M * N * G) return;
+    const int g = (int)(idx % G);
+    const int n = (int)((idx / G) % N);
+    const int m = (int)(idx / ((int64_t)G * N));
+    const uint8_t* row = W + (int64_t)n * row_bytes(T, K);
+    int acc = 0;
+#pragma unroll
+    for (int h = 0; h < ge / 16; h++) {
+        const int k = g * ge + 16 * h;
+        const uint4 c = codes16<T>(row, k);
+        const uint4 a = *(const uint4*)(qa + (int64_t)m * K + k);
+        acc = __builtin_amdgcn_sdot4((int)c.x, (int)a.x, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)c.y, (int)a.y, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)c.z, (int)a.z, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)c.w, (int)a.w, acc, false);
+    }
+    out[idx] = acc;
+}
+
+hipError_t launch_block_dot(uint32_t type, const void* W, int N, int K, const int8_t* qa, int M,
+                            int32_t* out, hipStream_t s) {
+    const int64_t total = (int64_t)M * N * (K / group_elems(type));
+    if (total == 0) return hipSuccess;
+    const dim3 grid((unsigned)((total + 255) / 256));
+#define L(TT) block_dot_kernel<TT><<<grid, 256, 0, s>>>((const uint8_t*)W, N, K, qa, M, out)
+    GGQ_DISPATCH_TYPE(type, L)
+#undef L
+    return hipGetLastError();
+}
+
+// ========================================================= activation quant
+// Reference: amd_xdna.cpp:633-639 (scale = amax/127, or 1 for a zero row) and
+// :598-603, :757-771 (q = clamp(nearbyint(a * (1/scale)), -128, 127)).
+// Division and rint are IEEE (correctly rounded / half-to-even).
+__device__ __forceinline__ int8_t to_i8(float v) {
+    float r = __builtin_rintf(v);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    return (int8_t)(int)r;
+}
+
+__global__ __launch_bounds__(256) void quant_act_row_kernel(const float* __restrict__ A, int lda, int K,
+                                                            int8_t* __restrict__ q, float* __restrict__ scales,
+                                                            float* __restrict__ x_eff) {
+    __shared__ float wmax[4];
+    const int m = blockIdx.x;
+    const float* a = A + (int64_t)m * lda;
+    float amax = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(a[k]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+    const float inv = __fdiv_rn(1.0f, sc);
+    if (threadIdx.x == 0 && scales) scales[m] = sc;
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const int8_t v = to_i8(__fmul_rn(a[k], inv));
+        if (q) q[(int64_t)m * K + k] = v;
+        if (x_eff) x_eff[(int64_t)m * K + k] = __fmul_rn((float)v, sc);
+    }
+}
+
+__global__ __launch_bounds__(256) void quant_act_b32_kernel(const float* __restrict__ A, int lda, int M, int K,
+                                                            int8_t* __restrict__ q, float* __restrict__ scales,
+                                                            float* __restrict__ x_eff) {
+    const int nb = K / 32;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)M * nb) return;
+    const int m = (int)(idx / nb), b = (int)(idx % nb);
+    const float* a = A + (int64_t)m * lda + 32 * b;
+    float amax = 0.0f;
+    for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(a[k]));
+    const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+    const float inv = __fdiv_rn(1.0f, sc);
+    if (scales) scales[idx] = sc;
+    for (int k = 0; k < 32; k++) {
+        const int8_t v = to_i8(__fmul_rn(a[k], inv));
+        if (q) q[(int64_t)m * K + 32 * b + k] = v;
+        if (x_eff) x_eff[(int64_t)m * K + 32 * b + k] = __fmul_rn((float)v, sc);
+    }
+}
+
+hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int8_t* q,
+                            float* scales, float* x_eff, hipStream_t s) {
+    if (M == 0 || K == 0) return hipSuccess;
+    if (mode == 1) {
+        quant_act_row_kernel<<<M, 256, 0, s>>>(A, lda, K, q, scales, x_eff);
+    } else {
+        const int64_t n = (int64_t)M * (K / 32);
+        quant_act_b32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(A, lda, M, K, q, scales, x_eff);
+    }
+    return hipGetLastError();
+}
+
+// ===================================================================== GEMV
+// Work layout (256 threads, 4 wavefronts):
+//   * a row of K values is P = K/32 pieces; LPR = 2^lpr_log2 threads share a
+//     row (LPR = min(256, pow2ceil(P))), so one row-iteration covers 256/LPR
+//     rows; thread t owns pieces lp, lp+LPR, ... (PPT of them) of row t/LPR.
+//   * the thread's activation values for its pieces (32 fp32 per piece and
+//     batch row) stay in VGPRs for the whole row loop, so HBM carries only
+//     weight blocks; activations are read once per workgroup and M-chunk.
+//   * weight dwords are fetched one row-iteration ahead (register double
+//     buffer), so each wavefront keeps two rows of loads in flight while it
+//     decodes, multiplies and reduces the current one.  The first fetch is
+//     issued before the activation loads.
+//   * partial sums are reduced with cross-lane shuffles inside a wavefront,
+//     and through LDS when a row spans several wavefronts (LPR >= 128).
+struct GemvArgs {
+    const uint8_t* W;
+    int64_t w_group_stride;
+    int64_t row_bytes;
+    int N, K;
+    const float* X;
+    int ldx;
+    float* Y;
+    int ldy;
+    int M;
+    const int* grp_off;
+    const int* x_idx;
+    int lpr_log2;
+    int x_vec4;  // X rows are 16-byte aligned (float4 loads)
+};
+
+template <int T, int PPT>
+__device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[PPT], const uint8_t* W, int64_t row_bytes,
+                                           int row, bool rvalid, int lp, int lpr, int P) {
+#pragma unroll
+    for (int i = 0; i < PPT; i++) {
+        const int p = lp + i * lpr;
+        if (rvalid && p < P) raw[i] = Piece<T>::fetch(W + (int64_t)row * row_bytes, p);
+    }
+}
+
+template <int T, int MB, int PPT>
+__device__ __forceinline__ void gemv_row(const typename Piece<T>::Raw (&raw)[PPT], const GemvArgs& a, const uint8_t* W,
+                                         int row, bool rvalid, int lp, int lpr, int P, int wave, int lane, int rsub,
+                                         int m0, int mc, int mcount, float (&xr)[PPT][MB][32],
+                                         const float (&xs0)[PPT][MB], const float (&xs1)[PPT][MB],
+                                         float (&red)[2][4][MB], int& parity) {
+    float acc[MB];
+#pragma unroll
+    for (int m = 0; m < MB; m++) acc[m] = 0.0f;
+    const uint8_t* wrow = W + (int64_t)row * a.row_bytes;
+#pragma unroll
+    for (int i = 0; i < PPT; i++) {
+        const int p = lp + i * lpr;
+        if (rvalid && p < P) {
+            const PieceCodes pc = Piece<T>::decode(raw[i], wrow, p);
+            float u0[16], u1[16];
+            ubytes_to_f32(pc.u0, u0);
+            ubytes_to_f32(pc.u1, u1);
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    s0 = fmaf(xr[i][m][j], u0[j], s0);
+                    s1 = fmaf(xr[i][m][16 + j], u1[j], s1);
+                }
+                float r = fmaf(pc.a0, s0, pc.b0 * xs0[i][m]);
+                r = fmaf(pc.a1, s1, fmaf(pc.b1, xs1[i][m], r));
+                acc[m] += r;
+            }
+        }
+    }
+    if (a.lpr_log2 <= 6) {
+        for (int off = lpr >> 1; off > 0; off >>= 1) {
+#pragma unroll
+            for (int m = 0; m < MB; m++) acc[m] += __shfl_xor(acc[m], off, 64);
+        }
+    } else {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+            for (int m = 0; m < MB; m++) acc[m] += __shfl_xor(acc[m], off, 64);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MB; m++) red[parity][wave][m] = acc[m];
+        }
+        __syncthreads();
+        if (lp == 0) {
+            const int wpr = lpr >> 6, w0 = rsub * wpr;
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                float sum = 0.0f;
+                for (int w = 0; w < wpr; w++) sum += red[parity][w0 + w][m];
+                acc[m] = sum;
+            }
+        }
+        parity ^= 1;
+    }
+    if (lp == 0 && rvalid) {
+#pragma unroll
+        for (int m = 0; m < MB; m++)
+            if (mc + m < mcount) a.Y[(int64_t)(m0 + mc + m) * a.ldy + row] = acc[m];
+    }
+}
+
+template <int T, int MB, int PPT>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    typedef typename Piece<T>::Raw Raw;
+    __shared__ float red[2][4][MB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lpr_log2 = a.lpr_log2;
+    const int lpr = 1 << lpr_log2, lp = tid & (lpr - 1), rsub = tid >> lpr_log2;
+    const int rpi = 256 >> lpr_log2;
+    const int P = a.K >> 5;
+    const uint8_t* W = a.W + (int64_t)blockIdx.y * a.w_group_stride;
+    int m0 = 0, mcount = a.M;
+    if (a.grp_off) {
+        m0 = a.grp_off[blockIdx.y];
+        mcount = a.grp_off[blockIdx.y + 1] - m0;
+    }
+    const int n_iters = (a.N + rpi - 1) / rpi;
+    const int stride = gridDim.x;
+    int parity = 0;
+
+    for (int mc = 0; mc < mcount; mc += MB) {
+        Raw ra[PPT], rb[PPT];
+        int it = blockIdx.x;
+        {
+            const int row = it * rpi + rsub;
+            gemv_fetch<T, PPT>(ra, W, a.row_bytes, row, it < n_iters && row < a.N, lp, lpr, P);
+        }
+        float xr[PPT][MB][32];
+        float xs0[PPT][MB], xs1[PPT][MB];
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int p = lp + i * lpr;
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                xs0[i][m] = 0.0f;
+                xs1[i][m] = 0.0f;
+                const bool ok = p < P && mc + m < mcount;
+                int xrow = m0 + mc + m;
+                if (ok && a.x_idx) xrow = a.x_idx[xrow];
+                const float* xp = a.X + (int64_t)xrow * a.ldx;
+                const int k0 = ok ? Piece<T>::run0(p) : 0;
+                if (ok && a.x_vec4) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float4 v0 = *(const float4*)(xp + k0 + 4 * j);
+                        const float4 v1 = *(const float4*)(xp + k0 + Piece<T>::kRun1 + 4 * j);
+                        xr[i][m][4 * j + 0] = v0.x; xr[i][m][4 * j + 1] = v0.y;
+                        xr[i][m][4 * j + 2] = v0.z; xr[i][m][4 * j + 3] = v0.w;
+                        xr[i][m][16 + 4 * j + 0] = v1.x; xr[i][m][16 + 4 * j + 1] = v1.y;
+                        xr[i][m][16 + 4 * j + 2] = v1.z; xr[i][m][16 + 4 * j + 3] = v1.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; j++) {
+                        xr[i][m][j] = ok ? xp[k0 + j] : 0.0f;
+                        xr[i][m][16 + j] = ok ? xp[k0 + Piece<T>::kRun1 + j] : 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    xs0[i][m] += xr[i][m][j];
+                    xs1[i][m] += xr[i][m][16 + j];
+                }
+            }
+        }
+
+        // Ping-pong between ra and rb: fetch the next row-iteration, then
+        // decode/multiply/reduce the current one.
+        while (it < n_iters) {
+            {
+                const int nx = it + stride, row = it * rpi + rsub, nrow = nx * rpi + rsub;
+                gemv_fetch<T, PPT>(rb, W, a.row_bytes, nrow, nx < n_iters && nrow < a.N, lp, lpr, P);
+                gemv_row<T, MB, PPT>(ra, a, W, row, row < a.N, lp, lpr, P, wave, lane, rsub, m0, mc, mcount, xr,
+                                     xs0, xs1, red, parity);
+                it = nx;
+            }
+            if (it >= n_iters) break;
+            {
+                const int nx = it + stride, row = it * rpi + rsub, nrow = nx * rpi + rsub;
+                gemv_fetch<T, PPT>(ra, W, a.row_bytes, nrow, nx < n_iters && nrow < a.N, lp, lpr, P);
+                gemv_row<T, MB, PPT>(rb, a, W, row, row < a.N, lp, lpr, P, wave, lane, rsub, m0, mc, mcount, xr,
+                                     xs0, xs1, red, parity);
+                it = nx;
+            }
+        }
+    }
+}
+
+static int ilog2_ceil(int v) {
+    int l = 0;
+    while ((1 << l) < v) l++;
+    return l;
+}
+
+static int gemv_target_blocks() {
+    static int v = [] {
+        const char* e = getenv("GGQ_GEMV_BLOCKS");
+        return e && *e ? atoi(e) : 512;
+    }();
+    return v;
+}
+
+template <int T>
+static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
+    const int P = p.K / 32;
+    const int lpr_log2 = ilog2_ceil(P < 256 ? P : 256);
+    const int lpr = 1 << lpr_log2;
+    const int ppt = (P + lpr - 1) / lpr;
+    const int rpi = 256 / lpr;
+    const int mrows = p.grp_off ? p.max_group_rows : p.M;
+    GemvArgs a;
+    a.W = (const uint8_t*)p.W;
+    a.w_group_stride = p.w_group_stride;
+    a.row_bytes = row_bytes(T, p.K);
+    a.N = p.N; a.K = p.K;
+    a.X = p.X; a.ldx = p.ldx;
+    a.Y = p.Y; a.ldy = p.ldy;
+    a.M = p.M;
+    a.grp_off = p.grp_off;
+    a.x_idx = p.x_idx;
+    a.lpr_log2 = lpr_log2;
+    a.x_vec4 = ((uintptr_t)p.X % 16 == 0) && (p.ldx % 4 == 0);
+    const int n_iters = (p.N + rpi - 1) / rpi;
+    // Grouped (MoE) launches spread ~16 workgroups over each expert's rows.
+    int gx = p.groups > 1 ? 16 : gemv_target_blocks();
+    if (gx < 1) gx = 1;
+    if (gx > n_iters) gx = n_iters;
+    const dim3 grid(gx, p.groups > 0 ? p.groups : 1);
+    // Batch-rows per pass (MB) and pieces per thread (PPT) keep the
+    // activation registers at <= 4*32*(MB*PPT) floats.
+#define GO(MB_, PPT_) gemv_kernel<T, MB_, PPT_><<<grid, 256, 0, s>>>(a)
+    if (ppt == 1) {
+        if (mrows <= 1) GO(1, 1);
+        else if (mrows == 2) GO(2, 1);
+        else GO(4, 1);
+    } else if (ppt == 2) {
+        if (mrows <= 1) GO(1, 2);
+        else GO(2, 2);
+    } else if (ppt <= 4) {
+        GO(1, 4);
+    } else {
+        return hipErrorInvalidValue;
+    }
+#undef GO
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv(const GemvProblem& p, hipStream_t s) {
+    if (p.N == 0 || p.M == 0) return hipSuccess;
+#define L(TT) return launch_gemv_t<TT>(p, s)
+    GGQ_DISPATCH_TYPE(p.type, L)
+#undef L
+    return hipSuccess;
+}
+
+// ================================================================ GEMM (i8)
+// 128x128 output tile per 256-thread workgroup; each wavefront owns a 64x64
+// quadrant as 2x2 blocks of v_mfma_i32_32x32x32_i8 (A = activation rows,
+// B = weight rows, so every lane's output column n is fixed and the
+// per-group weight scale is one scalar per lane).  Each MFMA covers one
+// 32-value scale group: the int32 result is converted and scaled into fp32
+// accumulators; the Q4_K/Q5_K min term uses the activation group sums from
+// a second MFMA against a ones operand.  Q6_K (16-value groups) uses
+// v_mfma_i32_32x32x16_i8.
+//
+// MFMA operand layout: lane l supplies row/column (l % 32) and the K-slice
+// 16*(l/32) .. +16; output element r of lane l is row 8*(r/4) + 4*(l/32) +
+// r%4, column l%32.
+struct GemmArgs {
+    const uint8_t* W;
+    int64_t row_bytes;
+    int N, K;
+    const int8_t* QA;
+    const float* sa;
+    float* C;
+    int ldc;
+    int M;
+};
+
+template <int T>
+__global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
+    constexpr bool kMin = T == T_Q4_K || T == T_Q5_K;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lk = lane >> 5;
+    const int m_base = blockIdx.y * 128 + (wave >> 1) * 64;
+    const int n_base = blockIdx.x * 128 + (wave & 1) * 64;
+
+    const int8_t* arow[2];
+    bool aval[2];
+    const uint8_t* brow[2];
+    bool bval[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int m = m_base + 32 * i + li;
+        aval[i] = m < a.M;
+        arow[i] = a.QA + (int64_t)(aval[i] ? m : 0) * a.K;
+        const int n = n_base + 32 * i + li;
+        bval[i] = n < a.N;
+        brow[i] = a.W + (int64_t)(bval[i] ? n : 0) * a.row_bytes;
+    }
+
+    float acc[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    const v16i zero = {};
+    for (int k0 = 0; k0 < a.K; k0 += 32) {
+        if constexpr (T != T_Q6_K) {
+            v4i A[2], B[2];
+            GroupScale gs[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint4 av = aval[i] ? *(const uint4*)(arow[i] + k0 + 16 * lk) : make_uint4(0, 0, 0, 0);
+                A[i] = v4i{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+                const uint4 bv = bval[i] ? codes16<T>(brow[i], k0 + 16 * lk) : make_uint4(0, 0, 0, 0);
+                B[i] = v4i{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
+                gs[i] = bval[i] ? group_scale<T>(brow[i], k0) : GroupScale{0.0f, 0.0f};
+            }
+            v16i S[2];
+            if constexpr (kMin) {
+                const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+#pragma unroll
+                for (int i = 0; i < 2; i++) S[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], ones, zero, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const v16i Pm = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B[j], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        acc[i][j][r] = fmaf(gs[j].dl, (float)Pm[r], acc[i][j][r]);
+                        if constexpr (kMin) acc[i][j][r] = fmaf(-gs[j].ml, (float)S[i][r], acc[i][j][r]);
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int kk = k0 + 16 * h;
+                long A[2], B[2];
+                GroupScale gs[2];
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    A[i] = aval[i] ? *(const long*)(arow[i] + kk + 8 * lk) : 0;
+                    const uint4 c = bval[i] ? codes16<T>(brow[i], kk) : make_uint4(0, 0, 0, 0);
+                    const uint32_t lo = lk ? c.z : c.x, hi = lk ? c.w : c.y;
+                    B[i] = (long)(((uint64_t)hi << 32) | lo);
+                    gs[i] = bval[i] ? group_scale<T>(brow[i], kk) : GroupScale{0.0f, 0.0f};
+                }
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const v16i Pm = __builtin_amdgcn_mfma_i32_32x32x16_i8(A[i], B[j], zero, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf(gs[j].dl, (float)Pm[r], acc[i][j][r]);
+                    }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m_base + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
+            if (m >= a.M) continue;
+            const float s = a.sa[m];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int n = n_base + 32 * j + li;
+                if (n < a.N) a.C[(int64_t)m * a.ldc + n] = acc[i][j][r] * s;
+            }
+        }
+}
+
+hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa,
+                          const float* sa, int M, float* C, int ldc, hipStream_t s) {
+    if (M == 0 || N == 0) return hipSuccess;
+    GemmArgs a;
+    a.W = (const uint8_t*)W;
+    a.row_bytes = row_bytes(type, K);
+    a.N = N; a.K = K;
+    a.QA = qa; a.sa = sa;
+    a.C = C; a.ldc = ldc; a.M = M;
+    const dim3 grid((N + 127) / 128, (M + 127) / 128);
+#define L(TT) gemm_i8_kernel<TT><<<grid, 256, 0, s>>>(a)
+    GGQ_DISPATCH_TYPE(type, L)
+#undef L
+    return hipGetLastError();
+}
+
+// ====================================================================== MoE
+// Routing (main.cpp:3126-3135): top-k experts by descending logit, then a
+// softmax over the selected logits only: w_j = exp(l_j - l_0) / sum.
+// One wavefront per token; ties break toward the lower expert id.
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int E, int topk,
+                                                       int32_t* __restrict__ sel, float* __restrict__ wsel) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float* l = logits + (int64_t)t * E;
+    uint64_t taken[16] = {};  // up to 1024 experts
+    float lsel[64];
+    for (int j = 0; j < topk; j++) {
+        float best = -INFINITY;
+        int bi = 0x7FFFFFFF;
+        for (int e = lane; e < E; e += 64) {
+            if ((taken[e >> 6] >> (e & 63)) & 1) continue;
+            const float v = l[e];
+            if (v > best || (v == best && e < bi)) { best = v; bi = e; }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(best, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+        }
+        taken[bi >> 6] |= 1ull << (bi & 63);
+        lsel[j] = best;
+        if (lane == 0) sel[t * topk + j] = bi;
+    }
+    if (lane == 0) {
+        float sum = 0.0f;
+        for (int j = 0; j < topk; j++) sum += expf(lsel[j] - lsel[0]);
+        for (int j = 0; j < topk; j++) wsel[t * topk + j] = expf(lsel[j] - lsel[0]) / sum;
+    }
+}
+
+hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel, float* wsel,
+                            hipStream_t s) {
+    if (T == 0) return hipSuccess;
+    moe_route_kernel<<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
+    return hipGetLastError();
+}
+
+// Expert grouping: stable counting sort of the T*topk (token, slot) pairs by
+// expert id.  grp_off[E+1] are the group boundaries, tok_idx[pos] the token of
+// each sorted pair and pos_of[t*topk+j] its position.  One workgroup.
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restrict__ sel, int n, int E,
+                                                         int topk, int32_t* __restrict__ grp_off,
+                                                         int32_t* __restrict__ tok_idx,
+                                                         int32_t* __restrict__ pos_of) {
+    extern __shared__ int32_t cnt[];  // E + 1
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int f = threadIdx.x; f < n; f += blockDim.x) atomicAdd(&cnt[sel[f]], 1);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int e = 0; e < E; e++) {
+            const int c = cnt[e];
+            cnt[e] = run;
+            grp_off[e] = run;
+            run += c;
+        }
+        grp_off[E] = run;
+    }
+    __syncthreads();
+    for (int f = threadIdx.x; f < n; f += blockDim.x) {
+        const int e = sel[f];
+        int rank = 0;
+        for (int g = 0; g < f; g++) rank += sel[g] == e;
+        const int pos = cnt[e] + rank;
+        tok_idx[pos] = f / topk;
+        pos_of[f] = pos;
+    }
+}
+
+hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
+                            int32_t* tok_idx, int32_t* pos_of, hipStream_t s) {
+    moe_group_kernel<<<1, 1024, (E + 1) * sizeof(int32_t), s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);
+    return hipGetLastError();
+}
+
+// SwiGLU as main.cpp:3164-3165: h = (g / (1 + exp(-g))) * u.
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                     float* __restrict__ h, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float gv = g[i];
+        h[i] = (gv / (1.0f + expf(-gv))) * u[i];
+    }
+}
+
+hipError_t launch_swiglu(const float* g, const float* u, float* h, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(g, u, h, n);
+    return hipGetLastError();
+}
+
+// Weighted combine in the reference's order (main.cpp:3166-3193): routed
+// experts j = 0..topk-1 by descending logit, then the shared expert.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ D, const int32_t* __restrict__ pos_of,
+                                                          const float* __restrict__ wsel, int topk, int H,
+                                                          const float* __restrict__ Dsh,
+                                                          const float* __restrict__ shared_w,
+                                                          float* __restrict__ out) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H) return;
+    float acc = 0.0f;
+    for (int j = 0; j < topk; j++)
+        acc += wsel[t * topk + j] * D[(int64_t)pos_of[t * topk + j] * H + i];
+    if (Dsh) acc += (shared_w ? shared_w[t] : 1.0f) * Dsh[(int64_t)t * H + i];
+    out[(int64_t)t * H + i] = acc;
+}
+
+hipError_t launch_moe_combine(const float* D, const int32_t* pos_of, const float* wsel, int T,
+                              int topk, int H, const float* Dsh, const float* shared_w, float* out,
+                              hipStream_t s) {
+    if (T == 0) return hipSuccess;
+    moe_combine_kernel<<<dim3((H + 255) / 256, T), 256, 0, s>>>(D, pos_of, wsel, topk, H, Dsh, shared_w, out);
+    return hipGetLastError();
+}
+
+}  // namespace ggq

@@ -1,0 +1,60 @@
+// ggq_launch.h -- host-side launchers of the HIP kernels (ggq_kernels.hip).
+// All launchers are asynchronous on `stream` and return hipError_t from the
+// launch; shape validation is done by the caller (ggq_api.cpp).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ggq {
+
+// Standalone bit-exact dequant of n_blocks consecutive blocks.
+hipError_t launch_dequant(uint32_t type, const void* raw, int64_t n_blocks, float* out, hipStream_t s);
+
+// int32 dot products per scale group: out[(m*N+n)*G + g], G = K/group_elems.
+hipError_t launch_block_dot(uint32_t type, const void* W, int N, int K, const int8_t* qa, int M,
+                            int32_t* out, hipStream_t s);
+
+// Activation quantization (mode 1 = per row, 2 = per 32-block).  Any of q,
+// scales, x_eff may be null.  x_eff[m][k] = q*scale as fp32 (dense, ld = K).
+hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int8_t* q,
+                            float* scales, float* x_eff, hipStream_t s);
+
+// Decode GEMV with fp32 activations: Y[y_row][n] = sum_k X[x_row][k] W[n][k].
+// Plain mode: grp_off == null, rows 0..M-1.  Grouped mode (MoE): group g uses
+// weights W + g*w_group_stride and output rows grp_off[g]..grp_off[g+1]-1,
+// whose activation rows are x_idx[row] (or the row itself when x_idx is null).
+struct GemvProblem {
+    uint32_t type;
+    const void* W;
+    int64_t w_group_stride;
+    int N, K;
+    const float* X;
+    int ldx;
+    float* Y;
+    int ldy;
+    int M;
+    int groups;
+    const int* grp_off;
+    const int* x_idx;
+    int max_group_rows;  // upper bound of rows per group (grouped mode)
+};
+hipError_t launch_gemv(const GemvProblem& p, hipStream_t s);
+// Largest K the register-resident GEMV supports.
+constexpr int kGemvMaxK = 32768;
+
+// int8-MFMA GEMM on per-row int8 activations:
+//   C[m][n] = sa[m] * sum_groups dl[n,g]*P[m,n,g] - ml[n,g]*S[m,g]
+hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa,
+                          const float* sa, int M, float* C, int ldc, hipStream_t s);
+
+// MoE helpers.
+hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel,
+                            float* wsel, hipStream_t s);
+hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
+                            int32_t* tok_idx, int32_t* pos_of, hipStream_t s);
+hipError_t launch_swiglu(const float* g, const float* u, float* h, int64_t n, hipStream_t s);
+hipError_t launch_moe_combine(const float* D, const int32_t* pos_of, const float* wsel, int T,
+                              int topk, int H, const float* Dsh, const float* shared_w, float* out,
+                              hipStream_t s);
+
+}  // namespace ggq

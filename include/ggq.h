@@ -1,0 +1,191 @@
+/*
+ * ggq.h -- C ABI of the MI355X (gfx950) quantized-matmul backend for ggnpu.
+ *
+ * This is the drop-in boundary for ggnpu's `Backend::mul_mat_q` hot path
+ * (include/ggnpu/backend.h:117 in the ggnpu tree) when B holds raw GGUF
+ * blocks (the non-NPU branch of the caller, src/cli/main.cpp:1430-1432).
+ * Plain C types only: pointers, sizes, integer status codes.  No C++ or torch
+ * types cross this boundary and no exception escapes it.
+ *
+ * Status codes are ggnpu's `Status` values (include/ggnpu/backend.h:12-19).
+ * Weight type ids are GGML ids (include/ggnpu/tensor.h:11-42); supported:
+ * Q8_0 (8), Q4_K (12), Q5_K (13), Q6_K (14), IQ4_NL (20), IQ4_XS (23).
+ *
+ * Layouts (as in the reference, src/backends/cpu_ref/cpu_ref.cpp:87-117):
+ *   W  raw GGUF bytes, N rows of K values, row n at n * (K/blck) * type_size
+ *   A  fp32 activations [M][lda], C fp32 output [M][ldc] (fully overwritten)
+ *
+ * Activation treatments (act_mode):
+ *   GGQ_ACT_F32         fp32 activations, as CpuRefBackend::mul_mat_q
+ *                       (cpu_ref.cpp:87-117)
+ *   GGQ_ACT_Q8_ROW      per-row int8 activations, as the XDNA backend
+ *                       (amd_xdna.cpp:598-603, 633-639, 757-771): scale =
+ *                       amax/127, q = clamp(rint(a*(1/scale)))
+ *   GGQ_ACT_Q8_BLOCK32  per-32-value int8 activations (extension; no
+ *                       reference counterpart)
+ */
+#ifndef GGQ_H
+#define GGQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status, include/ggnpu/backend.h:12-19. */
+#define GGQ_OK 0
+#define GGQ_ERROR 1
+#define GGQ_NOT_FOUND 2
+#define GGQ_INVALID_PARAM 3
+#define GGQ_DEVICE_UNAVAILABLE 4 /* Status::NPU_UNAVAILABLE */
+#define GGQ_OUT_OF_MEMORY 5
+
+/* GGML type ids, include/ggnpu/tensor.h:11-42. */
+#define GGQ_TYPE_Q8_0 8
+#define GGQ_TYPE_Q4_K 12
+#define GGQ_TYPE_Q5_K 13
+#define GGQ_TYPE_Q6_K 14
+#define GGQ_TYPE_IQ4_NL 20
+#define GGQ_TYPE_IQ4_XS 23
+
+#define GGQ_ACT_F32 0
+#define GGQ_ACT_Q8_ROW 1
+#define GGQ_ACT_Q8_BLOCK32 2
+
+typedef struct ggq_ctx ggq_ctx;
+typedef struct ggq_weight ggq_weight;
+
+/* ---------------------------------------------------------------- context */
+
+/* Replaces create_amd_xdna_backend(int device_id) (backend.h:162-165).
+ * Returns GGQ_DEVICE_UNAVAILABLE when no HIP device with that id exists. */
+int ggq_create(int device, ggq_ctx** out);
+/* Frees every device allocation the context owns (uploaded weights,
+ * workspace) and its stream. */
+void ggq_destroy(ggq_ctx* ctx);
+/* Backend::last_error (backend.h:159): status of the most recent call. */
+int ggq_last_error(const ggq_ctx* ctx);
+/* Human-readable detail of the most recent error ("" when none). */
+const char* ggq_last_error_message(const ggq_ctx* ctx);
+/* Backend::name (backend.h:158). */
+const char* ggq_name(const ggq_ctx* ctx);
+/* Backend::is_available (backend.h:157). */
+int ggq_is_available(const ggq_ctx* ctx);
+/* Backend::sync (backend.h:155): waits for all work on the context stream. */
+int ggq_sync(ggq_ctx* ctx);
+
+/* ------------------------------------------------ host-pointer, synchronous */
+
+/* MulMatParams (backend.h:21-35) with B = raw GGUF bytes; field order and
+ * meaning as in the reference.  `scales`/`n_weight_scales` must be 0 (they
+ * carry the XDNA path's re-quantized row scales, which this backend never
+ * uses).  lda/ldc of 0 mean K/N. */
+typedef struct {
+    const void* A;
+    const void* B;
+    void* C;
+    int M;
+    int N;
+    int K;
+    int lda;
+    int ldb;
+    int ldc;
+    int32_t n_batches;
+    const void* scales;
+    int n_weight_scales;
+    uint32_t B_type;
+} ggq_mul_mat_params;
+
+/* Replaces Backend::mul_mat_q (backend.h:117) for raw-block weights.  B is
+ * uploaded to HBM unchanged on first use and kept resident, keyed by
+ * (B pointer, type, N, K) like the XDNA backend's resident weight BOs
+ * (amd_xdna.cpp:279-310, 726-748); the caller keeps B alive and unchanged
+ * while the context lives (it is an mmap'd GGUF tensor in the reference).
+ * Synchronous: C is complete on return (as cpu_ref.cpp and amd_xdna.cpp). */
+int ggq_mul_mat_q(ggq_ctx* ctx, const ggq_mul_mat_params* params, int act_mode);
+
+/* Explicit upload of raw blocks (copied unchanged; host bytes stay owned by
+ * the caller).  No reference counterpart: the reference re-reads mmap'd
+ * bytes per call; this is the HBM-resident form of the same tensor. */
+int ggq_weight_upload(ggq_ctx* ctx, const void* raw, uint32_t type, int64_t N, int64_t K,
+                      ggq_weight** out);
+int ggq_weight_free(ggq_ctx* ctx, ggq_weight* w);
+/* Device address of an uploaded weight (for the *_dev entry points). */
+const void* ggq_weight_device_ptr(const ggq_weight* w);
+/* Synchronous matmul against an uploaded weight with host A and C. */
+int ggq_mul_mat(ggq_ctx* ctx, const ggq_weight* w, const float* A, int lda, float* C, int ldc,
+                int M, int act_mode);
+
+/* --------------------------------------- device-pointer, asynchronous */
+/* All pointers below are device pointers; work is queued on `stream`
+ * (a hipStream_t; NULL = the context's stream) and the call returns without
+ * waiting.  W must be 16-byte aligned and readable for 256 bytes past its
+ * last block (allocations made by ggq_weight_upload are). */
+
+/* Same semantics as ggq_mul_mat_q. */
+int ggq_mul_mat_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
+                    const float* A, int lda, float* C, int ldc, int M, int act_mode, void* stream);
+
+/* Bit-exact fp32 dequant of n_blocks consecutive blocks, equal to the
+ * reference's dequant_*_block functions (kquant.h:133-202, q8_0.cpp:19-25,
+ * iq4_nl.cpp:24-31, iq4_xs.cpp:21-38). */
+int ggq_dequant_dev(ggq_ctx* ctx, const void* raw, uint32_t type, int64_t n_blocks, float* out,
+                    void* stream);
+
+/* Activation quantization (act_mode GGQ_ACT_Q8_ROW or GGQ_ACT_Q8_BLOCK32).
+ * q: [M][K] int8; scales: [M] (row) or [M][K/32] (block32).  Bit-exact with
+ * amd_xdna.cpp:598-603, 633-639, 757-771 for the row mode. */
+int ggq_quantize_act_dev(ggq_ctx* ctx, const float* A, int lda, int M, int K, int act_mode,
+                         int8_t* q, float* scales, void* stream);
+
+/* int32 dot products of the raw weight codes with int8 activations, per
+ * scale group (32 values; 16 for Q6_K): out[(m*N + n)*G + g], G = K/group.
+ * Codes: Q4_K nibble, Q5_K 5-bit value, Q6_K 6-bit - 32, Q8_0 int8, IQ4
+ * codebook value.  These are the products the int8 tile kernel forms
+ * (kernels/triton/compile_kernels.py:558-574 tl.dot int8 -> int32), here on
+ * raw codes instead of re-quantized rows. */
+int ggq_block_dot_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
+                      const int8_t* qa, int M, int32_t* out, void* stream);
+
+/* Expert-grouped MoE FFN for a batch of T tokens, replacing the per-token
+ * expert loop of src/cli/main.cpp:3110-3193: top-k routing on the given
+ * router logits, softmax over the selected, SwiGLU experts
+ * down(silu(gate x) * up x), weighted combine, plus an optional shared
+ * expert weighted by shared_w[t] (1 when NULL).  Expert tensors hold E
+ * consecutive matrices (expert e at e * rows * row_bytes, main.cpp:3140-3150):
+ * gate/up [F][H], down [H][F].  Device pointers; asynchronous. */
+typedef struct {
+    int T, H, F, E, top_k;
+    const float* x;             /* [T][H] */
+    const float* router_logits; /* [T][E] */
+    uint32_t gate_type, up_type, down_type;
+    const void* gate_exps;
+    const void* up_exps;
+    const void* down_exps;
+    const void* gate_shexp; /* NULL: no shared expert */
+    const void* up_shexp;
+    const void* down_shexp;
+    const float* shared_w; /* [T] or NULL */
+    float* out;            /* [T][H] */
+    int32_t* sel_experts;  /* optional [T][top_k] */
+    float* sel_weights;    /* optional [T][top_k] */
+} ggq_moe_params;
+int ggq_moe_ffn_dev(ggq_ctx* ctx, const ggq_moe_params* p, void* stream);
+
+/* ------------------------------------------------------- synthetic data */
+
+/* Host-side encoder float -> GGUF blocks for seeded synthetic weights (the
+ * reference ships no quantizer).  x is [n_rows][K] fp32; out receives
+ * n_rows * (K/blck) * type_size bytes.  Multi-threaded. */
+int ggq_encode(uint32_t type, const float* x, int64_t n_rows, int64_t K, void* out);
+
+/* Bytes of one row of K values of `type` (0 if unsupported or K not a
+ * multiple of the block size). */
+int64_t ggq_row_bytes(uint32_t type, int64_t K);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GGQ_H */

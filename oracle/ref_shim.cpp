@@ -1,0 +1,73 @@
+// ref_shim.cpp -- extern "C" entry points over the ggnpu reference sources,
+// compiled (by oracle/Makefile) straight from /root/reference into
+// oracle/_ref/libggnpu_ref.so.  TEST INFRASTRUCTURE ONLY: used by
+// tests/golden/make_golden.py and the CPU tests in this container to check the
+// oracle restatement against the reference's own code.  No reference source is
+// copied; this file only calls the reference's public functions.
+#include <cstdint>
+#include <cstring>
+#include <vector>
+#include "backend.h"
+#include "tensor.h"
+#include "quant/kquant.h"
+#include "quant/q8_0.h"
+#include "quant/iq4_nl.h"
+#include "quant/iq4_xs.h"
+#include "quant/quant.h"
+
+using namespace ggnpu;
+
+extern "C" {
+
+float ref_fp16_to_f32(uint16_t h) { return fp16_to_f32(h); }
+
+void ref_q4k_scale_min(int j, const uint8_t* q, uint8_t* sc, uint8_t* m) {
+    q4k_get_scale_min(j, q, sc, m);
+}
+
+// Dequantize n consecutive blocks of the given ggml type id.
+int ref_dequant_blocks(uint32_t type, const uint8_t* raw, int64_t n, float* out) {
+    const size_t bs = ggml_type_size(static_cast<GgmlType>(type));
+    const size_t be = ggml_blck_size(static_cast<GgmlType>(type));
+    for (int64_t i = 0; i < n; i++) {
+        const uint8_t* b = raw + i * bs;
+        float* o = out + i * be;
+        switch (static_cast<GgmlType>(type)) {
+        case GgmlType::Q4_K: dequant_q4_k_block(b, o); break;
+        case GgmlType::Q5_K: dequant_q5_k_block(b, o); break;
+        case GgmlType::Q6_K: dequant_q6_k_block(b, o); break;
+        case GgmlType::Q8_0: dequant_q8_0_block(b, o); break;
+        case GgmlType::IQ4_NL: dequant_iq4_nl_block(b, o); break;
+        case GgmlType::IQ4_XS: dequant_iq4_xs_block(b, o); break;
+        default: return 3;
+        }
+    }
+    return 0;
+}
+
+uint64_t ref_type_size(uint32_t type) { return ggml_type_size(static_cast<GgmlType>(type)); }
+uint64_t ref_blck_size(uint32_t type) { return ggml_blck_size(static_cast<GgmlType>(type)); }
+
+// Per-row int8 weight requant (decode_*_for_npu): outputs [N][K] int8 + [N] scales.
+int ref_decode_for_npu(uint32_t type, const uint8_t* raw, uint64_t size, int64_t N, int64_t K,
+                       int8_t* q, float* scales) {
+    std::vector<int8_t> qo;
+    std::vector<float> so;
+    decode_for_npu(static_cast<GgmlType>(type), raw, size, N, K, qo, so);
+    if (qo.size() != static_cast<size_t>(N * K) || so.size() != static_cast<size_t>(N)) return 1;
+    std::memcpy(q, qo.data(), qo.size());
+    std::memcpy(scales, so.data(), so.size() * sizeof(float));
+    return 0;
+}
+
+// CpuRefBackend::mul_mat_q on raw blocks (valid for Q4_K / Q6_K).
+int ref_cpuref_mul_mat(uint32_t type, const void* W, int N, int K, const float* A, int M, float* C) {
+    auto be = create_cpu_ref_backend();
+    MulMatParams p;
+    p.A = A; p.B = W; p.C = C; p.M = M; p.N = N; p.K = K;
+    p.lda = K; p.ldb = K; p.ldc = N; p.n_batches = 1;
+    p.B_type = static_cast<GgmlType>(type);
+    return static_cast<int>(be->mul_mat_q(p));
+}
+
+}  // extern "C"

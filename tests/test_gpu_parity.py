@@ -1,0 +1,306 @@
+"""GPU parity of every kernel against the CPU oracle, through the C ABI.
+
+Bar (north star): dequantized values, int8 activation quantization and int32
+block dot products bit-exact; matmul / MoE outputs within relative L2 1e-4
+of the fp64 oracle that uses the same activation treatment.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import ggnpu_amd.lib as gl
+from tests.gpu_util import dev, empty, host, ptr, stream_handle
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23}
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import torch
+    assert torch.cuda.is_available()
+    c = gl.Context(0)
+    yield c
+    c.close()
+
+
+def weights(t, N, K, seed, scale=0.02):
+    rng = np.random.default_rng(seed)
+    return gl.encode(t, (rng.standard_normal((N, K)) * scale).astype(np.float32))
+
+
+def run_mm(ctx, t, raw, N, K, A, act_mode, lda=None, ldc=None):
+    import torch
+    M = A.shape[0]
+    lda = lda or K
+    ldc = ldc or N
+    Ap = np.zeros((M, lda), np.float32)
+    Ap[:, :K] = A
+    dA = dev(Ap)
+    dW = dev(raw)
+    dC = torch.full((max(M, 1), ldc), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.check(ctx.lib.ggq_mul_mat_dev(ctx.h, ptr(dW), t, N, K, ptr(dA), lda, ptr(dC), ldc, M, act_mode,
+                                      stream_handle()), "mul_mat_dev")
+    C = host(dC)[:M]
+    if ldc > N:
+        assert np.all(np.isnan(C[:, N:])), "wrote past N"
+    return C[:, :N]
+
+
+# ------------------------------------------------------------- bit-exact
+@pytest.mark.parametrize("name", list(TYPES))
+def test_dequant_bitexact_vs_reference_vectors(ctx, golden, name):
+    t = TYPES[name]
+    raw = golden[f"{name}_raw"]
+    exp = golden[f"{name}_deq"]
+    nb = raw.size // gl.BLOCK[gl.GgmlType(t)][1]
+    out = empty(exp.size, dtype=__import__("torch").float32)
+    dW = dev(raw)
+    ctx.check(ctx.lib.ggq_dequant_dev(ctx.h, ptr(dW), t, nb, ptr(out), stream_handle()), "dequant")
+    assert np.array_equal(host(out).view(np.uint32), exp.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_dequant_bitexact_encoded_weights(ctx, orc, name):
+    t = TYPES[name]
+    raw = weights(t, 64, 1024, seed=t)
+    nb = raw.size // gl.BLOCK[gl.GgmlType(t)][1]
+    out = empty(64 * 1024, dtype=__import__("torch").float32)
+    dW = dev(raw)
+    ctx.check(ctx.lib.ggq_dequant_dev(ctx.h, ptr(dW), t, nb, ptr(out), stream_handle()), "dequant")
+    assert np.array_equal(host(out).view(np.uint32), orc.dequant(t, raw).view(np.uint32))
+
+
+def test_fp16_conversion_all_patterns(ctx, golden):
+    """Every fp16 scale bit pattern through Q8_0 blocks with q = 1: out = d."""
+    n = 65536
+    raw = np.zeros((n, 34), np.uint8)
+    h = np.arange(n, dtype=np.uint32)
+    raw[:, 0] = h & 0xFF
+    raw[:, 1] = h >> 8
+    raw[:, 2] = 1
+    out = empty(n * 32, dtype=__import__("torch").float32)
+    dW = dev(raw.reshape(-1))
+    ctx.check(ctx.lib.ggq_dequant_dev(ctx.h, ptr(dW), 8, n, ptr(out), stream_handle()), "dequant")
+    got = host(out).reshape(n, 32)[:, 0]
+    ref = golden["fp16_all"]
+    ok = ~np.isnan(ref)
+    assert np.array_equal(got.view(np.uint32)[ok], ref.view(np.uint32)[ok])
+    assert np.all(np.isnan(got[~ok]))
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("M,K", [(1, 2048), (7, 1536), (64, 8960), (3, 32)])
+def test_quant_act_bitexact(ctx, orc, mode, M, K):
+    import torch
+    rng = np.random.default_rng(M * K + mode)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    if M > 1:
+        A[1] = 0.0
+    A[0, :32] *= 1e3
+    q_ref, s_ref = orc.quant_act(A, mode)
+    dq = empty((M, K), torch.int8)
+    ds = empty(s_ref.shape, torch.float32)
+    dA = dev(A)
+    ctx.check(ctx.lib.ggq_quantize_act_dev(ctx.h, ptr(dA), K, M, K, mode, ptr(dq), ptr(ds),
+                                           stream_handle()), "quant_act")
+    assert np.array_equal(host(dq), q_ref)
+    assert np.array_equal(host(ds).view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_block_dot_bitexact(ctx, orc, golden, name):
+    import torch
+    t = TYPES[name]
+    be, bb = gl.BLOCK[gl.GgmlType(t)]
+    K = 512
+    for src in ("golden", "encoded"):
+        if src == "golden":
+            N = (golden[f"{name}_raw"].size // bb) * be // K
+            raw = golden[f"{name}_raw"][: N * (K // be) * bb]
+        else:
+            N = 33
+            raw = weights(t, N, K, seed=100 + t)
+        rng = np.random.default_rng(t)
+        qa = rng.integers(-128, 128, size=(3, K), dtype=np.int8)
+        ref = orc.block_dot(t, raw, N, K, qa)
+        out = empty(ref.shape, torch.int32)
+        dW, dq = dev(raw), dev(qa)  # keep both alive until the kernel has run
+        ctx.check(ctx.lib.ggq_block_dot_dev(ctx.h, ptr(dW), t, N, K, ptr(dq), 3, ptr(out),
+                                            stream_handle()), "block_dot")
+        assert np.array_equal(host(out), ref), src
+
+
+# ------------------------------------------------------------------ GEMV
+GEMV_K = {8: [32, 256, 2048, 3072, 8960], 20: [64, 1024, 3072], 12: [256, 2048, 8192, 16384],
+          13: [512, 3072], 14: [512, 2048, 8192], 23: [1024, 2048, 8960 - 8960 % 256]}
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+def test_gemv_f32_vs_oracle(ctx, orc, name, M):
+    t = TYPES[name]
+    for K in GEMV_K[t]:
+        N = 67
+        raw = weights(t, N, K, seed=K + t)
+        A = np.random.default_rng(K + M).standard_normal((M, K)).astype(np.float32)
+        got = run_mm(ctx, t, raw, N, K, A, 0)
+        err = orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 0))
+        assert err < TOL, (K, err)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("mode", [1, 2])
+def test_gemv_q8_act_vs_oracle(ctx, orc, name, mode):
+    t = TYPES[name]
+    K = 1024
+    N = 129
+    raw = weights(t, N, K, seed=7)
+    for M in (1, 4, 8):
+        A = np.random.default_rng(M).standard_normal((M, K)).astype(np.float32)
+        got = run_mm(ctx, t, raw, N, K, A, mode)
+        assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, mode)) < TOL
+
+
+def test_gemv_strided_rows(ctx, orc):
+    t, N, K, M = 12, 50, 512, 3
+    raw = weights(t, N, K, seed=1)
+    A = np.random.default_rng(0).standard_normal((M, K)).astype(np.float32)
+    got = run_mm(ctx, t, raw, N, K, A, 0, lda=K + 17, ldc=N + 5)
+    assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 0)) < TOL
+
+
+def test_gemv_random_byte_blocks(ctx, orc, golden):
+    """Blocks with arbitrary payload bytes (not from the encoder)."""
+    for name, t in TYPES.items():
+        be, bb = gl.BLOCK[gl.GgmlType(t)]
+        raw = golden[f"{name}_raw"][: 64 * bb]
+        K = be * 4 if be == 256 else be * 16
+        N = 64 * be // K
+        A = np.random.default_rng(t).standard_normal((2, K)).astype(np.float32)
+        got = run_mm(ctx, t, raw, N, K, A, 0)
+        assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 0)) < TOL, name
+
+
+def test_config1_q4k_gemv_llama_ffn_up(ctx, orc):
+    """Config 1: Q4_K 8192x2048, batch 1, fp32 activation."""
+    t, N, K = 12, 8192, 2048
+    raw = weights(t, N, K, seed=1)
+    A = np.random.default_rng(2).standard_normal((1, K)).astype(np.float32)
+    got = run_mm(ctx, t, raw, N, K, A, 0)
+    assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 0)) < TOL
+
+
+# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("name", list(TYPES))
+def test_prefill_gemm_q8_row_vs_oracle(ctx, orc, name):
+    """M > 8 with per-row int8 activations runs the int8-MFMA GEMM."""
+    t = TYPES[name]
+    be = gl.BLOCK[gl.GgmlType(t)][0]
+    K = 1536 if be == 32 else 1024
+    for M, N in ((200, 300), (128, 128), (9, 40)):
+        raw = weights(t, N, K, seed=M + t)
+        A = np.random.default_rng(M).standard_normal((M, K)).astype(np.float32)
+        got = run_mm(ctx, t, raw, N, K, A, 1)
+        err = orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 1))
+        assert err < TOL, (M, N, err)
+
+
+def test_prefill_f32_large_m(ctx, orc):
+    t, N, K, M = 8, 96, 1536, 40
+    raw = weights(t, N, K, seed=3)
+    A = np.random.default_rng(3).standard_normal((M, K)).astype(np.float32)
+    got = run_mm(ctx, t, raw, N, K, A, 0)
+    assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 0)) < TOL
+
+
+# ------------------------------------------------------------------- MoE
+def run_moe(ctx, T, H, F, E, k, shared, seed, tg=12, tu=12, td=14):
+    import torch
+    rng = np.random.default_rng(seed)
+    Wg = gl.encode(tg, (rng.standard_normal((E * F, H)) * 0.02).astype(np.float32))
+    Wu = gl.encode(tu, (rng.standard_normal((E * F, H)) * 0.02).astype(np.float32))
+    Wd = gl.encode(td, (rng.standard_normal((E * H, F)) * 0.02).astype(np.float32))
+    Sg = Su = Sd = sw = None
+    if shared:
+        Sg = gl.encode(tg, (rng.standard_normal((F, H)) * 0.02).astype(np.float32))
+        Su = gl.encode(tu, (rng.standard_normal((F, H)) * 0.02).astype(np.float32))
+        Sd = gl.encode(td, (rng.standard_normal((H, F)) * 0.02).astype(np.float32))
+        sw = (1.0 / (1.0 + np.exp(-rng.standard_normal(T)))).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    keep = [dev(a) if a is not None else None for a in (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw)]
+    out = empty((T, H), torch.float32)
+    sel = empty((T, k), torch.int32)
+    wsel = empty((T, k), torch.float32)
+    p = gl.MoeParams()
+    p.T, p.H, p.F, p.E, p.top_k = T, H, F, E, k
+    p.x, p.router_logits = keep[0].data_ptr(), keep[1].data_ptr()
+    p.gate_type, p.up_type, p.down_type = tg, tu, td
+    p.gate_exps, p.up_exps, p.down_exps = keep[2].data_ptr(), keep[3].data_ptr(), keep[4].data_ptr()
+    if shared:
+        p.gate_shexp, p.up_shexp, p.down_shexp = keep[5].data_ptr(), keep[6].data_ptr(), keep[7].data_ptr()
+        p.shared_w = keep[8].data_ptr()
+    p.out, p.sel_experts, p.sel_weights = out.data_ptr(), sel.data_ptr(), wsel.data_ptr()
+    ctx.check(ctx.lib.ggq_moe_ffn_dev(ctx.h, ctypes.byref(p), stream_handle()), "moe")
+    return (host(out), host(sel), host(wsel)), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw)
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_moe_small_vs_oracle(ctx, orc, shared):
+    T, H, F, E, k = 16, 512, 256, 16, 4
+    (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(ctx, T, H, F, E, k, shared, seed=11)
+    ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, 12, Wg, 12, Wu, 14, Wd, Sg, Su, Sd, sw)
+    assert np.array_equal(sel, rsel)
+    assert np.allclose(wsel, rw, rtol=1e-6)
+    assert orc.rel_l2(out, ref) < TOL
+
+
+def test_moe_qwen35moe_shape_vs_oracle(ctx, orc):
+    """Config 5 shapes (H 2048, 256 experts of FFN 512, top-8, shared), 8 tokens."""
+    T, H, F, E, k = 8, 2048, 512, 256, 8
+    (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(ctx, T, H, F, E, k, True, seed=12)
+    ref, rsel, _ = orc.moe_ffn_f64(x, logits, H, F, E, k, 12, Wg, 12, Wu, 14, Wd, Sg, Su, Sd, sw)
+    assert np.array_equal(sel, rsel)
+    assert orc.rel_l2(out, ref) < TOL
+
+
+# --------------------------------------------------------- host boundary
+def test_mul_mat_q_host_api_and_errors(ctx, orc):
+    t, N, K, M = 14, 70, 512, 2
+    raw = weights(t, N, K, seed=5)
+    A = np.random.default_rng(5).standard_normal((M, K)).astype(np.float32)
+    C = np.full((M, N), np.nan, np.float32)
+    p = gl.MulMatParams()
+    p.A, p.B, p.C = A.ctypes.data, raw.ctypes.data, C.ctypes.data
+    p.M, p.N, p.K, p.lda, p.ldb, p.ldc, p.n_batches, p.B_type = M, N, K, K, K, N, 1, t
+    for _ in range(2):  # second call hits the resident-weight cache
+        ctx.check(ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(p), 0), "mul_mat_q")
+        assert orc.rel_l2(C, orc.mul_mat_f64(t, raw, N, K, A, 0)) < TOL
+    bad = gl.MulMatParams.from_buffer_copy(p)
+    bad.A = None
+    assert ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(bad), 0) == gl.Status.INVALID_PARAM
+    assert ctx.lib.ggq_last_error(ctx.h) == gl.Status.INVALID_PARAM
+    bad = gl.MulMatParams.from_buffer_copy(p)
+    bad.K = 500
+    assert ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(bad), 0) == gl.Status.INVALID_PARAM
+    bad = gl.MulMatParams.from_buffer_copy(p)
+    bad.B_type = 2
+    assert ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(bad), 0) == gl.Status.INVALID_PARAM
+    assert ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(p), 7) == gl.Status.INVALID_PARAM
+
+
+def test_weight_upload_roundtrip(ctx, orc):
+    t, N, K = 23, 40, 1024
+    raw = weights(t, N, K, seed=9)
+    w = ctypes.c_void_p()
+    ctx.check(ctx.lib.ggq_weight_upload(ctx.h, raw.ctypes.data, t, N, K, ctypes.byref(w)), "upload")
+    A = np.random.default_rng(9).standard_normal((3, K)).astype(np.float32)
+    C = np.zeros((3, N), np.float32)
+    ctx.check(ctx.lib.ggq_mul_mat(ctx.h, w, A.ctypes.data, K, C.ctypes.data, N, 3, 1), "mul_mat")
+    assert orc.rel_l2(C, orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL
+    ctx.check(ctx.lib.ggq_weight_free(ctx.h, w), "free")
+    assert ctx.lib.ggq_weight_free(ctx.h, w) == gl.Status.INVALID_PARAM

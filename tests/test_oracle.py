@@ -1,0 +1,238 @@
+"""Pins the CPU oracle (oracle/ggq_oracle.c) before anything is checked
+against it.  CPU only.
+
+Each oracle function is checked against at least one of:
+  * the reference's own unit-test goldens (tests/test_quant.cpp:209-288)
+  * vectors produced by the reference sources (tests/golden/ref_vectors.npz)
+  * closed forms / brute force computed independently in numpy
+"""
+import numpy as np
+import pytest
+
+TYPES = {"Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23}
+KV = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.int8)
+
+
+def f16(v):
+    return int(np.array(v, dtype=np.float16).view(np.uint16))
+
+
+# ---------------------------------------------------------------- goldens
+def test_q4_k_reference_golden(orc):
+    # tests/test_quant.cpp:209-236: d=0.5, dmin=0.25, scales 2 / mins 1 for
+    # groups 0..3, qs[0]=0x31 -> out[0]=0.75, out[1]=-0.25, out[32]=2.75
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.frombuffer(np.uint16(f16(0.5)).tobytes(), np.uint8)
+    b[2:4] = np.frombuffer(np.uint16(f16(0.25)).tobytes(), np.uint8)
+    b[4:8] = 2
+    b[8:12] = 1
+    b[16] = 0x31
+    out = orc.dequant(12, b)
+    assert out[0] == 0.75 and out[1] == -0.25 and out[32] == 2.75
+
+
+def test_q6_k_reference_golden(orc):
+    # tests/test_quant.cpp:251-275: d=0.25, sc[0]=4, sc[4]=2, ql[0]=0x21
+    b = np.zeros(210, np.uint8)
+    b[208:210] = np.frombuffer(np.uint16(f16(0.25)).tobytes(), np.uint8)
+    b[192] = 4
+    b[196] = 2
+    b[0] = 0x21
+    out = orc.dequant(14, b)
+    assert out[0] == -31.0 and out[64] == -15.0 and out[1] == -32.0
+
+
+def test_q8_0_reference_values(orc):
+    # tests/test_quant.cpp:130-152: d=1.0, qs[0]=3, qs[31]=1
+    b = np.zeros(34, np.uint8)
+    b[0:2] = [0x00, 0x3C]
+    b[2] = 3
+    b[33] = 1
+    out = orc.dequant(8, b)
+    assert out[0] == 3.0 and out[31] == 1.0 and np.count_nonzero(out) == 2
+
+
+def test_type_table(orc, golden):
+    # src/gguf/tensor.cpp:18-38 via the compiled reference, and the sizes
+    # asserted by tests/test_quant.cpp:194-207 / tests/test_gguf.cpp:42-73
+    for t, be, bb in golden["type_table"]:
+        assert orc.block_elems(int(t)) == be and orc.block_bytes(int(t)) == bb
+    assert orc.block_bytes(12) == 144 and orc.block_bytes(14) == 210
+
+
+# ------------------------------------------------------ reference vectors
+@pytest.mark.parametrize("name", list(TYPES))
+def test_dequant_matches_reference_bitexact(orc, golden, name):
+    t = TYPES[name]
+    got = orc.dequant(t, golden[f"{name}_raw"])
+    exp = golden[f"{name}_deq"]
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+def test_fp16_all_patterns(orc, golden):
+    got = np.array([orc.lib().orc_fp16_to_f32(h) for h in range(65536)], dtype=np.float32)
+    ref = golden["fp16_all"]
+    finite = np.isfinite(ref) | np.isinf(ref)
+    assert np.array_equal(got.view(np.uint32)[finite], ref.view(np.uint32)[finite])
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    # closed form: numpy's IEEE half conversion
+    halves = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    ok = ~np.isnan(halves)
+    assert np.array_equal(got.view(np.uint32)[ok], halves.view(np.uint32)[ok])
+
+
+def test_scale_min_unpack(orc, golden):
+    import ctypes
+    a, b = ctypes.c_uint8(), ctypes.c_uint8()
+    for i, row in enumerate(golden["scale_min_in"]):
+        row = np.ascontiguousarray(row)
+        for j in range(8):
+            orc.lib().orc_q4k_scale_min(j, row.ctypes.data, ctypes.byref(a), ctypes.byref(b))
+            assert (a.value, b.value) == tuple(golden["scale_min_out"][i, j])
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K"])
+def test_f64_oracle_vs_reference_cpuref(orc, golden, name):
+    """orc_mul_mat_f64 vs the compiled CpuRefBackend::mul_mat_q (fp32)."""
+    M, N, K = golden[f"cpuref_{name}_shape"]
+    W, A, C = golden[f"cpuref_{name}_W"], golden[f"cpuref_{name}_A"], golden[f"cpuref_{name}_C"]
+    got = orc.mul_mat_f64(TYPES[name], W, int(N), int(K), A)
+    assert orc.rel_l2(got, C) < 1e-5
+    # the fp32 restatement reproduces the reference's own summation order
+    got32 = orc.mul_mat_cpuref_f32(TYPES[name], W, int(N), int(K), A)
+    assert np.array_equal(got32, C)
+
+
+# ------------------------------------------------------------ closed forms
+def test_iq4_nl_closed_form(orc, golden):
+    raw = golden["IQ4_NL_raw"].reshape(-1, 18)
+    d = raw[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1, 1)
+    lo, hi = raw[:, 2:] & 15, raw[:, 2:] >> 4
+    exp = np.concatenate([d * KV[lo].astype(np.float32), d * KV[hi].astype(np.float32)], axis=1)
+    assert np.array_equal(orc.dequant(20, raw.reshape(-1)).reshape(-1, 32), exp)
+
+
+def test_q8_0_closed_form(orc, golden):
+    raw = golden["Q8_0_raw"].reshape(-1, 34)
+    d = raw[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1, 1)
+    exp = raw[:, 2:].view(np.int8).astype(np.float32) * d
+    assert np.array_equal(orc.dequant(8, raw.reshape(-1)).reshape(-1, 32), exp)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_codes_times_scale_is_dequant(orc, golden, name):
+    """Integer codes (the MFMA/dot operands) reproduce the dequant values:
+    for formats without a min, value == scale * code with a per-group scale,
+    so value/code is constant within each group."""
+    t = TYPES[name]
+    raw = golden[f"{name}_raw"][: 64 * orc.block_bytes(t)]
+    q = orc.codes(t, raw).astype(np.float64)
+    v = orc.dequant(t, raw).astype(np.float64)
+    ge = 16 if t == 14 else 32
+    q, v = q.reshape(-1, ge), v.reshape(-1, ge)
+    if t in (12, 13):
+        # affine: v = dl*q - ml -> dl = slope, check linearity within a group
+        for g in range(q.shape[0]):
+            if np.ptp(q[g]) == 0:
+                continue
+            A = np.stack([q[g], np.ones(ge)], 1)
+            sol, *_ = np.linalg.lstsq(A, v[g], rcond=None)
+            assert np.allclose(A @ sol, v[g], rtol=1e-6, atol=1e-6 * np.abs(v[g]).max())
+    else:
+        for g in range(q.shape[0]):
+            nz = q[g] != 0
+            assert np.all(v[g][~nz] == 0)
+            if nz.any():
+                r = v[g][nz] / q[g][nz]
+                assert np.allclose(r, r[0], rtol=1e-6)
+
+
+def test_quant_act_row_closed_form(orc):
+    rng = np.random.default_rng(1)
+    A = rng.standard_normal((5, 300)).astype(np.float32)
+    A[1] = 0.0                              # zero row -> scale 1, all zero
+    A[2, 7] = 0.5 * (np.abs(A[2]).max() / 127.0) * 3  # near a rounding tie
+    q, s = orc.quant_act(A, 1)
+    amax = np.abs(A).max(axis=1)
+    s_exp = np.where(amax > 0, (amax / np.float32(127.0)).astype(np.float32), np.float32(1.0)).astype(np.float32)
+    assert np.array_equal(s, s_exp)
+    inv = (np.float32(1.0) / s_exp).astype(np.float32)
+    q_exp = np.clip(np.rint((A * inv[:, None]).astype(np.float32)), -128, 127).astype(np.int8)
+    assert np.array_equal(q, q_exp)
+    assert np.all(q[1] == 0) and s[1] == 1.0
+    # the row maximum maps to +-127
+    assert np.all(np.abs(q[[0, 2, 3, 4]]).max(axis=1) == 127)
+
+
+def test_quant_act_block32_closed_form(orc):
+    rng = np.random.default_rng(2)
+    A = rng.standard_normal((3, 128)).astype(np.float32)
+    A[0, :32] = 0
+    q, s = orc.quant_act(A, 2)
+    blk = A.reshape(3, 4, 32)
+    amax = np.abs(blk).max(axis=2)
+    s_exp = np.where(amax > 0, (amax / np.float32(127.0)).astype(np.float32), np.float32(1.0)).astype(np.float32)
+    assert np.array_equal(s, s_exp)
+    inv = (np.float32(1.0) / s_exp).astype(np.float32)
+    q_exp = np.clip(np.rint((blk * inv[:, :, None]).astype(np.float32)), -128, 127).astype(np.int8)
+    assert np.array_equal(q, q_exp.reshape(3, 128))
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_block_dot_brute_force(orc, golden, name):
+    t = TYPES[name]
+    be, bb = orc.block_elems(t), orc.block_bytes(t)
+    K = 256 if be == 256 else 64
+    N = 3
+    raw = golden[f"{name}_raw"][: N * (K // be) * bb]
+    rng = np.random.default_rng(3)
+    qa = rng.integers(-128, 128, size=(2, K), dtype=np.int8)
+    got = orc.block_dot(t, raw, N, K, qa)
+    codes = orc.codes(t, raw).astype(np.int64).reshape(N, K)
+    ge = 16 if t == 14 else 32
+    exp = (qa.astype(np.int64)[:, None, :] * codes[None, :, :]).reshape(2, N, K // ge, ge).sum(-1)
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_f64_oracle_vs_numpy(orc, golden, mode):
+    t = 23
+    be, bb = 256, 136
+    N, K = 5, 512
+    raw = golden["IQ4_XS_raw"][: N * (K // be) * bb]
+    rng = np.random.default_rng(4)
+    A = rng.standard_normal((3, K)).astype(np.float32)
+    W = orc.dequant(t, raw).astype(np.float64).reshape(N, K)
+    if mode == 0:
+        Ae = A.astype(np.float64)
+    else:
+        q, s = orc.quant_act(A, mode)
+        Ae = q.astype(np.float64) * (s[:, None] if mode == 1 else np.repeat(s, 32, axis=1))
+    assert orc.rel_l2(orc.mul_mat_f64(t, raw, N, K, A, mode), Ae @ W.T) < 1e-13
+
+
+def test_moe_oracle_vs_numpy_loop(orc):
+    """orc_moe_ffn_f64 vs a numpy restatement of main.cpp:3110-3193."""
+    import ggnpu_amd.lib as gl
+    rng = np.random.default_rng(5)
+    T, H, F, E, k = 3, 256, 256, 6, 2
+    Wg = gl.encode(12, (rng.standard_normal((E * F, H)) * 0.02).astype(np.float32))
+    Wu = gl.encode(12, (rng.standard_normal((E * F, H)) * 0.02).astype(np.float32))
+    Wd = gl.encode(14, (rng.standard_normal((E * H, F)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    out, sel, wsel = orc.moe_ffn_f64(x, logits, H, F, E, k, 12, Wg, 12, Wu, 14, Wd)
+    dg = orc.dequant(12, Wg).astype(np.float64).reshape(E, F, H)
+    du = orc.dequant(12, Wu).astype(np.float64).reshape(E, F, H)
+    dd = orc.dequant(14, Wd).astype(np.float64).reshape(E, H, F)
+    for t in range(T):
+        order = np.argsort(-logits[t], kind="stable")[:k]
+        assert list(sel[t]) == list(order)
+        w = np.exp(logits[t, order].astype(np.float64) - logits[t, order[0]])
+        w /= w.sum()
+        ref = np.zeros(H)
+        for j, e in enumerate(order):
+            g, u = dg[e] @ x[t], du[e] @ x[t]
+            h = (g / (1 + np.exp(-g)) * u).astype(np.float32).astype(np.float64)
+            ref += w[j] * (dd[e] @ h)
+        assert orc.rel_l2(out[t], ref) < 1e-12
