@@ -77,6 +77,17 @@ def make_weight(torch, gen, t, N, K):
     return dev, raw
 
 
+def launch_batch(ctx, ms, stream):
+    """Independent M=1 matmuls of one dependency level in one call."""
+    descs = (gl.GemvDesc * len(ms))()
+    for i, m in enumerate(ms):
+        descs[i].W, descs[i].type, descs[i].N, descs[i].K = m.w.data_ptr(), m.t, m.N, m.K
+        descs[i].A, descs[i].C = m.x.data_ptr(), m.y.data_ptr()
+    st = ctx.lib.ggq_mul_mat_batch_dev(ctx.h, descs, len(ms), stream)
+    if st != 0:
+        ctx.check(st, "mul_mat_batch_dev")
+
+
 def launch(ctx, m, act_mode, stream):
     st = ctx.lib.ggq_mul_mat_dev(ctx.h, ctypes.c_void_p(m.w.data_ptr()), m.t, m.N, m.K,
                                  ctypes.c_void_p(m.x.data_ptr()), m.K, ctypes.c_void_p(m.y.data_ptr()), m.N,
@@ -96,21 +107,22 @@ def time_steps(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
-def per_launch_times(torch, ctx, mats, act_mode, stream, reps):
-    """HIP events around every launch, on the launch stream; returns the
-    mean duration (s) of each matrix's kernel(s) over `reps` steps."""
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in mats]
+def per_launch_times(torch, fns, reps):
+    """HIP events around every launch (on the stream the kernels run on,
+    which is torch's current stream); returns the mean duration (s) of each
+    callable's kernel over `reps` rounds."""
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in fns]
           for _ in range(reps)]
     for r in range(reps):
-        for i, m in enumerate(mats):
+        for i, fn in enumerate(fns):
             ev[r][i][0].record()
-            launch(ctx, m, act_mode, stream)
+            fn()
             ev[r][i][1].record()
     torch.cuda.synchronize()
-    return [sum(ev[r][i][0].elapsed_time(ev[r][i][1]) for r in range(reps)) / reps / 1e3 for i in range(len(mats))]
+    return [sum(ev[r][i][0].elapsed_time(ev[r][i][1]) for r in range(reps)) / reps / 1e3 for i in range(len(fns))]
 
 
-def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream):
+def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream, fuse_levels=True):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
     mats, host_layer0 = [], []
@@ -129,9 +141,25 @@ def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream):
     log(f"decode step: {len(mats)} matrices resident ({sum(m.bytes() for m in mats) / 1e6:.1f} MB) "
         f"in {time.time() - t0:.1f}s")
 
+    # Dependency levels of a real decode step: q/k/v read the same normed
+    # input, gate/up read the same normed residual; o, down and the output
+    # projection each depend on the previous level.  One call per level.
+    levels = []
+    for layer in range(LLAMA_LAYERS):
+        q, k, v, o, gate, up, down = mats[7 * layer: 7 * layer + 7]
+        levels += [[q, k, v], [o], [gate, up], [down]]
+    levels.append([mats[-1]])
+
+    def step_levels(strm):
+        for lv in levels:
+            if len(lv) == 1 or not fuse_levels:
+                for m in lv:
+                    launch(ctx, m, 0, strm)
+            else:
+                launch_batch(ctx, lv, strm)
+
     def step():
-        for m in mats:
-            launch(ctx, m, 0, stream)
+        step_levels(stream)
 
     fn = step
     if use_graph:
@@ -140,17 +168,21 @@ def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream):
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             step_stream = ctypes.c_void_p(s.cuda_stream)
-            for m in mats:  # warm the kernels outside capture
-                launch(ctx, m, 0, step_stream)
+            step_levels(step_stream)  # warm the kernels outside capture
             torch.cuda.synchronize()
             with torch.cuda.graph(g, stream=s):
-                for m in mats:
-                    launch(ctx, m, 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                step_levels(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         fn = g.replay
     sec = time_steps(torch, fn, steps, warmup)
     step_bytes = sum(m.bytes() for m in mats)
-    kt = per_launch_times(torch, ctx, mats, 0, stream, reps=3)
-    return mats, host_layer0, sec, step_bytes, kt
+
+    def level_fn(lv):
+        if len(lv) == 1 or not fuse_levels:
+            return lambda: [launch(ctx, m, 0, stream) for m in lv]
+        return lambda: launch_batch(ctx, lv, stream)
+
+    kt = per_launch_times(torch, [level_fn(lv) for lv in levels], reps=3)
+    return levels, host_layer0, sec, step_bytes, kt
 
 
 def bench_config1(torch, ctx, stream, reps=200):
@@ -167,7 +199,7 @@ def bench_config1(torch, ctx, stream, reps=200):
             launch(ctx, m, 0, stream)
 
     sec = time_steps(torch, run, max(1, reps // 32), 2) / len(mats)
-    kt = per_launch_times(torch, ctx, mats, 0, stream, reps=2)
+    kt = per_launch_times(torch, [lambda m=m: launch(ctx, m, 0, stream) for m in mats], reps=2)
     kmean = sum(kt) / len(kt)
     b = mats[0].bytes()
     return {"workload": "Q4_K GEMV 8192x2048 batch 1 fp32 (32 rotated copies)", "bytes_per_call": b,
@@ -229,6 +261,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
+    ap.add_argument("--per-matmul", action="store_true",
+                    help="one launch per matmul instead of one per dependency level")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the backend is a single-device hot path "
@@ -246,8 +280,8 @@ def main():
     stream = ctypes.c_void_p(side.cuda_stream)
     assert stream.value, "expected a non-null stream handle"
 
-    mats, host_layer0, sec, step_bytes, kt = bench_decode_step(torch, ctx, args.steps, args.warmup,
-                                                               args.graph, stream)
+    levels, host_layer0, sec, step_bytes, kt = bench_decode_step(torch, ctx, args.steps, args.warmup,
+                                                               args.graph, stream, not args.per_matmul)
     value = step_bytes / sec / 1e9
     ktot = sum(kt)
     achieved = step_bytes / ktot / 1e9
@@ -266,11 +300,14 @@ def main():
         "data": "synthetic: seeded N(0,0.02) weights encoded to GGUF blocks, N(0,1) activations",
         "config": {"workload": "Llama-3.2-1B decode step matmuls (configs[1]): 16 layers q/k/v/o/gate/up/down "
                                "Q4_K (v, down Q6_K) + 128256x2048 Q4_K output, batch 1",
-                   "matmuls_per_step": len(mats), "bytes_per_step": step_bytes,
-                   "graph": bool(args.graph)},
+                   "matmuls_per_step": sum(len(lv) for lv in levels), "launch_groups_per_step": len(levels),
+                   "bytes_per_step": step_bytes,
+                   "graph": bool(args.graph),
+                   "launches": "one per dependency level (q/k/v, o, gate/up, down, output)"
+                   if not args.per_matmul else "one per matmul"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel (sum of per-launch HIP-event durations over one step)",
+                     "kernel": "decode GEMV kernels (sum of per-launch HIP-event durations over one step)",
                      "kernel_us_per_step": round(ktot * 1e6, 1)},
     }
     if not args.no_extra:
@@ -281,10 +318,10 @@ def main():
             out["extra"]["config3_prefill"] = {"error": str(e)}
         out["cpu_baseline"] = cpu_baseline(host_layer0)
     per = {}
-    for m, d in zip(mats[:7], kt[:7]):
-        per[m.name.split(".")[1]] = {"us": round(d * 1e6, 2), "GBps": round(m.bytes() / d / 1e9, 1)}
-    per["output"] = {"us": round(kt[-1] * 1e6, 2), "GBps": round(mats[-1].bytes() / kt[-1] / 1e9, 1)}
-    out["per_matmul_layer0"] = per
+    for lv, d in list(zip(levels[:4], kt[:4])) + [(levels[-1], kt[-1])]:
+        key = "+".join(m.name.split(".")[-1] for m in lv)
+        per[key] = {"us": round(d * 1e6, 2), "GBps": round(sum(m.bytes() for m in lv) / d / 1e9, 1)}
+    out["per_level_layer0"] = per
     ctx.close()
     print(json.dumps(out), flush=True)
 

@@ -234,15 +234,20 @@ __device__ __forceinline__ float dequant_value(GroupScale g, int code) {
 }
 
 // ------------------------------------------------------------ pieces -----
-// Decode-GEMV piece: 32 values = two runs of 16 consecutive k.  Pieces of a
-// row are numbered p = 0..K/32-1.  Each format provides
-//   fetch(row, p)  -> Raw: the dwords covering the piece, loaded with plain
-//                     dword-aligned loads and not yet inspected, so a caller
-//                     can keep loads of later rows in flight;
-//   decode(raw, row, p) -> PieceCodes (realignment, unpacking, scales).
+// Decode-GEMV piece: 32 values of one row, as two runs of 16 consecutive k.
+// Pieces of a row are numbered p = 0..K/32-1; run r of piece p starts at
+// k = run_k(p, r).  Each format provides
+//   fetch(row, p)       -> Raw: the dwords covering the piece, loaded with
+//                          plain dword-aligned loads and not yet inspected, so
+//                          a caller can keep loads of later rows in flight;
+//   decode(raw, row, p) -> PieceCodes: unsigned byte codes u[r] and
+//                          coefficients such that
+//     sum_k x_k w_k = sum_r a[r] * sum(x_run_r * u[r]) + b[r] * sum(x_run_r).
+// Signed codes are biased to unsigned bytes (converted by v_cvt_f32_ubyteN in
+// one instruction); b[r] removes the bias (and carries the K-quant mins).
 struct PieceCodes {
-    uint4 u0, u1;        // unsigned byte codes of run 0 / run 1
-    float a0, b0, a1, b1;
+    uint4 u[2];
+    float a[2], b[2];
 };
 
 template <int NW> struct RawW { uint32_t w[NW]; };
@@ -260,15 +265,23 @@ __device__ __forceinline__ uint32_t align2(uint32_t hi, uint32_t lo, uint32_t s)
     return __builtin_amdgcn_alignbyte(hi, lo, s);
 }
 
+__device__ __forceinline__ uint4 uint4_at(const uint32_t* w) { return make_uint4(w[0], w[1], w[2], w[3]); }
+
+// Dwords i..i+3 of a byte stream held as a window shifted by `s` bytes.
+__device__ __forceinline__ uint4 realign4(const uint32_t* w, uint32_t s) {
+    return make_uint4(align2(w[1], w[0], s), align2(w[2], w[1], s), align2(w[3], w[2], s), align2(w[4], w[3], s));
+}
+
 template <int T> struct Piece;
 
-// Q4_K: piece j of block b covers qs bytes [32c+16h, +16) (c=j/2, h=j%2):
-// low nibbles are values 64c+16h+i (sub-block 2c), high nibbles values
-// 64c+32+16h+i (sub-block 2c+1).
+// Q4_K: piece j = p%8 of block b covers qs bytes [32c+16h, +16) (c = j/2,
+// h = j%2): low nibbles are values 64c+16h+i (sub-block 2c), high nibbles
+// values 64c+32+16h+i (sub-block 2c+1).
 template <> struct Piece<T_Q4_K> {
     typedef RawW<8> Raw;
-    static __device__ __forceinline__ int run0(int p) { return (p >> 3) * 256 + ((p >> 1) & 3) * 64 + (p & 1) * 16; }
-    static constexpr int kRun1 = 32;
+    static __device__ __forceinline__ int run_k(int p, int r) {
+        return (p >> 3) * 256 + ((p >> 1) & 3) * 64 + (p & 1) * 16 + 32 * r;
+    }
     static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
         const uint8_t* b = row + (p >> 3) * 144;
         const int c = (p >> 1) & 3, h = p & 1;
@@ -284,12 +297,12 @@ template <> struct Piece<T_Q4_K> {
         kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c, sc0, m0);
         kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c + 1, sc1, m1);
         const float d = h2f(r.w[0] & 0xFFFFu), dm = h2f(r.w[0] >> 16);
-        const uint4 q = make_uint4(r.w[4], r.w[5], r.w[6], r.w[7]);
+        const uint4 q = uint4_at(r.w + 4);
         PieceCodes o;
-        o.u0 = and4(q, 0x0F0F0F0Fu);
-        o.u1 = and4(shr4(q, 4), 0x0F0F0F0Fu);
-        o.a0 = d * (float)sc0; o.b0 = -(dm * (float)m0);
-        o.a1 = d * (float)sc1; o.b1 = -(dm * (float)m1);
+        o.u[0] = and4(q, 0x0F0F0F0Fu);
+        o.u[1] = and4(shr4(q, 4), 0x0F0F0F0Fu);
+        o.a[0] = d * (float)sc0; o.b[0] = -(dm * (float)m0);
+        o.a[1] = d * (float)sc1; o.b[1] = -(dm * (float)m1);
         return o;
     }
 };
@@ -297,8 +310,7 @@ template <> struct Piece<T_Q4_K> {
 // Q5_K: as Q4_K, plus bits 2c (run 0) and 2c+1 (run 1) of qh[16h+i].
 template <> struct Piece<T_Q5_K> {
     typedef RawW<12> Raw;
-    static __device__ __forceinline__ int run0(int p) { return Piece<T_Q4_K>::run0(p); }
-    static constexpr int kRun1 = 32;
+    static __device__ __forceinline__ int run_k(int p, int r) { return Piece<T_Q4_K>::run_k(p, r); }
     static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
         const uint8_t* b = row + (p >> 3) * 176;
         const int c = (p >> 1) & 3, h = p & 1;
@@ -315,29 +327,27 @@ template <> struct Piece<T_Q5_K> {
         kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c, sc0, m0);
         kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c + 1, sc1, m1);
         const float d = h2f(r.w[0] & 0xFFFFu), dm = h2f(r.w[0] >> 16);
-        const uint4 qh = make_uint4(r.w[4], r.w[5], r.w[6], r.w[7]);
-        const uint4 q = make_uint4(r.w[8], r.w[9], r.w[10], r.w[11]);
+        const uint4 qh = uint4_at(r.w + 4), q = uint4_at(r.w + 8);
         PieceCodes o;
-        o.u0 = or4(and4(q, 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * c), 0x01010101u), 4));
-        o.u1 = or4(and4(shr4(q, 4), 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * c + 1), 0x01010101u), 4));
-        o.a0 = d * (float)sc0; o.b0 = -(dm * (float)m0);
-        o.a1 = d * (float)sc1; o.b1 = -(dm * (float)m1);
+        o.u[0] = or4(and4(q, 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * c), 0x01010101u), 4));
+        o.u[1] = or4(and4(shr4(q, 4), 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * c + 1), 0x01010101u), 4));
+        o.a[0] = d * (float)sc0; o.b[0] = -(dm * (float)m0);
+        o.a[1] = d * (float)sc1; o.b[1] = -(dm * (float)m1);
         return o;
     }
 };
 
-// Q6_K: piece j of block b: half n=j/4, l0=16*((j/2)%2), s=j%2.  ql bytes
-// [64n+32s+l0, +16) low nibbles + qh[32n+l0+i] bits 2s..2s+1 -> values
-// 128n+32s+l0+i (scale sc[8n+l0/16+2s]); the high nibbles + qh bits 4+2s..
-// -> values 128n+64+32s+l0+i (scale index +4).  Codes are 6-bit offset 32.
-// Blocks are 210 bytes, so fields are only 2-byte aligned: each field is
-// fetched as the dword window covering it and realigned in decode.
+// Q6_K: piece j = p%8 of block b: half n = j/4, l0 = 16*((j/2)%2), s = j%2.
+// ql bytes [64n+32s+l0, +16) low nibbles + qh[32n+l0+i] bits 2s..2s+1 ->
+// values 128n+32s+l0+i (scale sc[8n+l0/16+2s]); the high nibbles + qh bits
+// 4+2s.. -> values 128n+64+32s+l0+i (scale index +4).  Codes are 6-bit,
+// offset 32.  Blocks are 210 bytes, so the fields are only 2-byte aligned:
+// each is fetched as the dword window covering it and realigned in decode.
 template <> struct Piece<T_Q6_K> {
     typedef RawW<14> Raw;
-    static __device__ __forceinline__ int run0(int p) {
-        return (p >> 3) * 256 + ((p >> 2) & 1) * 128 + (p & 1) * 32 + ((p >> 1) & 1) * 16;
+    static __device__ __forceinline__ int run_k(int p, int r) {
+        return (p >> 3) * 256 + ((p >> 2) & 1) * 128 + (p & 1) * 32 + ((p >> 1) & 1) * 16 + 64 * r;
     }
-    static constexpr int kRun1 = 64;
     static __device__ __forceinline__ int sc_index(int p) { return 8 * ((p >> 2) & 1) + ((p >> 1) & 1) + 2 * (p & 1); }
     static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
         const uint8_t* b = row + (p >> 3) * 210;
@@ -351,22 +361,19 @@ template <> struct Piece<T_Q6_K> {
     }
     static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
         const uint8_t* b = row + (p >> 3) * 210;
-        const uint32_t sh = (uint32_t)(uintptr_t)b & 3u;                 // ql / qh windows
+        const uint32_t sh = (uint32_t)(uintptr_t)b & 3u;  // ql / qh windows (offsets are multiples of 16)
         const uint32_t ss = (uint32_t)(uintptr_t)(b + 192 + sc_index(p)) & 3u;
         const int s = p & 1;
-        const uint4 ql = make_uint4(align2(r.w[1], r.w[0], sh), align2(r.w[2], r.w[1], sh),
-                                    align2(r.w[3], r.w[2], sh), align2(r.w[4], r.w[3], sh));
-        const uint4 qh = make_uint4(align2(r.w[6], r.w[5], sh), align2(r.w[7], r.w[6], sh),
-                                    align2(r.w[8], r.w[7], sh), align2(r.w[9], r.w[8], sh));
+        const uint4 ql = realign4(r.w, sh), qh = realign4(r.w + 5, sh);
         const uint32_t sc0 = align2(r.w[11], r.w[10], ss), sc1 = align2(r.w[12], r.w[11], ss);
         const float d = h2f(r.w[13]);
         PieceCodes o;
-        o.u0 = or4(and4(ql, 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * s), 0x03030303u), 4));
-        o.u1 = or4(and4(shr4(ql, 4), 0x0F0F0F0Fu), shl4(and4(shr4(qh, 4 + 2 * s), 0x03030303u), 4));
-        o.a0 = d * (float)(int8_t)(sc0 & 0xFFu);
-        o.a1 = d * (float)(int8_t)(sc1 & 0xFFu);
-        o.b0 = -32.0f * o.a0;
-        o.b1 = -32.0f * o.a1;
+        o.u[0] = or4(and4(ql, 0x0F0F0F0Fu), shl4(and4(shr4(qh, 2 * s), 0x03030303u), 4));
+        o.u[1] = or4(and4(shr4(ql, 4), 0x0F0F0F0Fu), shl4(and4(shr4(qh, 4 + 2 * s), 0x03030303u), 4));
+        o.a[0] = d * (float)(int8_t)(sc0 & 0xFFu);
+        o.a[1] = d * (float)(int8_t)(sc1 & 0xFFu);
+        o.b[0] = -32.0f * o.a[0];
+        o.b[1] = -32.0f * o.a[1];
         return o;
     }
 };
@@ -376,8 +383,7 @@ template <> struct Piece<T_Q6_K> {
 // 9-dword window from the aligned-down base covers d and qs.
 template <> struct Piece<T_Q8_0> {
     typedef RawW<9> Raw;
-    static __device__ __forceinline__ int run0(int p) { return p * 32; }
-    static constexpr int kRun1 = 16;
+    static __device__ __forceinline__ int run_k(int p, int r) { return p * 32 + 16 * r; }
     static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
         Raw r;
         ld_dw<9>(align_down4(row + p * 34), r.w);
@@ -390,10 +396,10 @@ template <> struct Piece<T_Q8_0> {
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = (odd ? r.w[i + 1] : align2(r.w[i + 1], r.w[i], 2)) ^ 0x80808080u;
         PieceCodes o;
-        o.u0 = make_uint4(q[0], q[1], q[2], q[3]);
-        o.u1 = make_uint4(q[4], q[5], q[6], q[7]);
-        o.a0 = o.a1 = d;
-        o.b0 = o.b1 = -128.0f * d;
+        o.u[0] = make_uint4(q[0], q[1], q[2], q[3]);
+        o.u[1] = make_uint4(q[4], q[5], q[6], q[7]);
+        o.a[0] = o.a[1] = d;
+        o.b[0] = o.b[1] = -128.0f * d;
         return o;
     }
 };
@@ -402,8 +408,7 @@ template <> struct Piece<T_Q8_0> {
 // 16..31.  5-dword window from the aligned-down (even) base.
 template <> struct Piece<T_IQ4_NL> {
     typedef RawW<5> Raw;
-    static __device__ __forceinline__ int run0(int p) { return p * 32; }
-    static constexpr int kRun1 = 16;
+    static __device__ __forceinline__ int run_k(int p, int r) { return p * 32 + 16 * r; }
     static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
         Raw r;
         ld_dw<5>(align_down4(row + p * 18), r.w);
@@ -417,19 +422,18 @@ template <> struct Piece<T_IQ4_NL> {
         for (int i = 0; i < 4; i++) q[i] = odd ? r.w[i + 1] : align2(r.w[i + 1], r.w[i], 2);
         const uint4 qq = make_uint4(q[0], q[1], q[2], q[3]);
         PieceCodes o;
-        o.u0 = lut16x4(and4(qq, 0x0F0F0F0Fu), true);
-        o.u1 = lut16x4(and4(shr4(qq, 4), 0x0F0F0F0Fu), true);
-        o.a0 = o.a1 = d;
-        o.b0 = o.b1 = -128.0f * d;
+        o.u[0] = lut16x4(and4(qq, 0x0F0F0F0Fu), true);
+        o.u[1] = lut16x4(and4(shr4(qq, 4), 0x0F0F0F0Fu), true);
+        o.a[0] = o.a[1] = d;
+        o.b[0] = o.b[1] = -128.0f * d;
         return o;
     }
 };
 
-// IQ4_XS: piece = sub-block ib of block b (32 values, scale d*(ls-32)).
+// IQ4_XS: piece = sub-block ib = p%8 of block b (32 values, scale d*(ls-32)).
 template <> struct Piece<T_IQ4_XS> {
     typedef RawW<6> Raw;
-    static __device__ __forceinline__ int run0(int p) { return p * 32; }
-    static constexpr int kRun1 = 16;
+    static __device__ __forceinline__ int run_k(int p, int r) { return p * 32 + 16 * r; }
     static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
         const uint8_t* b = row + (p >> 3) * 136;
         const int ib = p & 7;
@@ -444,19 +448,27 @@ template <> struct Piece<T_IQ4_XS> {
         const int ib = p & 7;
         const int ls = (int)(((r.w[1] >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15u) | (((r.w[0] >> (16 + 2 * ib)) & 3u) << 4));
         const float dl = h2f(r.w[0] & 0xFFFFu) * (float)(ls - 32);
-        const uint4 q = make_uint4(r.w[2], r.w[3], r.w[4], r.w[5]);
+        const uint4 q = uint4_at(r.w + 2);
         PieceCodes o;
-        o.u0 = lut16x4(and4(q, 0x0F0F0F0Fu), true);
-        o.u1 = lut16x4(and4(shr4(q, 4), 0x0F0F0F0Fu), true);
-        o.a0 = o.a1 = dl;
-        o.b0 = o.b1 = -128.0f * dl;
+        o.u[0] = lut16x4(and4(q, 0x0F0F0F0Fu), true);
+        o.u[1] = lut16x4(and4(shr4(q, 4), 0x0F0F0F0Fu), true);
+        o.a[0] = o.a[1] = dl;
+        o.b[0] = o.b[1] = -128.0f * dl;
         return o;
     }
 };
 
+// Hides the known-zero bits of a masked word from the optimizer, so byte
+// extraction stays v_cvt_f32_ubyteN (one instruction) instead of being
+// narrowed to v_bfe_u32 + v_cvt_f32_ubyte0.  Emits no instruction.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // Unsigned byte codes -> floats (v_cvt_f32_ubyte0..3).
 __device__ __forceinline__ void ubytes_to_f32(uint4 u, float* f) {
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    const uint32_t w[4] = {opaque(u.x), opaque(u.y), opaque(u.z), opaque(u.w)};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         f[4 * i + 0] = (float)(w[i] & 0xFFu);

@@ -181,14 +181,16 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
 //   * a row of K values is P = K/32 pieces; LPR = 2^lpr_log2 threads share a
 //     row (LPR = min(256, pow2ceil(P))), so one row-iteration covers 256/LPR
 //     rows; thread t owns pieces lp, lp+LPR, ... (PPT of them) of row t/LPR.
-//   * the thread's activation values for its pieces (32 fp32 per piece and
-//     batch row) stay in VGPRs for the whole row loop, so HBM carries only
-//     weight blocks; activations are read once per workgroup and M-chunk.
+//   * the thread's activations for its pieces (32 fp32 per piece and batch
+//     row) stay in VGPRs for the whole row loop, so HBM carries only weight
+//     blocks; activations are read once per wavefront and M-chunk.
 //   * weight dwords are fetched one row-iteration ahead (register double
-//     buffer), so each wavefront keeps two rows of loads in flight while it
-//     decodes, multiplies and reduces the current one.  The first fetch is
-//     issued before the activation loads.
-//   * partial sums are reduced with cross-lane shuffles inside a wavefront,
+//     buffer) when `prefetch` is set; the first fetch is issued before the
+//     activations are read.
+//   * the grid is sized to the resident capacity (occupancy x CUs) and each
+//     workgroup loops over its rows, so no launch runs a partial second
+//     round of workgroups.
+//   * partial sums are reduced with DPP / swizzle steps inside a wavefront
 //     and through LDS when a row spans several wavefronts (LPR >= 128).
 struct GemvArgs {
     const uint8_t* W;
@@ -203,169 +205,280 @@ struct GemvArgs {
     const int* grp_off;
     const int* x_idx;
     int lpr_log2;
-    int x_vec4;  // X rows are 16-byte aligned (float4 loads)
+    int x_vec4;    // X rows are 16-byte aligned (float4 loads)
+    int prefetch;  // fetch the next row-iteration while computing the current one
 };
 
-template <int T, int PPT>
-__device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[PPT], const uint8_t* W, int64_t row_bytes,
-                                           int row, bool rvalid, int lp, int lpr, int P) {
+// Sum over aligned groups of 2^lg lanes (lg = 0..6): afterwards every lane of
+// a group of <= 32 lanes holds the group sum; for lg = 6 lane 0 holds the
+// wavefront sum.
+template <int CTRL> __device__ __forceinline__ float dpp_addc(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float group_sum(float v, int lg) {
+    if (lg >= 1) v = dpp_addc<0xB1>(v);   // quad_perm [1,0,3,2]: xor 1
+    if (lg >= 2) v = dpp_addc<0x4E>(v);   // quad_perm [2,3,0,1]: xor 2
+    if (lg >= 3) v = dpp_addc<0x141>(v);  // row_half_mirror: the other quad of 8
+    if (lg >= 4) v = dpp_addc<0x140>(v);  // row_mirror: the other half of 16
+    if (lg >= 5) v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));  // xor 16
+    if (lg >= 6) v += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    return v;
+}
+
+// Fetches are unconditional: out-of-range rows / pieces read row 0 / piece 0
+// (always valid memory) and their contribution is discarded later.  Keeping
+// the loads unpredicated avoids per-lane branches and register copies.
+template <int T, int PPT, int U>
+__device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[U][PPT], const uint8_t* W, int64_t row_bytes,
+                                           int it, int stride, int n_iters, int rpi, int rsub, int N, int lp, int lpr,
+                                           int P) {
 #pragma unroll
-    for (int i = 0; i < PPT; i++) {
-        const int p = lp + i * lpr;
-        if (rvalid && p < P) raw[i] = Piece<T>::fetch(W + (int64_t)row * row_bytes, p);
+    for (int u = 0; u < U; u++) {
+        const int iu = it + u * stride, row = iu * rpi + rsub;
+        const bool rvalid = iu < n_iters && row < N;
+        const uint8_t* wrow = W + (int64_t)(rvalid ? row : 0) * row_bytes;
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int p = lp + i * lpr;
+            raw[u][i] = Piece<T>::fetch(wrow, p < P ? p : 0);
+        }
     }
 }
 
-template <int T, int MB, int PPT>
-__device__ __forceinline__ void gemv_row(const typename Piece<T>::Raw (&raw)[PPT], const GemvArgs& a, const uint8_t* W,
-                                         int row, bool rvalid, int lp, int lpr, int P, int wave, int lane, int rsub,
-                                         int m0, int mc, int mcount, float (&xr)[PPT][MB][32],
-                                         const float (&xs0)[PPT][MB], const float (&xs1)[PPT][MB],
-                                         float (&red)[2][4][MB], int& parity) {
-    float acc[MB];
+template <int T, int MB, int PPT, int U>
+__device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U][PPT], const GemvArgs& a,
+                                          const uint8_t* W, int it, int stride, int n_iters, int rpi, int lp, int lpr,
+                                          int P, int wave, int lane, int rsub, int m0, int mc, int mcount,
+                                          const float (&xr)[PPT][MB][32], const float (&xs)[PPT][MB][2],
+                                          float (&red)[2][4][U * MB], int& parity) {
+    float acc[U][MB];
 #pragma unroll
-    for (int m = 0; m < MB; m++) acc[m] = 0.0f;
-    const uint8_t* wrow = W + (int64_t)row * a.row_bytes;
+    for (int u = 0; u < U; u++) {
 #pragma unroll
-    for (int i = 0; i < PPT; i++) {
-        const int p = lp + i * lpr;
-        if (rvalid && p < P) {
-            const PieceCodes pc = Piece<T>::decode(raw[i], wrow, p);
-            float u0[16], u1[16];
-            ubytes_to_f32(pc.u0, u0);
-            ubytes_to_f32(pc.u1, u1);
+        for (int m = 0; m < MB; m++) acc[u][m] = 0.0f;
+        const int iu = it + u * stride, row = iu * rpi + rsub;
+        const bool rvalid = iu < n_iters && row < a.N;
+        const uint8_t* wrow = W + (int64_t)(rvalid ? row : 0) * a.row_bytes;
 #pragma unroll
-            for (int m = 0; m < MB; m++) {
-                float s0 = 0.0f, s1 = 0.0f;
+        for (int i = 0; i < PPT; i++) {
+            const int p = lp + i * lpr;
+            const bool ok = p < P;
+            const PieceCodes pc = Piece<T>::decode(raw[u][i], wrow, ok ? p : 0);
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    s0 = fmaf(xr[i][m][j], u0[j], s0);
-                    s1 = fmaf(xr[i][m][16 + j], u1[j], s1);
+            for (int r = 0; r < 2; r++) {
+                float f[16];
+                ubytes_to_f32(pc.u[r], f);
+#pragma unroll
+                for (int m = 0; m < MB; m++) {
+                    float s0 = 0.0f, s1 = 0.0f;  // two chains for ILP
+#pragma unroll
+                    for (int j = 0; j < 16; j += 2) {
+                        s0 = fmaf(xr[i][m][16 * r + j], f[j], s0);
+                        s1 = fmaf(xr[i][m][16 * r + j + 1], f[j + 1], s1);
+                    }
+                    const float t = fmaf(pc.a[r], s0 + s1, pc.b[r] * xs[i][m][r]);
+                    acc[u][m] += ok ? t : 0.0f;
                 }
-                float r = fmaf(pc.a0, s0, pc.b0 * xs0[i][m]);
-                r = fmaf(pc.a1, s1, fmaf(pc.b1, xs1[i][m], r));
-                acc[m] += r;
             }
         }
     }
-    if (a.lpr_log2 <= 6) {
-        for (int off = lpr >> 1; off > 0; off >>= 1) {
+    const int lg = a.lpr_log2 < 6 ? a.lpr_log2 : 6;
 #pragma unroll
-            for (int m = 0; m < MB; m++) acc[m] += __shfl_xor(acc[m], off, 64);
-        }
-    } else {
+    for (int u = 0; u < U; u++)
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-            for (int m = 0; m < MB; m++) acc[m] += __shfl_xor(acc[m], off, 64);
-        }
+        for (int m = 0; m < MB; m++) acc[u][m] = group_sum(acc[u][m], lg);
+    if (a.lpr_log2 > 6) {
         if (lane == 0) {
 #pragma unroll
-            for (int m = 0; m < MB; m++) red[parity][wave][m] = acc[m];
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int m = 0; m < MB; m++) red[parity][wave][u * MB + m] = acc[u][m];
         }
         __syncthreads();
         if (lp == 0) {
             const int wpr = lpr >> 6, w0 = rsub * wpr;
 #pragma unroll
-            for (int m = 0; m < MB; m++) {
-                float sum = 0.0f;
-                for (int w = 0; w < wpr; w++) sum += red[parity][w0 + w][m];
-                acc[m] = sum;
-            }
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int m = 0; m < MB; m++) {
+                    float sum = 0.0f;
+                    for (int w = 0; w < wpr; w++) sum += red[parity][w0 + w][u * MB + m];
+                    acc[u][m] = sum;
+                }
         }
         parity ^= 1;
     }
-    if (lp == 0 && rvalid) {
+    if (lp == 0) {
 #pragma unroll
-        for (int m = 0; m < MB; m++)
-            if (mc + m < mcount) a.Y[(int64_t)(m0 + mc + m) * a.ldy + row] = acc[m];
+        for (int u = 0; u < U; u++) {
+            const int iu = it + u * stride, row = iu * rpi + rsub;
+            if (iu < n_iters && row < a.N) {
+#pragma unroll
+                for (int m = 0; m < MB; m++)
+                    if (mc + m < mcount) a.Y[(int64_t)(m0 + mc + m) * a.ldy + row] = acc[u][m];
+            }
+        }
     }
 }
 
-template <int T, int MB, int PPT>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+// One workgroup's share of a GEMV problem: workgroup bx of gx working on
+// group `by` (the expert in grouped mode).
+template <int T, int MB, int PPT, int U>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, float (&red)[2][4][U * MB]) {
     typedef typename Piece<T>::Raw Raw;
-    __shared__ float red[2][4][MB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lpr_log2 = a.lpr_log2;
     const int lpr = 1 << lpr_log2, lp = tid & (lpr - 1), rsub = tid >> lpr_log2;
     const int rpi = 256 >> lpr_log2;
     const int P = a.K >> 5;
-    const uint8_t* W = a.W + (int64_t)blockIdx.y * a.w_group_stride;
+    const uint8_t* W = a.W + (int64_t)by * a.w_group_stride;
     int m0 = 0, mcount = a.M;
     if (a.grp_off) {
-        m0 = a.grp_off[blockIdx.y];
-        mcount = a.grp_off[blockIdx.y + 1] - m0;
+        m0 = a.grp_off[by];
+        mcount = a.grp_off[by + 1] - m0;
     }
     const int n_iters = (a.N + rpi - 1) / rpi;
-    const int stride = gridDim.x;
+    const int stride = gx;
+    const int step = U * stride;
     int parity = 0;
 
     for (int mc = 0; mc < mcount; mc += MB) {
-        Raw ra[PPT], rb[PPT];
-        int it = blockIdx.x;
-        {
-            const int row = it * rpi + rsub;
-            gemv_fetch<T, PPT>(ra, W, a.row_bytes, row, it < n_iters && row < a.N, lp, lpr, P);
-        }
+        Raw ra[U][PPT], rb[U][PPT];
+        int it = bx;
+        // The first weight fetch is issued before the activations are read.
+        gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
         float xr[PPT][MB][32];
-        float xs0[PPT][MB], xs1[PPT][MB];
+        float xs[PPT][MB][2];
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = lp + i * lpr;
+            const int pc = p < P ? p : 0;
 #pragma unroll
             for (int m = 0; m < MB; m++) {
-                xs0[i][m] = 0.0f;
-                xs1[i][m] = 0.0f;
                 const bool ok = p < P && mc + m < mcount;
-                int xrow = m0 + mc + m;
-                if (ok && a.x_idx) xrow = a.x_idx[xrow];
+                int xrow = m0 + mc + (mc + m < mcount ? m : 0);
+                if (a.x_idx) xrow = a.x_idx[xrow];
                 const float* xp = a.X + (int64_t)xrow * a.ldx;
-                const int k0 = ok ? Piece<T>::run0(p) : 0;
-                if (ok && a.x_vec4) {
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const float4 v0 = *(const float4*)(xp + k0 + 4 * j);
-                        const float4 v1 = *(const float4*)(xp + k0 + Piece<T>::kRun1 + 4 * j);
-                        xr[i][m][4 * j + 0] = v0.x; xr[i][m][4 * j + 1] = v0.y;
-                        xr[i][m][4 * j + 2] = v0.z; xr[i][m][4 * j + 3] = v0.w;
-                        xr[i][m][16 + 4 * j + 0] = v1.x; xr[i][m][16 + 4 * j + 1] = v1.y;
-                        xr[i][m][16 + 4 * j + 2] = v1.z; xr[i][m][16 + 4 * j + 3] = v1.w;
+                for (int r = 0; r < 2; r++) {
+                    const int k0 = Piece<T>::run_k(pc, r);
+                    if (a.x_vec4) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const float4 v = *(const float4*)(xp + k0 + 4 * j);
+                            xr[i][m][16 * r + 4 * j + 0] = v.x; xr[i][m][16 * r + 4 * j + 1] = v.y;
+                            xr[i][m][16 * r + 4 * j + 2] = v.z; xr[i][m][16 * r + 4 * j + 3] = v.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 16; j++) xr[i][m][16 * r + j] = xp[k0 + j];
                     }
-                } else {
+                    float sum = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 16; j++) {
-                        xr[i][m][j] = ok ? xp[k0 + j] : 0.0f;
-                        xr[i][m][16 + j] = ok ? xp[k0 + Piece<T>::kRun1 + j] : 0.0f;
+                        xr[i][m][16 * r + j] = ok ? xr[i][m][16 * r + j] : 0.0f;
+                        sum += xr[i][m][16 * r + j];
                     }
-                }
-#pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    xs0[i][m] += xr[i][m][j];
-                    xs1[i][m] += xr[i][m][16 + j];
+                    xs[i][m][r] = sum;
                 }
             }
         }
 
-        // Ping-pong between ra and rb: fetch the next row-iteration, then
-        // decode/multiply/reduce the current one.
-        while (it < n_iters) {
-            {
-                const int nx = it + stride, row = it * rpi + rsub, nrow = nx * rpi + rsub;
-                gemv_fetch<T, PPT>(rb, W, a.row_bytes, nrow, nx < n_iters && nrow < a.N, lp, lpr, P);
-                gemv_row<T, MB, PPT>(ra, a, W, row, row < a.N, lp, lpr, P, wave, lane, rsub, m0, mc, mcount, xr,
-                                     xs0, xs1, red, parity);
-                it = nx;
+        if (!a.prefetch) {
+            // Fetch, then decode/multiply/reduce; latency is hidden by the
+            // other resident wavefronts.
+            while (true) {
+                gemv_rows<T, MB, PPT, U>(ra, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc,
+                                         mcount, xr, xs, red, parity);
+                it += step;
+                if (it >= n_iters) break;
+                gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
             }
-            if (it >= n_iters) break;
-            {
-                const int nx = it + stride, row = it * rpi + rsub, nrow = nx * rpi + rsub;
-                gemv_fetch<T, PPT>(ra, W, a.row_bytes, nrow, nx < n_iters && nrow < a.N, lp, lpr, P);
-                gemv_row<T, MB, PPT>(rb, a, W, row, row < a.N, lp, lpr, P, wave, lane, rsub, m0, mc, mcount, xr,
-                                     xs0, xs1, red, parity);
-                it = nx;
-            }
+            continue;
         }
+        // Ping-pong between ra and rb: fetch the next U row-iterations, then
+        // decode/multiply/reduce the current ones.
+        while (it < n_iters) {
+            gemv_fetch<T, PPT, U>(rb, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
+            gemv_rows<T, MB, PPT, U>(ra, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
+                                     xr, xs, red, parity);
+            it += step;
+            if (it >= n_iters) break;
+            gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
+            gemv_rows<T, MB, PPT, U>(rb, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
+                                     xr, xs, red, parity);
+            it += step;
+        }
+    }
+}
+
+template <int T, int MB, int PPT, int U>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    __shared__ float red[2][4][U * MB];
+    gemv_body<T, MB, PPT, U>(a, blockIdx.x, gridDim.x, blockIdx.y, red);
+}
+
+// Several independent GEMV problems (any mix of formats, same pieces-per-
+// thread) in one launch: workgroups [begin[q], begin[q+1]) serve problem q.
+// Used where matmuls share a dependency level, e.g. the q/k/v projections
+// (one input) or gate/up of a decode step.
+constexpr int kMaxMulti = 8;
+struct MultiArgs {
+    GemvArgs p[kMaxMulti];
+    uint32_t type[kMaxMulti];
+    int begin[kMaxMulti + 1];
+    int n;
+};
+
+template <int MB, int PPT, int U>
+__global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
+    __shared__ float red[2][4][U * MB];
+    int q = 0;
+    while (q + 1 < ma.n && (int)blockIdx.x >= ma.begin[q + 1]) q++;
+    const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
+    switch (ma.type[q]) {
+    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
+    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
+    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
+    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
+    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
+    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
+    default: break;
+    }
+}
+
+// Straightforward GEMV for shapes the piece kernel does not take (K not a
+// multiple of 64, i.e. an odd number of 32-value blocks): one thread per
+// (row, batch row), codes16 + group scales.
+template <int T>
+__global__ __launch_bounds__(256) void gemv_simple_kernel(GemvArgs a) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int g = blockIdx.y;
+    if (n >= a.N) return;
+    int m0 = 0, mcount = a.M;
+    if (a.grp_off) {
+        m0 = a.grp_off[g];
+        mcount = a.grp_off[g + 1] - m0;
+    }
+    const uint8_t* row = a.W + (int64_t)g * a.w_group_stride + (int64_t)n * a.row_bytes;
+    for (int mi = 0; mi < mcount; mi++) {
+        int xrow = m0 + mi;
+        if (a.x_idx) xrow = a.x_idx[xrow];
+        const float* x = a.X + (int64_t)xrow * a.ldx;
+        float acc = 0.0f;
+        for (int k = 0; k < a.K; k += 16) {
+            const uint4 c = codes16<T>(row, k);
+            const GroupScale gs = group_scale<T>(row, k);
+            const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+            float s = 0.0f, sx = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                s = fmaf(x[k + j], (float)(int8_t)(w[j >> 2] >> (8 * (j & 3))), s);
+                sx += x[k + j];
+            }
+            acc += gs.dl * s - gs.ml * sx;
+        }
+        a.Y[(int64_t)(m0 + mi) * a.ldy + n] = acc;
     }
 }
 
@@ -375,26 +488,80 @@ static int ilog2_ceil(int v) {
     return l;
 }
 
-static int gemv_target_blocks() {
+// Workgroups of a non-grouped launch: by default exactly as many as can be
+// resident at once (occupancy x CUs), each looping over its share of rows, so
+// no launch runs a partial second round.  GGQ_GEMV_BLOCKS overrides.
+static int gemv_blocks_override() {
     static int v = [] {
         const char* e = getenv("GGQ_GEMV_BLOCKS");
-        return e && *e ? atoi(e) : 512;
+        return e && *e ? atoi(e) : 0;
     }();
     return v;
 }
 
-template <int T>
-static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
-    const int P = p.K / 32;
-    const int lpr_log2 = ilog2_ceil(P < 256 ? P : 256);
-    const int lpr = 1 << lpr_log2;
-    const int ppt = (P + lpr - 1) / lpr;
-    const int rpi = 256 / lpr;
-    const int mrows = p.grp_off ? p.max_group_rows : p.M;
+static int device_cus() {
+    static int v = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    return v;
+}
+
+template <typename K>
+static int resident_blocks(K kernel, size_t lds) {
+    if (gemv_blocks_override() > 0) return gemv_blocks_override();
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) != hipSuccess || per_cu <= 0) per_cu = 1;
+    return per_cu * device_cus();
+}
+
+// Row-iterations processed together per wavefront (their loads are issued
+// together and their reductions interleave).
+static int gemv_rows_per_iter() {
+    static int v = [] {
+        const char* e = getenv("GGQ_GEMV_U");
+        return e && *e ? atoi(e) : 1;
+    }();
+    return v;
+}
+
+
+static int gemv_prefetch() {
+    static int v = [] {
+        const char* e = getenv("GGQ_GEMV_PREFETCH");
+        return e && *e ? atoi(e) : 1;
+    }();
+    return v;
+}
+
+static int gemv_max_lpr() {
+    static int v = [] {
+        const char* e = getenv("GGQ_GEMV_MAXLPR");
+        const int x = e && *e ? atoi(e) : 256;
+        return x == 64 || x == 128 ? x : 256;
+    }();
+    return v;
+}
+
+struct GemvPlan {
     GemvArgs a;
+    int ppt, n_iters, mrows;
+    bool simple;
+};
+
+static GemvPlan plan_gemv(const GemvProblem& p) {
+    GemvPlan g;
+    GemvArgs& a = g.a;
+    g.simple = (p.K % 32) != 0;
+    const int P = p.K / 32 > 0 ? p.K / 32 : 1;
+    const int lpr_log2 = ilog2_ceil(P < gemv_max_lpr() ? P : gemv_max_lpr());
+    const int lpr = 1 << lpr_log2;
+    const int rpi = 256 / lpr;
     a.W = (const uint8_t*)p.W;
     a.w_group_stride = p.w_group_stride;
-    a.row_bytes = row_bytes(T, p.K);
+    a.row_bytes = row_bytes(p.type, p.K);
     a.N = p.N; a.K = p.K;
     a.X = p.X; a.ldx = p.ldx;
     a.Y = p.Y; a.ldy = p.ldy;
@@ -403,28 +570,97 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     a.x_idx = p.x_idx;
     a.lpr_log2 = lpr_log2;
     a.x_vec4 = ((uintptr_t)p.X % 16 == 0) && (p.ldx % 4 == 0);
-    const int n_iters = (p.N + rpi - 1) / rpi;
-    // Grouped (MoE) launches spread ~16 workgroups over each expert's rows.
-    int gx = p.groups > 1 ? 16 : gemv_target_blocks();
-    if (gx < 1) gx = 1;
-    if (gx > n_iters) gx = n_iters;
-    const dim3 grid(gx, p.groups > 0 ? p.groups : 1);
-    // Batch-rows per pass (MB) and pieces per thread (PPT) keep the
-    // activation registers at <= 4*32*(MB*PPT) floats.
-#define GO(MB_, PPT_) gemv_kernel<T, MB_, PPT_><<<grid, 256, 0, s>>>(a)
+    a.prefetch = gemv_prefetch();
+    g.ppt = (P + lpr - 1) / lpr;
+    g.n_iters = (p.N + rpi - 1) / rpi;
+    g.mrows = p.grp_off ? p.max_group_rows : p.M;
+    return g;
+}
+
+template <int T>
+static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
+    const GemvPlan g = plan_gemv(p);
+    GemvArgs a = g.a;
+    const int groups = p.groups > 0 ? p.groups : 1;
+    if (g.simple) {
+        gemv_simple_kernel<T><<<dim3((p.N + 255) / 256, groups), 256, 0, s>>>(a);
+        return hipGetLastError();
+    }
+    const int ppt = g.ppt, mrows = g.mrows;
+    // Batch rows per pass (MB) and pieces per thread (PPT) keep the
+    // activation registers at 64*MB*PPT <= 128 floats.  Grouped (MoE)
+    // launches spread 16 workgroups over each expert's rows.
+#define GO(MB_, PPT_, U_)                                                                  \
+    do {                                                                                   \
+        int gx = groups > 1 ? 16 : resident_blocks(gemv_kernel<T, MB_, PPT_, U_>, 0);     \
+        gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                               \
+        gemv_kernel<T, MB_, PPT_, U_><<<dim3(gx, groups), 256, 0, s>>>(a);                 \
+    } while (0)
+    const int u = gemv_rows_per_iter();
     if (ppt == 1) {
-        if (mrows <= 1) GO(1, 1);
-        else if (mrows == 2) GO(2, 1);
-        else GO(4, 1);
+        if (mrows <= 1) { if (u >= 2) GO(1, 1, 2); else GO(1, 1, 1); }
+        else if (mrows == 2) GO(2, 1, 1);
+        else GO(4, 1, 1);
     } else if (ppt == 2) {
-        if (mrows <= 1) GO(1, 2);
-        else GO(2, 2);
+        if (mrows <= 1) GO(1, 2, 1);
+        else GO(2, 2, 1);
     } else if (ppt <= 4) {
-        GO(1, 4);
+        GO(1, 4, 1);
     } else {
         return hipErrorInvalidValue;
     }
 #undef GO
+    return hipGetLastError();
+}
+
+// Independent single-row (M = 1) problems in one launch when they share the
+// pieces-per-thread count; otherwise one launch per problem.
+hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    MultiArgs ma;
+    int ppt = -1, total_iters = 0;
+    bool fuse = n <= kMaxMulti;
+    GemvPlan plans[kMaxMulti];
+    for (int i = 0; fuse && i < n; i++) {
+        if (ps[i].M != 1 || ps[i].grp_off || !supported(ps[i].type)) {
+            fuse = false;
+        } else {
+            plans[i] = plan_gemv(ps[i]);
+            if (ppt < 0) ppt = plans[i].ppt;
+            if (plans[i].simple || plans[i].ppt != ppt || ppt > 2) fuse = false;
+            total_iters += plans[i].n_iters;
+        }
+    }
+    const size_t shmem = 0;
+    if (!fuse) {
+        for (int i = 0; i < n; i++) {
+            const hipError_t e = launch_gemv(ps[i], s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const int u = gemv_rows_per_iter();
+    const int target = ppt == 1 ? (u >= 2 ? resident_blocks(gemv_multi_kernel<1, 1, 2>, shmem)
+                                          : resident_blocks(gemv_multi_kernel<1, 1, 1>, shmem))
+                                : resident_blocks(gemv_multi_kernel<1, 2, 1>, shmem);
+    int b = 0;
+    for (int i = 0; i < n; i++) {
+        ma.p[i] = plans[i].a;
+        ma.type[i] = ps[i].type;
+        ma.begin[i] = b;
+        int nb = (int)((int64_t)target * plans[i].n_iters / (total_iters > 0 ? total_iters : 1));
+        if (nb < 1) nb = 1;
+        if (nb > plans[i].n_iters) nb = plans[i].n_iters;
+        b += nb;
+    }
+    ma.begin[n] = b;
+    ma.n = n;
+    if (ppt == 1) {
+        if (u >= 2) gemv_multi_kernel<1, 1, 2><<<b, 256, shmem, s>>>(ma);
+        else gemv_multi_kernel<1, 1, 1><<<b, 256, shmem, s>>>(ma);
+    } else {
+        gemv_multi_kernel<1, 2, 1><<<b, 256, shmem, s>>>(ma);
+    }
     return hipGetLastError();
 }
 

@@ -39,6 +39,8 @@ struct GemvProblem {
     int max_group_rows;  // upper bound of rows per group (grouped mode)
 };
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t s);
+// Several independent M = 1 problems in as few launches as possible.
+hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s);
 // Largest K the register-resident GEMV supports.
 constexpr int kGemvMaxK = 32768;
 

@@ -73,6 +73,11 @@ class MoeParams(ctypes.Structure):
     ]
 
 
+class GemvDesc(ctypes.Structure):
+    _fields_ = [("W", ctypes.c_void_p), ("type", ctypes.c_uint32), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
+                ("A", ctypes.c_void_p), ("C", ctypes.c_void_p)]
+
+
 class MulMatParams(ctypes.Structure):
     """MulMatParams (include/ggnpu/backend.h:21-35)."""
     _fields_ = [
@@ -101,6 +106,7 @@ SIGNATURES = {
     "ggq_weight_device_ptr": (_P, [_P]),
     "ggq_mul_mat": (_I, [_P, _P, _P, _I, _P, _I, _I, _I]),
     "ggq_mul_mat_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _I, _I, _I, _P]),
+    "ggq_mul_mat_batch_dev": (_I, [_P, _P, _I, _P]),
     "ggq_dequant_dev": (_I, [_P, _P, _U32, _I64, _P, _P]),
     "ggq_quantize_act_dev": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P]),
     "ggq_block_dot_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _P]),

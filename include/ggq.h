@@ -128,6 +128,22 @@ int ggq_mul_mat(ggq_ctx* ctx, const ggq_weight* w, const float* A, int lda, floa
 int ggq_mul_mat_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
                     const float* A, int lda, float* C, int ldc, int M, int act_mode, void* stream);
 
+/* Several independent single-row (decode) matmuls with fp32 activations,
+ * queued as one launch where their shapes allow (a mix of weight types is
+ * fine), e.g. the q/k/v projections of one token, which share an input.  No
+ * reference counterpart: the reference issues one mul_mat_q per weight
+ * (src/cli/main.cpp:3256-3267).  Same result as one ggq_mul_mat_dev call per
+ * entry with M = 1 and GGQ_ACT_F32.  At most GGQ_MAX_BATCH entries. */
+#define GGQ_MAX_BATCH 8
+typedef struct {
+    const void* W;
+    uint32_t type;
+    int64_t N, K;
+    const float* A; /* [K] */
+    float* C;       /* [N] */
+} ggq_gemv_desc;
+int ggq_mul_mat_batch_dev(ggq_ctx* ctx, const ggq_gemv_desc* descs, int n, void* stream);
+
 /* Bit-exact fp32 dequant of n_blocks consecutive blocks, equal to the
  * reference's dequant_*_block functions (kquant.h:133-202, q8_0.cpp:19-25,
  * iq4_nl.cpp:24-31, iq4_xs.cpp:21-38). */

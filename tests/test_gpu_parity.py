@@ -304,3 +304,28 @@ def test_weight_upload_roundtrip(ctx, orc):
     assert orc.rel_l2(C, orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL
     ctx.check(ctx.lib.ggq_weight_free(ctx.h, w), "free")
     assert ctx.lib.ggq_weight_free(ctx.h, w) == gl.Status.INVALID_PARAM
+
+
+def test_batched_decode_gemv_mixed_types(ctx, orc):
+    """ggq_mul_mat_batch_dev: q/k (Q4_K) + v (Q6_K) with one shared input,
+    plus shapes whose pieces-per-thread differ (falls back to per-problem
+    launches)."""
+    import torch
+    rng = np.random.default_rng(21)
+    for shapes in ([(12, 2048, 2048), (12, 512, 2048), (14, 512, 2048)],
+                   [(12, 300, 2048), (14, 70, 8192), (8, 64, 1536), (20, 33, 1024), (23, 129, 1024), (13, 5, 512)]):
+        descs = (gl.GemvDesc * len(shapes))()
+        keep, refs = [], []
+        for i, (t, N, K) in enumerate(shapes):
+            raw = weights(t, N, K, seed=i + N)
+            A = rng.standard_normal((1, K)).astype(np.float32)
+            dW, dA = dev(raw), dev(A)
+            dC = torch.full((N,), float("nan"), device="cuda")
+            keep += [dW, dA, dC]
+            descs[i].W, descs[i].type, descs[i].N, descs[i].K = dW.data_ptr(), t, N, K
+            descs[i].A, descs[i].C = dA.data_ptr(), dC.data_ptr()
+            refs.append((dC, orc.mul_mat_f64(t, raw, N, K, A, 0)))
+        ctx.check(ctx.lib.ggq_mul_mat_batch_dev(ctx.h, descs, len(shapes), stream_handle()), "batch")
+        for dC, ref in refs:
+            assert orc.rel_l2(host(dC)[None, :], ref) < TOL
+    assert ctx.lib.ggq_mul_mat_batch_dev(ctx.h, descs, 9, stream_handle()) == gl.Status.INVALID_PARAM
