@@ -209,27 +209,60 @@ def bench_config1(torch, ctx, stream, reps=200):
 
 def bench_prefill(torch, ctx, stream, steps=3):
     """28 layers of Q8_0 matmuls on 512 tokens, per-row int8
-    activations (reference XDNA semantics) -> int8 MFMA GEMM."""
+    activations (reference XDNA semantics) on the int8-MFMA GEMM.  Each
+    layer quantizes its four distinct inputs once (q/k/v share one, gate/up
+    share one; o and down have their own), as a forward pass would, and the
+    quantization kernels are inside the timed region."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2)
     layer = []
     for name, t, N, K in QWEN_LAYER:
         dev, _ = make_weight(torch, gen, t, N, K)
         layer.append((name, t, N, K, dev))
-    xs = {K: torch.randn((PREFILL_TOKENS, K), device="cuda") for K in (1536, 8960)}
+    T = PREFILL_TOKENS
+    # four distinct fp32 inputs per layer and their int8 buffers
+    xin = {lv: torch.randn((T, K), device="cuda") for lv, K in (("qkv", 1536), ("o", 1536), ("gu", 1536), ("down", 8960))}
+    qin = {lv: (torch.empty((T, x.shape[1]), dtype=torch.int8, device="cuda"), torch.empty((T,), device="cuda"))
+           for lv, x in xin.items()}
+    level_of = {"q": "qkv", "k": "qkv", "v": "qkv", "o": "o", "gate": "gu", "up": "gu", "down": "down"}
     mats = []
     for li in range(QWEN_LAYERS):
         for name, t, N, K, dev in layer:
             w = dev if li == 0 else dev.clone()
-            mats.append(Mat(torch, f"blk{li}.{name}", t, N, K, w, M=PREFILL_TOKENS, x=xs[K]))
+            mats.append(Mat(torch, f"blk{li}.{name}", t, N, K, w, M=T, x=xin[level_of[name]]))
+
+    def quant(lv):
+        x = xin[lv]
+        q, sc = qin[lv]
+        st = ctx.lib.ggq_quantize_act_dev(ctx.h, ctypes.c_void_p(x.data_ptr()), x.shape[1], T, x.shape[1], 1,
+                                          ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), stream)
+        ctx.check(st, "quantize_act")
+
+    def mm(m):
+        q, sc = qin[level_of[m.name.split(".")[1]]]
+        st = ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ctypes.c_void_p(m.w.data_ptr()), m.t, m.N, m.K,
+                                        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), T,
+                                        ctypes.c_void_p(m.y.data_ptr()), m.N, stream)
+        ctx.check(st, "mul_mat_q8_dev")
 
     def run():
-        for m in mats:
-            launch(ctx, m, 1, stream)
+        for li in range(QWEN_LAYERS):
+            lm = mats[7 * li: 7 * li + 7]
+            quant("qkv")
+            for m in lm[:3]:
+                mm(m)
+            quant("o")
+            mm(lm[3])
+            quant("gu")
+            mm(lm[4])
+            mm(lm[5])
+            quant("down")
+            mm(lm[6])
 
     sec = time_steps(torch, run, steps, 1)
     ops = sum(2 * m.M * m.N * m.K for m in mats)
-    return {"workload": "Qwen2.5-1.5B Q8_0 prefill, 512 tokens x 28 layers, per-row int8 activations",
+    return {"workload": "Qwen2.5-1.5B Q8_0 prefill, 512 tokens x 28 layers, per-row int8 activations "
+                        "(4 activation quantizations per layer included)",
             "int8_ops": ops, "ms_per_step": sec * 1e3, "TOPS": ops / sec / 1e12,
             "frac_int8_peak": ops / sec / 1e12 / INT8_PEAK_TOPS}
 
@@ -261,6 +294,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
+    ap.add_argument("--only", choices=["decode", "config1", "prefill", "copy"], default=None,
+                    help="run one workload only and print its result (profiling aid)")
     ap.add_argument("--per-matmul", action="store_true",
                     help="one launch per matmul instead of one per dependency level")
     args = ap.parse_args()
@@ -280,6 +315,21 @@ def main():
     stream = ctypes.c_void_p(side.cuda_stream)
     assert stream.value, "expected a non-null stream handle"
 
+    if args.only == "copy":
+        # Known-size device copy: the calibration kernel for the HBM byte
+        # counters (FETCH_SIZE / WRITE_SIZE) of the profiles.
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "copy", "bytes_per_copy": src.numel(), "copies": 4}), flush=True)
+        return
+    if args.only in ("config1", "prefill"):
+        res = bench_config1(torch, ctx, stream) if args.only == "config1" else bench_prefill(torch, ctx, stream)
+        print(json.dumps({"only": args.only, **res}), flush=True)
+        ctx.close()
+        return
     levels, host_layer0, sec, step_bytes, kt = bench_decode_step(torch, ctx, args.steps, args.warmup,
                                                                args.graph, stream, not args.per_matmul)
     value = step_bytes / sec / 1e9
@@ -310,6 +360,15 @@ def main():
                      "kernel": "decode GEMV kernels (sum of per-launch HIP-event durations over one step)",
                      "kernel_us_per_step": round(ktot * 1e6, 1)},
     }
+    # HBM bytes per step from the FETCH_SIZE / WRITE_SIZE profiles (scaled by
+    # the copy-kernel calibration recorded with them).
+    tpath = os.path.join(ROOT, "profiles", "decode_step_traffic.json")
+    if os.path.exists(tpath) and not args.per_matmul:
+        with open(tpath) as f:
+            t = json.load(f)
+        out["roofline"]["traffic"] = round(1024 * (t["fetch_kib_per_step_raw"] * t["fetch_scale"]
+                                                   + t["write_kib_per_step_raw"] * t["write_scale"]))
+        out["roofline"]["traffic_unit"] = "HBM bytes per step (rocprofv3 FETCH_SIZE + WRITE_SIZE, " + t["source"] + ")"
     if not args.no_extra:
         out["extra"] = {"config1": bench_config1(torch, ctx, stream)}
         try:

@@ -27,6 +27,9 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
+    # MFMA results in VGPRs rather than AGPRs: the GEMM epilogue reads every
+    # int32 product once, and the AGPR form costs a v_accvgpr_read for each.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

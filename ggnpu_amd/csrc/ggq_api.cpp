@@ -129,7 +129,8 @@ int mul_mat_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K
     const size_t s_off = align256(q_off + (size_t)M * K);
     const size_t x_off = align256(s_off + sizeof(float) * (size_t)M * (K / 32));
     const bool use_gemm = act_mode == GGQ_ACT_Q8_ROW && M > 8;
-    const size_t need = use_gemm ? x_off : align256(x_off + sizeof(float) * (size_t)M * K);
+    const size_t need = use_gemm ? x_off + align256(sizeof(float) * (size_t)ggq::gemm_splits(type, (int)N, (int)K, M) * M * N)
+                                 : align256(x_off + sizeof(float) * (size_t)M * K);
     if ((e = ensure(c->ws, need)) != hipSuccess) return hip_status(c, e, "workspace");
     int8_t* q = (int8_t*)c->ws.ptr + q_off;
     float* sc = (float*)((char*)c->ws.ptr + s_off);
@@ -137,12 +138,40 @@ int mul_mat_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K
     if (use_gemm) {
         if ((e = ggq::launch_quant_act(A, lda, M, (int)K, act_mode, q, sc, nullptr, s)) != hipSuccess)
             return hip_status(c, e, "quant_act");
-        return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, q, sc, M, C, ldc, s), "gemm_i8");
+        return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, q, sc, M, C, ldc, xe, s), "gemm_i8");
     }
     if ((e = ggq::launch_quant_act(A, lda, M, (int)K, act_mode, nullptr, nullptr, xe, s)) != hipSuccess)
         return hip_status(c, e, "quant_act");
     g.X = xe;
     g.ldx = (int)K;
+    return hip_status(c, ggq::launch_gemv(g, s), "gemv");
+}
+
+// C = sa * (qa . W^T) from activations already quantized per row.
+int mul_mat_q8_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const int8_t* qa,
+                     const float* sa, int M, float* C, int ldc, hipStream_t s) {
+    if (M == 0) return set_status(c, GGQ_OK);
+    hipError_t e;
+    if (M > 8) {
+        const size_t need = align256(sizeof(float) * (size_t)ggq::gemm_splits(type, (int)N, (int)K, M) * M * N);
+        if ((e = ensure(c->ws, need)) != hipSuccess) return hip_status(c, e, "workspace");
+        return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, qa, sa, M, C, ldc, (float*)c->ws.ptr, s),
+                          "gemm_i8");
+    }
+    if ((e = ensure(c->ws, sizeof(float) * (size_t)M * K)) != hipSuccess) return hip_status(c, e, "workspace");
+    float* xe = (float*)c->ws.ptr;
+    if ((e = ggq::launch_dequant_act(qa, sa, M, (int)K, xe, s)) != hipSuccess) return hip_status(c, e, "dequant_act");
+    ggq::GemvProblem g{};
+    g.type = type;
+    g.W = W;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.X = xe;
+    g.ldx = (int)K;
+    g.Y = C;
+    g.ldy = ldc;
+    g.M = M;
+    g.groups = 1;
     return hip_status(c, ggq::launch_gemv(g, s), "gemv");
 }
 
@@ -325,6 +354,17 @@ int ggq_mul_mat_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t
     int st = check_matmul_shape(c, type, N, K, M, lda, ldc, act_mode);
     if (st != GGQ_OK) return st;
     return mul_mat_queue(c, W, type, N, K, A, lda, C, ldc, M, act_mode, pick_stream(c, stream));
+    GGQ_END(c)
+}
+
+int ggq_mul_mat_q8_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const int8_t* qa,
+                       const float* sa, int M, float* C, int ldc, void* stream) {
+    GGQ_GUARD(c)
+    if (!W || !qa || !sa || !C) return set_status(c, GGQ_INVALID_PARAM, "null W/qa/sa/C");
+    if (!aligned16(W) || ((uintptr_t)qa & 15u)) return set_status(c, GGQ_INVALID_PARAM, "W and qa must be 16-byte aligned");
+    int st = check_matmul_shape(c, type, N, K, M, (int)K, ldc, GGQ_ACT_Q8_ROW);
+    if (st != GGQ_OK) return st;
+    return mul_mat_q8_queue(c, W, type, N, K, qa, sa, M, C, ldc, pick_stream(c, stream));
     GGQ_END(c)
 }
 

@@ -694,6 +694,8 @@ struct GemmArgs {
     float* C;
     int ldc;
     int M;
+    int steps_per_split;  // K-steps per blockIdx.z slice (split-K)
+    float* Cpart;         // [splits][M][N] partial sums when split, else null
 };
 
 template <int T>
@@ -797,8 +799,254 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
         }
 }
 
+// ------------------------------------------------------ LDS-tiled GEMM (i8)
+// Workgroup tile BM x BN x BK(=128, four 32-value scale groups), 4
+// wavefronts in a 2x2 layout, each computing (BM/2) x (BN/2) with
+// v_mfma_i32_32x32x32_i8.  Per K-step the workgroup stages
+//   As[m][k]   int8 activations (16-byte rows padded by 16 B: conflict-free)
+//   Bs[n][k]   int8 weight codes decoded once from the raw blocks
+//   Bd[n][g]   fp32 group scales dl (and Bm[n][g] mins ml for Q4_K/Q5_K)
+// in LDS, double-buffered: the global loads of step k+1 are issued before
+// the MFMAs of step k and written to the other buffer after them.  Each
+// MFMA covers one scale group; its int32 result is converted and scaled
+// into fp32 accumulators (acc += dl * P, and -= ml * S with S the
+// activation group sums from an MFMA against a ones operand).
+constexpr int kGemmBK = 128;
+constexpr int kGemmPad = 16;
+constexpr int kGemmLd = kGemmBK + kGemmPad;
+
+// Weight staging: fetch() issues the global loads of one (row, 32-group)
+// slot, store() decodes it into LDS codes + scales.  The generic version
+// loads at store time through codes16 / group_scale; Q8_0 prefetches the
+// raw block window.
+template <int T> struct BStage {
+    const uint8_t* row;
+    int k;
+    bool ok;
+    __device__ __forceinline__ void fetch(const uint8_t* r, int kk, bool v) { row = r; k = kk; ok = v; }
+    __device__ __forceinline__ void store(int8_t* codes, float* dl, float* ml) const {
+        uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
+        GroupScale gs{0.0f, 0.0f};
+        if (ok) {
+            c0 = codes16<T>(row, k);
+            c1 = codes16<T>(row, k + 16);
+            gs = group_scale<T>(row, k);
+        }
+        *(uint4*)codes = c0;
+        *(uint4*)(codes + 16) = c1;
+        *dl = gs.dl;
+        *ml = gs.ml;
+    }
+};
+
+template <> struct BStage<T_Q8_0> {
+    uint32_t w[9];
+    bool ok, odd;
+    __device__ __forceinline__ void fetch(const uint8_t* r, int kk, bool v) {
+        const uint8_t* b = r + (kk >> 5) * 34;
+        ok = v;
+        odd = ((uint32_t)(uintptr_t)b & 2u) != 0;
+        ld_dw<9>(align_down4(b), w);
+    }
+    __device__ __forceinline__ void store(int8_t* codes, float* dl, float* ml) const {
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = ok ? (odd ? w[i + 1] : align2(w[i + 1], w[i], 2)) : 0u;
+        *(uint4*)codes = make_uint4(q[0], q[1], q[2], q[3]);
+        *(uint4*)(codes + 16) = make_uint4(q[4], q[5], q[6], q[7]);
+        *dl = ok ? h2f(odd ? (w[0] >> 16) : (w[0] & 0xFFFFu)) : 0.0f;
+        *ml = 0.0f;
+    }
+};
+
+template <int T, int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmArgs a) {
+    constexpr bool kMin = T == T_Q4_K || T == T_Q5_K;
+    constexpr int WM = BM / 2, WN = BN / 2;       // wavefront tile
+    constexpr int TM = WM / 32, TN = WN / 32;     // MFMA tiles per wavefront
+    constexpr int G = kGemmBK / 32;               // scale groups per K-step
+    constexpr int A_CHUNKS = BM * kGemmBK / 16;   // 16-byte chunks of the A tile
+    constexpr int A_PER_T = A_CHUNKS / 256;
+    constexpr int B_SLOTS = BN * G;               // (row, group) slots of the B tile
+    constexpr int B_PER_T = (B_SLOTS + 255) / 256;
+    static_assert(A_CHUNKS % 256 == 0, "A tile must split evenly");
+
+    __shared__ __attribute__((aligned(16))) int8_t As[2][BM][kGemmLd];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN][kGemmLd];
+    __shared__ float Bd[2][BN][G];
+    __shared__ float Bm[2][BN][G];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lk = lane >> 5;
+    const int m_tile = blockIdx.y * BM, n_tile = blockIdx.x * BN;
+    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+    const int nsteps = (a.K + kGemmBK - 1) / kGemmBK;
+
+    uint4 areg[A_PER_T];
+    BStage<T> breg[B_PER_T];
+    // Per-thread source rows, computed once; each K-step advances k.
+    const int8_t* aptr[A_PER_T];
+    bool arow_ok[A_PER_T];
+    int akc[A_PER_T];
+#pragma unroll
+    for (int i = 0; i < A_PER_T; i++) {
+        const int c = tid + 256 * i, r = c / (kGemmBK / 16);
+        akc[i] = (c % (kGemmBK / 16)) * 16;
+        const int m = m_tile + r;
+        arow_ok[i] = m < a.M;
+        aptr[i] = a.QA + (int64_t)(arow_ok[i] ? m : 0) * a.K + akc[i];
+    }
+    const uint8_t* bptr[B_PER_T];
+    bool brow_ok[B_PER_T];
+    int bkg[B_PER_T];
+#pragma unroll
+    for (int i = 0; i < B_PER_T; i++) {
+        const int sl = tid + 256 * i;
+        const int r = sl / G, n = n_tile + r;
+        bkg[i] = 32 * (sl % G);
+        brow_ok[i] = sl < B_SLOTS && n < a.N;
+        bptr[i] = a.W + (int64_t)(brow_ok[i] ? n : 0) * a.row_bytes;
+    }
+
+    auto fetch = [&](int step) {
+        const int k0 = step * kGemmBK;
+#pragma unroll
+        for (int i = 0; i < A_PER_T; i++) {
+            const bool ok = arow_ok[i] && k0 + akc[i] < a.K;
+            areg[i] = ok ? *(const uint4*)(aptr[i] + k0) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < B_PER_T; i++) {
+            const int k = k0 + bkg[i];
+            const bool ok = brow_ok[i] && k < a.K;
+            breg[i].fetch(bptr[i], ok ? k : 0, ok);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_PER_T; i++) {
+            const int c = tid + 256 * i, r = c / (kGemmBK / 16), kc = (c % (kGemmBK / 16)) * 16;
+            *(uint4*)&As[buf][r][kc] = areg[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_PER_T; i++) {
+            const int sl = tid + 256 * i;
+            if (sl < B_SLOTS) {
+                const int r = sl / G, g = sl % G;
+                breg[i].store(&Bs[buf][r][32 * g], &Bd[buf][r][g], &Bm[buf][r][g]);
+            }
+        }
+    };
+
+    float acc[TM][TN][16];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    const v16i zero = {};
+    // Split-K: slice z covers K-steps [st0, st1).
+    const int st0 = blockIdx.z * a.steps_per_split;
+    const int st1 = st0 + a.steps_per_split < nsteps ? st0 + a.steps_per_split : nsteps;
+    fetch(st0);
+    store(0);
+    __syncthreads();
+    for (int st = st0; st < st1; st++) {
+        const int buf = (st - st0) & 1;
+        if (st + 1 < st1) fetch(st + 1);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            v4i A[TM], B[TN];
+            float dl[TN], ml[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const uint4 v = *(const uint4*)&As[buf][wm + 32 * i + li][32 * g + 16 * lk];
+                A[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint4 v = *(const uint4*)&Bs[buf][wn + 32 * j + li][32 * g + 16 * lk];
+                B[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                dl[j] = Bd[buf][wn + 32 * j + li][g];
+                ml[j] = Bm[buf][wn + 32 * j + li][g];
+            }
+            v16i S[TM];
+            if constexpr (kMin) {
+                const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+#pragma unroll
+                for (int i = 0; i < TM; i++) S[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], ones, zero, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const v16i Pm = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B[j], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        acc[i][j][r] = fmaf(dl[j], (float)Pm[r], acc[i][j][r]);
+                        if constexpr (kMin) acc[i][j][r] = fmaf(-ml[j], (float)S[i][r], acc[i][j][r]);
+                    }
+                }
+        }
+        if (st + 1 < st1) {
+            store(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    float* out = a.Cpart ? a.Cpart + (int64_t)blockIdx.z * a.M * a.N : a.C;
+    const int ldo = a.Cpart ? a.N : a.ldc;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m_tile + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
+            if (m >= a.M) continue;
+            const float s = a.sa[m];
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = n_tile + wn + 32 * j + li;
+                if (n < a.N) out[(int64_t)m * ldo + n] = acc[i][j][r] * s;
+            }
+        }
+}
+
+// Deterministic split-K reduction: C = sum over slices in slice order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
+                                                            float* __restrict__ C, int ldc) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)M * N) return;
+    const int m = (int)(i / N), n = (int)(i % N);
+    float acc = 0.0f;
+    for (int z = 0; z < splits; z++) acc += part[(int64_t)z * M * N + i];
+    C[(int64_t)m * ldc + n] = acc;
+}
+
+// Workgroup tile: 64x64 (32x32 per wavefront, + split-K where the tiles do
+// not fill the chip).  GGQ_GEMM_TILE=128 selects 128x64 tiles (64x32 per
+// wavefront) where they fill the chip; measured slower on gfx950 because the
+// larger accumulator set limits occupancy to two wavefronts per SIMD.
+static bool gemm_big_tile(int N, int M) {
+    static int force = [] {
+        const char* e = getenv("GGQ_GEMM_TILE");
+        return e && *e ? atoi(e) : 64;
+    }();
+    return force == 128 && (int64_t)((M + 127) / 128) * ((N + 63) / 64) >= device_cus();
+}
+
+int gemm_splits(uint32_t type, int N, int K, int M) {
+    if (type == T_Q6_K || gemm_big_tile(N, M)) return 1;
+    const int tiles = ((N + 63) / 64) * ((M + 63) / 64);
+    const int nsteps = (K + kGemmBK - 1) / kGemmBK;
+    int splits = 1;
+    while (splits < 8 && tiles * splits < 2 * device_cus() && nsteps / (splits * 2) >= 2) splits *= 2;
+    return splits;
+}
+
 hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa,
-                          const float* sa, int M, float* C, int ldc, hipStream_t s) {
+                          const float* sa, int M, float* C, int ldc, float* part, hipStream_t s) {
     if (M == 0 || N == 0) return hipSuccess;
     GemmArgs a;
     a.W = (const uint8_t*)W;
@@ -806,10 +1054,51 @@ hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8
     a.N = N; a.K = K;
     a.QA = qa; a.sa = sa;
     a.C = C; a.ldc = ldc; a.M = M;
-    const dim3 grid((N + 127) / 128, (M + 127) / 128);
-#define L(TT) gemm_i8_kernel<TT><<<grid, 256, 0, s>>>(a)
-    GGQ_DISPATCH_TYPE(type, L)
+    a.Cpart = nullptr;
+    if (type == T_Q6_K) {  // 16-value groups: direct-load kernel with 32x32x16 MFMAs
+        const dim3 grid((N + 127) / 128, (M + 127) / 128);
+        gemm_i8_kernel<T_Q6_K><<<grid, 256, 0, s>>>(a);
+        return hipGetLastError();
+    }
+    const int nsteps = (K + kGemmBK - 1) / kGemmBK;
+    const int splits = part ? gemm_splits(type, N, K, M) : 1;
+    a.steps_per_split = (nsteps + splits - 1) / splits;
+    const int zs = (nsteps + a.steps_per_split - 1) / a.steps_per_split;
+    if (zs > 1) a.Cpart = part;
+    // 128x128 tiles would need more VGPRs than the accumulators leave.
+    const bool big = gemm_big_tile(N, M);
+    const dim3 grid((N + 63) / 64, big ? (M + 127) / 128 : (M + 63) / 64, zs);
+#define L(TT)                                                                    \
+    if (big) gemm_i8_lds_kernel<TT, 128, 64><<<grid, 256, 0, s>>>(a);            \
+    else gemm_i8_lds_kernel<TT, 64, 64><<<grid, 256, 0, s>>>(a)
+    switch (type) {
+    case T_Q4_K: L(T_Q4_K); break;
+    case T_Q5_K: L(T_Q5_K); break;
+    case T_Q8_0: L(T_Q8_0); break;
+    case T_IQ4_NL: L(T_IQ4_NL); break;
+    case T_IQ4_XS: L(T_IQ4_XS); break;
+    default: return hipErrorInvalidValue;
+    }
 #undef L
+    if (zs > 1) {
+        const int64_t n = (int64_t)M * N;
+        splitk_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(part, zs, M, N, C, ldc);
+    }
+    return hipGetLastError();
+}
+
+// x_eff[m][k] = q[m][k] * scale[m] (fp32) from pre-quantized activations.
+__global__ __launch_bounds__(256) void dequant_act_kernel(const int8_t* __restrict__ q, const float* __restrict__ sa,
+                                                          int M, int K, float* __restrict__ x) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)M * K) return;
+    x[i] = __fmul_rn((float)q[i], sa[i / K]);
+}
+
+hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, float* x, hipStream_t s) {
+    const int64_t n = (int64_t)M * K;
+    if (n == 0) return hipSuccess;
+    dequant_act_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(q, sa, M, K, x);
     return hipGetLastError();
 }
 

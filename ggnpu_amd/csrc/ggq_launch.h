@@ -46,8 +46,13 @@ constexpr int kGemvMaxK = 32768;
 
 // int8-MFMA GEMM on per-row int8 activations:
 //   C[m][n] = sa[m] * sum_groups dl[n,g]*P[m,n,g] - ml[n,g]*S[m,g]
+// `part` is workspace for split-K partial sums (gemm_splits() * M * N
+// floats) or null to disable split-K.
 hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa,
-                          const float* sa, int M, float* C, int ldc, hipStream_t s);
+                          const float* sa, int M, float* C, int ldc, float* part, hipStream_t s);
+int gemm_splits(uint32_t type, int N, int K, int M);
+// x[m][k] = q[m][k] * sa[m] (dense fp32 [M][K]).
+hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, float* x, hipStream_t s);
 
 // MoE helpers.
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel,

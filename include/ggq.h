@@ -128,6 +128,15 @@ int ggq_mul_mat(ggq_ctx* ctx, const ggq_weight* w, const float* A, int lda, floa
 int ggq_mul_mat_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
                     const float* A, int lda, float* C, int ldc, int M, int act_mode, void* stream);
 
+/* C = sa[m] * sum_k qa[m][k] * w[n][k]: the GGQ_ACT_Q8_ROW matmul on
+ * activations already quantized by ggq_quantize_act_dev (row mode; qa dense
+ * [M][K], 16-byte aligned, sa [M]).  Lets callers quantize an input once
+ * when several weights consume it (q/k/v, gate/up).  The reference
+ * quantizes inside every mul_mat_q call (amd_xdna.cpp:633-639, 757-771);
+ * results are identical to ggq_mul_mat_dev with GGQ_ACT_Q8_ROW. */
+int ggq_mul_mat_q8_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K, const int8_t* qa,
+                       const float* sa, int M, float* C, int ldc, void* stream);
+
 /* Several independent single-row (decode) matmuls with fp32 activations,
  * queued as one launch where their shapes allow (a mix of weight types is
  * fine), e.g. the q/k/v projections of one token, which share an input.  No

@@ -329,3 +329,23 @@ def test_batched_decode_gemv_mixed_types(ctx, orc):
         for dC, ref in refs:
             assert orc.rel_l2(host(dC)[None, :], ref) < TOL
     assert ctx.lib.ggq_mul_mat_batch_dev(ctx.h, descs, 9, stream_handle()) == gl.Status.INVALID_PARAM
+
+
+@pytest.mark.parametrize("t", [8, 12, 20, 23])
+def test_prequantized_q8_entry(ctx, orc, t):
+    """ggq_mul_mat_q8_dev on activations from ggq_quantize_act_dev equals the
+    Q8_ROW oracle: split-K GEMM (small N, long K) and the M <= 8 route."""
+    import torch
+    be = gl.BLOCK[gl.GgmlType(t)][0]
+    for M, N, K in ((512, 96, 2048 if be == 256 else 1536), (64, 256, 4096), (3, 70, 1024)):
+        raw = weights(t, N, K, seed=M + N)
+        A = np.random.default_rng(M).standard_normal((M, K)).astype(np.float32)
+        dA, dW = dev(A), dev(raw)
+        dq = empty((M, K), torch.int8)
+        ds = empty((M,), torch.float32)
+        ctx.check(ctx.lib.ggq_quantize_act_dev(ctx.h, ptr(dA), K, M, K, 1, ptr(dq), ptr(ds), stream_handle()), "q")
+        dC = torch.full((M, N), float("nan"), device="cuda")
+        ctx.check(ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ptr(dW), t, N, K, ptr(dq), ptr(ds), M, ptr(dC), N,
+                                             stream_handle()), "q8 mm")
+        err = orc.rel_l2(host(dC), orc.mul_mat_f64(t, raw, N, K, A, 1))
+        assert err < TOL, (M, N, K, err)
