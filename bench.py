@@ -267,6 +267,80 @@ def bench_prefill(torch, ctx, stream, steps=3):
             "frac_int8_peak": ops / sec / 1e12 / INT8_PEAK_TOPS}
 
 
+# Qwen3-0.6B, hidden 1024, FFN 3072, 16 q / 8 kv heads of 128, 28 layers;
+# the type of tensor i (q, k, v, o, gate, up, down order) is [IQ4_NL, IQ4_XS, Q5_K][i % 3].
+IQ4NL, IQ4XS, Q5K = int(gl.GgmlType.IQ4_NL), int(gl.GgmlType.IQ4_XS), int(gl.GgmlType.Q5_K)
+QWEN3_SHAPES = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048),
+                ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072)]
+QWEN3_LAYERS = 28
+
+
+def bench_config4(torch, ctx, stream, steps=10):
+    """28 Qwen3-0.6B layers of IQ4_NL / IQ4_XS / Q5_K matmuls with
+    batch 1, 4 and 8 fp32 activation rows (one launch per matmul)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    cycle = [IQ4NL, IQ4XS, Q5K]
+    layer = []
+    for i, (name, N, K) in enumerate(QWEN3_SHAPES):
+        dev, _ = make_weight(torch, gen, cycle[i % 3], N, K)
+        layer.append((name, cycle[i % 3], N, K, dev))
+    weights = [[(n, t, N, K, d if li == 0 else d.clone()) for n, t, N, K, d in layer] for li in range(QWEN3_LAYERS)]
+    res = {"workload": "Qwen3-0.6B shapes x 28 layers, types [IQ4_NL, IQ4_XS, Q5_K][i % 3] over q,k,v,o,gate,up,down",
+           "types": {n: gl.GgmlType(t).name for n, t, _, _, _ in layer}}
+    for M in (1, 4, 8):
+        mats = [Mat(torch, f"b{M}.{li}.{n}", t, N, K, d, M=M) for li in range(QWEN3_LAYERS) for n, t, N, K, d in weights[li]]
+
+        def run():
+            for m in mats:
+                launch(ctx, m, 0, stream)
+
+        sec = time_steps(torch, run, steps, 2)
+        b = sum(m.bytes() for m in mats)
+        res[f"batch{M}"] = {"bytes": b, "us": round(sec * 1e6, 1), "GBps": round(b / sec / 1e9, 1),
+                            "frac_hbm_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
+    return res
+
+
+def bench_config5(torch, ctx, stream, steps=20):
+    """one qwen35moe-A3B MoE FFN layer, 64 tokens, top-8 of 256
+    experts (FFN 512, Q4_K gate/up, Q6_K down) + 1 shared expert, as one
+    expert-grouped ggq_moe_ffn_dev call."""
+    T, H, F, E, k = 64, 2048, 512, 256, 8
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    wg, _ = make_weight(torch, gen, Q4K, E * F, H)
+    wu, _ = make_weight(torch, gen, Q4K, E * F, H)
+    wd, _ = make_weight(torch, gen, Q6K, E * H, F)
+    sg, _ = make_weight(torch, gen, Q4K, F, H)
+    su, _ = make_weight(torch, gen, Q4K, F, H)
+    sd, _ = make_weight(torch, gen, Q6K, H, F)
+    x = torch.randn((T, H), device="cuda", generator=gen)
+    logits = torch.randn((T, E), device="cuda", generator=gen)
+    sw = torch.sigmoid(torch.randn((T,), device="cuda", generator=gen))
+    out = torch.empty((T, H), device="cuda")
+    sel = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    p = gl.MoeParams()
+    p.T, p.H, p.F, p.E, p.top_k = T, H, F, E, k
+    p.x, p.router_logits = x.data_ptr(), logits.data_ptr()
+    p.gate_type, p.up_type, p.down_type = Q4K, Q4K, Q6K
+    p.gate_exps, p.up_exps, p.down_exps = wg.data_ptr(), wu.data_ptr(), wd.data_ptr()
+    p.gate_shexp, p.up_shexp, p.down_shexp = sg.data_ptr(), su.data_ptr(), sd.data_ptr()
+    p.shared_w, p.out, p.sel_experts = sw.data_ptr(), out.data_ptr(), sel.data_ptr()
+
+    def run():
+        ctx.check(ctx.lib.ggq_moe_ffn_dev(ctx.h, ctypes.byref(p), stream), "moe_ffn")
+
+    sec = time_steps(torch, run, steps, 2)
+    hit = int(torch.unique(sel).numel())
+    per_expert = 2 * gl.row_bytes(Q4K, H) * F + gl.row_bytes(Q6K, F) * H
+    b = (hit + 1) * per_expert + 4 * T * H * 2 + 4 * T * E
+    return {"workload": "qwen35moe-A3B MoE FFN layer: 64 tokens, top-8 of 256 experts (FFN 512) + shared, "
+                        "Q4_K gate/up, Q6_K down, one grouped call", "experts_hit": hit,
+            "bytes": b, "us": round(sec * 1e6, 1), "GBps": round(b / sec / 1e9, 1),
+            "frac_hbm_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def cpu_baseline(host_layer0, budget_s=8.0):
     """Single-core fp32 CpuRefBackend::mul_mat_q restatement (oracle, bit-exact
     with the reference's output) on layer 0 of the decode step."""
@@ -294,7 +368,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
-    ap.add_argument("--only", choices=["decode", "config1", "prefill", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "copy"], default=None,
                     help="run one workload only and print its result (profiling aid)")
     ap.add_argument("--per-matmul", action="store_true",
                     help="one launch per matmul instead of one per dependency level")
@@ -325,8 +399,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_per_copy": src.numel(), "copies": 4}), flush=True)
         return
-    if args.only in ("config1", "prefill"):
-        res = bench_config1(torch, ctx, stream) if args.only == "config1" else bench_prefill(torch, ctx, stream)
+    if args.only in ("config1", "prefill", "config4", "moe"):
+        res = {"config1": bench_config1, "prefill": bench_prefill, "config4": bench_config4,
+               "moe": bench_config5}[args.only](torch, ctx, stream)
         print(json.dumps({"only": args.only, **res}), flush=True)
         ctx.close()
         return
@@ -371,10 +446,12 @@ def main():
         out["roofline"]["traffic_unit"] = "HBM bytes per step (rocprofv3 FETCH_SIZE + WRITE_SIZE, " + t["source"] + ")"
     if not args.no_extra:
         out["extra"] = {"config1": bench_config1(torch, ctx, stream)}
-        try:
-            out["extra"]["config3_prefill"] = bench_prefill(torch, ctx, stream)
-        except Exception as e:  # reported, never silently replaced
-            out["extra"]["config3_prefill"] = {"error": str(e)}
+        for key, fn in (("config3_prefill", bench_prefill), ("config4_iq4_q5k", bench_config4),
+                        ("config5_moe", bench_config5)):
+            try:
+                out["extra"][key] = fn(torch, ctx, stream)
+            except Exception as e:  # reported, never silently replaced
+                out["extra"][key] = {"error": str(e)}
         out["cpu_baseline"] = cpu_baseline(host_layer0)
     per = {}
     for lv, d in list(zip(levels[:4], kt[:4])) + [(levels[-1], kt[-1])]:

@@ -598,7 +598,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     } while (0)
     const int u = gemv_rows_per_iter();
     if (ppt == 1) {
-        if (mrows <= 1) { if (u >= 2) GO(1, 1, 2); else GO(1, 1, 1); }
+        if (mrows <= 1) { if (u >= 4) GO(1, 1, 4); else if (u >= 2) GO(1, 1, 2); else GO(1, 1, 1); }
         else if (mrows == 2) GO(2, 1, 1);
         else GO(4, 1, 1);
     } else if (ppt == 2) {
@@ -640,8 +640,9 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
         return hipSuccess;
     }
     const int u = gemv_rows_per_iter();
-    const int target = ppt == 1 ? (u >= 2 ? resident_blocks(gemv_multi_kernel<1, 1, 2>, shmem)
-                                          : resident_blocks(gemv_multi_kernel<1, 1, 1>, shmem))
+    const int target = ppt == 1 ? (u >= 4 ? resident_blocks(gemv_multi_kernel<1, 1, 4>, shmem)
+                                   : u >= 2 ? resident_blocks(gemv_multi_kernel<1, 1, 2>, shmem)
+                                            : resident_blocks(gemv_multi_kernel<1, 1, 1>, shmem))
                                 : resident_blocks(gemv_multi_kernel<1, 2, 1>, shmem);
     int b = 0;
     for (int i = 0; i < n; i++) {
@@ -656,7 +657,8 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     ma.begin[n] = b;
     ma.n = n;
     if (ppt == 1) {
-        if (u >= 2) gemv_multi_kernel<1, 1, 2><<<b, 256, shmem, s>>>(ma);
+        if (u >= 4) gemv_multi_kernel<1, 1, 4><<<b, 256, shmem, s>>>(ma);
+        else if (u >= 2) gemv_multi_kernel<1, 1, 2><<<b, 256, shmem, s>>>(ma);
         else gemv_multi_kernel<1, 1, 1><<<b, 256, shmem, s>>>(ma);
     } else {
         gemv_multi_kernel<1, 2, 1><<<b, 256, shmem, s>>>(ma);
