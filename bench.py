@@ -245,17 +245,24 @@ def bench_prefill(torch, ctx, stream, steps=3):
                                         ctypes.c_void_p(m.y.data_ptr()), m.N, stream)
         ctx.check(st, "mul_mat_q8_dev")
 
+    def mm_batch(ms):
+        """Weights sharing one quantized input: one multi-weight launch."""
+        q, sc = qin[level_of[ms[0].name.split(".")[1]]]
+        descs = (gl.GemmDesc * len(ms))(*[gl.GemmDesc(m.w.data_ptr(), m.N, m.y.data_ptr(), m.N) for m in ms])
+        st = ctx.lib.ggq_mul_mat_q8_batch_dev(ctx.h, descs, len(ms), ms[0].t, ms[0].K,
+                                              ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), T,
+                                              stream)
+        ctx.check(st, "mul_mat_q8_batch_dev")
+
     def run():
         for li in range(QWEN_LAYERS):
             lm = mats[7 * li: 7 * li + 7]
             quant("qkv")
-            for m in lm[:3]:
-                mm(m)
+            mm_batch(lm[:3])
             quant("o")
             mm(lm[3])
             quant("gu")
-            mm(lm[4])
-            mm(lm[5])
+            mm_batch(lm[4:6])
             quant("down")
             mm(lm[6])
 

@@ -48,6 +48,7 @@ struct ggq_ctx {
     std::set<ggq_weight*> weights;
     Buffer ws;  // kernel workspace (activation quant, MoE intermediates)
     Buffer io;  // staging of host A / C for the synchronous entry points
+    Buffer part;  // GEMM split-K partial tiles
 };
 
 namespace {
@@ -93,6 +94,15 @@ hipError_t ensure(Buffer& b, size_t need) {
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Split-K workspace for a GEMM plan (null when the plan does not split).
+hipError_t ensure_gemm_ws(ggq_ctx* c, const ggq::GemmPlan& pl, float** part) {
+    *part = nullptr;
+    if (pl.splits <= 1) return hipSuccess;
+    hipError_t e = ensure(c->part, sizeof(float) * pl.part_floats);
+    if (e == hipSuccess) *part = (float*)c->part.ptr;
+    return e;
+}
+
 hipStream_t pick_stream(ggq_ctx* c, void* s) { return s ? (hipStream_t)s : c->stream; }
 
 int check_matmul_shape(ggq_ctx* c, uint32_t type, int64_t N, int64_t K, int M, int lda, int ldc,
@@ -129,8 +139,7 @@ int mul_mat_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K
     const size_t s_off = align256(q_off + (size_t)M * K);
     const size_t x_off = align256(s_off + sizeof(float) * (size_t)M * (K / 32));
     const bool use_gemm = act_mode == GGQ_ACT_Q8_ROW && M > 8;
-    const size_t need = use_gemm ? x_off + align256(sizeof(float) * (size_t)ggq::gemm_splits(type, (int)N, (int)K, M) * M * N)
-                                 : align256(x_off + sizeof(float) * (size_t)M * K);
+    const size_t need = use_gemm ? x_off : align256(x_off + sizeof(float) * (size_t)M * K);
     if ((e = ensure(c->ws, need)) != hipSuccess) return hip_status(c, e, "workspace");
     int8_t* q = (int8_t*)c->ws.ptr + q_off;
     float* sc = (float*)((char*)c->ws.ptr + s_off);
@@ -138,7 +147,11 @@ int mul_mat_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K
     if (use_gemm) {
         if ((e = ggq::launch_quant_act(A, lda, M, (int)K, act_mode, q, sc, nullptr, s)) != hipSuccess)
             return hip_status(c, e, "quant_act");
-        return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, q, sc, M, C, ldc, xe, s), "gemm_i8");
+        const int n32 = (int)N;
+        float* part;
+        if ((e = ensure_gemm_ws(c, ggq::plan_gemm_i8(type, &n32, 1, (int)K, M), &part)) != hipSuccess)
+            return hip_status(c, e, "workspace");
+        return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, q, sc, M, C, ldc, part, s), "gemm_i8");
     }
     if ((e = ggq::launch_quant_act(A, lda, M, (int)K, act_mode, nullptr, nullptr, xe, s)) != hipSuccess)
         return hip_status(c, e, "quant_act");
@@ -153,10 +166,11 @@ int mul_mat_q8_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_
     if (M == 0) return set_status(c, GGQ_OK);
     hipError_t e;
     if (M > 8) {
-        const size_t need = align256(sizeof(float) * (size_t)ggq::gemm_splits(type, (int)N, (int)K, M) * M * N);
-        if ((e = ensure(c->ws, need)) != hipSuccess) return hip_status(c, e, "workspace");
-        return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, qa, sa, M, C, ldc, (float*)c->ws.ptr, s),
-                          "gemm_i8");
+        const int n32 = (int)N;
+        float* part;
+        if ((e = ensure_gemm_ws(c, ggq::plan_gemm_i8(type, &n32, 1, (int)K, M), &part)) != hipSuccess)
+            return hip_status(c, e, "workspace");
+        return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, qa, sa, M, C, ldc, part, s), "gemm_i8");
     }
     if ((e = ensure(c->ws, sizeof(float) * (size_t)M * K)) != hipSuccess) return hip_status(c, e, "workspace");
     float* xe = (float*)c->ws.ptr;
@@ -268,6 +282,7 @@ void ggq_destroy(ggq_ctx* c) {
     }
     if (c->ws.ptr) hipFree(c->ws.ptr);
     if (c->io.ptr) hipFree(c->io.ptr);
+    if (c->part.ptr) hipFree(c->part.ptr);
     hipStreamDestroy(c->stream);
     delete c;
 }
@@ -365,6 +380,40 @@ int ggq_mul_mat_q8_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int6
     int st = check_matmul_shape(c, type, N, K, M, (int)K, ldc, GGQ_ACT_Q8_ROW);
     if (st != GGQ_OK) return st;
     return mul_mat_q8_queue(c, W, type, N, K, qa, sa, M, C, ldc, pick_stream(c, stream));
+    GGQ_END(c)
+}
+
+int ggq_mul_mat_q8_batch_dev(ggq_ctx* c, const ggq_gemm_desc* d, int n, uint32_t type, int64_t K, const int8_t* qa,
+                             const float* sa, int M, void* stream) {
+    GGQ_GUARD(c)
+    if (!d || n < 1 || n > GGQ_MAX_GEMM_BATCH) return set_status(c, GGQ_INVALID_PARAM, "need 1..%d descriptors", GGQ_MAX_GEMM_BATCH);
+    if (M < 0 || (M > 0 && (!qa || !sa))) return set_status(c, GGQ_INVALID_PARAM, "bad activations");
+    if (!aligned16(qa) || K % 16) return set_status(c, GGQ_INVALID_PARAM, "qa must be 16-byte aligned with K %% 16 == 0");
+    for (int i = 0; i < n; i++) {
+        if (!d[i].W || !d[i].C) return set_status(c, GGQ_INVALID_PARAM, "null pointer in entry %d", i);
+        if (!aligned16(d[i].W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
+        const int st = check_matmul_shape(c, type, d[i].N, K, M, (int)K, d[i].ldc, GGQ_ACT_Q8_ROW);
+        if (st != GGQ_OK) return st;
+    }
+    if (M == 0) return set_status(c, GGQ_OK);
+    const hipStream_t s = pick_stream(c, stream);
+    if (M <= 8 || type == GGQ_TYPE_Q6_K) {
+        for (int i = 0; i < n; i++) {
+            const int st = mul_mat_q8_queue(c, d[i].W, type, d[i].N, K, qa, sa, M, d[i].C, d[i].ldc, s);
+            if (st != GGQ_OK) return st;
+        }
+        return set_status(c, GGQ_OK);
+    }
+    ggq::GemmDesc gd[GGQ_MAX_GEMM_BATCH];
+    int Ns[GGQ_MAX_GEMM_BATCH];
+    for (int i = 0; i < n; i++) {
+        gd[i] = ggq::GemmDesc{d[i].W, d[i].C, (int)d[i].N, d[i].ldc};
+        Ns[i] = (int)d[i].N;
+    }
+    float* part;
+    hipError_t e = ensure_gemm_ws(c, ggq::plan_gemm_i8(type, Ns, n, (int)K, M), &part);
+    if (e != hipSuccess) return hip_status(c, e, "workspace");
+    return hip_status(c, ggq::launch_gemm_i8_multi(type, gd, n, (int)K, qa, sa, M, part, s), "gemm_i8 batch");
     GGQ_END(c)
 }
 

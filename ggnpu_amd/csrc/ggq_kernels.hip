@@ -121,14 +121,24 @@ __device__ __forceinline__ int8_t to_i8(float v) {
     return (int8_t)(int)r;
 }
 
+// One workgroup per row: absolute maximum, then codes.  With 16-byte
+// aligned rows (lda, K multiples of 4) each thread moves float4 / 4 codes
+// at a time; the arithmetic per element is the same either way.
 __global__ __launch_bounds__(256) void quant_act_row_kernel(const float* __restrict__ A, int lda, int K,
                                                             int8_t* __restrict__ q, float* __restrict__ scales,
-                                                            float* __restrict__ x_eff) {
+                                                            float* __restrict__ x_eff, int vec4) {
     __shared__ float wmax[4];
     const int m = blockIdx.x;
     const float* a = A + (int64_t)m * lda;
     float amax = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(a[k]));
+    if (vec4) {
+        for (int k = 4 * threadIdx.x; k < K; k += 1024) {
+            const float4 v = *(const float4*)(a + k);
+            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+        }
+    } else {
+        for (int k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(a[k]));
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
@@ -137,6 +147,21 @@ __global__ __launch_bounds__(256) void quant_act_row_kernel(const float* __restr
     const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
     const float inv = __fdiv_rn(1.0f, sc);
     if (threadIdx.x == 0 && scales) scales[m] = sc;
+    if (vec4) {
+        for (int k = 4 * threadIdx.x; k < K; k += 1024) {
+            const float4 v = *(const float4*)(a + k);
+            const int8_t c0 = to_i8(__fmul_rn(v.x, inv)), c1 = to_i8(__fmul_rn(v.y, inv));
+            const int8_t c2 = to_i8(__fmul_rn(v.z, inv)), c3 = to_i8(__fmul_rn(v.w, inv));
+            if (q)
+                *(uint32_t*)(q + (int64_t)m * K + k) = (uint32_t)(uint8_t)c0 | (uint32_t)(uint8_t)c1 << 8 |
+                                                       (uint32_t)(uint8_t)c2 << 16 | (uint32_t)(uint8_t)c3 << 24;
+            if (x_eff)
+                *(float4*)(x_eff + (int64_t)m * K + k) =
+                    make_float4(__fmul_rn((float)c0, sc), __fmul_rn((float)c1, sc), __fmul_rn((float)c2, sc),
+                                __fmul_rn((float)c3, sc));
+        }
+        return;
+    }
     for (int k = threadIdx.x; k < K; k += 256) {
         const int8_t v = to_i8(__fmul_rn(a[k], inv));
         if (q) q[(int64_t)m * K + k] = v;
@@ -168,7 +193,9 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
                             float* scales, float* x_eff, hipStream_t s) {
     if (M == 0 || K == 0) return hipSuccess;
     if (mode == 1) {
-        quant_act_row_kernel<<<M, 256, 0, s>>>(A, lda, K, q, scales, x_eff);
+        const int vec4 = ((uintptr_t)A % 16 == 0) && lda % 4 == 0 && K % 4 == 0 && ((uintptr_t)q % 4 == 0) &&
+                         ((uintptr_t)x_eff % 16 == 0);
+        quant_act_row_kernel<<<M, 256, 0, s>>>(A, lda, K, q, scales, x_eff, vec4);
     } else {
         const int64_t n = (int64_t)M * (K / 32);
         quant_act_b32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(A, lda, M, K, q, scales, x_eff);
@@ -700,6 +727,25 @@ struct GemmArgs {
     float* Cpart;         // [splits][M][N] partial sums when split, else null
 };
 
+constexpr int kGemmMaxProb = 4;
+struct GemmProb {
+    const uint8_t* W;
+    float* C;
+    int N;
+    int ldc;
+    int tile_begin;  // first blockIdx.x of this weight
+};
+struct GemmMultiArgs {
+    GemmProb p[kGemmMaxProb];
+    int np;
+    int64_t row_bytes;
+    int K, M;
+    const int8_t* QA;
+    const float* sa;
+    int splits, steps_per_split;
+    float* part;  // [tiles][splits][BM*BN] partial sums when splits > 1
+};
+
 template <int T>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     constexpr bool kMin = T == T_Q4_K || T == T_Q5_K;
@@ -861,8 +907,19 @@ template <> struct BStage<T_Q8_0> {
     }
 };
 
-template <int T, int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmArgs a) {
+// One launch serves up to kGemmMaxProb weights of one type that share the
+// activation rows (q/k/v, or gate/up): blockIdx.x runs over the N-tiles of
+// all of them, blockIdx.y over M-tiles, blockIdx.z over K-slices.
+//
+// With split-K every slice writes its partial tile to workspace in
+// accumulator register order (element e of thread t at e*256 + t, so writes
+// and reads are coalesced) and gemm_reduce_kernel adds the slices in slice
+// order, which keeps results independent of scheduling.  (A last-arriving-
+// workgroup reduction inside this kernel needs an agent-scope release fence
+// per workgroup, which writes back the XCD's L2 and measured several times
+// slower than the extra launch.)
+template <int T, int BM, int BN, int PF>
+__global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmMultiArgs a) {
     constexpr bool kMin = T == T_Q4_K || T == T_Q5_K;
     constexpr int WM = BM / 2, WN = BN / 2;       // wavefront tile
     constexpr int TM = WM / 32, TN = WN / 32;     // MFMA tiles per wavefront
@@ -878,14 +935,21 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmArgs a) {
     __shared__ float Bd[2][BN][G];
     __shared__ float Bm[2][BN][G];
 
+    int q = 0;
+    while (q + 1 < a.np && (int)blockIdx.x >= a.p[q + 1].tile_begin) q++;
+    const uint8_t* const W = a.p[q].W;
+    const int N = a.p[q].N;
+
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, lk = lane >> 5;
-    const int m_tile = blockIdx.y * BM, n_tile = blockIdx.x * BN;
+    const int m_tile = blockIdx.y * BM, n_tile = ((int)blockIdx.x - a.p[q].tile_begin) * BN;
     const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
     const int nsteps = (a.K + kGemmBK - 1) / kGemmBK;
 
-    uint4 areg[A_PER_T];
-    BStage<T> breg[B_PER_T];
+    // PF register stages: the global loads of K-step st+PF are in flight
+    // while step st computes.
+    uint4 areg[PF][A_PER_T];
+    BStage<T> breg[PF][B_PER_T];
     // Per-thread source rows, computed once; each K-step advances k.
     const int8_t* aptr[A_PER_T];
     bool arow_ok[A_PER_T];
@@ -906,36 +970,36 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmArgs a) {
         const int sl = tid + 256 * i;
         const int r = sl / G, n = n_tile + r;
         bkg[i] = 32 * (sl % G);
-        brow_ok[i] = sl < B_SLOTS && n < a.N;
-        bptr[i] = a.W + (int64_t)(brow_ok[i] ? n : 0) * a.row_bytes;
+        brow_ok[i] = sl < B_SLOTS && n < N;
+        bptr[i] = W + (int64_t)(brow_ok[i] ? n : 0) * a.row_bytes;
     }
 
-    auto fetch = [&](int step) {
+    auto fetch = [&](int step, uint4 (&ar)[A_PER_T], BStage<T> (&br)[B_PER_T]) {
         const int k0 = step * kGemmBK;
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) {
             const bool ok = arow_ok[i] && k0 + akc[i] < a.K;
-            areg[i] = ok ? *(const uint4*)(aptr[i] + k0) : make_uint4(0, 0, 0, 0);
+            ar[i] = ok ? *(const uint4*)(aptr[i] + k0) : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < B_PER_T; i++) {
             const int k = k0 + bkg[i];
             const bool ok = brow_ok[i] && k < a.K;
-            breg[i].fetch(bptr[i], ok ? k : 0, ok);
+            br[i].fetch(bptr[i], ok ? k : 0, ok);
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, const uint4 (&ar)[A_PER_T], const BStage<T> (&br)[B_PER_T]) {
 #pragma unroll
         for (int i = 0; i < A_PER_T; i++) {
             const int c = tid + 256 * i, r = c / (kGemmBK / 16), kc = (c % (kGemmBK / 16)) * 16;
-            *(uint4*)&As[buf][r][kc] = areg[i];
+            *(uint4*)&As[buf][r][kc] = ar[i];
         }
 #pragma unroll
         for (int i = 0; i < B_PER_T; i++) {
             const int sl = tid + 256 * i;
             if (sl < B_SLOTS) {
                 const int r = sl / G, g = sl % G;
-                breg[i].store(&Bs[buf][r][32 * g], &Bd[buf][r][g], &Bm[buf][r][g]);
+                br[i].store(&Bs[buf][r][32 * g], &Bd[buf][r][g], &Bm[buf][r][g]);
             }
         }
     };
@@ -952,54 +1016,78 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmArgs a) {
     // Split-K: slice z covers K-steps [st0, st1).
     const int st0 = blockIdx.z * a.steps_per_split;
     const int st1 = st0 + a.steps_per_split < nsteps ? st0 + a.steps_per_split : nsteps;
-    fetch(st0);
-    store(0);
+    // Step st lives in register stage (st - st0) % PF until it is stored to
+    // LDS buffer (st - st0) & 1 at the end of step st - 1.
+    fetch(st0, areg[0], breg[0]);
+    store(0, areg[0], breg[0]);
+#pragma unroll
+    for (int j = 1; j <= PF; j++)
+        if (st0 + j < st1) fetch(st0 + j, areg[j % PF], breg[j % PF]);
     __syncthreads();
-    for (int st = st0; st < st1; st++) {
-        const int buf = (st - st0) & 1;
-        if (st + 1 < st1) fetch(st + 1);
+    for (int sb = st0; sb < st1; sb += PF) {
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            v4i A[TM], B[TN];
-            float dl[TN], ml[TN];
+        for (int d = 0; d < PF; d++) {
+            const int st = sb + d;
+            if (st >= st1) break;
+            const int buf = (st - st0) & 1;
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const uint4 v = *(const uint4*)&As[buf][wm + 32 * i + li][32 * g + 16 * lk];
-                A[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-            }
+            for (int g = 0; g < G; g++) {
+                v4i A[TM], B[TN];
+                float dl[TN], ml[TN];
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const uint4 v = *(const uint4*)&Bs[buf][wn + 32 * j + li][32 * g + 16 * lk];
-                B[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-                dl[j] = Bd[buf][wn + 32 * j + li][g];
-                ml[j] = Bm[buf][wn + 32 * j + li][g];
-            }
-            v16i S[TM];
-            if constexpr (kMin) {
-                const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-#pragma unroll
-                for (int i = 0; i < TM; i++) S[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], ones, zero, 0, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < TM; i++)
+                for (int i = 0; i < TM; i++) {
+                    const uint4 v = *(const uint4*)&As[buf][wm + 32 * i + li][32 * g + 16 * lk];
+                    A[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                }
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    const v16i Pm = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B[j], zero, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        acc[i][j][r] = fmaf(dl[j], (float)Pm[r], acc[i][j][r]);
-                        if constexpr (kMin) acc[i][j][r] = fmaf(-ml[j], (float)S[i][r], acc[i][j][r]);
-                    }
+                    const uint4 v = *(const uint4*)&Bs[buf][wn + 32 * j + li][32 * g + 16 * lk];
+                    B[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                    dl[j] = Bd[buf][wn + 32 * j + li][g];
+                    ml[j] = Bm[buf][wn + 32 * j + li][g];
                 }
-        }
-        if (st + 1 < st1) {
-            store(buf ^ 1);
-            __syncthreads();
+                v16i S[TM];
+                if constexpr (kMin) {
+                    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+#pragma unroll
+                    for (int i = 0; i < TM; i++) S[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], ones, zero, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        const v16i Pm = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B[j], zero, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            acc[i][j][r] = fmaf(dl[j], (float)Pm[r], acc[i][j][r]);
+                            if constexpr (kMin) acc[i][j][r] = fmaf(-ml[j], (float)S[i][r], acc[i][j][r]);
+                        }
+                    }
+            }
+            if (st + 1 < st1) {
+                const int nx = (d + 1) % PF;  // a constant once the d loop is unrolled
+                store(buf ^ 1, areg[nx], breg[nx]);
+                if (st + 1 + PF < st1) fetch(st + 1 + PF, areg[nx], breg[nx]);
+                __syncthreads();
+            }
         }
     }
 
-    float* out = a.Cpart ? a.Cpart + (int64_t)blockIdx.z * a.M * a.N : a.C;
-    const int ldo = a.Cpart ? a.N : a.ldc;
+    if (a.splits > 1) {
+        // Partial tile in accumulator register order; gemm_reduce_kernel
+        // adds the slices in slice order.
+        const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+        float* mine = a.part + ((int64_t)tile * a.splits + blockIdx.z) * (BM * BN);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) mine[((i * TN + j) * 16 + r) * 256 + tid] = acc[i][j][r];
+        return;
+    }
+    float* const C = a.p[q].C;
+    const int ldc = a.p[q].ldc;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -1010,83 +1098,184 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmArgs a) {
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const int n = n_tile + wn + 32 * j + li;
-                if (n < a.N) out[(int64_t)m * ldo + n] = acc[i][j][r] * s;
+                if (n < N) C[(int64_t)m * ldc + n] = acc[i][j][r] * s;
             }
         }
 }
 
-// Deterministic split-K reduction: C = sum over slices in slice order.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
-                                                            float* __restrict__ C, int ldc) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)M * N) return;
-    const int m = (int)(i / N), n = (int)(i % N);
-    float acc = 0.0f;
-    for (int z = 0; z < splits; z++) acc += part[(int64_t)z * M * N + i];
-    C[(int64_t)m * ldc + n] = acc;
+// C = sa * (slice 0 + slice 1 + ...) for each output tile, with the (m, n)
+// of each register element as in gemm_i8_lds_kernel.  Workgroup (x, y, z)
+// covers tile (x, y) and register elements [4z, 4z + 4) of every thread, so
+// each thread has four independent load streams.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmMultiArgs a) {
+    constexpr int WM = BM / 2, WN = BN / 2, TN = WN / 32;
+    int q = 0;
+    while (q + 1 < a.np && (int)blockIdx.x >= a.p[q + 1].tile_begin) q++;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lk = lane >> 5;
+    const int m_tile = blockIdx.y * BM, n_tile = ((int)blockIdx.x - a.p[q].tile_begin) * BN;
+    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+    const int N = a.p[q].N, ldc = a.p[q].ldc;
+    float* const C = a.p[q].C;
+    const float* part = a.part + (int64_t)(blockIdx.y * gridDim.x + blockIdx.x) * a.splits * (BM * BN);
+    const int e0 = 4 * blockIdx.z;
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int z = 0; z < a.splits; z++)
+#pragma unroll
+        for (int u = 0; u < 4; u++) sum[u] += part[(int64_t)z * (BM * BN) + (e0 + u) * 256 + tid];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int e = e0 + u, r = e & 15, ij = e >> 4, i = ij / TN, j = ij % TN;
+        const int m = m_tile + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
+        const int n = n_tile + wn + 32 * j + li;
+        if (m < a.M && n < N) C[(int64_t)m * ldc + n] = sum[u] * a.sa[m];
+    }
 }
 
-// Workgroup tile: 64x64 (32x32 per wavefront, + split-K where the tiles do
-// not fill the chip).  GGQ_GEMM_TILE=128 selects 128x64 tiles (64x32 per
-// wavefront) where they fill the chip; measured slower on gfx950 because the
-// larger accumulator set limits occupancy to two wavefronts per SIMD.
-static bool gemm_big_tile(int N, int M) {
-    static int force = [] {
+// Workgroup tile: 64x64 (32x32 per wavefront).  GGQ_GEMM_TILE=128 selects
+// 128x64 tiles (64x32 per wavefront).
+static bool gemm_big_tile() {
+    static int v = [] {
         const char* e = getenv("GGQ_GEMM_TILE");
         return e && *e ? atoi(e) : 64;
     }();
-    return force == 128 && (int64_t)((M + 127) / 128) * ((N + 63) / 64) >= device_cus();
+    return v == 128;
 }
 
-int gemm_splits(uint32_t type, int N, int K, int M) {
-    if (type == T_Q6_K || gemm_big_tile(N, M)) return 1;
-    const int tiles = ((N + 63) / 64) * ((M + 63) / 64);
+// Register prefetch depth of the LDS GEMM in K-steps (GGQ_GEMM_PF, 1..4).
+static int gemm_prefetch() {
+    static int v = [] {
+        const char* e = getenv("GGQ_GEMM_PF");
+        const int x = e && *e ? atoi(e) : 2;
+        return x < 1 ? 1 : (x > 4 ? 4 : x);
+    }();
+    return v;
+}
+
+template <int T>
+static const void* gemm_kernel_ptr(bool big, int pf) {
+    if (big) return (const void*)gemm_i8_lds_kernel<T, 128, 64, 1>;
+    switch (pf) {
+    case 1: return (const void*)gemm_i8_lds_kernel<T, 64, 64, 1>;
+    case 3: return (const void*)gemm_i8_lds_kernel<T, 64, 64, 3>;
+    case 4: return (const void*)gemm_i8_lds_kernel<T, 64, 64, 4>;
+    default: return (const void*)gemm_i8_lds_kernel<T, 64, 64, 2>;
+    }
+}
+
+static const void* gemm_kernel_for(uint32_t type) {
+    const bool big = gemm_big_tile();
+    const int pf = gemm_prefetch();
+    switch (type) {
+    case T_Q4_K: return gemm_kernel_ptr<T_Q4_K>(big, pf);
+    case T_Q5_K: return gemm_kernel_ptr<T_Q5_K>(big, pf);
+    case T_Q8_0: return gemm_kernel_ptr<T_Q8_0>(big, pf);
+    case T_IQ4_NL: return gemm_kernel_ptr<T_IQ4_NL>(big, pf);
+    case T_IQ4_XS: return gemm_kernel_ptr<T_IQ4_XS>(big, pf);
+    default: return nullptr;
+    }
+}
+
+// Split count for T tiles of S K-steps on R resident workgroups: minimises
+// rounds x steps per slice + the reduction launch (about 1.5 K-steps plus
+// a quarter step per slice read).
+static int choose_splits(int64_t tiles, int nsteps, int resident) {
+    int best = 1;
+    double best_cost = 1e300;
+    for (int s = 1; s <= 8; s *= 2) {
+        if (s > 1 && nsteps / s < 2) break;
+        const int64_t rounds = (tiles * s + resident - 1) / resident;
+        const double cost = (double)rounds * ((nsteps + s - 1) / s) + (s > 1 ? 1.5 + 0.25 * s : 0.0);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = s;
+        }
+    }
+    return best;
+}
+
+GemmPlan plan_gemm_i8(uint32_t type, const int* Ns, int n, int K, int M) {
+    GemmPlan pl{};
+    const bool big = gemm_big_tile();
+    pl.bm = big ? 128 : 64;
+    pl.bn = 64;
+    pl.n_tiles = 0;
+    for (int i = 0; i < n; i++) pl.n_tiles += (Ns[i] + pl.bn - 1) / pl.bn;
+    pl.m_tiles = (M + pl.bm - 1) / pl.bm;
     const int nsteps = (K + kGemmBK - 1) / kGemmBK;
-    int splits = 1;
-    while (splits < 8 && tiles * splits < 2 * device_cus() && nsteps / (splits * 2) >= 2) splits *= 2;
-    return splits;
+    pl.splits = 1;
+    if (type != T_Q6_K) {
+        const void* k = gemm_kernel_for(type);
+        int per_cu = 0;
+        if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 256, 0) != hipSuccess || per_cu <= 0)
+            per_cu = 1;
+        pl.splits = choose_splits((int64_t)pl.n_tiles * pl.m_tiles, nsteps, per_cu * device_cus());
+    }
+    pl.steps_per_split = (nsteps + pl.splits - 1) / pl.splits;
+    pl.splits = (nsteps + pl.steps_per_split - 1) / pl.steps_per_split;
+    pl.part_floats = pl.splits > 1 ? (size_t)pl.n_tiles * pl.m_tiles * pl.splits * pl.bm * pl.bn : 0;
+    return pl;
 }
 
-hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa,
-                          const float* sa, int M, float* C, int ldc, float* part, hipStream_t s) {
-    if (M == 0 || N == 0) return hipSuccess;
-    GemmArgs a;
-    a.W = (const uint8_t*)W;
-    a.row_bytes = row_bytes(type, K);
-    a.N = N; a.K = K;
-    a.QA = qa; a.sa = sa;
-    a.C = C; a.ldc = ldc; a.M = M;
-    a.Cpart = nullptr;
+hipError_t launch_gemm_i8_multi(uint32_t type, const GemmDesc* d, int n, int K, const int8_t* qa, const float* sa,
+                                int M, float* part, hipStream_t s) {
+    if (M == 0 || n == 0) return hipSuccess;
+    if (n > kGemmMaxProb) return hipErrorInvalidValue;
     if (type == T_Q6_K) {  // 16-value groups: direct-load kernel with 32x32x16 MFMAs
-        const dim3 grid((N + 127) / 128, (M + 127) / 128);
-        gemm_i8_kernel<T_Q6_K><<<grid, 256, 0, s>>>(a);
+        for (int i = 0; i < n; i++) {
+            GemmArgs a;
+            a.W = (const uint8_t*)d[i].W;
+            a.row_bytes = row_bytes(type, K);
+            a.N = d[i].N; a.K = K;
+            a.QA = qa; a.sa = sa;
+            a.C = d[i].C; a.ldc = d[i].ldc; a.M = M;
+            a.Cpart = nullptr;
+            a.steps_per_split = 0;
+            const dim3 grid((d[i].N + 127) / 128, (M + 127) / 128);
+            gemm_i8_kernel<T_Q6_K><<<grid, 256, 0, s>>>(a);
+        }
         return hipGetLastError();
     }
-    const int nsteps = (K + kGemmBK - 1) / kGemmBK;
-    const int splits = part ? gemm_splits(type, N, K, M) : 1;
-    a.steps_per_split = (nsteps + splits - 1) / splits;
-    const int zs = (nsteps + a.steps_per_split - 1) / a.steps_per_split;
-    if (zs > 1) a.Cpart = part;
-    // 128x128 tiles would need more VGPRs than the accumulators leave.
-    const bool big = gemm_big_tile(N, M);
-    const dim3 grid((N + 63) / 64, big ? (M + 127) / 128 : (M + 63) / 64, zs);
-#define L(TT)                                                                    \
-    if (big) gemm_i8_lds_kernel<TT, 128, 64><<<grid, 256, 0, s>>>(a);            \
-    else gemm_i8_lds_kernel<TT, 64, 64><<<grid, 256, 0, s>>>(a)
-    switch (type) {
-    case T_Q4_K: L(T_Q4_K); break;
-    case T_Q5_K: L(T_Q5_K); break;
-    case T_Q8_0: L(T_Q8_0); break;
-    case T_IQ4_NL: L(T_IQ4_NL); break;
-    case T_IQ4_XS: L(T_IQ4_XS); break;
-    default: return hipErrorInvalidValue;
+    int Ns[kGemmMaxProb];
+    for (int i = 0; i < n; i++) Ns[i] = d[i].N;
+    const GemmPlan pl = plan_gemm_i8(type, Ns, n, K, M);
+    GemmMultiArgs a;
+    int tb = 0;
+    for (int i = 0; i < n; i++) {
+        a.p[i].W = (const uint8_t*)d[i].W;
+        a.p[i].C = d[i].C;
+        a.p[i].N = d[i].N;
+        a.p[i].ldc = d[i].ldc;
+        a.p[i].tile_begin = tb;
+        tb += (d[i].N + pl.bn - 1) / pl.bn;
     }
-#undef L
-    if (zs > 1) {
-        const int64_t n = (int64_t)M * N;
-        splitk_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(part, zs, M, N, C, ldc);
-    }
+    a.np = n;
+    a.row_bytes = row_bytes(type, K);
+    a.K = K;
+    a.M = M;
+    a.QA = qa;
+    a.sa = sa;
+    a.splits = pl.splits;
+    a.steps_per_split = pl.steps_per_split;
+    a.part = part;
+    if (pl.splits > 1 && !part) return hipErrorInvalidValue;
+    const dim3 grid(pl.n_tiles, pl.m_tiles, pl.splits);
+    const void* k = gemm_kernel_for(type);
+    if (!k) return hipErrorInvalidValue;
+    void* args[] = {&a};
+    hipError_t e = hipLaunchKernel(k, grid, dim3(256), args, 0, s);
+    if (e != hipSuccess || pl.splits == 1) return e;
+    // (BM*BN/256) register elements per thread, four per workgroup.
+    if (pl.bm == 128) gemm_reduce_kernel<128, 64><<<dim3(pl.n_tiles, pl.m_tiles, 128 * 64 / 1024), 256, 0, s>>>(a);
+    else gemm_reduce_kernel<64, 64><<<dim3(pl.n_tiles, pl.m_tiles, 64 * 64 / 1024), 256, 0, s>>>(a);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa, const float* sa, int M,
+                          float* C, int ldc, float* part, hipStream_t s) {
+    const GemmDesc d{W, C, N, ldc};
+    return launch_gemm_i8_multi(type, &d, 1, K, qa, sa, M, part, s);
 }
 
 // x_eff[m][k] = q[m][k] * scale[m] (fp32) from pre-quantized activations.

@@ -46,11 +46,23 @@ constexpr int kGemvMaxK = 32768;
 
 // int8-MFMA GEMM on per-row int8 activations:
 //   C[m][n] = sa[m] * sum_groups dl[n,g]*P[m,n,g] - ml[n,g]*S[m,g]
-// `part` is workspace for split-K partial sums (gemm_splits() * M * N
-// floats) or null to disable split-K.
-hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa,
-                          const float* sa, int M, float* C, int ldc, float* part, hipStream_t s);
-int gemm_splits(uint32_t type, int N, int K, int M);
+// One launch covers up to 4 weights of one type sharing the activations.
+struct GemmDesc {
+    const void* W;
+    float* C;
+    int N;
+    int ldc;
+};
+struct GemmPlan {
+    int bm, bn, n_tiles, m_tiles, splits, steps_per_split;
+    size_t part_floats;  // split-K workspace (floats), 0 when not split
+};
+GemmPlan plan_gemm_i8(uint32_t type, const int* Ns, int n, int K, int M);
+// `part` sized by plan_gemm_i8 (may be null when it plans no split).
+hipError_t launch_gemm_i8_multi(uint32_t type, const GemmDesc* d, int n, int K, const int8_t* qa, const float* sa,
+                                int M, float* part, hipStream_t s);
+hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa, const float* sa, int M,
+                          float* C, int ldc, float* part, hipStream_t s);
 // x[m][k] = q[m][k] * sa[m] (dense fp32 [M][K]).
 hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, float* x, hipStream_t s);
 

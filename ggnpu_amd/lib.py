@@ -78,6 +78,10 @@ class GemvDesc(ctypes.Structure):
                 ("A", ctypes.c_void_p), ("C", ctypes.c_void_p)]
 
 
+class GemmDesc(ctypes.Structure):
+    _fields_ = [("W", ctypes.c_void_p), ("N", ctypes.c_int64), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int)]
+
+
 class MulMatParams(ctypes.Structure):
     """MulMatParams (include/ggnpu/backend.h:21-35)."""
     _fields_ = [
@@ -108,6 +112,7 @@ SIGNATURES = {
     "ggq_mul_mat_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _I, _I, _I, _P]),
     "ggq_mul_mat_batch_dev": (_I, [_P, _P, _I, _P]),
     "ggq_mul_mat_q8_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _P, _I, _P, _I, _P]),
+    "ggq_mul_mat_q8_batch_dev": (_I, [_P, _P, _I, _U32, _I64, _P, _P, _I, _P]),
     "ggq_dequant_dev": (_I, [_P, _P, _U32, _I64, _P, _P]),
     "ggq_quantize_act_dev": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P]),
     "ggq_block_dot_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _P]),

@@ -137,6 +137,23 @@ int ggq_mul_mat_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64
 int ggq_mul_mat_q8_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K, const int8_t* qa,
                        const float* sa, int M, float* C, int ldc, void* stream);
 
+/* Several weights of one type and one K that consume the same activations
+ * quantized by ggq_quantize_act_dev (the q/k/v or the gate/up projections
+ * of a prefill batch), as one int8-MFMA launch.  Each entry gets what
+ * ggq_mul_mat_q8_dev gives for it, up to fp32 summation order (the split of
+ * K over workgroups depends on the launch's total size).  No reference
+ * counterpart: the reference issues one mul_mat_q per weight
+ * (src/cli/main.cpp:3256-3267).  At most GGQ_MAX_GEMM_BATCH entries. */
+#define GGQ_MAX_GEMM_BATCH 4
+typedef struct {
+    const void* W; /* raw blocks, device memory, 16-byte aligned */
+    int64_t N;     /* weight rows */
+    float* C;      /* [M][ldc] device output */
+    int ldc;
+} ggq_gemm_desc;
+int ggq_mul_mat_q8_batch_dev(ggq_ctx* ctx, const ggq_gemm_desc* descs, int n, uint32_t type, int64_t K,
+                             const int8_t* qa, const float* sa, int M, void* stream);
+
 /* Several independent single-row (decode) matmuls with fp32 activations,
  * queued as one launch where their shapes allow (a mix of weight types is
  * fine), e.g. the q/k/v projections of one token, which share an input.  No

@@ -111,6 +111,22 @@ def test_quant_act_bitexact(ctx, orc, mode, M, K):
     assert np.array_equal(host(ds).view(np.uint32), s_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,K,lda", [(5, 1001, 1001), (4, 64, 67)])
+def test_quant_act_row_unaligned_bitexact(ctx, orc, M, K, lda):
+    """Rows that are not 16-byte aligned take the scalar path; same codes."""
+    import torch
+    rng = np.random.default_rng(K)
+    A = rng.standard_normal((M, lda)).astype(np.float32)
+    q_ref, s_ref = orc.quant_act(np.ascontiguousarray(A[:, :K]), 1)
+    dq = empty((M, K), torch.int8)
+    ds = empty(s_ref.shape, torch.float32)
+    dA = dev(A)
+    ctx.check(ctx.lib.ggq_quantize_act_dev(ctx.h, ptr(dA), lda, M, K, 1, ptr(dq), ptr(ds),
+                                           stream_handle()), "quant_act")
+    assert np.array_equal(host(dq), q_ref)
+    assert np.array_equal(host(ds).view(np.uint32), s_ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("name", list(TYPES))
 def test_block_dot_bitexact(ctx, orc, golden, name):
     import torch
@@ -349,3 +365,72 @@ def test_prequantized_q8_entry(ctx, orc, t):
                                              stream_handle()), "q8 mm")
         err = orc.rel_l2(host(dC), orc.mul_mat_f64(t, raw, N, K, A, 1))
         assert err < TOL, (M, N, K, err)
+
+
+def _quantized(ctx, A):
+    import torch
+    M, K = A.shape
+    dA = dev(A)
+    dq = empty((M, K), torch.int8)
+    ds = empty((M,), torch.float32)
+    ctx.check(ctx.lib.ggq_quantize_act_dev(ctx.h, ptr(dA), K, M, K, 1, ptr(dq), ptr(ds), stream_handle()), "q")
+    return dA, dq, ds
+
+
+@pytest.mark.parametrize("t", [8, 12, 20])
+def test_q8_batch_matches_single_and_oracle(ctx, orc, t):
+    """One multi-weight GEMM launch (q/k/v-like: different N, shared
+    activations) against one ggq_mul_mat_q8_dev per weight and the oracle."""
+    import torch
+    be = gl.BLOCK[gl.GgmlType(t)][0]
+    K = 1536 if be == 32 else 2048
+    M = 200
+    Ns = (300, 64, 100)
+    raws = [weights(t, N, K, seed=40 + i) for i, N in enumerate(Ns)]
+    A = np.random.default_rng(7).standard_normal((M, K)).astype(np.float32)
+    dA, dq, ds = _quantized(ctx, A)
+    dWs = [dev(r) for r in raws]
+    outs = [torch.full((M, N + 3), float("nan"), device="cuda") for N in Ns]
+    descs = (gl.GemmDesc * 3)(*[gl.GemmDesc(ptr(w), N, ptr(o), N + 3) for w, N, o in zip(dWs, Ns, outs)])
+    ctx.check(ctx.lib.ggq_mul_mat_q8_batch_dev(ctx.h, descs, 3, t, K, ptr(dq), ptr(ds), M, stream_handle()),
+              "q8 batch")
+    for w, raw, N, o in zip(dWs, raws, Ns, outs):
+        got = host(o)
+        assert np.all(np.isnan(got[:, N:])), "wrote past N"
+        single = torch.full((M, N), float("nan"), device="cuda")
+        ctx.check(ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ptr(w), t, N, K, ptr(dq), ptr(ds), M, ptr(single), N,
+                                             stream_handle()), "q8 mm")
+        assert orc.rel_l2(got[:, :N], host(single)) < 1e-6
+        assert orc.rel_l2(got[:, :N], orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL
+    bad = (gl.GemmDesc * 5)()
+    assert ctx.lib.ggq_mul_mat_q8_batch_dev(ctx.h, bad, 5, t, K, ptr(dq), ptr(ds), M,
+                                            stream_handle()) == gl.Status.INVALID_PARAM
+
+
+def test_gemm_split_k_deterministic(ctx, orc):
+    """Long K over few tiles splits K across workgroups; the reduction adds
+    slices in a fixed order, so repeated calls are bitwise identical, and a
+    following call with another split count is still right."""
+    import torch
+    t, M, N, K = 8, 64, 1536, 8960
+    raw = weights(t, N, K, seed=5)
+    A = np.random.default_rng(5).standard_normal((M, K)).astype(np.float32)
+    dA, dq, ds = _quantized(ctx, A)
+    dW = dev(raw)
+    res = []
+    for _ in range(3):
+        dC = torch.full((M, N), float("nan"), device="cuda")
+        ctx.check(ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ptr(dW), t, N, K, ptr(dq), ptr(ds), M, ptr(dC), N,
+                                             stream_handle()), "q8 mm")
+        res.append(host(dC))
+    assert np.array_equal(res[0], res[1]) and np.array_equal(res[0], res[2])
+    assert orc.rel_l2(res[0], orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL
+    # a different shape (different tile count / split) right after
+    M2, N2 = 40, 512
+    A2 = A[:M2].copy()
+    dA2, dq2, ds2 = _quantized(ctx, A2)
+    dC2 = torch.full((M2, N2), float("nan"), device="cuda")
+    ctx.check(ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ptr(dW), t, N2, K, ptr(dq2), ptr(ds2), M2, ptr(dC2), N2,
+                                         stream_handle()), "q8 mm 2")
+    raw2 = raw[: N2 * (K // 32) * 34]
+    assert orc.rel_l2(host(dC2), orc.mul_mat_f64(t, raw2, N2, K, A2, 1)) < TOL
