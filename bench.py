@@ -284,7 +284,8 @@ QWEN3_LAYERS = 28
 
 def bench_config4(torch, ctx, stream, steps=10):
     """28 Qwen3-0.6B layers of IQ4_NL / IQ4_XS / Q5_K matmuls with
-    batch 1, 4 and 8 fp32 activation rows (one launch per matmul)."""
+    batch 1, 4 and 8 fp32 activation rows; one launch per dependency level
+    (q/k/v, o, gate/up, down) through ggq_mul_mat_batch_rows_dev."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(4)
     cycle = [IQ4NL, IQ4XS, Q5K]
@@ -297,10 +298,21 @@ def bench_config4(torch, ctx, stream, steps=10):
            "types": {n: gl.GgmlType(t).name for n, t, _, _, _ in layer}}
     for M in (1, 4, 8):
         mats = [Mat(torch, f"b{M}.{li}.{n}", t, N, K, d, M=M) for li in range(QWEN3_LAYERS) for n, t, N, K, d in weights[li]]
+        levels = []
+        for li in range(QWEN3_LAYERS):
+            q, k, v, o, g, u, dn = mats[7 * li: 7 * li + 7]
+            levels += [[q, k, v], [o], [g, u], [dn]]
+        descs = []
+        for lv in levels:
+            arr = (gl.GemvDesc * len(lv))()
+            for i, m in enumerate(lv):
+                arr[i].W, arr[i].type, arr[i].N, arr[i].K = m.w.data_ptr(), m.t, m.N, m.K
+                arr[i].A, arr[i].C = m.x.data_ptr(), m.y.data_ptr()
+            descs.append((arr, len(lv)))
 
-        def run():
-            for m in mats:
-                launch(ctx, m, 0, stream)
+        def run(M=M, descs=descs):
+            for arr, n in descs:
+                ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, arr, n, M, stream), "batch rows")
 
         sec = time_steps(torch, run, steps, 2)
         b = sum(m.bytes() for m in mats)

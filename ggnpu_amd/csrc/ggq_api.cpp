@@ -417,14 +417,15 @@ int ggq_mul_mat_q8_batch_dev(ggq_ctx* c, const ggq_gemm_desc* d, int n, uint32_t
     GGQ_END(c)
 }
 
-int ggq_mul_mat_batch_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, void* stream) {
+int ggq_mul_mat_batch_rows_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, int M, void* stream) {
     GGQ_GUARD(c)
     if (!d || n < 1 || n > GGQ_MAX_BATCH) return set_status(c, GGQ_INVALID_PARAM, "need 1..%d descriptors", GGQ_MAX_BATCH);
+    if (M < 0 || M > GGQ_MAX_BATCH_ROWS) return set_status(c, GGQ_INVALID_PARAM, "M=%d outside 0..%d", M, GGQ_MAX_BATCH_ROWS);
     ggq::GemvProblem ps[GGQ_MAX_BATCH];
     for (int i = 0; i < n; i++) {
         if (!d[i].W || !d[i].A || !d[i].C) return set_status(c, GGQ_INVALID_PARAM, "null pointer in entry %d", i);
         if (!aligned16(d[i].W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
-        int st = check_matmul_shape(c, d[i].type, d[i].N, d[i].K, 1, (int)d[i].K, (int)d[i].N, GGQ_ACT_F32);
+        int st = check_matmul_shape(c, d[i].type, d[i].N, d[i].K, M, (int)d[i].K, (int)d[i].N, GGQ_ACT_F32);
         if (st != GGQ_OK) return st;
         ps[i] = ggq::GemvProblem{};
         ps[i].type = d[i].type;
@@ -435,11 +436,16 @@ int ggq_mul_mat_batch_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, void* strea
         ps[i].ldx = (int)d[i].K;
         ps[i].Y = d[i].C;
         ps[i].ldy = (int)d[i].N;
-        ps[i].M = 1;
+        ps[i].M = M;
         ps[i].groups = 1;
     }
+    if (M == 0) return set_status(c, GGQ_OK);
     return hip_status(c, ggq::launch_gemv_multi(ps, n, pick_stream(c, stream)), "gemv batch");
     GGQ_END(c)
+}
+
+int ggq_mul_mat_batch_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, void* stream) {
+    return ggq_mul_mat_batch_rows_dev(c, d, n, 1, stream);
 }
 
 int ggq_dequant_dev(ggq_ctx* c, const void* raw, uint32_t type, int64_t n_blocks, float* out, void* stream) {

@@ -349,9 +349,11 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
 }
 
 // One workgroup's share of a GEMV problem: workgroup bx of gx working on
-// group `by` (the expert in grouped mode).
+// group `by` (the expert in grouped mode) and on the MB-row chunks
+// bz, bz + gz, ... of its activation rows.
 template <int T, int MB, int PPT, int U>
-__device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, float (&red)[2][4][U * MB]) {
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
+                                          float (&red)[2][4][U * MB]) {
     typedef typename Piece<T>::Raw Raw;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lpr_log2 = a.lpr_log2;
@@ -369,7 +371,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
     const int step = U * stride;
     int parity = 0;
 
-    for (int mc = 0; mc < mcount; mc += MB) {
+    for (int mc = bz * MB; mc < mcount; mc += gz * MB) {
         Raw ra[U][PPT], rb[U][PPT];
         int it = bx;
         // The first weight fetch is issued before the activations are read.
@@ -383,7 +385,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
 #pragma unroll
             for (int m = 0; m < MB; m++) {
                 const bool ok = p < P && mc + m < mcount;
-                int xrow = m0 + mc + (mc + m < mcount ? m : 0);
+                if (mc + m >= mcount) {  // uniform over the workgroup: no load for absent rows
+#pragma unroll
+                    for (int j = 0; j < 32; j++) xr[i][m][j] = 0.0f;
+                    xs[i][m][0] = xs[i][m][1] = 0.0f;
+                    continue;
+                }
+                int xrow = m0 + mc + m;
                 if (a.x_idx) xrow = a.x_idx[xrow];
                 const float* xp = a.X + (int64_t)xrow * a.ldx;
 #pragma unroll
@@ -442,7 +450,25 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
 template <int T, int MB, int PPT, int U>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     __shared__ float red[2][4][U * MB];
-    gemv_body<T, MB, PPT, U>(a, blockIdx.x, gridDim.x, blockIdx.y, red);
+    if constexpr (MB > 1) {
+        if (a.grp_off) {
+            // Grouped launch: each group (expert) has its own row count, so
+            // the rows per pass follow it instead of the launch maximum.
+            const int cnt = a.grp_off[blockIdx.y + 1] - a.grp_off[blockIdx.y];
+            if (cnt <= 0) return;
+            if (cnt == 1) {
+                gemv_body<T, 1, PPT, U>(a, blockIdx.x, gridDim.x, blockIdx.y, 0, 1,
+                                        *reinterpret_cast<float(*)[2][4][U]>(&red));
+                return;
+            }
+            if (MB > 2 && cnt == 2) {
+                gemv_body<T, 2, PPT, U>(a, blockIdx.x, gridDim.x, blockIdx.y, 0, 1,
+                                        *reinterpret_cast<float(*)[2][4][U * 2]>(&red));
+                return;
+            }
+        }
+    }
+    gemv_body<T, MB, PPT, U>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
 }
 
 // Several independent GEMV problems (any mix of formats, same pieces-per-
@@ -463,13 +489,14 @@ __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     int q = 0;
     while (q + 1 < ma.n && (int)blockIdx.x >= ma.begin[q + 1]) q++;
     const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
+    const int bz = blockIdx.z, gz = gridDim.z;
     switch (ma.type[q]) {
-    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
-    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
-    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
-    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
-    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
-    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U>(ma.p[q], bx, gx, 0, red); break;
+    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
     default: break;
     }
 }
@@ -572,6 +599,23 @@ static int gemv_max_lpr() {
     return v;
 }
 
+static int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e && *e ? atoi(e) : dflt;
+}
+// Grouped (MoE) launches: largest rows per pass, workgroups per group
+// (0 = from the resident capacity) and resident rounds to fill.
+// Largest rows per pass of plain multi-row launches (1, 2 or 4).  One row
+// per pass measured fastest on gfx950 for 4 and 8 rows: MB = 2 / 4 keep
+// 2x / 4x the activations in VGPRs (178 / 250 registers), which halves the
+// resident wavefronts, and the extra weight passes of MB = 1 are served
+// from cache.  These knobs are read at every multi-row / grouped launch
+// (never on the single-row decode path), so a process can switch them.
+static int gemv_mb_cap() { const int v = env_int("GGQ_GEMV_MBCAP", 1); return v < 1 ? 1 : v; }
+static int moe_mb() { return env_int("GGQ_MOE_MB", 1); }
+static int moe_gx() { return env_int("GGQ_MOE_GX", 0); }
+static int moe_rounds() { const int v = env_int("GGQ_MOE_ROUNDS", 4); return v < 1 ? 1 : v; }
+
 struct GemvPlan {
     GemvArgs a;
     int ppt, n_iters, mrows;
@@ -615,21 +659,31 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     }
     const int ppt = g.ppt, mrows = g.mrows;
     // Batch rows per pass (MB) and pieces per thread (PPT) keep the
-    // activation registers at 64*MB*PPT <= 128 floats.  Grouped (MoE)
-    // launches spread 16 workgroups over each expert's rows.
-#define GO(MB_, PPT_, U_)                                                                  \
-    do {                                                                                   \
-        int gx = groups > 1 ? 16 : resident_blocks(gemv_kernel<T, MB_, PPT_, U_>, 0);     \
-        gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                               \
-        gemv_kernel<T, MB_, PPT_, U_><<<dim3(gx, groups), 256, 0, s>>>(a);                 \
+    // activation registers at 32*MB*PPT <= 128 floats.  Plain launches with
+    // more rows than MB run their MB-row chunks in parallel (grid z) and
+    // share the resident capacity among them; grouped (MoE) launches share
+    // it among the groups (experts), each looping over its own chunks, so
+    // each wavefront covers many weight rows per activation load.
+#define GO(MB_, PPT_, U_)                                                                        \
+    do {                                                                                         \
+        const int gz = groups > 1 ? 1 : (mrows + MB_ - 1) / MB_;                                 \
+        int gx = resident_blocks(gemv_kernel<T, MB_, PPT_, U_>, 0) * (groups > 1 ? moe_rounds() : 1) / (gz * groups); \
+        if (groups > 1 && moe_gx() > 0) gx = moe_gx();                                           \
+        gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
+        gemv_kernel<T, MB_, PPT_, U_><<<dim3(gx, groups, gz), 256, 0, s>>>(a);                   \
     } while (0)
     const int u = gemv_rows_per_iter();
-    if (ppt == 1) {
-        if (mrows <= 1) { if (u >= 4) GO(1, 1, 4); else if (u >= 2) GO(1, 1, 2); else GO(1, 1, 1); }
-        else if (mrows == 2) GO(2, 1, 1);
+    if (groups > 1 && ppt == 1 && mrows > 1) {
+        const int mb = moe_mb();
+        if (mb <= 1) GO(1, 1, 1);
+        else if (mb == 2) GO(2, 1, 1);
+        else GO(4, 1, 1);
+    } else if (ppt == 1) {
+        if (mrows <= 1 || gemv_mb_cap() <= 1) { if (u >= 4) GO(1, 1, 4); else if (u >= 2) GO(1, 1, 2); else GO(1, 1, 1); }
+        else if (mrows == 2 || gemv_mb_cap() == 2) GO(2, 1, 1);
         else GO(4, 1, 1);
     } else if (ppt == 2) {
-        if (mrows <= 1) GO(1, 2, 1);
+        if (mrows <= 1 || gemv_mb_cap() <= 1) GO(1, 2, 1);
         else GO(2, 2, 1);
     } else if (ppt <= 4) {
         GO(1, 4, 1);
@@ -640,16 +694,31 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Independent single-row (M = 1) problems in one launch when they share the
-// pieces-per-thread count; otherwise one launch per problem.
+// Rows per pass of a multi-problem launch for M activation rows.
+static int multi_mb(int ppt, int M) {
+    if (M <= 1) return 1;
+    const int mb = ppt == 1 ? (M == 2 ? 2 : 4) : 2;
+    const int cap = gemv_mb_cap();
+    return mb > cap ? cap : mb;
+}
+
+template <int MB, int PPT, int U>
+static int multi_resident() {
+    return resident_blocks(gemv_multi_kernel<MB, PPT, U>, 0);
+}
+
+// Independent problems with the same number of activation rows M in one
+// launch when they share the pieces-per-thread count; otherwise one launch
+// per problem.
 hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     MultiArgs ma;
     int ppt = -1, total_iters = 0;
+    const int M = ps[0].M;
     bool fuse = n <= kMaxMulti;
     GemvPlan plans[kMaxMulti];
     for (int i = 0; fuse && i < n; i++) {
-        if (ps[i].M != 1 || ps[i].grp_off || !supported(ps[i].type)) {
+        if (ps[i].M != M || ps[i].grp_off || !supported(ps[i].type)) {
             fuse = false;
         } else {
             plans[i] = plan_gemv(ps[i]);
@@ -658,8 +727,7 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
             total_iters += plans[i].n_iters;
         }
     }
-    const size_t shmem = 0;
-    if (!fuse) {
+    if (!fuse || M == 0) {
         for (int i = 0; i < n; i++) {
             const hipError_t e = launch_gemv(ps[i], s);
             if (e != hipSuccess) return e;
@@ -667,10 +735,17 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
         return hipSuccess;
     }
     const int u = gemv_rows_per_iter();
-    const int target = ppt == 1 ? (u >= 4 ? resident_blocks(gemv_multi_kernel<1, 1, 4>, shmem)
-                                   : u >= 2 ? resident_blocks(gemv_multi_kernel<1, 1, 2>, shmem)
-                                            : resident_blocks(gemv_multi_kernel<1, 1, 1>, shmem))
-                                : resident_blocks(gemv_multi_kernel<1, 2, 1>, shmem);
+    const int mb = multi_mb(ppt, M);
+    const int gz = (M + mb - 1) / mb;
+    int target;
+    if (ppt == 1) {
+        if (mb == 1) target = u >= 4 ? multi_resident<1, 1, 4>() : u >= 2 ? multi_resident<1, 1, 2>() : multi_resident<1, 1, 1>();
+        else if (mb == 2) target = multi_resident<2, 1, 1>();
+        else target = multi_resident<4, 1, 1>();
+    } else {
+        target = mb == 1 ? multi_resident<1, 2, 1>() : multi_resident<2, 2, 1>();
+    }
+    target = target / gz > 0 ? target / gz : 1;
     int b = 0;
     for (int i = 0; i < n; i++) {
         ma.p[i] = plans[i].a;
@@ -683,12 +758,20 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     }
     ma.begin[n] = b;
     ma.n = n;
+    const dim3 grid(b, 1, gz);
     if (ppt == 1) {
-        if (u >= 4) gemv_multi_kernel<1, 1, 4><<<b, 256, shmem, s>>>(ma);
-        else if (u >= 2) gemv_multi_kernel<1, 1, 2><<<b, 256, shmem, s>>>(ma);
-        else gemv_multi_kernel<1, 1, 1><<<b, 256, shmem, s>>>(ma);
+        if (mb == 1) {
+            if (u >= 4) gemv_multi_kernel<1, 1, 4><<<grid, 256, 0, s>>>(ma);
+            else if (u >= 2) gemv_multi_kernel<1, 1, 2><<<grid, 256, 0, s>>>(ma);
+            else gemv_multi_kernel<1, 1, 1><<<grid, 256, 0, s>>>(ma);
+        } else if (mb == 2) {
+            gemv_multi_kernel<2, 1, 1><<<grid, 256, 0, s>>>(ma);
+        } else {
+            gemv_multi_kernel<4, 1, 1><<<grid, 256, 0, s>>>(ma);
+        }
     } else {
-        gemv_multi_kernel<1, 2, 1><<<b, 256, shmem, s>>>(ma);
+        if (mb == 1) gemv_multi_kernel<1, 2, 1><<<grid, 256, 0, s>>>(ma);
+        else gemv_multi_kernel<2, 2, 1><<<grid, 256, 0, s>>>(ma);
     }
     return hipGetLastError();
 }
@@ -1296,20 +1379,35 @@ hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, fl
 // ====================================================================== MoE
 // Routing (main.cpp:3126-3135): top-k experts by descending logit, then a
 // softmax over the selected logits only: w_j = exp(l_j - l_0) / sum.
-// One wavefront per token; ties break toward the lower expert id.
+// One wavefront per token; lane i holds the logits of experts i, i+64, ...
+// in registers (E <= 1024) with a bitmask of the ones already taken; ties
+// break toward the lower expert id.  Selection j ends in lane j.
+constexpr int kRouteMaxPerLane = 16;
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int E, int topk,
                                                        int32_t* __restrict__ sel, float* __restrict__ wsel) {
     const int t = blockIdx.x, lane = threadIdx.x;
     const float* l = logits + (int64_t)t * E;
-    uint64_t taken[16] = {};  // up to 1024 experts
-    float lsel[64];
+    float v[kRouteMaxPerLane];
+    uint32_t taken = 0;
+#pragma unroll
+    for (int i = 0; i < kRouteMaxPerLane; i++) {
+        const int e = lane + 64 * i;
+        v[i] = e < E ? l[e] : -INFINITY;
+        if (e >= E) taken |= 1u << i;
+    }
+    int my_sel = 0;
+    float my_l = 0.0f;
     for (int j = 0; j < topk; j++) {
         float best = -INFINITY;
         int bi = 0x7FFFFFFF;
-        for (int e = lane; e < E; e += 64) {
-            if ((taken[e >> 6] >> (e & 63)) & 1) continue;
-            const float v = l[e];
-            if (v > best || (v == best && e < bi)) { best = v; bi = e; }
+#pragma unroll
+        for (int i = 0; i < kRouteMaxPerLane; i++) {
+            const int e = lane + 64 * i;
+            const bool free = !((taken >> i) & 1u);
+            if (free && (v[i] > best || (v[i] == best && e < bi))) {
+                best = v[i];
+                bi = e;
+            }
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {
@@ -1317,60 +1415,91 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
             const int oi = __shfl_xor(bi, off, 64);
             if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
         }
-        taken[bi >> 6] |= 1ull << (bi & 63);
-        lsel[j] = best;
-        if (lane == 0) sel[t * topk + j] = bi;
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == j) { my_sel = bi; my_l = best; }
     }
-    if (lane == 0) {
-        float sum = 0.0f;
-        for (int j = 0; j < topk; j++) sum += expf(lsel[j] - lsel[0]);
-        for (int j = 0; j < topk; j++) wsel[t * topk + j] = expf(lsel[j] - lsel[0]) / sum;
+    const float l0 = __shfl(my_l, 0, 64);
+    const float ex = lane < topk ? expf(my_l - l0) : 0.0f;
+    float sum = 0.0f;  // in selection order, as the reference adds them
+    for (int j = 0; j < topk; j++) sum += __shfl(ex, j, 64);
+    if (lane < topk) {
+        sel[t * topk + lane] = my_sel;
+        wsel[t * topk + lane] = ex / sum;
     }
 }
 
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel, float* wsel,
                             hipStream_t s) {
     if (T == 0) return hipSuccess;
+    if (E > 64 * kRouteMaxPerLane || topk > 64) return hipErrorInvalidValue;
     moe_route_kernel<<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
     return hipGetLastError();
 }
 
 // Expert grouping: stable counting sort of the T*topk (token, slot) pairs by
 // expert id.  grp_off[E+1] are the group boundaries, tok_idx[pos] the token of
-// each sorted pair and pos_of[t*topk+j] its position.  One workgroup.
+// each sorted pair and pos_of[t*topk+j] its position.  One workgroup of 1024
+// threads, E <= 1024: counts with LDS atomics, an exclusive scan over experts
+// (wavefront scans + a scan of the 16 wavefront totals), then every pair's
+// rank among earlier pairs of its expert, counted over an LDS copy of `sel`
+// (chunks of kGroupChunk pairs; `base` carries the counts of earlier chunks).
+constexpr int kGroupChunk = 8192;
 __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restrict__ sel, int n, int E,
                                                          int topk, int32_t* __restrict__ grp_off,
                                                          int32_t* __restrict__ tok_idx,
                                                          int32_t* __restrict__ pos_of) {
-    extern __shared__ int32_t cnt[];  // E + 1
-    for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
+    __shared__ __attribute__((aligned(16))) int32_t chunk[kGroupChunk];
+    __shared__ int32_t base[1024];
+    __shared__ int32_t wsum[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    base[tid] = 0;
     __syncthreads();
-    for (int f = threadIdx.x; f < n; f += blockDim.x) atomicAdd(&cnt[sel[f]], 1);
+    for (int f = tid; f < n; f += 1024) atomicAdd(&base[sel[f]], 1);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int e = 0; e < E; e++) {
-            const int c = cnt[e];
-            cnt[e] = run;
-            grp_off[e] = run;
-            run += c;
-        }
-        grp_off[E] = run;
+    // Exclusive scan of the counts: base[e] = first position of expert e.
+    const int c = base[tid];
+    int incl = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
     }
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    for (int f = threadIdx.x; f < n; f += blockDim.x) {
-        const int e = sel[f];
-        int rank = 0;
-        for (int g = 0; g < f; g++) rank += sel[g] == e;
-        const int pos = cnt[e] + rank;
-        tok_idx[pos] = f / topk;
-        pos_of[f] = pos;
+    int before = 0;
+    for (int w = 0; w < wave; w++) before += wsum[w];
+    const int start = before + incl - c;
+    __syncthreads();
+    base[tid] = start;
+    if (tid < E) grp_off[tid] = start;
+    if (tid == 0) grp_off[E] = n;
+    __syncthreads();
+    for (int c0 = 0; c0 < n; c0 += kGroupChunk) {
+        const int len = n - c0 < kGroupChunk ? n - c0 : kGroupChunk;
+        for (int f = tid; f < len; f += 1024) chunk[f] = sel[c0 + f];
+        __syncthreads();
+        for (int f = tid; f < len; f += 1024) {
+            const int e = chunk[f];
+            int rank = 0, g = 0;
+            for (; g + 4 <= f; g += 4) {
+                const int4 v = *(const int4*)&chunk[g];
+                rank += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
+            }
+            for (; g < f; g++) rank += chunk[g] == e;
+            const int pos = base[e] + rank;
+            tok_idx[pos] = (c0 + f) / topk;
+            pos_of[c0 + f] = pos;
+        }
+        __syncthreads();
+        for (int f = tid; f < len; f += 1024) atomicAdd(&base[chunk[f]], 1);
+        __syncthreads();
     }
 }
 
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s) {
-    moe_group_kernel<<<1, 1024, (E + 1) * sizeof(int32_t), s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);
+    if (E > 1024) return hipErrorInvalidValue;
+    moe_group_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);
     return hipGetLastError();
 }
 

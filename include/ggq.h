@@ -170,6 +170,14 @@ typedef struct {
 } ggq_gemv_desc;
 int ggq_mul_mat_batch_dev(ggq_ctx* ctx, const ggq_gemv_desc* descs, int n, void* stream);
 
+/* ggq_mul_mat_batch_dev for M activation rows per entry (A dense [M][K], C
+ * dense [M][N]; every entry has the same M, 0 <= M <= GGQ_MAX_BATCH_ROWS),
+ * e.g. the projections of a few decode sequences batched together.  Same
+ * result as one ggq_mul_mat_dev call per entry with GGQ_ACT_F32.  No
+ * reference counterpart (see ggq_mul_mat_batch_dev). */
+#define GGQ_MAX_BATCH_ROWS 64
+int ggq_mul_mat_batch_rows_dev(ggq_ctx* ctx, const ggq_gemv_desc* descs, int n, int M, void* stream);
+
 /* Bit-exact fp32 dequant of n_blocks consecutive blocks, equal to the
  * reference's dequant_*_block functions (kquant.h:133-202, q8_0.cpp:19-25,
  * iq4_nl.cpp:24-31, iq4_xs.cpp:21-38). */

@@ -347,6 +347,33 @@ def test_batched_decode_gemv_mixed_types(ctx, orc):
     assert ctx.lib.ggq_mul_mat_batch_dev(ctx.h, descs, 9, stream_handle()) == gl.Status.INVALID_PARAM
 
 
+@pytest.mark.parametrize("M", [2, 3, 4, 8, 13])
+def test_batched_rows_gemv(ctx, orc, M):
+    """ggq_mul_mat_batch_rows_dev: M activation rows per entry, entries of
+    mixed types in one launch (K = 1024 / 2048 / 8192: one piece per
+    thread), and a set with two pieces per thread (K = 16384)."""
+    import torch
+    rng = np.random.default_rng(M)
+    for shapes in ([(20, 2048, 1024), (23, 1024, 1024), (13, 1024, 1024)],
+                   [(12, 300, 2048), (14, 70, 8192), (8, 64, 2048)],
+                   [(12, 96, 16384), (8, 40, 16384)]):
+        descs = (gl.GemvDesc * len(shapes))()
+        keep, refs = [], []
+        for i, (t, N, K) in enumerate(shapes):
+            raw = weights(t, N, K, seed=i + N + M)
+            A = rng.standard_normal((M, K)).astype(np.float32)
+            dW, dA = dev(raw), dev(A)
+            dC = torch.full((M, N), float("nan"), device="cuda")
+            keep += [dW, dA, dC]
+            descs[i].W, descs[i].type, descs[i].N, descs[i].K = dW.data_ptr(), t, N, K
+            descs[i].A, descs[i].C = dA.data_ptr(), dC.data_ptr()
+            refs.append((dC, orc.mul_mat_f64(t, raw, N, K, A, 0)))
+        ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, descs, len(shapes), M, stream_handle()), "batch rows")
+        for dC, ref in refs:
+            assert orc.rel_l2(host(dC), ref) < TOL
+    assert ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, descs, 1, 65, stream_handle()) == gl.Status.INVALID_PARAM
+
+
 @pytest.mark.parametrize("t", [8, 12, 20, 23])
 def test_prequantized_q8_entry(ctx, orc, t):
     """ggq_mul_mat_q8_dev on activations from ggq_quantize_act_dev equals the
