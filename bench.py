@@ -209,10 +209,11 @@ def bench_config1(torch, ctx, stream, reps=200):
 
 def bench_prefill(torch, ctx, stream, steps=3):
     """28 layers of Q8_0 matmuls on 512 tokens, per-row int8
-    activations (reference XDNA semantics) on the int8-MFMA GEMM.  Each
-    layer quantizes its four distinct inputs once (q/k/v share one, gate/up
-    share one; o and down have their own), as a forward pass would, and the
-    quantization kernels are inside the timed region."""
+    activations (reference XDNA semantics).  Each layer quantizes its four
+    distinct inputs once (q/k/v share one, gate/up share one; o and down
+    have their own), as a forward pass would, and the quantization kernels
+    are inside the timed region.  int8-MFMA GEMM; weights sharing an input
+    run as one launch (ggq_mul_mat_q8_batch_dev)."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2)
     layer = []
@@ -224,6 +225,9 @@ def bench_prefill(torch, ctx, stream, steps=3):
     xin = {lv: torch.randn((T, K), device="cuda") for lv, K in (("qkv", 1536), ("o", 1536), ("gu", 1536), ("down", 8960))}
     qin = {lv: (torch.empty((T, x.shape[1]), dtype=torch.int8, device="cuda"), torch.empty((T,), device="cuda"))
            for lv, x in xin.items()}
+    qmode = int(gl.ActMode.Q8_ROW)
+    mm_single = ctx.lib.ggq_mul_mat_q8_dev
+    mm_multi = ctx.lib.ggq_mul_mat_q8_batch_dev
     level_of = {"q": "qkv", "k": "qkv", "v": "qkv", "o": "o", "gate": "gu", "up": "gu", "down": "down"}
     mats = []
     for li in range(QWEN_LAYERS):
@@ -234,25 +238,24 @@ def bench_prefill(torch, ctx, stream, steps=3):
     def quant(lv):
         x = xin[lv]
         q, sc = qin[lv]
-        st = ctx.lib.ggq_quantize_act_dev(ctx.h, ctypes.c_void_p(x.data_ptr()), x.shape[1], T, x.shape[1], 1,
+        st = ctx.lib.ggq_quantize_act_dev(ctx.h, ctypes.c_void_p(x.data_ptr()), x.shape[1], T, x.shape[1], qmode,
                                           ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), stream)
         ctx.check(st, "quantize_act")
 
     def mm(m):
         q, sc = qin[level_of[m.name.split(".")[1]]]
-        st = ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ctypes.c_void_p(m.w.data_ptr()), m.t, m.N, m.K,
-                                        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), T,
-                                        ctypes.c_void_p(m.y.data_ptr()), m.N, stream)
-        ctx.check(st, "mul_mat_q8_dev")
+        st = mm_single(ctx.h, ctypes.c_void_p(m.w.data_ptr()), m.t, m.N, m.K,
+                       ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), T,
+                       ctypes.c_void_p(m.y.data_ptr()), m.N, stream)
+        ctx.check(st, "mul_mat_q8(h)_dev")
 
     def mm_batch(ms):
         """Weights sharing one quantized input: one multi-weight launch."""
         q, sc = qin[level_of[ms[0].name.split(".")[1]]]
         descs = (gl.GemmDesc * len(ms))(*[gl.GemmDesc(m.w.data_ptr(), m.N, m.y.data_ptr(), m.N) for m in ms])
-        st = ctx.lib.ggq_mul_mat_q8_batch_dev(ctx.h, descs, len(ms), ms[0].t, ms[0].K,
-                                              ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), T,
-                                              stream)
-        ctx.check(st, "mul_mat_q8_batch_dev")
+        st = mm_multi(ctx.h, descs, len(ms), ms[0].t, ms[0].K,
+                      ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), T, stream)
+        ctx.check(st, "mul_mat_q8(h)_batch_dev")
 
     def run():
         for li in range(QWEN_LAYERS):

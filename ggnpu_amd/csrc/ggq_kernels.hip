@@ -1260,22 +1260,15 @@ static const void* gemm_kernel_for(uint32_t type) {
     }
 }
 
-// Split count for T tiles of S K-steps on R resident workgroups: minimises
-// rounds x steps per slice + the reduction launch (about 1.5 K-steps plus
-// a quarter step per slice read).
+// Split count for T tiles of S K-steps on R resident workgroups: split K
+// only to fill the chip (T * splits <= R) and keep at least two K-steps per
+// slice.  Once the tiles alone fill a round, the reduction's extra traffic
+// (splits x the output in fp32, written and read back) costs more than the
+// rounds it would even out.
 static int choose_splits(int64_t tiles, int nsteps, int resident) {
-    int best = 1;
-    double best_cost = 1e300;
-    for (int s = 1; s <= 8; s *= 2) {
-        if (s > 1 && nsteps / s < 2) break;
-        const int64_t rounds = (tiles * s + resident - 1) / resident;
-        const double cost = (double)rounds * ((nsteps + s - 1) / s) + (s > 1 ? 1.5 + 0.25 * s : 0.0);
-        if (cost < best_cost - 1e-9) {
-            best_cost = cost;
-            best = s;
-        }
-    }
-    return best;
+    int s = 1;
+    while (s < 8 && tiles * (s * 2) <= resident && nsteps / (s * 2) >= 2) s *= 2;
+    return s;
 }
 
 GemmPlan plan_gemm_i8(uint32_t type, const int* Ns, int n, int K, int M) {

@@ -461,3 +461,4 @@ def test_gemm_split_k_deterministic(ctx, orc):
                                          stream_handle()), "q8 mm 2")
     raw2 = raw[: N2 * (K // 32) * 34]
     assert orc.rel_l2(host(dC2), orc.mul_mat_f64(t, raw2, N2, K, A2, 1)) < TOL
+
