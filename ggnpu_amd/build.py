@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libggq_hip.so")
-SOURCES = ["ggq_kernels.hip", "ggq_api.cpp", "ggq_encode.cpp"]
+SOURCES = ["ggq_kernels.hip", "ggq_api.cpp", "ggq_encode.cpp", "ggq_gguf.cpp"]
 CXX = os.environ.get("CXX", "g++")
 # Host-only sources go through the host compiler against the HIP runtime API.
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",

@@ -122,6 +122,41 @@ SIGNATURES = {
     "ggq_row_bytes": (_I64, [_U32, _I64]),
 }
 
+
+class GgufTensor(ctypes.Structure):
+    """ggq_gguf_tensor (include/ggq_gguf.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_uint32), ("n_dims", ctypes.c_int32),
+                ("dims", ctypes.c_int64 * 4), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64),
+                ("data", ctypes.c_void_p)]
+
+
+_U64, _PC = ctypes.c_uint64, ctypes.c_char_p
+# Every function declared in include/ggq_gguf.h.
+SIGNATURES.update({
+    "ggq_gguf_open": (_I, [_PC, ctypes.POINTER(_P)]),
+    "ggq_gguf_close": (None, [_P]),
+    "ggq_gguf_last_error": (_PC, []),
+    "ggq_gguf_version": (ctypes.c_uint32, [_P]),
+    "ggq_gguf_alignment": (_U64, [_P]),
+    "ggq_gguf_data_offset": (_U64, [_P]),
+    "ggq_gguf_file_size": (_U64, [_P]),
+    "ggq_gguf_n_tensors": (_I64, [_P]),
+    "ggq_gguf_tensor_at": (_I, [_P, _I64, ctypes.POINTER(GgufTensor)]),
+    "ggq_gguf_find_tensor": (_I64, [_P, _PC]),
+    "ggq_gguf_n_kv": (_I64, [_P]),
+    "ggq_gguf_kv_key": (_PC, [_P, _I64]),
+    "ggq_gguf_find_kv": (_I64, [_P, _PC]),
+    "ggq_gguf_kv_type": (ctypes.c_uint32, [_P, _I64]),
+    "ggq_gguf_kv_int": (_I, [_P, _I64, ctypes.POINTER(_I64)]),
+    "ggq_gguf_kv_uint": (_I, [_P, _I64, ctypes.POINTER(_U64)]),
+    "ggq_gguf_kv_float": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_double)]),
+    "ggq_gguf_kv_str": (_I, [_P, _I64, ctypes.POINTER(_P), ctypes.POINTER(_U64)]),
+    "ggq_gguf_kv_array": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(_U64),
+                               ctypes.POINTER(_P)]),
+    "ggq_gguf_kv_array_str": (_I, [_P, _I64, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64)]),
+    "ggq_gguf_upload": (_I, [_P, _P, _PC, ctypes.POINTER(_P)]),
+})
+
 _lib = None
 
 
@@ -183,3 +218,85 @@ class Context:
 
     def sync(self):
         self.check(self.lib.ggq_sync(self.h), "sync")
+
+
+class GgufFile:
+    """A GGUF v3 file opened through ggq_gguf_open (read in place from the
+    mapping; no GPU needed).  `tensors` maps name -> dict(type, dims, offset,
+    nbytes, data pointer); `kv(key)` returns a metadata value as Python data
+    (ints, floats, str/bytes, lists for arrays)."""
+
+    _NUMERIC = {0: "<u1", 1: "<i1", 2: "<u2", 3: "<i2", 4: "<u4", 5: "<i4", 6: "<f4", 7: "<u1",
+                10: "<u8", 11: "<i8", 12: "<f8"}
+
+    def __init__(self, path):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        st = self.lib.ggq_gguf_open(os.fsencode(path), ctypes.byref(h))
+        if st != Status.OK:
+            raise GgqError(Status(st), self.lib.ggq_gguf_last_error().decode())
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.ggq_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def tensors(self):
+        out = {}
+        for i in range(self.lib.ggq_gguf_n_tensors(self.h)):
+            t = GgufTensor()
+            if self.lib.ggq_gguf_tensor_at(self.h, i, ctypes.byref(t)) != Status.OK:
+                raise GgqError(Status.ERROR, f"tensor {i}")
+            out[t.name.decode()] = {"type": t.type, "dims": list(t.dims[: t.n_dims]), "offset": t.offset,
+                                    "nbytes": t.nbytes, "data": t.data, "index": i}
+        return out
+
+    def tensor_bytes(self, name):
+        t = self.tensors[name]
+        return ctypes.string_at(t["data"], t["nbytes"])
+
+    def keys(self):
+        return [self.lib.ggq_gguf_kv_key(self.h, i).decode() for i in range(self.lib.ggq_gguf_n_kv(self.h))]
+
+    def kv(self, key):
+        import numpy as np
+        i = self.lib.ggq_gguf_find_kv(self.h, key.encode())
+        if i < 0:
+            raise KeyError(key)
+        t = self.lib.ggq_gguf_kv_type(self.h, i)
+        if t == 8:
+            p, n = ctypes.c_void_p(), ctypes.c_uint64()
+            self.lib.ggq_gguf_kv_str(self.h, i, ctypes.byref(p), ctypes.byref(n))
+            return ctypes.string_at(p, n.value).decode("utf-8", "replace")
+        if t in (6, 12):
+            v = ctypes.c_double()
+            self.lib.ggq_gguf_kv_float(self.h, i, ctypes.byref(v))
+            return v.value
+        if t == 9:
+            et, n, p = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_void_p()
+            self.lib.ggq_gguf_kv_array(self.h, i, ctypes.byref(et), ctypes.byref(n), ctypes.byref(p))
+            if et.value == 8:
+                out = []
+                for j in range(n.value):
+                    sp, sn = ctypes.c_void_p(), ctypes.c_uint64()
+                    self.lib.ggq_gguf_kv_array_str(self.h, i, j, ctypes.byref(sp), ctypes.byref(sn))
+                    out.append(ctypes.string_at(sp, sn.value).decode("utf-8", "replace"))
+                return out
+            dt = np.dtype(self._NUMERIC[et.value])
+            return np.frombuffer(ctypes.string_at(p, n.value * dt.itemsize), dt).tolist()
+        if t == 10:
+            v = ctypes.c_uint64()
+            self.lib.ggq_gguf_kv_uint(self.h, i, ctypes.byref(v))
+            return v.value
+        v = ctypes.c_int64()
+        if self.lib.ggq_gguf_kv_int(self.h, i, ctypes.byref(v)) != Status.OK:
+            raise GgqError(Status.INVALID_PARAM, f"{key}: type {t}")
+        return bool(v.value) if t == 7 else v.value

@@ -1,5 +1,5 @@
 """C ABI checks that need no GPU: the library loads, exports exactly what
-include/ggq.h declares, rejects bad arguments, and the synthetic-data
+include/ggq.h and include/ggq_gguf.h declare, rejects bad arguments, and the synthetic-data
 encoder produces valid blocks."""
 import os
 import re
@@ -13,9 +13,12 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def header_functions():
-    txt = open(os.path.join(ROOT, "include", "ggq.h")).read()
-    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-    return set(re.findall(r"\b(ggq_[a-z0-9_]+)\s*\(", txt))
+    names = set()
+    for h in ("ggq.h", "ggq_gguf.h"):
+        txt = open(os.path.join(ROOT, "include", h)).read()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        names |= set(re.findall(r"\b(ggq_[a-z0-9_]+)\s*\(", txt))
+    return names
 
 
 def test_library_exports_every_declared_symbol():
