@@ -221,6 +221,27 @@ def bench_config1(torch, ctx, stream, reps=200):
             "GBps": b / kmean / 1e9, "frac_hbm_peak": b / kmean / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_logits(torch, ctx, stream, reps=50):
+    """Output projection of configs[1] (128256x2048 Q4_K, batch 1) alone and
+    with the device-side greedy token choice (ggq_logits_argmax_dev, logits
+    not kept): GPU time per call from events around back-to-back calls."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    name, t, N, K = LLAMA_OUTPUT
+    w, _ = make_weight(torch, gen, t, N, K)
+    m = Mat(torch, name, t, N, K, w)
+    tok = torch.empty((1,), dtype=torch.int32, device="cuda")
+
+    def argmax():
+        ctx.check(ctx.lib.ggq_logits_argmax_dev(ctx.h, ctypes.c_void_p(w.data_ptr()), t, N, K,
+                                                ctypes.c_void_p(m.x.data_ptr()), 1, 0, None,
+                                                ctypes.c_void_p(tok.data_ptr()), None, stream), "argmax")
+
+    plain, fused = back_to_back_times(torch, [lambda: launch(ctx, m, 0, stream), argmax], reps)
+    return {"workload": "128256x2048 Q4_K projection, batch 1", "gemv_us": round(plain * 1e6, 2),
+            "gemv_argmax_us": round(fused * 1e6, 2), "GBps_with_argmax": round(m.bytes() / fused / 1e9, 1)}
+
+
 def bench_prefill(torch, ctx, stream, steps=3):
     """28 layers of Q8_0 matmuls on 512 tokens, per-row int8
     activations (reference XDNA semantics).  Each layer quantizes its four
@@ -404,7 +425,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
-    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "copy"],
+                    default=None,
                     help="run one workload only and print its result (profiling aid)")
     ap.add_argument("--per-matmul", action="store_true",
                     help="one launch per matmul instead of one per dependency level")
@@ -435,9 +457,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_per_copy": src.numel(), "copies": 4}), flush=True)
         return
-    if args.only in ("config1", "prefill", "config4", "moe"):
+    if args.only in ("config1", "prefill", "config4", "moe", "logits"):
         res = {"config1": bench_config1, "prefill": bench_prefill, "config4": bench_config4,
-               "moe": bench_config5}[args.only](torch, ctx, stream)
+               "moe": bench_config5, "logits": bench_logits}[args.only](torch, ctx, stream)
         print(json.dumps({"only": args.only, **res}), flush=True)
         ctx.close()
         return
@@ -483,7 +505,7 @@ def main():
     if not args.no_extra:
         out["extra"] = {"config1": bench_config1(torch, ctx, stream)}
         for key, fn in (("config3_prefill", bench_prefill), ("config4_iq4_q5k", bench_config4),
-                        ("config5_moe", bench_config5)):
+                        ("config5_moe", bench_config5), ("logits_argmax", bench_logits)):
             try:
                 out["extra"][key] = fn(torch, ctx, stream)
             except Exception as e:  # reported, never silently replaced

@@ -49,6 +49,7 @@ struct ggq_ctx {
     Buffer ws;  // kernel workspace (activation quant, MoE intermediates)
     Buffer io;  // staging of host A / C for the synchronous entry points
     Buffer part;  // GEMM split-K partial tiles
+    Buffer logits;  // vocab projection output when the caller does not keep it
 };
 
 namespace {
@@ -283,6 +284,7 @@ void ggq_destroy(ggq_ctx* c) {
     if (c->ws.ptr) hipFree(c->ws.ptr);
     if (c->io.ptr) hipFree(c->io.ptr);
     if (c->part.ptr) hipFree(c->part.ptr);
+    if (c->logits.ptr) hipFree(c->logits.ptr);
     hipStreamDestroy(c->stream);
     delete c;
 }
@@ -369,6 +371,28 @@ int ggq_mul_mat_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t
     int st = check_matmul_shape(c, type, N, K, M, lda, ldc, act_mode);
     if (st != GGQ_OK) return st;
     return mul_mat_queue(c, W, type, N, K, A, lda, C, ldc, M, act_mode, pick_stream(c, stream));
+    GGQ_END(c)
+}
+
+int ggq_logits_argmax_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const float* A, int M,
+                          int act_mode, float* logits, int32_t* token, float* value, void* stream) {
+    GGQ_GUARD(c)
+    if (!W || !A || !token) return set_status(c, GGQ_INVALID_PARAM, "null W/A/token");
+    if (!aligned16(W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
+    int st = check_matmul_shape(c, type, N, K, M, (int)K, (int)N, act_mode);
+    if (st != GGQ_OK) return st;
+    if (M == 0) return set_status(c, GGQ_OK);
+    // c->logits holds the argmax partials, then the logits if the caller
+    // does not keep them.
+    const size_t part_bytes = align256(ggq::argmax_workspace_bytes(M));
+    const size_t need = part_bytes + (logits ? 0 : sizeof(float) * (size_t)M * (size_t)N);
+    hipError_t e = ensure(c->logits, need);
+    if (e != hipSuccess) return hip_status(c, e, "logits workspace");
+    float* L = logits ? logits : (float*)((char*)c->logits.ptr + part_bytes);
+    const hipStream_t s = pick_stream(c, stream);
+    st = mul_mat_queue(c, W, type, N, K, A, (int)K, L, (int)N, M, act_mode, s);
+    if (st != GGQ_OK) return st;
+    return hip_status(c, ggq::launch_argmax_rows(L, M, (int)N, (int)N, token, value, c->logits.ptr, s), "argmax");
     GGQ_END(c)
 }
 

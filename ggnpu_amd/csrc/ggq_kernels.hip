@@ -1369,6 +1369,89 @@ hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, fl
     return hipGetLastError();
 }
 
+// ================================================================== argmax
+// Greedy token choice of sample_token (main.cpp:827-838): the first index
+// with the strictly largest value; NaN never wins, and a row with nothing
+// above -inf gives index 0.  (value, index) pairs merge with ties going to
+// the lower index, so the result does not depend on how the row is split.
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+// Stage 1: workgroup (p, m) reduces chunk p of row m (chunks of `chunk`
+// values, a multiple of 4; float4 loads when rows are 16-byte aligned) to
+// one (value, index) pair.  Each thread walks its elements in increasing
+// index order, so a strict > keeps the first of equal values.
+constexpr int kArgmaxParts = 64;
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float* __restrict__ L, int N, int ld, int chunk,
+                                                          int vec4, float* __restrict__ pv, int* __restrict__ pi) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int m = blockIdx.y, p = blockIdx.x;
+    const float* row = L + (int64_t)m * ld;
+    const int n0 = p * chunk, n1 = n0 + chunk < N ? n0 + chunk : N;
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    if (vec4) {
+        for (int n = n0 + 4 * threadIdx.x; n < n1; n += 1024) {
+            const float4 v = *(const float4*)(row + n);  // n1 - n >= 4: N and chunk are multiples of 4
+            if (v.x > bv) { bv = v.x; bi = n; }
+            if (v.y > bv) { bv = v.y; bi = n + 1; }
+            if (v.z > bv) { bv = v.z; bi = n + 2; }
+            if (v.w > bv) { bv = v.w; bi = n + 3; }
+        }
+    } else {
+        for (int n = n0 + threadIdx.x; n < n1; n += 256) {
+            const float v = row[n];
+            if (v > bv) { bv = v; bi = n; }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) argmax_merge(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) argmax_merge(bv, bi, sv[w], si[w]);
+        pv[m * kArgmaxParts + p] = bv;
+        pi[m * kArgmaxParts + p] = bi;
+    }
+}
+
+// Stage 2: one wavefront per row merges the chunk results.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ L, int ld, int parts,
+                                                          const float* __restrict__ pv, const int* __restrict__ pi,
+                                                          int32_t* __restrict__ idx, float* __restrict__ val) {
+    const int m = blockIdx.x, lane = threadIdx.x;
+    float bv = lane < parts ? pv[m * kArgmaxParts + lane] : -INFINITY;
+    int bi = lane < parts ? pi[m * kArgmaxParts + lane] : 0x7FFFFFFF;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) argmax_merge(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+    if (lane == 0) {
+        const int i = bi == 0x7FFFFFFF ? 0 : bi;
+        idx[m] = i;
+        if (val) val[m] = L[(int64_t)m * ld + i];  // the chosen token's logit (NaN / -inf when nothing won)
+    }
+}
+
+size_t argmax_workspace_bytes(int M) { return (size_t)M * kArgmaxParts * (sizeof(float) + sizeof(int)); }
+
+hipError_t launch_argmax_rows(const float* L, int M, int N, int ld, int32_t* idx, float* val, void* ws,
+                              hipStream_t s) {
+    if (M == 0) return hipSuccess;
+    int parts = (N + 2047) / 2048;
+    parts = parts < 1 ? 1 : (parts > kArgmaxParts ? kArgmaxParts : parts);
+    int chunk = (N + parts - 1) / parts;
+    chunk = (chunk + 3) & ~3;
+    parts = (N + chunk - 1) / chunk;
+    const int vec4 = ((uintptr_t)L % 16 == 0) && ld % 4 == 0 && N % 4 == 0;
+    float* pv = (float*)ws;
+    int* pi = (int*)((char*)ws + (size_t)M * kArgmaxParts * sizeof(float));
+    argmax_part_kernel<<<dim3(parts, M), 256, 0, s>>>(L, N, ld, chunk, vec4, pv, pi);
+    argmax_final_kernel<<<M, 64, 0, s>>>(L, ld, parts, pv, pi, idx, val);
+    return hipGetLastError();
+}
+
 // ====================================================================== MoE
 // Routing (main.cpp:3126-3135): top-k experts by descending logit, then a
 // softmax over the selected logits only: w_j = exp(l_j - l_0) / sum.

@@ -63,6 +63,12 @@ hipError_t launch_gemm_i8_multi(uint32_t type, const GemmDesc* d, int n, int K, 
                                 int M, float* part, hipStream_t s);
 hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa, const float* sa, int M,
                           float* C, int ldc, float* part, hipStream_t s);
+// idx[m] = first index of the largest value of row m of L ([M][ld], N
+// values); val[m] = that value (val may be null).  `ws`: device workspace
+// of argmax_workspace_bytes(M) bytes.
+size_t argmax_workspace_bytes(int M);
+hipError_t launch_argmax_rows(const float* L, int M, int N, int ld, int32_t* idx, float* val, void* ws,
+                              hipStream_t s);
 // x[m][k] = q[m][k] * sa[m] (dense fp32 [M][K]).
 hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, float* x, hipStream_t s);
 

@@ -128,6 +128,17 @@ int ggq_mul_mat(ggq_ctx* ctx, const ggq_weight* w, const float* A, int lda, floa
 int ggq_mul_mat_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
                     const float* A, int lda, float* C, int ldc, int M, int act_mode, void* stream);
 
+/* Vocab projection with the greedy token choice on the device: logits =
+ * A . W^T as ggq_mul_mat_dev (A dense [M][K], act_mode as there), then
+ * token[m] = the first index of the largest logit of row m and value[m]
+ * that logit, as sample_token with temperature 0 (src/cli/main.cpp:827-838:
+ * strict >, so ties go to the lower index and NaN never wins; a row with
+ * nothing above -inf gives 0).  Replaces compute_logits + sample_token
+ * (main.cpp:270-327, 827-838) without reading the logits back.  `logits`
+ * ([M][N]) and `value` ([M]) may be null; token ([M] int32) may not. */
+int ggq_logits_argmax_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K, const float* A,
+                          int M, int act_mode, float* logits, int32_t* token, float* value, void* stream);
+
 /* C = sa[m] * sum_k qa[m][k] * w[n][k]: the GGQ_ACT_Q8_ROW matmul on
  * activations already quantized by ggq_quantize_act_dev (row mode; qa dense
  * [M][K], 16-byte aligned, sa [M]).  Lets callers quantize an input once

@@ -462,3 +462,73 @@ def test_gemm_split_k_deterministic(ctx, orc):
     raw2 = raw[: N2 * (K // 32) * 34]
     assert orc.rel_l2(host(dC2), orc.mul_mat_f64(t, raw2, N2, K, A2, 1)) < TOL
 
+
+
+# ------------------------------------------------------- logits + argmax
+def _ref_greedy(row):
+    """sample_token with temperature 0 (main.cpp:827-838)."""
+    best, best_val = 0, -np.inf
+    for i, v in enumerate(row):
+        if v > best_val:
+            best_val, best = v, i
+    return best
+
+
+@pytest.mark.parametrize("t,act", [(12, 0), (14, 0), (8, 1), (20, 0)])
+def test_logits_argmax(ctx, orc, t, act):
+    import torch
+    N, K, M = 32000, 1024, 3
+    rng = np.random.default_rng(t)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    A[1] = A[0] * -1.0
+    # rows 5 and 9: the same bytes, aligned with token 0's activations, so
+    # they tie for the largest logit of row 0 (bitwise equal products)
+    w[9] = w[5] = (0.05 * np.sign(A[0])).astype(np.float32)
+    raw = gl.encode(t, w)
+    dW, dA = dev(raw), dev(A)
+    L = torch.full((M, N), float("nan"), device="cuda")
+    tok = torch.full((M,), -7, dtype=torch.int32, device="cuda")
+    val = torch.zeros((M,), device="cuda")
+    ctx.check(ctx.lib.ggq_logits_argmax_dev(ctx.h, ptr(dW), t, N, K, ptr(dA), M, act, ptr(L), ptr(tok), ptr(val),
+                                            stream_handle()), "logits")
+    got, toks, vals = host(L), host(tok), host(val)
+    ref = orc.mul_mat_f64(t, raw, N, K, A, act)
+    assert orc.rel_l2(got, ref) < TOL
+    for m in range(M):
+        assert toks[m] == _ref_greedy(got[m]), m
+        assert vals[m] == got[m, toks[m]]
+        top2 = np.sort(ref[m])[-2:]
+        if top2[1] - top2[0] > 1e-3 * abs(top2[1]):
+            assert toks[m] == int(np.argmax(ref[m])), m
+    assert toks[0] == 5  # rows 5 and 9 tie exactly; the lower index wins
+    # without the logits / value outputs, same tokens
+    tok2 = torch.full((M,), -7, dtype=torch.int32, device="cuda")
+    ctx.check(ctx.lib.ggq_logits_argmax_dev(ctx.h, ptr(dW), t, N, K, ptr(dA), M, act, None, ptr(tok2), None,
+                                            stream_handle()), "logits 2")
+    assert np.array_equal(host(tok2), toks)
+
+
+def test_logits_argmax_nan_row_and_errors(ctx):
+    """N not a multiple of 4 (scalar loads in the argmax), a NaN row, errors."""
+    import torch
+    t, N, K = 12, 3001, 256
+    raw = weights(t, N, K, seed=2)
+    A = np.ones((2, K), np.float32)
+    A[1, 7] = np.nan
+    dW, dA = dev(raw), dev(A)
+    tok = torch.full((2,), -7, dtype=torch.int32, device="cuda")
+    val = torch.zeros((2,), device="cuda")
+    ctx.check(ctx.lib.ggq_logits_argmax_dev(ctx.h, ptr(dW), t, N, K, ptr(dA), 2, 0, None, ptr(tok), ptr(val),
+                                            stream_handle()), "nan")
+    toks, vals = host(tok), host(val)
+    assert toks[1] == 0 and np.isnan(vals[1])  # every logit NaN: nothing beats -inf; value = logit 0
+    assert 0 <= toks[0] < N and np.isfinite(vals[0])
+    L = torch.full((2, N), float("nan"), device="cuda")
+    ctx.check(ctx.lib.ggq_logits_argmax_dev(ctx.h, ptr(dW), t, N, K, ptr(dA), 2, 0, ptr(L), ptr(tok), None,
+                                            stream_handle()), "with logits")
+    assert host(tok)[0] == _ref_greedy(host(L)[0])
+    assert ctx.lib.ggq_logits_argmax_dev(ctx.h, ptr(dW), t, N, K, ptr(dA), 2, 0, None, None, None,
+                                         stream_handle()) == gl.Status.INVALID_PARAM
+    assert ctx.lib.ggq_logits_argmax_dev(ctx.h, ptr(dW), t, N, K, ptr(dA), 0, 0, None, ptr(tok), None,
+                                         stream_handle()) == gl.Status.OK
