@@ -221,6 +221,66 @@ def bench_config1(torch, ctx, stream, reps=200):
             "GBps": b / kmean / 1e9, "frac_hbm_peak": b / kmean / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_decode_fused(torch, ctx, stream, steps=30):
+    """configs[1]'s matmuls with their neighbours fused in (ggq_mul_mat_fused_dev):
+    per layer RMSNorm + q/k/v (one launch), o + residual add, RMSNorm +
+    gate (silu epilogue) / up (one launch), down reading silu(gate) * up +
+    residual add; then
+    RMSNorm + output projection.  65 launches, as the matmul-only step.  Attention is out of
+    scope: o reads a synthetic attention output."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+    H, F = 2048, 8192
+    x = torch.randn((1, H), device="cuda", generator=gen)
+    attn = torch.randn((1, H), device="cuda", generator=gen)
+    gbuf = torch.empty((1, F), device="cuda")
+    ubuf = torch.empty((1, F), device="cuda")
+    nw = 1.0 + 0.1 * torch.randn((H,), device="cuda", generator=gen)
+    q, k, v = (torch.empty((1, n), device="cuda") for n in (2048, 512, 512))
+    logits = torch.empty((1, LLAMA_OUTPUT[2]), device="cuda")
+    layers, total = [], 0
+    for _ in range(LLAMA_LAYERS):
+        ws = {}
+        for name, t, N, K in LLAMA_LAYER:
+            ws[name], raw = make_weight(torch, gen, t, N, K)
+            total += raw.size
+        layers.append(ws)
+    wout, raw = make_weight(torch, gen, Q4K, LLAMA_OUTPUT[2], H)
+    total += raw.size
+
+    def desc(w, t, N, K, A, C, **kw):
+        d = gl.GemvFusedDesc()
+        d.W, d.type, d.N, d.K, d.A, d.C = w.data_ptr(), t, N, K, A.data_ptr(), C.data_ptr()
+        if "up" in kw:
+            d.A_up = kw["up"].data_ptr()
+        d.silu = int(bool(kw.get("silu")))
+        if kw.get("rms"):
+            d.rms_norm, d.rms_eps, d.rms_w = 1, 1e-5, nw.data_ptr()
+        if kw.get("res") is not None:
+            d.residual = kw["res"].data_ptr()
+        return d
+
+    plan = []
+    for ws in layers:
+        plan.append([desc(ws["q"], Q4K, 2048, H, x, q, rms=True), desc(ws["k"], Q4K, 512, H, x, k, rms=True),
+                     desc(ws["v"], Q6K, 512, H, x, v, rms=True)])
+        plan.append([desc(ws["o"], Q4K, H, H, attn, x, res=x)])
+        plan.append([desc(ws["gate"], Q4K, F, H, x, gbuf, rms=True, silu=True),
+                     desc(ws["up"], Q4K, F, H, x, ubuf, rms=True)])
+        plan.append([desc(ws["down"], Q6K, H, F, gbuf, x, up=ubuf, res=x)])
+    plan.append([desc(wout, Q4K, LLAMA_OUTPUT[2], H, x, logits, rms=True)])
+    arrays = [((gl.GemvFusedDesc * len(lv))(*lv), len(lv)) for lv in plan]
+
+    def run():
+        for arr, n in arrays:
+            ctx.check(ctx.lib.ggq_mul_mat_fused_dev(ctx.h, arr, n, 1, stream), "fused")
+
+    sec, gsec = time_steps(torch, run, steps, 3, gpu_time=True)
+    return {"workload": "Llama-3.2-1B decode matmuls with RMSNorm / SwiGLU / residual fused in (65 launches)",
+            "weight_bytes": total, "ms_per_step": round(sec * 1e3, 4), "gpu_ms_per_step": round(gsec * 1e3, 4),
+            "GBps": round(total / gsec / 1e9, 1)}
+
+
 def bench_logits(torch, ctx, stream, reps=50):
     """Output projection of configs[1] (128256x2048 Q4_K, batch 1) alone and
     with the device-side greedy token choice (ggq_logits_argmax_dev, logits
@@ -425,7 +485,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
-    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "copy"],
+    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "fused", "copy"],
                     default=None,
                     help="run one workload only and print its result (profiling aid)")
     ap.add_argument("--per-matmul", action="store_true",
@@ -457,9 +517,10 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_per_copy": src.numel(), "copies": 4}), flush=True)
         return
-    if args.only in ("config1", "prefill", "config4", "moe", "logits"):
+    if args.only in ("config1", "prefill", "config4", "moe", "logits", "fused"):
         res = {"config1": bench_config1, "prefill": bench_prefill, "config4": bench_config4,
-               "moe": bench_config5, "logits": bench_logits}[args.only](torch, ctx, stream)
+               "moe": bench_config5, "logits": bench_logits, "fused": bench_decode_fused}[args.only](
+                   torch, ctx, stream)
         print(json.dumps({"only": args.only, **res}), flush=True)
         ctx.close()
         return
@@ -505,7 +566,8 @@ def main():
     if not args.no_extra:
         out["extra"] = {"config1": bench_config1(torch, ctx, stream)}
         for key, fn in (("config3_prefill", bench_prefill), ("config4_iq4_q5k", bench_config4),
-                        ("config5_moe", bench_config5), ("logits_argmax", bench_logits)):
+                        ("config5_moe", bench_config5), ("logits_argmax", bench_logits),
+                        ("decode_fused", bench_decode_fused)):
             try:
                 out["extra"][key] = fn(torch, ctx, stream)
             except Exception as e:  # reported, never silently replaced

@@ -468,6 +468,47 @@ int ggq_mul_mat_batch_rows_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, int M,
     GGQ_END(c)
 }
 
+int ggq_mul_mat_fused_dev(ggq_ctx* c, const ggq_gemv_fused_desc* d, int n, int M, void* stream) {
+    GGQ_GUARD(c)
+    if (!d || n < 1 || n > GGQ_MAX_BATCH) return set_status(c, GGQ_INVALID_PARAM, "need 1..%d descriptors", GGQ_MAX_BATCH);
+    if (M < 0 || M > GGQ_MAX_BATCH_ROWS) return set_status(c, GGQ_INVALID_PARAM, "M=%d outside 0..%d", M, GGQ_MAX_BATCH_ROWS);
+    ggq::GemvProblem ps[GGQ_MAX_BATCH];
+    for (int i = 0; i < n; i++) {
+        const ggq_gemv_fused_desc& e = d[i];
+        if (!e.W || !e.A || !e.C) return set_status(c, GGQ_INVALID_PARAM, "null pointer in entry %d", i);
+        if (!aligned16(e.W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
+        int st = check_matmul_shape(c, e.type, e.N, e.K, M, (int)e.K, (int)e.N, GGQ_ACT_F32);
+        if (st != GGQ_OK) return st;
+        if ((e.A_up || e.rms_norm || e.residual || e.silu) && e.K % 32)
+            return set_status(c, GGQ_INVALID_PARAM, "fused options need K %% 32 == 0 (entry %d)", i);
+        if (e.A_up && e.rms_norm) return set_status(c, GGQ_INVALID_PARAM, "A_up and rms_norm exclude each other");
+        if (e.rms_norm && !(e.rms_eps >= 0.0f)) return set_status(c, GGQ_INVALID_PARAM, "rms_eps must be >= 0");
+        if (e.rms_norm && !aligned16(e.rms_w)) return set_status(c, GGQ_INVALID_PARAM, "rms_w must be 16-byte aligned");
+        ggq::GemvProblem& g = ps[i];
+        g = ggq::GemvProblem{};
+        g.type = e.type;
+        g.W = e.W;
+        g.N = (int)e.N;
+        g.K = (int)e.K;
+        g.X = e.A;
+        g.X2 = e.A_up;
+        g.ldx = (int)e.K;
+        g.Y = e.C;
+        g.ldy = (int)e.N;
+        g.M = M;
+        g.groups = 1;
+        g.rms = e.rms_norm != 0;
+        g.eps = e.rms_eps;
+        g.norm_w = e.rms_w;
+        g.R = e.residual;
+        g.ldr = (int)e.N;
+        g.silu = e.silu != 0;
+    }
+    if (M == 0) return set_status(c, GGQ_OK);
+    return hip_status(c, ggq::launch_gemv_multi(ps, n, pick_stream(c, stream)), "fused gemv");
+    GGQ_END(c)
+}
+
 int ggq_mul_mat_batch_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, void* stream) {
     return ggq_mul_mat_batch_rows_dev(c, d, n, 1, stream);
 }

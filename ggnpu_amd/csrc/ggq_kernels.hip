@@ -234,6 +234,14 @@ struct GemvArgs {
     int lpr_log2;
     int x_vec4;    // X rows are 16-byte aligned (float4 loads)
     int prefetch;  // fetch the next row-iteration while computing the current one
+    // Fused neighbours of the matmul (all off when zero / null):
+    const float* X2;       // elementwise product input: the activation is X * X2 (X2 like X)
+    int silu;              // epilogue: Y = silu(result), silu(v) = v / (1 + exp(-v))
+    int rms;               // RMSNorm each activation row first: x * (1/sqrt(mean(x^2) + eps)) * norm_w
+    float eps;
+    const float* norm_w;   // [K] or null (weight 1)
+    const float* R;        // residual: Y = R + result, R [M][ldr] (may alias Y)
+    int ldr;
 };
 
 // Sum over aligned groups of 2^lg lanes (lg = 0..6): afterwards every lane of
@@ -272,13 +280,25 @@ __device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[U][PPT]
     }
 }
 
-template <int T, int MB, int PPT, int U>
+template <int T, int MB, int PPT, int U, bool F>
 __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U][PPT], const GemvArgs& a,
                                           const uint8_t* W, int it, int stride, int n_iters, int rpi, int lp, int lpr,
                                           int P, int wave, int lane, int rsub, int m0, int mc, int mcount,
                                           const float (&xr)[PPT][MB][32], const float (&xs)[PPT][MB][2],
                                           float (&red)[2][4][U * MB], int& parity) {
     float acc[U][MB];
+    // The writer lane reads its residual values first, so their latency
+    // overlaps the row's decode and reduction.
+    float res[U][MB];
+    if (F && a.R && lp == 0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int iu = it + u * stride, row = iu * rpi + rsub;
+            const int rr = iu < n_iters && row < a.N ? row : 0;
+#pragma unroll
+            for (int m = 0; m < MB; m++) res[u][m] = a.R[(int64_t)(m0 + mc + (mc + m < mcount ? m : 0)) * a.ldr + rr];
+        }
+    }
 #pragma unroll
     for (int u = 0; u < U; u++) {
 #pragma unroll
@@ -342,7 +362,80 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
             if (iu < n_iters && row < a.N) {
 #pragma unroll
                 for (int m = 0; m < MB; m++)
-                    if (mc + m < mcount) a.Y[(int64_t)(m0 + mc + m) * a.ldy + row] = acc[u][m];
+                    if (mc + m < mcount) {
+                        float v = acc[u][m];
+                        if (F && a.silu) v = v / (1.0f + expf(-v));  // cpu_ref.cpp:200-209
+                        const int64_t mrow = m0 + mc + m;
+                        if (F && a.R) v = res[u][m] + v;
+                        a.Y[mrow * a.ldy + row] = v;
+                    }
+            }
+        }
+    }
+}
+
+// RMSNorm of the activation rows held in registers (cpu_ref.cpp:139-156):
+// x * (1 / sqrt(sum(x^2) / K + eps)) * w, in that order.  The sum of squares
+// of a row is spread over the LPR threads that hold its pieces: DPP inside a
+// wavefront, LDS across the wavefronts of a row when LPR > 64.  (The
+// reference adds the squares sequentially; the order differs, the rounding
+// of the sum by a few ulps.)
+template <int T, int MB, int PPT>
+__device__ __forceinline__ void gemv_rms_norm(const GemvArgs& a, float (&xr)[PPT][MB][32], int lp, int lpr, int P,
+                                              int wave, int lane, int rsub, int mc, int mcount) {
+    __shared__ float nrm[4][MB];
+    float tot[MB];
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PPT; i++)
+#pragma unroll
+            for (int j = 0; j < 32; j++) ss = fmaf(xr[i][m][j], xr[i][m][j], ss);
+        const int lg = a.lpr_log2 < 6 ? a.lpr_log2 : 6;
+        ss = group_sum(ss, lg);
+        if (lg == 6) ss = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, ss)));
+        tot[m] = ss;
+    }
+    if (a.lpr_log2 > 6) {
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MB; m++) nrm[wave][m] = tot[m];
+        }
+        __syncthreads();
+        const int wpr = lpr >> 6, w0 = rsub * wpr;
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            float t = 0.0f;
+            for (int w = 0; w < wpr; w++) t += nrm[w0 + w][m];
+            tot[m] = t;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        if (mc + m >= mcount) continue;
+        const float is = 1.0f / sqrtf(tot[m] / (float)a.K + a.eps);
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int p = lp + i * lpr;
+            const int pc = p < P ? p : 0;
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const int k0 = Piece<T>::run_k(pc, r);  // a multiple of 16: float4-aligned in norm_w
+                float w[16];
+                if (a.norm_w) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float4 v = *(const float4*)(a.norm_w + k0 + 4 * j);
+                        w[4 * j] = v.x; w[4 * j + 1] = v.y; w[4 * j + 2] = v.z; w[4 * j + 3] = v.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; j++) w[j] = 1.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < 16; j++) xr[i][m][16 * r + j] = __fmul_rn(__fmul_rn(xr[i][m][16 * r + j], is), w[j]);
             }
         }
     }
@@ -351,7 +444,9 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
 // One workgroup's share of a GEMV problem: workgroup bx of gx working on
 // group `by` (the expert in grouped mode) and on the MB-row chunks
 // bz, bz + gz, ... of its activation rows.
-template <int T, int MB, int PPT, int U>
+// F: compiled with the fused options (RMSNorm, product input, silu,
+// residual); the plain instantiations carry none of their code.
+template <int T, int MB, int PPT, int U, bool F>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
                                           float (&red)[2][4][U * MB]) {
     typedef typename Piece<T>::Raw Raw;
@@ -408,22 +503,45 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
 #pragma unroll
                         for (int j = 0; j < 16; j++) xr[i][m][16 * r + j] = xp[k0 + j];
                     }
-                    float sum = 0.0f;
+                    if (F && a.X2) {  // SwiGLU's product: silu(gate) (already applied) * up, main.cpp:3474-3477
+                        const float* up = a.X2 + (int64_t)xrow * a.ldx + k0;
+                        float uv[16];
+                        if (a.x_vec4) {
 #pragma unroll
-                    for (int j = 0; j < 16; j++) {
-                        xr[i][m][16 * r + j] = ok ? xr[i][m][16 * r + j] : 0.0f;
-                        sum += xr[i][m][16 * r + j];
+                            for (int j = 0; j < 4; j++) {
+                                const float4 v = *(const float4*)(up + 4 * j);
+                                uv[4 * j] = v.x; uv[4 * j + 1] = v.y; uv[4 * j + 2] = v.z; uv[4 * j + 3] = v.w;
+                            }
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 16; j++) uv[j] = up[j];
+                        }
+#pragma unroll
+                        for (int j = 0; j < 16; j++) xr[i][m][16 * r + j] = __fmul_rn(xr[i][m][16 * r + j], uv[j]);
                     }
-                    xs[i][m][r] = sum;
+#pragma unroll
+                    for (int j = 0; j < 16; j++) xr[i][m][16 * r + j] = ok ? xr[i][m][16 * r + j] : 0.0f;
                 }
             }
         }
+        if (F && a.rms) gemv_rms_norm<T, MB, PPT>(a, xr, lp, lpr, P, wave, lane, rsub, mc, mcount);
+#pragma unroll
+        for (int i = 0; i < PPT; i++)
+#pragma unroll
+            for (int m = 0; m < MB; m++)
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 16; j++) sum += xr[i][m][16 * r + j];
+                    xs[i][m][r] = sum;
+                }
 
         if (!a.prefetch) {
             // Fetch, then decode/multiply/reduce; latency is hidden by the
             // other resident wavefronts.
             while (true) {
-                gemv_rows<T, MB, PPT, U>(ra, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc,
+                gemv_rows<T, MB, PPT, U, F>(ra, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc,
                                          mcount, xr, xs, red, parity);
                 it += step;
                 if (it >= n_iters) break;
@@ -435,19 +553,19 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
         // decode/multiply/reduce the current ones.
         while (it < n_iters) {
             gemv_fetch<T, PPT, U>(rb, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
-            gemv_rows<T, MB, PPT, U>(ra, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
+            gemv_rows<T, MB, PPT, U, F>(ra, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
                                      xr, xs, red, parity);
             it += step;
             if (it >= n_iters) break;
             gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
-            gemv_rows<T, MB, PPT, U>(rb, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
+            gemv_rows<T, MB, PPT, U, F>(rb, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
                                      xr, xs, red, parity);
             it += step;
         }
     }
 }
 
-template <int T, int MB, int PPT, int U>
+template <int T, int MB, int PPT, int U, bool F = false>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     __shared__ float red[2][4][U * MB];
     if constexpr (MB > 1) {
@@ -457,18 +575,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
             const int cnt = a.grp_off[blockIdx.y + 1] - a.grp_off[blockIdx.y];
             if (cnt <= 0) return;
             if (cnt == 1) {
-                gemv_body<T, 1, PPT, U>(a, blockIdx.x, gridDim.x, blockIdx.y, 0, 1,
+                gemv_body<T, 1, PPT, U, F>(a, blockIdx.x, gridDim.x, blockIdx.y, 0, 1,
                                         *reinterpret_cast<float(*)[2][4][U]>(&red));
                 return;
             }
             if (MB > 2 && cnt == 2) {
-                gemv_body<T, 2, PPT, U>(a, blockIdx.x, gridDim.x, blockIdx.y, 0, 1,
+                gemv_body<T, 2, PPT, U, F>(a, blockIdx.x, gridDim.x, blockIdx.y, 0, 1,
                                         *reinterpret_cast<float(*)[2][4][U * 2]>(&red));
                 return;
             }
         }
     }
-    gemv_body<T, MB, PPT, U>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
+    gemv_body<T, MB, PPT, U, F>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
 }
 
 // Several independent GEMV problems (any mix of formats, same pieces-per-
@@ -483,7 +601,7 @@ struct MultiArgs {
     int n;
 };
 
-template <int MB, int PPT, int U>
+template <int MB, int PPT, int U, bool F = false>
 __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     __shared__ float red[2][4][U * MB];
     int q = 0;
@@ -491,12 +609,12 @@ __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
     const int bz = blockIdx.z, gz = gridDim.z;
     switch (ma.type[q]) {
-    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
     default: break;
     }
 }
@@ -616,6 +734,8 @@ static int moe_mb() { return env_int("GGQ_MOE_MB", 1); }
 static int moe_gx() { return env_int("GGQ_MOE_GX", 0); }
 static int moe_rounds() { const int v = env_int("GGQ_MOE_ROUNDS", 4); return v < 1 ? 1 : v; }
 
+static bool fused(const GemvProblem& p) { return p.rms || p.X2 || p.R || p.silu; }
+
 struct GemvPlan {
     GemvArgs a;
     int ppt, n_iters, mrows;
@@ -640,8 +760,15 @@ static GemvPlan plan_gemv(const GemvProblem& p) {
     a.grp_off = p.grp_off;
     a.x_idx = p.x_idx;
     a.lpr_log2 = lpr_log2;
-    a.x_vec4 = ((uintptr_t)p.X % 16 == 0) && (p.ldx % 4 == 0);
+    a.x_vec4 = ((uintptr_t)p.X % 16 == 0) && (p.ldx % 4 == 0) && ((uintptr_t)p.X2 % 16 == 0);
     a.prefetch = gemv_prefetch();
+    a.X2 = p.X2;
+    a.silu = p.silu;
+    a.rms = p.rms;
+    a.eps = p.eps;
+    a.norm_w = p.norm_w;
+    a.R = p.R;
+    a.ldr = p.ldr;
     g.ppt = (P + lpr - 1) / lpr;
     g.n_iters = (p.N + rpi - 1) / rpi;
     g.mrows = p.grp_off ? p.max_group_rows : p.M;
@@ -654,6 +781,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     GemvArgs a = g.a;
     const int groups = p.groups > 0 ? p.groups : 1;
     if (g.simple) {
+        if (p.X2 || p.rms || p.R || p.silu) return hipErrorInvalidValue;  // fused options need K % 32 == 0
         gemv_simple_kernel<T><<<dim3((p.N + 255) / 256, groups), 256, 0, s>>>(a);
         return hipGetLastError();
     }
@@ -672,8 +800,21 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
         gemv_kernel<T, MB_, PPT_, U_><<<dim3(gx, groups, gz), 256, 0, s>>>(a);                   \
     } while (0)
+#define GO_F(PPT_)                                                                               \
+    do {                                                                                         \
+        const int gz = mrows;                                                                    \
+        int gx = resident_blocks(gemv_kernel<T, 1, PPT_, 1, true>, 0) / gz;                      \
+        gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
+        gemv_kernel<T, 1, PPT_, 1, true><<<dim3(gx, 1, gz), 256, 0, s>>>(a);                     \
+    } while (0)
     const int u = gemv_rows_per_iter();
-    if (groups > 1 && ppt == 1 && mrows > 1) {
+    if (fused(p)) {  // one activation row per pass, the fused options compiled in
+        if (groups > 1) return hipErrorInvalidValue;
+        if (ppt == 1) GO_F(1);
+        else if (ppt == 2) GO_F(2);
+        else if (ppt <= 4) GO_F(4);
+        else return hipErrorInvalidValue;
+    } else if (groups > 1 && ppt == 1 && mrows > 1) {
         const int mb = moe_mb();
         if (mb <= 1) GO(1, 1, 1);
         else if (mb == 2) GO(2, 1, 1);
@@ -691,6 +832,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         return hipErrorInvalidValue;
     }
 #undef GO
+#undef GO_F
     return hipGetLastError();
 }
 
@@ -702,9 +844,9 @@ static int multi_mb(int ppt, int M) {
     return mb > cap ? cap : mb;
 }
 
-template <int MB, int PPT, int U>
+template <int MB, int PPT, int U, bool F = false>
 static int multi_resident() {
-    return resident_blocks(gemv_multi_kernel<MB, PPT, U>, 0);
+    return resident_blocks(gemv_multi_kernel<MB, PPT, U, F>, 0);
 }
 
 // Independent problems with the same number of activation rows M in one
@@ -712,6 +854,7 @@ static int multi_resident() {
 // per problem.
 hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
+    if (n == 1) return launch_gemv(ps[0], s);  // the single-problem kernel sizes its grid for one problem
     MultiArgs ma;
     int ppt = -1, total_iters = 0;
     const int M = ps[0].M;
@@ -734,11 +877,15 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
         }
         return hipSuccess;
     }
-    const int u = gemv_rows_per_iter();
-    const int mb = multi_mb(ppt, M);
+    bool any_fused = false;
+    for (int i = 0; i < n; i++) any_fused = any_fused || fused(ps[i]);
+    const int u = any_fused ? 1 : gemv_rows_per_iter();
+    const int mb = any_fused ? 1 : multi_mb(ppt, M);
     const int gz = (M + mb - 1) / mb;
     int target;
-    if (ppt == 1) {
+    if (any_fused) {
+        target = ppt == 1 ? multi_resident<1, 1, 1, true>() : multi_resident<1, 2, 1, true>();
+    } else if (ppt == 1) {
         if (mb == 1) target = u >= 4 ? multi_resident<1, 1, 4>() : u >= 2 ? multi_resident<1, 1, 2>() : multi_resident<1, 1, 1>();
         else if (mb == 2) target = multi_resident<2, 1, 1>();
         else target = multi_resident<4, 1, 1>();
@@ -759,7 +906,10 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     ma.begin[n] = b;
     ma.n = n;
     const dim3 grid(b, 1, gz);
-    if (ppt == 1) {
+    if (any_fused) {
+        if (ppt == 1) gemv_multi_kernel<1, 1, 1, true><<<grid, 256, 0, s>>>(ma);
+        else gemv_multi_kernel<1, 2, 1, true><<<grid, 256, 0, s>>>(ma);
+    } else if (ppt == 1) {
         if (mb == 1) {
             if (u >= 4) gemv_multi_kernel<1, 1, 4><<<grid, 256, 0, s>>>(ma);
             else if (u >= 2) gemv_multi_kernel<1, 1, 2><<<grid, 256, 0, s>>>(ma);

@@ -37,6 +37,14 @@ struct GemvProblem {
     const int* grp_off;
     const int* x_idx;
     int max_group_rows;  // upper bound of rows per group (grouped mode)
+    // Fused neighbours (zero / null = off; plain mode only):
+    const float* X2;       // the activation is X * X2 elementwise (X2 [M][ldx])
+    int silu;              // Y = silu(result) (before the residual add)
+    int rms;               // RMSNorm the activation rows first (norm_w may be null)
+    float eps;
+    const float* norm_w;
+    const float* R;        // Y = R + result, R [M][ldr]
+    int ldr;
 };
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t s);
 // Several independent M = 1 problems in as few launches as possible.

@@ -82,6 +82,14 @@ class GemmDesc(ctypes.Structure):
     _fields_ = [("W", ctypes.c_void_p), ("N", ctypes.c_int64), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int)]
 
 
+class GemvFusedDesc(ctypes.Structure):
+    """ggq_gemv_fused_desc (include/ggq.h)."""
+    _fields_ = [("W", ctypes.c_void_p), ("type", ctypes.c_uint32), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
+                ("A", ctypes.c_void_p), ("A_up", ctypes.c_void_p), ("C", ctypes.c_void_p),
+                ("residual", ctypes.c_void_p), ("rms_w", ctypes.c_void_p), ("rms_norm", ctypes.c_int),
+                ("rms_eps", ctypes.c_float), ("silu", ctypes.c_int)]
+
+
 class MulMatParams(ctypes.Structure):
     """MulMatParams (include/ggnpu/backend.h:21-35)."""
     _fields_ = [
@@ -112,6 +120,7 @@ SIGNATURES = {
     "ggq_mul_mat_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _I, _I, _I, _P]),
     "ggq_mul_mat_batch_dev": (_I, [_P, _P, _I, _P]),
     "ggq_mul_mat_batch_rows_dev": (_I, [_P, _P, _I, _I, _P]),
+    "ggq_mul_mat_fused_dev": (_I, [_P, _P, _I, _I, _P]),
     "ggq_mul_mat_q8_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _P, _I, _P, _I, _P]),
     "ggq_logits_argmax_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _I, _P, _P, _P, _P]),
     "ggq_mul_mat_q8_batch_dev": (_I, [_P, _P, _I, _U32, _I64, _P, _P, _I, _P]),

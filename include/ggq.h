@@ -128,6 +128,44 @@ int ggq_mul_mat(ggq_ctx* ctx, const ggq_weight* w, const float* A, int lda, floa
 int ggq_mul_mat_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
                     const float* A, int lda, float* C, int ldc, int M, int act_mode, void* stream);
 
+/* Decode GEMVs (fp32 activations, GGQ_ACT_F32 semantics) with their
+ * neighbours in the same launch, for the parts of a transformer layer that
+ * surround the matmuls (no reference counterpart as a fused call; each
+ * option restates a reference step):
+ *   rms_norm  RMSNorm of each A row before the matmul, as
+ *             CpuRefBackend::rms_norm (cpu_ref.cpp:139-156):
+ *             a * (1/sqrt(sum(a^2)/K + eps)) * rms_w[k] (rms_w null = 1,
+ *             else 16-byte aligned);
+ *   silu      C = silu(result), silu(x) = x / (1 + exp(-x))
+ *             (CpuRefBackend::silu, cpu_ref.cpp:200-209) -- the gate
+ *             projection of SwiGLU;
+ *   A_up      the activation is A * A_up elementwise (main.cpp:3474-3477:
+ *             silu(gate) *= up) -- the down projection reading the gate
+ *             (silu applied) and up outputs; A_up dense [M][K] with A's
+ *             alignment; not with rms_norm;
+ *   residual  C = residual + result (after silu), the residual adds of
+ *             main.cpp:3424-3431 and 3491-3498 (residual may be C itself).
+ * A dense [M][K], C and residual dense [M][N]; all entries share M
+ * (<= GGQ_MAX_BATCH_ROWS); entries that share the pieces-per-thread count
+ * run as one launch.  K must be a multiple of 32 when any option is set.
+ * Results match the unfused sequence within fp32 rounding (the norm's sum
+ * of squares is added in a different order). */
+typedef struct {
+    const void* W;
+    uint32_t type;
+    int64_t N;
+    int64_t K;
+    const float* A;
+    const float* A_up;
+    float* C;
+    const float* residual;
+    const float* rms_w;
+    int rms_norm;
+    float rms_eps;
+    int silu;
+} ggq_gemv_fused_desc;
+int ggq_mul_mat_fused_dev(ggq_ctx* ctx, const ggq_gemv_fused_desc* descs, int n, int M, void* stream);
+
 /* Vocab projection with the greedy token choice on the device: logits =
  * A . W^T as ggq_mul_mat_dev (A dense [M][K], act_mode as there), then
  * token[m] = the first index of the largest logit of row m and value[m]

@@ -410,7 +410,7 @@ int orc_mul_mat_cpuref_f32(uint32_t t, const uint8_t* W, int64_t N, int64_t K,
  * expert down(silu(gate x) * up x) accumulated with its weight (:3156-3169);
  * shared expert added with its gate weight (:3177-3191). Expert e of a 3-D
  * tensor starts at e * rows * row_bytes (:3140-3150). */
-static double orc_silu(double v) { return v / (1.0 + exp(-v)); }
+static double orc_silu_f64(double v) { return v / (1.0 + exp(-v)); }
 
 int orc_moe_ffn_f64(const float* x, const float* logits, int T, int H, int F, int E, int topk,
                     uint32_t tg, const uint8_t* Wg, uint32_t tu, const uint8_t* Wu,
@@ -458,11 +458,26 @@ int orc_moe_ffn_f64(const float* x, const float* logits, int T, int H, int F, in
             }
             orc_mul_mat_f64(tg, pg, F, H, xt, H, 1, ORC_ACT_F32, g, F);
             orc_mul_mat_f64(tu, pu, F, H, xt, H, 1, ORC_ACT_F32, u, F);
-            for (int i = 0; i < F; i++) act[i] = (float)(orc_silu(g[i]) * u[i]);
+            for (int i = 0; i < F; i++) act[i] = (float)(orc_silu_f64(g[i]) * u[i]);
             orc_mul_mat_f64(td, pd, H, F, act, F, 1, ORC_ACT_F32, d, H);
             for (int i = 0; i < H; i++) ot[i] += wj * d[i];
         }
     }
     free(g); free(u); free(d); free(act); free(idx);
     return 0;
+}
+
+/* cpu_ref.cpp:139-156: variance accumulated in fp32 in index order. */
+void orc_rms_norm(const float* x, int n, const float* w, float eps, float* out) {
+    float variance = 0.0f;
+    for (int i = 0; i < n; i++) variance += x[i] * x[i];
+    variance /= (float)n;
+    variance += eps;
+    const float inv_std = 1.0f / sqrtf(variance);
+    for (int i = 0; i < n; i++) out[i] = x[i] * inv_std * (w ? w[i] : 1.0f);
+}
+
+/* cpu_ref.cpp:200-209. */
+void orc_silu(const float* x, int n, float* out) {
+    for (int i = 0; i < n; i++) out[i] = x[i] / (1.0f + expf(-x[i]));
 }

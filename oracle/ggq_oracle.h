@@ -78,6 +78,14 @@ int    orc_mul_mat_f64(uint32_t type, const uint8_t* W, int64_t N, int64_t K,
 int    orc_mul_mat_cpuref_f32(uint32_t type, const uint8_t* W, int64_t N, int64_t K,
                               const float* A, int lda, int M, float* C, int ldc);
 
+/* RMSNorm, restating CpuRefBackend::rms_norm (cpu_ref.cpp:139-156) in its
+ * fp32 order: sum of squares in index order, / n, + eps, 1/sqrt, then
+ * out[i] = x[i] * inv * w[i] (w NULL = 1). */
+void   orc_rms_norm(const float* x, int n, const float* w, float eps, float* out);
+/* silu, restating CpuRefBackend::silu (cpu_ref.cpp:200-209):
+ * out[i] = x[i] / (1 + expf(-x[i])) in fp32. */
+void   orc_silu(const float* x, int n, float* out);
+
 /* MoE FFN oracle (main.cpp:3110-3193) in fp64 over dequantized weights.
  *   x [T][H] fp32, logits [T][E] fp32 router logits
  *   gate/up expert tensor: E consecutive [F][H] matrices (type tg, tu)

@@ -31,6 +31,8 @@ _ORC_SIGS = {
     "orc_mul_mat_cpuref_f32": (_I, [_U32, _P, _I64, _I64, _P, _I, _I, _P, _I]),
     "orc_moe_ffn_f64": (_I, [_P, _P, _I, _I, _I, _I, _I, _U32, _P, _U32, _P, _U32, _P,
                              _P, _P, _P, _P, _P, _P, _P]),
+    "orc_rms_norm": (None, [_P, _I, _P, ctypes.c_float, _P]),
+    "orc_silu": (None, [_P, _I, _P]),
 }
 
 _REF_SIGS = {
@@ -41,6 +43,8 @@ _REF_SIGS = {
     "ref_blck_size": (ctypes.c_uint64, [_U32]),
     "ref_decode_for_npu": (_I, [_U32, _P, ctypes.c_uint64, _I64, _I64, _P, _P]),
     "ref_cpuref_mul_mat": (_I, [_U32, _P, _I, _I, _P, _I, _P]),
+    "ref_rms_norm": (_I, [_P, _I, _P, ctypes.c_float, _P]),
+    "ref_silu": (_I, [_P, _I, _P]),
 }
 
 
@@ -168,3 +172,22 @@ def rel_l2(got, ref):
     ref = np.asarray(ref, dtype=np.float64)
     den = np.linalg.norm(ref)
     return float(np.linalg.norm(got - ref) / (den if den > 0 else 1.0))
+
+
+def rms_norm(x, w=None, eps=1e-5):
+    """Row-wise orc_rms_norm of a [M][K] (or [K]) fp32 array."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows = x.reshape(-1, x.shape[-1])
+    out = np.empty_like(rows)
+    wp = None if w is None else np.ascontiguousarray(w, np.float32)
+    for m in range(rows.shape[0]):
+        lib().orc_rms_norm(rows[m].ctypes.data, rows.shape[1], None if wp is None else wp.ctypes.data,
+                           float(eps), out[m].ctypes.data)
+    return out.reshape(x.shape)
+
+
+def silu(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().orc_silu(x.ctypes.data, x.size, out.ctypes.data)
+    return out

@@ -70,4 +70,19 @@ int ref_cpuref_mul_mat(uint32_t type, const void* W, int N, int K, const float* 
     return static_cast<int>(be->mul_mat_q(p));
 }
 
+// CpuRefBackend::rms_norm (cpu_ref.cpp:139-156) and silu (:200-209).
+int ref_rms_norm(const float* x, int n, const float* w, float eps, float* out) {
+    auto be = create_cpu_ref_backend();
+    RmsNormParams p;
+    p.input = x; p.output = out; p.size = n; p.eps = eps; p.weight = w;
+    return static_cast<int>(be->rms_norm(p));
+}
+
+int ref_silu(const float* x, int n, float* out) {
+    auto be = create_cpu_ref_backend();
+    SiluParams p;
+    p.input = x; p.output = out; p.size = n;
+    return static_cast<int>(be->silu(p));
+}
+
 }  // extern "C"

@@ -532,3 +532,107 @@ def test_logits_argmax_nan_row_and_errors(ctx):
                                          stream_handle()) == gl.Status.INVALID_PARAM
     assert ctx.lib.ggq_logits_argmax_dev(ctx.h, ptr(dW), t, N, K, ptr(dA), 0, 0, None, ptr(tok), None,
                                          stream_handle()) == gl.Status.OK
+
+
+# --------------------------------------------- fused GEMV neighbours (§8f)
+def _fused(ctx, entries, M):
+    """entries: dicts with W (raw), type, N, K, A (np [M][K]), optional Aup
+    (np [M][K]), rms_w (np [K] or None), rms (bool), eps, residual (np [M][N])."""
+    import torch
+    keep, descs = [], (gl.GemvFusedDesc * len(entries))()
+    outs = []
+    for i, e in enumerate(entries):
+        dW, dA = dev(e["W"]), dev(e["A"])
+        keep += [dW, dA]
+        d = descs[i]
+        d.W, d.type, d.N, d.K, d.A = dW.data_ptr(), e["type"], e["N"], e["K"], dA.data_ptr()
+        if e.get("Aup") is not None:
+            dU = dev(e["Aup"])
+            keep.append(dU)
+            d.A_up = dU.data_ptr()
+        d.silu = int(bool(e.get("silu")))
+        if e.get("rms"):
+            d.rms_norm, d.rms_eps = 1, e.get("eps", 1e-5)
+            if e.get("rms_w") is not None:
+                dn = dev(e["rms_w"])
+                keep.append(dn)
+                d.rms_w = dn.data_ptr()
+        C = torch.full((M, e["N"]), float("nan"), device="cuda")
+        if e.get("residual") is not None:
+            C.copy_(torch.from_numpy(e["residual"]))
+            d.residual = C.data_ptr()  # in place: C = C + result
+        d.C = C.data_ptr()
+        outs.append(C)
+    ctx.check(ctx.lib.ggq_mul_mat_fused_dev(ctx.h, descs, len(entries), M, stream_handle()), "fused")
+    return [host(c) for c in outs]
+
+
+def _fused_ref(orc, e, M):
+    A = e["A"]
+    if e.get("rms"):
+        A = orc.rms_norm(A, e.get("rms_w"), e.get("eps", 1e-5))
+    if e.get("Aup") is not None:
+        A = A * e["Aup"]  # fp32 product, as the reference's ffn_silu *= up
+    y = orc.mul_mat_f64(e["type"], e["W"], e["N"], e["K"], A, 0)
+    if e.get("silu"):
+        y = y / (1.0 + np.exp(-y))
+    if e.get("residual") is not None:
+        y = y + e["residual"]
+    return y
+
+
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("K", [1024, 2048, 8192])
+def test_fused_rmsnorm_qkv_and_residual(ctx, orc, M, K):
+    """q/k/v-like entries sharing one input with the RMSNorm prologue (one
+    launch; K 8192 spreads a row over 4 wavefronts), plus an o-like entry
+    with a residual add in place."""
+    rng = np.random.default_rng(K + M)
+    A = (rng.standard_normal((M, K)) * 4.0).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    ents = [dict(W=weights(t, N, K, seed=N + t), type=t, N=N, K=K, A=A, rms=True, rms_w=nw, eps=1e-5)
+            for t, N in ((12, 256), (12, 64), (14, 64))]
+    res = rng.standard_normal((M, 96)).astype(np.float32)
+    ents.append(dict(W=weights(8, 96, K, seed=3), type=8, N=96, K=K, A=A, residual=res))
+    outs = _fused(ctx, ents, M)
+    for e, got in zip(ents, outs):
+        assert orc.rel_l2(got, _fused_ref(orc, e, M)) < TOL, (e["type"], e["N"])
+
+
+@pytest.mark.parametrize("t,K", [(14, 8192), (23, 1024), (13, 3072)])
+def test_fused_swiglu(ctx, orc, t, K):
+    """SwiGLU around the matmuls: a gate projection with the silu epilogue
+    (and the FFN RMSNorm in front) next to the plain up projection in one
+    launch, then the down projection reading silu(gate) * up on load, with
+    and without the residual add."""
+    M, N, H = 2, 320, 1024
+    rng = np.random.default_rng(t)
+    x = (rng.standard_normal((M, H)) * 2.0).astype(np.float32)
+    gate = dict(W=weights(t, K, H, seed=1, scale=0.05), type=t, N=K, K=H, A=x, rms=True, silu=True)
+    up = dict(W=weights(t, K, H, seed=2, scale=0.05), type=t, N=K, K=H, A=x, rms=True)
+    g, u = _fused(ctx, [gate, up], M)
+    assert orc.rel_l2(g, _fused_ref(orc, gate, M)) < TOL
+    assert orc.rel_l2(u, _fused_ref(orc, up, M)) < TOL
+    down = dict(W=weights(t, N, K, seed=3), type=t, N=N, K=K, A=g, Aup=u)
+    got = _fused(ctx, [down], M)[0]
+    assert orc.rel_l2(got, _fused_ref(orc, down, M)) < TOL
+    down2 = dict(down, residual=rng.standard_normal((M, N)).astype(np.float32))
+    got2 = _fused(ctx, [down2], M)[0]
+    assert orc.rel_l2(got2, _fused_ref(orc, down2, M)) < TOL
+
+
+def test_fused_errors(ctx):
+    import torch
+    d = (gl.GemvFusedDesc * 1)()
+    raw = dev(weights(12, 8, 256, seed=1))
+    A = torch.zeros((1, 256), device="cuda")
+    C = torch.zeros((1, 8), device="cuda")
+    d[0].W, d[0].type, d[0].N, d[0].K, d[0].A, d[0].C = raw.data_ptr(), 12, 8, 256, A.data_ptr(), C.data_ptr()
+    d[0].rms_norm, d[0].rms_eps = 1, -1.0
+    assert ctx.lib.ggq_mul_mat_fused_dev(ctx.h, d, 1, 1, stream_handle()) == gl.Status.INVALID_PARAM
+    d[0].rms_eps, d[0].A_up = 1e-5, A.data_ptr()
+    assert ctx.lib.ggq_mul_mat_fused_dev(ctx.h, d, 1, 1, stream_handle()) == gl.Status.INVALID_PARAM
+    d[0].A_up = None
+    d[0].rms_eps = 1e-5
+    assert ctx.lib.ggq_mul_mat_fused_dev(ctx.h, d, 1, 65, stream_handle()) == gl.Status.INVALID_PARAM
+    ctx.check(ctx.lib.ggq_mul_mat_fused_dev(ctx.h, d, 1, 1, stream_handle()), "ok")

@@ -236,3 +236,41 @@ def test_moe_oracle_vs_numpy_loop(orc):
             h = (g / (1 + np.exp(-g)) * u).astype(np.float32).astype(np.float64)
             ref += w[j] * (dd[e] @ h)
         assert orc.rel_l2(out[t], ref) < 1e-12
+
+
+# ------------------------------------------- RMSNorm / silu (fused GEMV)
+@pytest.mark.parametrize("n,with_w,eps", [(2048, True, 1e-5), (1001, False, 1e-6), (64, True, 0.0)])
+def test_rms_norm_matches_reference_and_closed_form(orc, n, with_w, eps):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32) * 3.0
+    w = rng.standard_normal(n).astype(np.float32) if with_w else None
+    got = orc.rms_norm(x, w, eps)
+    ref = orc.ref_lib()
+    if ref is not None:  # the compiled CpuRefBackend::rms_norm, bit for bit
+        out = np.empty_like(x)
+        assert ref.ref_rms_norm(x.ctypes.data, n, None if w is None else w.ctypes.data, eps, out.ctypes.data) == 0
+        assert np.array_equal(got.view(np.uint32), out.view(np.uint32))
+    # closed form in fp64
+    xd = x.astype(np.float64)
+    exp = xd / np.sqrt(np.mean(xd * xd) + eps) * (1.0 if w is None else w.astype(np.float64))
+    assert np.allclose(got, exp, rtol=3e-6, atol=1e-6)
+
+
+def test_rms_norm_special_cases(orc):
+    c = np.full(256, -2.5, np.float32)
+    assert np.allclose(orc.rms_norm(c, None, 0.0), -1.0, rtol=2e-7, atol=0)  # constant row: sign
+    z = np.zeros(64, np.float32)
+    assert np.array_equal(orc.rms_norm(z, None, 1e-5), z)  # zero row stays zero (eps keeps it finite)
+
+
+def test_silu_matches_reference_and_closed_form(orc):
+    x = np.concatenate([np.linspace(-30, 30, 601), [0.0, -0.0, 1e-30, 88.0, -88.0]]).astype(np.float32)
+    got = orc.silu(x)
+    ref = orc.ref_lib()
+    if ref is not None:
+        out = np.empty_like(x)
+        assert ref.ref_silu(x.ctypes.data, x.size, out.ctypes.data) == 0
+        assert np.array_equal(got.view(np.uint32), out.view(np.uint32))
+    xd = x.astype(np.float64)
+    assert np.allclose(got, xd / (1.0 + np.exp(-xd)), rtol=2e-6, atol=1e-30)
+    assert got[601] == 0.0 and got[605] == pytest.approx(-88.0 * np.exp(-88.0), rel=1e-3, abs=1e-36)
