@@ -302,6 +302,31 @@ def bench_logits(torch, ctx, stream, reps=50):
             "gemv_argmax_us": round(fused * 1e6, 2), "GBps_with_argmax": round(m.bytes() / fused / 1e9, 1)}
 
 
+def bench_attention(torch, ctx, stream, reps=50):
+    """Decode attention of one token over a layer's KV cache
+    (ggq_attention_decode_dev), Llama-3.2-1B heads (32 query heads, 8 kv
+    heads, head_dim 64) at contexts 1024 / 4096 / 16384, and Llama-3-8B heads
+    (head_dim 128) at 4096.  Algorithmic bytes: K and V of the visible
+    positions once (2 * ctx * n_kv * head_dim * 4) plus q and out."""
+    res = {}
+    for tag, n_head, n_kv, hd, ctx_len in (("1b_ctx1024", 32, 8, 64, 1024), ("1b_ctx4096", 32, 8, 64, 4096),
+                                           ("1b_ctx16384", 32, 8, 64, 16384), ("8b_ctx4096", 32, 8, 128, 4096)):
+        q = torch.randn((1, n_head, hd), device="cuda")
+        Kc = torch.randn((ctx_len, n_kv, hd), device="cuda")
+        Vc = torch.randn((ctx_len, n_kv, hd), device="cuda")
+        out = torch.empty_like(q)
+
+        def run():
+            ctx.check(ctx.lib.ggq_attention_decode_dev(ctx.h, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(Kc.data_ptr()),
+                                                       ctypes.c_void_p(Vc.data_ptr()), 1, n_head, n_kv, hd, ctx_len,
+                                                       ctx_len - 1, ctypes.c_void_p(out.data_ptr()), stream), "attn")
+
+        (sec,) = back_to_back_times(torch, [run], reps)
+        nbytes = 2 * ctx_len * n_kv * hd * 4 + 2 * n_head * hd * 4
+        res[tag] = {"us": round(sec * 1e6, 2), "GBps": round(nbytes / sec / 1e9, 1)}
+    return {"workload": "decode attention, 1 token, fp32 KV cache", **res}
+
+
 def bench_prefill(torch, ctx, stream, steps=3):
     """28 layers of Q8_0 matmuls on 512 tokens, per-row int8
     activations (reference XDNA semantics).  Each layer quantizes its four
@@ -485,7 +510,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
-    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "fused", "copy"],
+    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "fused", "attention", "copy"],
                     default=None,
                     help="run one workload only and print its result (profiling aid)")
     ap.add_argument("--per-matmul", action="store_true",
@@ -517,9 +542,10 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_per_copy": src.numel(), "copies": 4}), flush=True)
         return
-    if args.only in ("config1", "prefill", "config4", "moe", "logits", "fused"):
+    if args.only in ("config1", "prefill", "config4", "moe", "logits", "fused", "attention"):
         res = {"config1": bench_config1, "prefill": bench_prefill, "config4": bench_config4,
-               "moe": bench_config5, "logits": bench_logits, "fused": bench_decode_fused}[args.only](
+               "moe": bench_config5, "logits": bench_logits, "fused": bench_decode_fused,
+               "attention": bench_attention}[args.only](
                    torch, ctx, stream)
         print(json.dumps({"only": args.only, **res}), flush=True)
         ctx.close()
@@ -566,7 +592,7 @@ def main():
     if not args.no_extra:
         out["extra"] = {"config1": bench_config1(torch, ctx, stream)}
         for key, fn in (("config3_prefill", bench_prefill), ("config4_iq4_q5k", bench_config4),
-                        ("config5_moe", bench_config5), ("logits_argmax", bench_logits),
+                        ("config5_moe", bench_config5), ("logits_argmax", bench_logits), ("attention_decode", bench_attention),
                         ("decode_fused", bench_decode_fused)):
             try:
                 out["extra"][key] = fn(torch, ctx, stream)

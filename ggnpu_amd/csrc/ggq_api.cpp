@@ -50,6 +50,7 @@ struct ggq_ctx {
     Buffer io;  // staging of host A / C for the synchronous entry points
     Buffer part;  // GEMM split-K partial tiles
     Buffer logits;  // vocab projection output when the caller does not keep it
+    Buffer attn;  // attention chunk partials
 };
 
 namespace {
@@ -285,6 +286,7 @@ void ggq_destroy(ggq_ctx* c) {
     if (c->io.ptr) hipFree(c->io.ptr);
     if (c->part.ptr) hipFree(c->part.ptr);
     if (c->logits.ptr) hipFree(c->logits.ptr);
+    if (c->attn.ptr) hipFree(c->attn.ptr);
     hipStreamDestroy(c->stream);
     delete c;
 }
@@ -393,6 +395,30 @@ int ggq_logits_argmax_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, i
     st = mul_mat_queue(c, W, type, N, K, A, (int)K, L, (int)N, M, act_mode, s);
     if (st != GGQ_OK) return st;
     return hip_status(c, ggq::launch_argmax_rows(L, M, (int)N, (int)N, token, value, c->logits.ptr, s), "argmax");
+    GGQ_END(c)
+}
+
+int ggq_attention_decode_dev(ggq_ctx* c, const float* Q, const float* K, const float* V, int n_tok, int n_head,
+                             int n_kv_head, int head_dim, int64_t ctx_len, int64_t pos0, float* out, void* stream) {
+    GGQ_GUARD(c)
+    if (n_tok < 0 || n_head < 1 || n_kv_head < 1 || n_head % n_kv_head)
+        return set_status(c, GGQ_INVALID_PARAM, "need n_tok >= 0 and n_head a multiple of n_kv_head");
+    const int g = n_head / n_kv_head;
+    if (g != 1 && g != 2 && g != 4 && g != 8)
+        return set_status(c, GGQ_INVALID_PARAM, "n_head / n_kv_head must be 1, 2, 4 or 8 (got %d)", g);
+    if (head_dim != 64 && head_dim != 128)
+        return set_status(c, GGQ_INVALID_PARAM, "head_dim must be 64 or 128 (got %d)", head_dim);
+    if (ctx_len < 1 || pos0 < 0) return set_status(c, GGQ_INVALID_PARAM, "need ctx_len >= 1 and pos0 >= 0");
+    if (n_tok == 0) return set_status(c, GGQ_OK);
+    if (!Q || !K || !V || !out) return set_status(c, GGQ_INVALID_PARAM, "null Q/K/V/out");
+    if (!aligned16(Q) || !aligned16(K) || !aligned16(V))
+        return set_status(c, GGQ_INVALID_PARAM, "Q, K and V must be 16-byte aligned");
+    const size_t need = sizeof(float) * ggq::attn_workspace_floats(n_tok, n_head, head_dim, ctx_len, pos0, n_kv_head);
+    hipError_t e = ensure(c->attn, need);
+    if (e != hipSuccess) return hip_status(c, e, "attention workspace");
+    return hip_status(c, ggq::launch_attn_decode(Q, K, V, n_tok, n_head, n_kv_head, head_dim, ctx_len, pos0, out,
+                                                 (float*)c->attn.ptr, pick_stream(c, stream)),
+                      "attention");
     GGQ_END(c)
 }
 

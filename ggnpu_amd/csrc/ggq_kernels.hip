@@ -1602,6 +1602,291 @@ hipError_t launch_argmax_rows(const float* L, int M, int N, int ld, int32_t* idx
     return hipGetLastError();
 }
 
+// =============================================================== attention
+// Decode attention over one layer's KV cache in its native layout
+// [position][kv head][head_dim] (kv_cache.cpp:42-59), for query rows at
+// positions pos0, pos0+1, ... (causal: row t sees positions <= pos0 + t).
+// Same result as CpuRefBackend::flash_attn (cpu_ref.cpp:223-280) over the GQA-
+// expanded K/V (main.cpp:3358-3379), without materialising the expansion:
+// workgroup (span c, kv head h, row t) reads the positions of span c of kv
+// head h once for all G = n_head / n_kv query heads that share it.
+//
+// A span is a whole number of 64-position steps; the span count is chosen so
+// the grid fills the chip.  Per step (4 wavefronts, 16 positions each):
+//   phase 1: score[g][j] = (q_g . k_j) * scale, 16 lanes per position
+//            (head_dim/16 values each, DPP sum), 4 positions per wave step;
+//   phase 2: online softmax, one wavefront per query head: m' = max(m, s),
+//            p = exp(s - m'), alpha = exp(m - m'), l = l * alpha + sum p;
+//   phase 3: o_g = o_g * alpha_g + sum_j p_gj v_j (lane layout of phase 1).
+// K of the next step is fetched during phases 2-3 and V of a step during
+// phases 1-2.  Scores and alphas are double-buffered in LDS, so a step needs
+// two barriers.  With one span the kernel writes o / l directly; otherwise it
+// writes (m, l, o) and attn_combine_kernel merges the spans:
+// m = max m_c, out = sum_c e^(m_c-m) o_c / sum_c e^(m_c-m) l_c.  The
+// reference does one softmax over the whole row; the results differ by fp32
+// rounding.
+constexpr int kAttnStep = 64;
+
+struct AttnArgs {
+    const float* Q;   // [n_tok][n_head][HD]
+    const float* K;   // [ctx][n_kv][HD]
+    const float* V;
+    float* part_o;    // [n_tok][n_head][n_spans][HD]
+    float* part_ml;   // [n_tok][n_head][n_spans][2]
+    float* out;       // [n_tok][n_head][HD]
+    int n_head, n_kv, n_spans, span_steps;
+    int64_t ctx_len, pos0;
+    float scale;
+};
+
+template <int N> __device__ __forceinline__ void ld_floats(const float* p, float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+        const float4 f = *(const float4*)(p + i);
+        v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+    }
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(256) void attn_span_kernel(AttnArgs a) {
+    constexpr int DPL = HD / 16;
+    constexpr int IT = kAttnStep / 16;  // wave steps of 4 positions
+    __shared__ float sc[2][G][kAttnStep];
+    __shared__ float al[2][G];
+    __shared__ float ml[G][2];
+    __shared__ float ored[4][G][HD];
+    const int span = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, pg = lane >> 4;
+    const int64_t qpos = a.pos0 + t;
+    const int64_t last = qpos < a.ctx_len - 1 ? qpos : a.ctx_len - 1;
+    const int64_t s0 = (int64_t)span * a.span_steps * kAttnStep;
+    int64_t s1 = s0 + (int64_t)a.span_steps * kAttnStep;
+    if (s1 > last + 1) s1 = last + 1;
+    const int steps = s1 > s0 ? (int)((s1 - s0 + kAttnStep - 1) / kAttnStep) : 0;
+    const int64_t kstride = (int64_t)a.n_kv * HD;
+    const float* Kb = a.K + (int64_t)kvh * HD + l16 * DPL;
+    const float* Vb = a.V + (int64_t)kvh * HD + l16 * DPL;
+    const int jbase = wave * (kAttnStep / 4) + pg;  // + it * 4
+
+    float q[G][DPL], o[G][DPL];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        ld_floats<DPL>(a.Q + ((int64_t)t * a.n_head + kvh * G + g) * HD + l16 * DPL, q[g]);
+#pragma unroll
+        for (int i = 0; i < DPL; i++) o[g][i] = 0.0f;
+    }
+    float m_run = -INFINITY, l_run = 0.0f;  // for heads g == wave (+4): per wave, G <= 8
+    float m_run2 = -INFINITY, l_run2 = 0.0f;
+
+    float kk[IT][DPL], vv[IT][DPL];
+    auto fetch = [&](float (&r)[IT][DPL], const float* base, int step) {
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int64_t j = s0 + (int64_t)step * kAttnStep + jbase + it * 4;
+            ld_floats<DPL>(base + (j < s1 ? j : s0) * kstride, r[it]);
+        }
+    };
+    if (steps > 0) fetch(kk, Kb, 0);
+    for (int st = 0; st < steps; st++) {
+        const int b = st & 1;
+        const int64_t jb = s0 + (int64_t)st * kAttnStep;
+        fetch(vv, Vb, st);
+        // phase 1
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int jl = jbase + it * 4;
+            const bool vis = jb + jl < s1;
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float sv = 0.0f;
+#pragma unroll
+                for (int i = 0; i < DPL; i++) sv = fmaf(q[g][i], kk[it][i], sv);
+                sv = group_sum(sv, 4);
+                if (l16 == 0) sc[b][g][jl] = vis ? sv * a.scale : -INFINITY;
+            }
+        }
+        if (st + 1 < steps) fetch(kk, Kb, st + 1);
+        __syncthreads();
+        // phase 2: wavefront w owns heads w and w + 4
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int g = wave + 4 * r;
+            if (g < G) {
+                float& mr = r ? m_run2 : m_run;
+                float& lr = r ? l_run2 : l_run;
+                const float v = sc[b][g][lane];
+                float mx = v;
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+                const float mn = fmaxf(mr, mx);
+                const float pv = mn == -INFINITY ? 0.0f : expf(v - mn);
+                const float alpha = mr == -INFINITY ? 0.0f : expf(mr - mn);
+                sc[b][g][lane] = pv;
+                float ls = pv;
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off, 64);
+                lr = lr * alpha + ls;
+                mr = mn;
+                if (lane == 0) al[b][g] = alpha;
+            }
+        }
+        __syncthreads();
+        // phase 3
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float alpha = al[b][g];
+#pragma unroll
+            for (int i = 0; i < DPL; i++) o[g][i] *= alpha;
+        }
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int jl = jbase + it * 4;
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float pv = sc[b][g][jl];  // 0 where not visible
+#pragma unroll
+                for (int i = 0; i < DPL; i++) o[g][i] = fmaf(pv, vv[it][i], o[g][i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int g = wave + 4 * r;
+        if (g < G && lane == 0) { ml[g][0] = r ? m_run2 : m_run; ml[g][1] = r ? l_run2 : l_run; }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < DPL; i++) {
+            float v = o[g][i];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (pg == 0) ored[wave][g][l16 * DPL + i] = v;
+        }
+    __syncthreads();
+    const int64_t hb = (int64_t)t * a.n_head + kvh * G;
+    if (a.n_spans == 1) {
+        for (int e = tid; e < G * HD; e += 256) {
+            const int g = e / HD, d = e % HD;
+            a.out[(hb + g) * HD + d] = (ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d]) / ml[g][1];
+        }
+        return;
+    }
+    for (int e = tid; e < G * HD; e += 256) {
+        const int g = e / HD, d = e % HD;
+        a.part_o[((hb + g) * a.n_spans + span) * HD + d] = ored[0][g][d] + ored[1][g][d] + ored[2][g][d] + ored[3][g][d];
+    }
+    if (tid < G) {
+        a.part_ml[((hb + tid) * a.n_spans + span) * 2 + 0] = ml[tid][0];
+        a.part_ml[((hb + tid) * a.n_spans + span) * 2 + 1] = ml[tid][1];
+    }
+}
+
+// One workgroup of 256 threads per (head, row): merge the span partials.
+// Thread (grp, d) with d = tid % HD sums spans grp, grp + 256/HD, ...; the
+// groups are then added in a fixed order, so results are deterministic.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    constexpr int NG = 256 / HD;
+    __shared__ float red[256];
+    __shared__ float accL[NG], acc[NG][HD];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int64_t hb = (int64_t)t * a.n_head + h;
+    const int ns = a.n_spans;
+    const float* pml = a.part_ml + hb * ns * 2;
+    float m = -INFINITY;
+    for (int c = tid; c < ns; c += 256) m = fmaxf(m, pml[2 * c]);
+    red[tid] = m;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+        __syncthreads();
+    }
+    m = red[0];
+    const int d = tid % HD, grp = tid / HD;
+    const float* po = a.part_o + hb * ns * HD + d;
+    float L = 0.0f, o = 0.0f;
+#pragma unroll 4
+    for (int c = grp; c < ns; c += NG) {
+        const float mc = pml[2 * c];
+        const float e = mc == -INFINITY ? 0.0f : expf(mc - m);  // spans past this row's position
+        L = fmaf(pml[2 * c + 1], e, L);
+        o = fmaf(po[(int64_t)c * HD], e, o);
+    }
+    acc[grp][d] = o;
+    if (d == 0) accL[grp] = L;
+    __syncthreads();
+    if (grp == 0) {
+        float os = acc[0][d], ls = accL[0];
+#pragma unroll
+        for (int k = 1; k < NG; k++) { os += acc[k][d]; ls += accL[k]; }
+        a.out[hb * HD + d] = os / ls;
+    }
+}
+
+static int attn_span_wgs() {
+    static int v = -1;
+    if (v < 0) {
+        const int r = resident_blocks(attn_span_kernel<64, 4>, 0);
+        v = r > 0 ? r : 1024;
+    }
+    return v;
+}
+
+static void attn_plan(int n_tok, int n_kv, int64_t ctx_len, int64_t pos0, int* n_spans, int* span_steps) {
+    const int64_t last = pos0 + n_tok - 1 < ctx_len - 1 ? pos0 + n_tok - 1 : ctx_len - 1;
+    const int64_t steps = (last + kAttnStep) / kAttnStep;
+    int64_t want = env_int("GGQ_ATTN_SPANS", 0);
+    if (want <= 0) want = (attn_span_wgs() + (int64_t)n_kv * n_tok - 1) / ((int64_t)n_kv * n_tok);
+    if (want > steps) want = steps;
+    if (want < 1) want = 1;
+    const int64_t per = (steps + want - 1) / want;
+    *span_steps = (int)per;
+    *n_spans = (int)((steps + per - 1) / per);
+}
+
+size_t attn_workspace_floats(int n_tok, int n_head, int head_dim, int64_t ctx_len, int64_t pos0, int n_kv) {
+    int ns, ss;
+    attn_plan(n_tok, n_kv, ctx_len, pos0, &ns, &ss);
+    return ns > 1 ? (size_t)n_tok * n_head * ns * (head_dim + 2) : 0;
+}
+
+hipError_t launch_attn_decode(const float* Q, const float* K, const float* V, int n_tok, int n_head, int n_kv,
+                              int head_dim, int64_t ctx_len, int64_t pos0, float* out, float* ws, hipStream_t s) {
+    if (n_tok == 0) return hipSuccess;
+    const int G = n_head / n_kv;
+    AttnArgs a;
+    a.Q = Q; a.K = K; a.V = V; a.out = out;
+    a.n_head = n_head; a.n_kv = n_kv;
+    attn_plan(n_tok, n_kv, ctx_len, pos0, &a.n_spans, &a.span_steps);
+    a.ctx_len = ctx_len; a.pos0 = pos0;
+    a.scale = 1.0f / sqrtf((float)head_dim);  // cpu_ref.cpp:237
+    a.part_o = ws;
+    a.part_ml = ws ? ws + (size_t)n_tok * n_head * a.n_spans * head_dim : nullptr;
+    if (a.n_spans > 1 && !ws) return hipErrorInvalidValue;
+    const dim3 grid(a.n_spans, n_kv, n_tok);
+#define L(HD_, G_) attn_span_kernel<HD_, G_><<<grid, 256, 0, s>>>(a)
+#define BY_G(HD_)                                 \
+    switch (G) {                                  \
+    case 1: L(HD_, 1); break;                     \
+    case 2: L(HD_, 2); break;                     \
+    case 4: L(HD_, 4); break;                     \
+    case 8: L(HD_, 8); break;                     \
+    default: return hipErrorInvalidValue;         \
+    }
+    if (head_dim == 64) { BY_G(64) }
+    else if (head_dim == 128) { BY_G(128) }
+    else return hipErrorInvalidValue;
+#undef BY_G
+#undef L
+    if (a.n_spans > 1) {
+        if (head_dim == 64) attn_combine_kernel<64><<<dim3(n_head, n_tok), 256, 0, s>>>(a);
+        else attn_combine_kernel<128><<<dim3(n_head, n_tok), 256, 0, s>>>(a);
+    }
+    return hipGetLastError();
+}
+
 // ====================================================================== MoE
 // Routing (main.cpp:3126-3135): top-k experts by descending logit, then a
 // softmax over the selected logits only: w_j = exp(l_j - l_0) / sum.

@@ -77,6 +77,12 @@ hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8
 size_t argmax_workspace_bytes(int M);
 hipError_t launch_argmax_rows(const float* L, int M, int N, int ld, int32_t* idx, float* val, void* ws,
                               hipStream_t s);
+// Decode attention over one layer's KV cache [ctx][n_kv][head_dim] for n_tok
+// query rows at positions pos0.. (head_dim 64 or 128, n_head / n_kv in
+// {1, 2, 4, 8}); ws holds attn_workspace_floats(...) floats.
+size_t attn_workspace_floats(int n_tok, int n_head, int head_dim, int64_t ctx_len, int64_t pos0, int n_kv);
+hipError_t launch_attn_decode(const float* Q, const float* K, const float* V, int n_tok, int n_head, int n_kv,
+                              int head_dim, int64_t ctx_len, int64_t pos0, float* out, float* ws, hipStream_t s);
 // x[m][k] = q[m][k] * sa[m] (dense fp32 [M][K]).
 hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, float* x, hipStream_t s);
 

@@ -123,6 +123,7 @@ SIGNATURES = {
     "ggq_mul_mat_fused_dev": (_I, [_P, _P, _I, _I, _P]),
     "ggq_mul_mat_q8_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _P, _I, _P, _I, _P]),
     "ggq_logits_argmax_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _I, _P, _P, _P, _P]),
+    "ggq_attention_decode_dev": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I64, _I64, _P, _P]),
     "ggq_mul_mat_q8_batch_dev": (_I, [_P, _P, _I, _U32, _I64, _P, _P, _I, _P]),
     "ggq_dequant_dev": (_I, [_P, _P, _U32, _I64, _P, _P]),
     "ggq_quantize_act_dev": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P]),

@@ -177,6 +177,21 @@ int ggq_mul_mat_fused_dev(ggq_ctx* ctx, const ggq_gemv_fused_desc* descs, int n,
 int ggq_logits_argmax_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K, const float* A,
                           int M, int act_mode, float* logits, int32_t* token, float* value, void* stream);
 
+/* Decode attention of n_tok query rows over one layer's KV cache, on the
+ * device.  Q is [n_tok][n_head][head_dim]; K and V are the layer's cache
+ * slabs [ctx_len][n_kv_head][head_dim] (the layout of kv_cache.cpp:42-59,
+ * row p = position p); out is [n_tok][n_head][head_dim]; all fp32, Q/K/V
+ * 16-byte aligned.  Query row t sits at position pos0 + t and attends to
+ * positions 0 .. min(pos0 + t, ctx_len - 1); query head h reads kv head
+ * h / (n_head / n_kv_head).  Result: softmax(q.k / sqrt(head_dim)) . V as
+ * CpuRefBackend::flash_attn (src/backends/cpu_ref.cpp:223-280) computes it
+ * over the GQA-expanded K/V that src/cli/main.cpp:3358-3379 builds with
+ * query_pos = pos + bt; no expanded copy is made here.  head_dim 64 or 128,
+ * n_head / n_kv_head in {1, 2, 4, 8}.  Matches the reference within fp32
+ * rounding (the softmax sum is taken per 64-position chunk, then merged). */
+int ggq_attention_decode_dev(ggq_ctx* ctx, const float* Q, const float* K, const float* V, int n_tok, int n_head,
+                             int n_kv_head, int head_dim, int64_t ctx_len, int64_t pos0, float* out, void* stream);
+
 /* C = sa[m] * sum_k qa[m][k] * w[n][k]: the GGQ_ACT_Q8_ROW matmul on
  * activations already quantized by ggq_quantize_act_dev (row mode; qa dense
  * [M][K], 16-byte aligned, sa [M]).  Lets callers quantize an input once

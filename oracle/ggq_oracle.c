@@ -481,3 +481,69 @@ void orc_rms_norm(const float* x, int n, const float* w, float eps, float* out) 
 void orc_silu(const float* x, int n, float* out) {
     for (int i = 0; i < n; i++) out[i] = x[i] / (1.0f + expf(-x[i]));
 }
+
+/* cpu_ref.cpp:223-280, fp32, one query row. */
+void orc_flash_attn(const float* Q, const float* K, const float* V, int n_head, int hd, int64_t cl,
+                    int64_t query_pos, float* out) {
+    const int64_t qpos = query_pos >= 0 ? query_pos : cl - 1;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(cl > 0 ? cl : 1));
+    float* weights = (float*)malloc(sizeof(float) * (size_t)(cl > 0 ? cl : 1));
+    for (int h = 0; h < n_head; h++) {
+        const float* Qh = Q + (int64_t)h * hd;
+        const float* Kh = K + (int64_t)h * cl * hd;
+        const float* Vh = V + (int64_t)h * cl * hd;
+        float* outh = out + (int64_t)h * hd;
+        for (int64_t j = 0; j < cl; j++) scores[j] = -INFINITY;
+        for (int64_t j = 0; j <= qpos && j < cl; j++) {
+            float sum = 0.0f;
+            for (int d = 0; d < hd; d++) sum += Qh[d] * Kh[j * hd + d];
+            scores[j] = sum * scale;
+        }
+        float max_val = -INFINITY;
+        for (int64_t j = 0; j < cl; j++)
+            if (scores[j] > max_val) max_val = scores[j];
+        float sum = 0.0f;
+        for (int64_t j = 0; j < cl; j++) {
+            weights[j] = expf(scores[j] - max_val);
+            sum += weights[j];
+        }
+        for (int64_t j = 0; j < cl; j++) weights[j] /= sum;
+        for (int d = 0; d < hd; d++) outh[d] = 0.0f;
+        for (int64_t j = 0; j < cl; j++)
+            for (int d = 0; d < hd; d++) outh[d] += weights[j] * Vh[j * hd + d];
+    }
+    free(scores);
+    free(weights);
+}
+
+void orc_flash_attn_f64(const float* Q, const float* K, const float* V, int n_head, int hd, int64_t cl,
+                        int64_t query_pos, double* out) {
+    const int64_t qpos = query_pos >= 0 ? query_pos : cl - 1;
+    const double scale = 1.0 / sqrt((double)hd);
+    const int64_t n = qpos + 1 < cl ? qpos + 1 : cl;
+    double* w = (double*)malloc(sizeof(double) * (size_t)(n > 0 ? n : 1));
+    for (int h = 0; h < n_head; h++) {
+        const float* Qh = Q + (int64_t)h * hd;
+        const float* Kh = K + (int64_t)h * cl * hd;
+        const float* Vh = V + (int64_t)h * cl * hd;
+        double m = -INFINITY;
+        for (int64_t j = 0; j < n; j++) {
+            double s = 0.0;
+            for (int d = 0; d < hd; d++) s += (double)Qh[d] * (double)Kh[j * hd + d];
+            w[j] = s * scale;
+            if (w[j] > m) m = w[j];
+        }
+        double tot = 0.0;
+        for (int64_t j = 0; j < n; j++) {
+            w[j] = exp(w[j] - m);
+            tot += w[j];
+        }
+        for (int d = 0; d < hd; d++) {
+            double acc = 0.0;
+            for (int64_t j = 0; j < n; j++) acc += w[j] * (double)Vh[j * hd + d];
+            out[(int64_t)h * hd + d] = acc / tot;
+        }
+    }
+    free(w);
+}

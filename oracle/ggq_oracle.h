@@ -86,6 +86,17 @@ void   orc_rms_norm(const float* x, int n, const float* w, float eps, float* out
  * out[i] = x[i] / (1 + expf(-x[i])) in fp32. */
 void   orc_silu(const float* x, int n, float* out);
 
+/* Decode attention, restating CpuRefBackend::flash_attn (cpu_ref.cpp:223-280)
+ * in its fp32 order for one query row: Q [n_head][hd]; K, V head-major
+ * [n_head][ctx_len][hd] (the GQA expansion of main.cpp:3358-3379); scores for
+ * positions <= query_pos (< 0: ctx_len - 1), softmax with the max
+ * subtracted, out [n_head][hd] = sum_j w_j V_j. */
+void   orc_flash_attn(const float* Q, const float* K, const float* V, int n_head, int hd, int64_t ctx_len,
+                      int64_t query_pos, float* out);
+/* The same in fp64 (the parity target). */
+void   orc_flash_attn_f64(const float* Q, const float* K, const float* V, int n_head, int hd, int64_t ctx_len,
+                          int64_t query_pos, double* out);
+
 /* MoE FFN oracle (main.cpp:3110-3193) in fp64 over dequantized weights.
  *   x [T][H] fp32, logits [T][E] fp32 router logits
  *   gate/up expert tensor: E consecutive [F][H] matrices (type tg, tu)

@@ -33,6 +33,8 @@ _ORC_SIGS = {
                              _P, _P, _P, _P, _P, _P, _P]),
     "orc_rms_norm": (None, [_P, _I, _P, ctypes.c_float, _P]),
     "orc_silu": (None, [_P, _I, _P]),
+    "orc_flash_attn": (None, [_P, _P, _P, _I, _I, _I64, _I64, _P]),
+    "orc_flash_attn_f64": (None, [_P, _P, _P, _I, _I, _I64, _I64, _P]),
 }
 
 _REF_SIGS = {
@@ -45,6 +47,7 @@ _REF_SIGS = {
     "ref_cpuref_mul_mat": (_I, [_U32, _P, _I, _I, _P, _I, _P]),
     "ref_rms_norm": (_I, [_P, _I, _P, ctypes.c_float, _P]),
     "ref_silu": (_I, [_P, _I, _P]),
+    "ref_flash_attn": (_I, [_P, _P, _P, _I, _I, _I64, _I64, _P]),
 }
 
 
@@ -190,4 +193,25 @@ def silu(x):
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty_like(x)
     lib().orc_silu(x.ctypes.data, x.size, out.ctypes.data)
+    return out
+
+
+def expand_kv(cache, n_head):
+    """main.cpp:3358-3379: the [ctx][n_kv][hd] cache of one layer as head-major
+    [n_head][ctx][hd] with query head h reading kv head h // (n_head / n_kv)."""
+    ctx, n_kv, hd = cache.shape
+    groups = n_head // n_kv
+    return np.ascontiguousarray(np.stack([cache[:, h // groups, :] for h in range(n_head)]), np.float32)
+
+
+def flash_attn(q, Kc, Vc, n_head, query_pos, f64=True):
+    """Attention of query rows q [n_tok][n_head][hd] over cache slabs Kc, Vc
+    [ctx][n_kv][hd]; row t uses query_pos[t]."""
+    ctx, n_kv, hd = Kc.shape
+    K, V = expand_kv(Kc, n_head), expand_kv(Vc, n_head)
+    out = np.empty((q.shape[0], n_head, hd), np.float64 if f64 else np.float32)
+    for t in range(q.shape[0]):
+        qt = np.ascontiguousarray(q[t], np.float32)
+        fn = lib().orc_flash_attn_f64 if f64 else lib().orc_flash_attn
+        fn(qt.ctypes.data, K.ctypes.data, V.ctypes.data, n_head, hd, ctx, int(query_pos[t]), out[t].ctypes.data)
     return out

@@ -85,4 +85,15 @@ int ref_silu(const float* x, int n, float* out) {
     return static_cast<int>(be->silu(p));
 }
 
+// CpuRefBackend::flash_attn (cpu_ref.cpp:223-280) for one query row.
+int ref_flash_attn(const float* Q, const float* K, const float* V, int n_head, int hd, int64_t ctx_len,
+                   int64_t query_pos, float* out) {
+    auto be = create_cpu_ref_backend();
+    AttnParams p;
+    p.Q = Q; p.K = K; p.V = V; p.output = out;
+    p.batch_size = 1; p.n_head = n_head; p.head_dim = hd; p.ctx_len = ctx_len;
+    p.query_pos = query_pos; p.freq_factors = nullptr;
+    return static_cast<int>(be->flash_attn(p));
+}
+
 }  // extern "C"

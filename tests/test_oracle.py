@@ -274,3 +274,30 @@ def test_silu_matches_reference_and_closed_form(orc):
     xd = x.astype(np.float64)
     assert np.allclose(got, xd / (1.0 + np.exp(-xd)), rtol=2e-6, atol=1e-30)
     assert got[601] == 0.0 and got[605] == pytest.approx(-88.0 * np.exp(-88.0), rel=1e-3, abs=1e-36)
+
+
+# ------------------------------------------------------- decode attention
+@pytest.mark.parametrize("n_head,n_kv,hd,ctx,qpos", [(8, 2, 64, 300, 299), (4, 4, 128, 70, 40), (6, 1, 64, 33, 0)])
+def test_flash_attn_matches_reference_and_f64(orc, n_head, n_kv, hd, ctx, qpos):
+    rng = np.random.default_rng(ctx)
+    q = rng.standard_normal((1, n_head, hd)).astype(np.float32)
+    Kc = rng.standard_normal((ctx, n_kv, hd)).astype(np.float32)
+    Vc = rng.standard_normal((ctx, n_kv, hd)).astype(np.float32)
+    got32 = orc.flash_attn(q, Kc, Vc, n_head, [qpos], f64=False)
+    ref = orc.ref_lib()
+    if ref is not None:  # the compiled CpuRefBackend::flash_attn on the expanded K/V, bit for bit
+        K, V = orc.expand_kv(Kc, n_head), orc.expand_kv(Vc, n_head)
+        out = np.empty((n_head, hd), np.float32)
+        assert ref.ref_flash_attn(q[0].ctypes.data, K.ctypes.data, V.ctypes.data, n_head, hd, ctx, qpos,
+                                  out.ctypes.data) == 0
+        assert np.array_equal(got32[0].view(np.uint32), out.view(np.uint32))
+    got64 = orc.flash_attn(q, Kc, Vc, n_head, [qpos])
+    assert orc.rel_l2(got32, got64) < 1e-5
+    # closed form in numpy (fp64), positions past qpos masked
+    K, V = orc.expand_kv(Kc, n_head).astype(np.float64), orc.expand_kv(Vc, n_head).astype(np.float64)
+    s = np.einsum("hd,hjd->hj", q[0].astype(np.float64), K[:, : qpos + 1]) / np.sqrt(hd)
+    w = np.exp(s - s.max(axis=1, keepdims=True))
+    w /= w.sum(axis=1, keepdims=True)
+    assert np.allclose(got64[0], np.einsum("hj,hjd->hd", w, V[:, : qpos + 1]), rtol=1e-10, atol=1e-12)
+    if qpos == 0:  # one visible position: the output is V[0] of each head's kv head
+        assert np.allclose(got64[0], V[:, 0], rtol=0, atol=1e-15)
