@@ -1604,7 +1604,7 @@ hipError_t launch_argmax_rows(const float* L, int M, int N, int ld, int32_t* idx
 
 // =============================================================== attention
 // Decode attention over one layer's KV cache in its native layout
-// [position][kv head][head_dim] (kv_cache.cpp:42-59), for query rows at
+// [position][kv head][head_dim] (kv_cache.cpp:38-48), for query rows at
 // positions pos0, pos0+1, ... (causal: row t sees positions <= pos0 + t).
 // Same result as CpuRefBackend::flash_attn (cpu_ref.cpp:223-280) over the GQA-
 // expanded K/V (main.cpp:3358-3379), without materialising the expansion:
@@ -1783,44 +1783,64 @@ __global__ __launch_bounds__(256) void attn_span_kernel(AttnArgs a) {
     }
 }
 
-// One workgroup of 256 threads per (head, row): merge the span partials.
-// Thread (grp, d) with d = tid % HD sums spans grp, grp + 256/HD, ...; the
-// groups are then added in a fixed order, so results are deterministic.
+// One workgroup of 512 threads per (head, row): merge the span partials in
+// one pass.  Thread (grp, d), d = tid % HD, folds spans grp, grp + 512/HD, ...
+// into a running (m, l, o) (rescaling when the maximum grows); the groups
+// are then merged in a fixed order, so results are deterministic.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    constexpr int NG = 256 / HD;
-    __shared__ float red[256];
-    __shared__ float accL[NG], acc[NG][HD];
+__global__ __launch_bounds__(512) void attn_combine_kernel(AttnArgs a) {
+    constexpr int NG = 512 / HD;
+    __shared__ float gm[NG], gl[NG], go[NG][HD];
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
     const int64_t hb = (int64_t)t * a.n_head + h;
     const int ns = a.n_spans;
     const float* pml = a.part_ml + hb * ns * 2;
-    float m = -INFINITY;
-    for (int c = tid; c < ns; c += 256) m = fmaxf(m, pml[2 * c]);
-    red[tid] = m;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
-        __syncthreads();
-    }
-    m = red[0];
     const int d = tid % HD, grp = tid / HD;
     const float* po = a.part_o + hb * ns * HD + d;
-    float L = 0.0f, o = 0.0f;
-#pragma unroll 4
-    for (int c = grp; c < ns; c += NG) {
-        const float mc = pml[2 * c];
-        const float e = mc == -INFINITY ? 0.0f : expf(mc - m);  // spans past this row's position
-        L = fmaf(pml[2 * c + 1], e, L);
-        o = fmaf(po[(int64_t)c * HD], e, o);
+    // batches of 16 spans: all loads first, then one rescale per batch
+    constexpr int B = 16;
+    float m = -INFINITY, L = 0.0f, o = 0.0f;
+    for (int c0 = grp; c0 < ns; c0 += NG * B) {
+        float mc[B], lc[B], oc[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const int c = c0 + u * NG;
+            const bool ok = c < ns;
+            const float2 v = *(const float2*)(pml + 2 * (ok ? c : 0));
+            const float ov = po[(int64_t)(ok ? c : 0) * HD];
+            mc[u] = ok ? v.x : -INFINITY;  // -inf also marks a span past this row's position
+            lc[u] = v.y;
+            oc[u] = ov;
+        }
+        float mb = m;
+#pragma unroll
+        for (int u = 0; u < B; u++) mb = fmaxf(mb, mc[u]);
+        if (mb == -INFINITY) continue;
+        const float r = m == -INFINITY ? 0.0f : expf(m - mb);
+        L *= r;
+        o *= r;
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const float e = mc[u] == -INFINITY ? 0.0f : expf(mc[u] - mb);
+            L = fmaf(lc[u], e, L);
+            o = fmaf(oc[u], e, o);
+        }
+        m = mb;
     }
-    acc[grp][d] = o;
-    if (d == 0) accL[grp] = L;
+    go[grp][d] = o;
+    if (d == 0) { gm[grp] = m; gl[grp] = L; }
     __syncthreads();
     if (grp == 0) {
-        float os = acc[0][d], ls = accL[0];
+        float mx = gm[0];
 #pragma unroll
-        for (int k = 1; k < NG; k++) { os += acc[k][d]; ls += accL[k]; }
+        for (int k = 1; k < NG; k++) mx = fmaxf(mx, gm[k]);
+        float os = 0.0f, ls = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NG; k++) {
+            const float e = gm[k] == -INFINITY ? 0.0f : expf(gm[k] - mx);
+            os = fmaf(go[k][d], e, os);
+            ls = fmaf(gl[k], e, ls);
+        }
         a.out[hb * HD + d] = os / ls;
     }
 }
@@ -1881,8 +1901,8 @@ hipError_t launch_attn_decode(const float* Q, const float* K, const float* V, in
 #undef BY_G
 #undef L
     if (a.n_spans > 1) {
-        if (head_dim == 64) attn_combine_kernel<64><<<dim3(n_head, n_tok), 256, 0, s>>>(a);
-        else attn_combine_kernel<128><<<dim3(n_head, n_tok), 256, 0, s>>>(a);
+        if (head_dim == 64) attn_combine_kernel<64><<<dim3(n_head, n_tok), 512, 0, s>>>(a);
+        else attn_combine_kernel<128><<<dim3(n_head, n_tok), 512, 0, s>>>(a);
     }
     return hipGetLastError();
 }

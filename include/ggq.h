@@ -179,7 +179,7 @@ int ggq_logits_argmax_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N,
 
 /* Decode attention of n_tok query rows over one layer's KV cache, on the
  * device.  Q is [n_tok][n_head][head_dim]; K and V are the layer's cache
- * slabs [ctx_len][n_kv_head][head_dim] (the layout of kv_cache.cpp:42-59,
+ * slabs [ctx_len][n_kv_head][head_dim] (the layout of kv_cache.cpp:38-48,
  * row p = position p); out is [n_tok][n_head][head_dim]; all fp32, Q/K/V
  * 16-byte aligned.  Query row t sits at position pos0 + t and attends to
  * positions 0 .. min(pos0 + t, ctx_len - 1); query head h reads kv head
