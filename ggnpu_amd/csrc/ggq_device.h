@@ -84,6 +84,21 @@ __device__ __forceinline__ void kq_scale_min(uint32_t w0, uint32_t w1, uint32_t 
     }
 }
 
+// Scales and mins of the sub-block pair 2c, 2c+1 of a K-quant block as four
+// bytes [sc(2c), sc(2c+1), m(2c), m(2c+1)]: the same values as kq_scale_min,
+// gathered with v_perm (the byte pattern depends only on c, which is fixed
+// per lane in the decode GEMV) and without branches.  With b = 2*(c&1),
+// A = scale bytes b, b+1, b+4, b+5 and B = bytes b, b+1, b, b+1 of w2:
+// c < 2 keeps the low 6 bits of A; c >= 2 takes the low / high nibbles of B
+// for sc / m and bits 6-7 of A as bits 4-5.
+__device__ __forceinline__ uint32_t kq_pair(uint32_t w0, uint32_t w1, uint32_t w2, int c) {
+    const uint32_t b = 2u * (uint32_t)(c & 1);
+    const uint32_t a = __builtin_amdgcn_perm(w1, w0, b | (b + 1) << 8 | (b + 4) << 16 | (b + 5) << 24);
+    const uint32_t q = __builtin_amdgcn_perm(w2, w2, b | (b + 1) << 8 | b << 16 | (b + 1) << 24);
+    const uint32_t hi = ((a >> 2) & 0x30303030u) | (q & 0x00000F0Fu) | ((q >> 4) & 0x0F0F0000u);
+    return c >= 2 ? hi : a & 0x3F3F3F3Fu;
+}
+
 // ---------------------------------------------------- IQ4 codebook lookup --
 // Codebook of IQ4_NL/IQ4_XS (src/quant/iq4_nl.cpp:16-18), packed 4 per dword
 // little-endian.  kIq4S: signed entries.  kIq4U: entries + 128 (unsigned).
@@ -293,9 +308,8 @@ template <> struct Piece<T_Q4_K> {
     }
     static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t*, int p) {
         const int c = (p >> 1) & 3;
-        uint32_t sc0, m0, sc1, m1;
-        kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c, sc0, m0);
-        kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c + 1, sc1, m1);
+        const uint32_t sm = kq_pair(r.w[1], r.w[2], r.w[3], c);
+        const uint32_t sc0 = sm & 0xFFu, sc1 = (sm >> 8) & 0xFFu, m0 = (sm >> 16) & 0xFFu, m1 = sm >> 24;
         const float d = h2f(r.w[0] & 0xFFFFu), dm = h2f(r.w[0] >> 16);
         const uint4 q = uint4_at(r.w + 4);
         PieceCodes o;
@@ -323,9 +337,8 @@ template <> struct Piece<T_Q5_K> {
     }
     static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t*, int p) {
         const int c = (p >> 1) & 3;
-        uint32_t sc0, m0, sc1, m1;
-        kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c, sc0, m0);
-        kq_scale_min(r.w[1], r.w[2], r.w[3], 2 * c + 1, sc1, m1);
+        const uint32_t sm = kq_pair(r.w[1], r.w[2], r.w[3], c);
+        const uint32_t sc0 = sm & 0xFFu, sc1 = (sm >> 8) & 0xFFu, m0 = (sm >> 16) & 0xFFu, m1 = sm >> 24;
         const float d = h2f(r.w[0] & 0xFFFFu), dm = h2f(r.w[0] >> 16);
         const uint4 qh = uint4_at(r.w + 4), q = uint4_at(r.w + 8);
         PieceCodes o;

@@ -271,7 +271,7 @@ __device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[U][PPT]
     for (int u = 0; u < U; u++) {
         const int iu = it + u * stride, row = iu * rpi + rsub;
         const bool rvalid = iu < n_iters && row < N;
-        const uint8_t* wrow = W + (int64_t)(rvalid ? row : 0) * row_bytes;
+        const uint8_t* wrow = W + (uint64_t)(uint32_t)(rvalid ? row : 0) * (uint32_t)row_bytes;
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = lp + i * lpr;
@@ -305,7 +305,7 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
         for (int m = 0; m < MB; m++) acc[u][m] = 0.0f;
         const int iu = it + u * stride, row = iu * rpi + rsub;
         const bool rvalid = iu < n_iters && row < a.N;
-        const uint8_t* wrow = W + (int64_t)(rvalid ? row : 0) * a.row_bytes;
+        const uint8_t* wrow = W + (uint64_t)(uint32_t)(rvalid ? row : 0) * (uint32_t)a.row_bytes;
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = lp + i * lpr;
@@ -329,11 +329,20 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
             }
         }
     }
-    const int lg = a.lpr_log2 < 6 ? a.lpr_log2 : 6;
+    // A row spans at least a wavefront in the common case (K >= 2048): the
+    // fixed-count reduction has no per-step branches.
+    if (a.lpr_log2 >= 6) {
 #pragma unroll
-    for (int u = 0; u < U; u++)
+        for (int u = 0; u < U; u++)
 #pragma unroll
-        for (int m = 0; m < MB; m++) acc[u][m] = group_sum(acc[u][m], lg);
+            for (int m = 0; m < MB; m++) acc[u][m] = group_sum(acc[u][m], 6);
+    } else {
+        const int lg = a.lpr_log2;
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int m = 0; m < MB; m++) acc[u][m] = group_sum(acc[u][m], lg);
+    }
     if (a.lpr_log2 > 6) {
         if (lane == 0) {
 #pragma unroll
