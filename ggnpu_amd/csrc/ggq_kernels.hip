@@ -610,13 +610,21 @@ struct MultiArgs {
     int n;
 };
 
-template <int MB, int PPT, int U, bool F = false>
+// KQ: compiled for Q4_K and Q6_K only (the Q4_K_M decode levels), so the
+// register budget is not set by the other formats' decoders (Q5_K's needs
+// one more wavefront's worth of VGPRs than Q4_K's).
+template <int MB, int PPT, int U, bool F = false, bool KQ = false>
 __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     __shared__ float red[2][4][U * MB];
     int q = 0;
     while (q + 1 < ma.n && (int)blockIdx.x >= ma.begin[q + 1]) q++;
     const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
     const int bz = blockIdx.z, gz = gridDim.z;
+    if constexpr (KQ) {
+        if (ma.type[q] == T_Q4_K) gemv_body<T_Q4_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red);
+        else gemv_body<T_Q6_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red);
+        return;
+    }
     switch (ma.type[q]) {
     case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
     case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
@@ -853,9 +861,9 @@ static int multi_mb(int ppt, int M) {
     return mb > cap ? cap : mb;
 }
 
-template <int MB, int PPT, int U, bool F = false>
+template <int MB, int PPT, int U, bool F = false, bool KQ = false>
 static int multi_resident() {
-    return resident_blocks(gemv_multi_kernel<MB, PPT, U, F>, 0);
+    return resident_blocks(gemv_multi_kernel<MB, PPT, U, F, KQ>, 0);
 }
 
 // Independent problems with the same number of activation rows M in one
@@ -886,14 +894,21 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
         }
         return hipSuccess;
     }
-    bool any_fused = false;
-    for (int i = 0; i < n; i++) any_fused = any_fused || fused(ps[i]);
+    bool any_fused = false, kq = true;
+    for (int i = 0; i < n; i++) {
+        any_fused = any_fused || fused(ps[i]);
+        kq = kq && (ps[i].type == T_Q4_K || ps[i].type == T_Q6_K);
+    }
     const int u = any_fused ? 1 : gemv_rows_per_iter();
     const int mb = any_fused ? 1 : multi_mb(ppt, M);
     const int gz = (M + mb - 1) / mb;
+    kq = kq && ppt == 1 && mb == 1 && u == 1;  // the variants compiled with KQ
     int target;
     if (any_fused) {
-        target = ppt == 1 ? multi_resident<1, 1, 1, true>() : multi_resident<1, 2, 1, true>();
+        target = ppt == 1 ? (kq ? multi_resident<1, 1, 1, true, true>() : multi_resident<1, 1, 1, true>())
+                          : multi_resident<1, 2, 1, true>();
+    } else if (kq) {
+        target = multi_resident<1, 1, 1, false, true>();
     } else if (ppt == 1) {
         if (mb == 1) target = u >= 4 ? multi_resident<1, 1, 4>() : u >= 2 ? multi_resident<1, 1, 2>() : multi_resident<1, 1, 1>();
         else if (mb == 2) target = multi_resident<2, 1, 1>();
@@ -916,8 +931,11 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     ma.n = n;
     const dim3 grid(b, 1, gz);
     if (any_fused) {
-        if (ppt == 1) gemv_multi_kernel<1, 1, 1, true><<<grid, 256, 0, s>>>(ma);
+        if (kq) gemv_multi_kernel<1, 1, 1, true, true><<<grid, 256, 0, s>>>(ma);
+        else if (ppt == 1) gemv_multi_kernel<1, 1, 1, true><<<grid, 256, 0, s>>>(ma);
         else gemv_multi_kernel<1, 2, 1, true><<<grid, 256, 0, s>>>(ma);
+    } else if (kq) {
+        gemv_multi_kernel<1, 1, 1, false, true><<<grid, 256, 0, s>>>(ma);
     } else if (ppt == 1) {
         if (mb == 1) {
             if (u >= 4) gemv_multi_kernel<1, 1, 4><<<grid, 256, 0, s>>>(ma);
