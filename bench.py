@@ -327,6 +327,53 @@ def bench_attention(torch, ctx, stream, reps=50):
     return {"workload": "decode attention, 1 token, fp32 KV cache", **res}
 
 
+def bench_host_api(torch, ctx, stream, steps=5, warmup=2):
+    """configs[1] through the drop-in entry point the reference's backend
+    calls, ggq_mul_mat_q (MulMatParams with host A, B and C, synchronous):
+    113 calls per step, one per matmul as main.cpp issues them.  B is the
+    host copy of the raw blocks; the first call of each uploads it to HBM
+    and later calls find it resident (keyed by pointer).  Each call copies
+    A in and C out over PCIe and waits: this is the PCIe-inclusive rate, not
+    the benchmark value."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(99)
+    host = []
+    for layer in range(LLAMA_LAYERS):
+        for name, t, N, K in LLAMA_LAYER:
+            x = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).cpu().numpy()
+            host.append((t, N, K, gl.encode(t, x)))
+    t, N, K = LLAMA_OUTPUT[1:]
+    x = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).cpu().numpy()
+    host.append((t, N, K, gl.encode(t, x)))
+    rng = np.random.default_rng(5)
+    acts = {K: rng.standard_normal(K).astype(np.float32) for K in {h[2] for h in host}}
+    outs = [np.empty(N, np.float32) for _, N, _, _ in host]
+    params = []
+    for (t, N, K, raw), out in zip(host, outs):
+        p = gl.MulMatParams()
+        p.A, p.B, p.C = acts[K].ctypes.data, raw.ctypes.data, out.ctypes.data
+        p.M, p.N, p.K, p.n_batches, p.B_type = 1, N, K, 1, t
+        params.append(p)
+
+    def step():
+        for p in params:
+            st = ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(p), 0)
+            if st != 0:
+                ctx.check(st, "mul_mat_q")
+
+    for _ in range(warmup):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    sec = (time.perf_counter() - t0) / steps
+    nbytes = sum(gl.row_bytes(t, K) * N + 4 * (K + N) for t, N, K, _ in host)
+    return {"workload": "configs[1] decode step as 113 synchronous ggq_mul_mat_q calls (host A/B/C, weights "
+                        "resident after the first call)",
+            "ms_per_step": round(sec * 1e3, 3), "GBps": round(nbytes / sec / 1e9, 1),
+            "us_per_call": round(sec * 1e6 / len(params), 2)}
+
+
 def bench_prefill(torch, ctx, stream, steps=3):
     """28 layers of Q8_0 matmuls on 512 tokens, per-row int8
     activations (reference XDNA semantics).  Each layer quantizes its four
@@ -510,7 +557,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
-    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "fused", "attention", "copy"],
+    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "fused", "attention", "host", "copy"],
                     default=None,
                     help="run one workload only and print its result (profiling aid)")
     ap.add_argument("--per-matmul", action="store_true",
@@ -542,10 +589,10 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_per_copy": src.numel(), "copies": 4}), flush=True)
         return
-    if args.only in ("config1", "prefill", "config4", "moe", "logits", "fused", "attention"):
+    if args.only in ("config1", "prefill", "config4", "moe", "logits", "fused", "attention", "host"):
         res = {"config1": bench_config1, "prefill": bench_prefill, "config4": bench_config4,
                "moe": bench_config5, "logits": bench_logits, "fused": bench_decode_fused,
-               "attention": bench_attention}[args.only](
+               "attention": bench_attention, "host": bench_host_api}[args.only](
                    torch, ctx, stream)
         print(json.dumps({"only": args.only, **res}), flush=True)
         ctx.close()
@@ -592,7 +639,7 @@ def main():
     if not args.no_extra:
         out["extra"] = {"config1": bench_config1(torch, ctx, stream)}
         for key, fn in (("config3_prefill", bench_prefill), ("config4_iq4_q5k", bench_config4),
-                        ("config5_moe", bench_config5), ("logits_argmax", bench_logits), ("attention_decode", bench_attention),
+                        ("config5_moe", bench_config5), ("logits_argmax", bench_logits), ("attention_decode", bench_attention), ("host_api_decode", bench_host_api),
                         ("decode_fused", bench_decode_fused)):
             try:
                 out["extra"][key] = fn(torch, ctx, stream)

@@ -51,6 +51,7 @@ struct ggq_ctx {
     Buffer part;  // GEMM split-K partial tiles
     Buffer logits;  // vocab projection output when the caller does not keep it
     Buffer attn;  // attention chunk partials
+    Buffer pin;   // pinned host staging of A and C for the synchronous host-pointer entry points
 };
 
 namespace {
@@ -215,6 +216,25 @@ ggq_weight* upload(ggq_ctx* c, const void* raw, uint32_t type, int64_t N, int64_
 }
 
 // Synchronous host-pointer matmul against a resident weight.
+// Pinned host buffer of at least `need` bytes (grown by reallocation;
+// hipHostFree waits for the device).
+hipError_t ensure_pinned(Buffer& b, size_t need) {
+    if (b.size >= need) return hipSuccess;
+    if (b.ptr) hipHostFree(b.ptr);
+    b.ptr = nullptr;
+    b.size = 0;
+    const size_t sz = need + need / 4 + 4096;
+    hipError_t e = hipHostMalloc(&b.ptr, sz, hipHostMallocDefault);
+    if (e != hipSuccess) return e;
+    b.size = sz;
+    return hipSuccess;
+}
+
+// Synchronous matmul with host A and C: the caller's rows are packed into a
+// pinned staging buffer that a copy kernel reads (and the result is written
+// back the same way).  Copies from pageable memory go through the runtime's
+// own staging and DMA-engine copies have a fixed latency; both measured
+// slower than a copy kernel for the small vectors of a decode step.
 int mul_mat_host(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float* C, int ldc, int M,
                  int act_mode) {
     int st = check_matmul_shape(c, w->type, w->N, w->K, M, lda, ldc, act_mode);
@@ -224,17 +244,21 @@ int mul_mat_host(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float
     const size_t c_bytes = sizeof(float) * (size_t)M * w->N;
     hipError_t e = ensure(c->io, align256(a_bytes) + c_bytes);
     if (e != hipSuccess) return hip_status(c, e, "io buffer");
+    if ((e = ensure_pinned(c->pin, align256(a_bytes) + c_bytes)) != hipSuccess) return hip_status(c, e, "pinned buffer");
     float* dA = (float*)c->io.ptr;
     float* dC = (float*)((char*)c->io.ptr + align256(a_bytes));
-    e = hipMemcpy2DAsync(dA, sizeof(float) * w->K, A, sizeof(float) * (size_t)lda, sizeof(float) * w->K, M,
-                         hipMemcpyHostToDevice, c->stream);
+    float* hA = (float*)c->pin.ptr;
+    float* hC = (float*)((char*)c->pin.ptr + align256(a_bytes));
+    for (int m = 0; m < M; m++) memcpy(hA + (size_t)m * w->K, A + (size_t)m * lda, sizeof(float) * w->K);
+    e = ggq::launch_copy_bytes(dA, hA, a_bytes, c->stream);
     if (e != hipSuccess) return hip_status(c, e, "copy A");
     st = mul_mat_queue(c, w->dev, w->type, w->N, w->K, dA, (int)w->K, dC, (int)w->N, M, act_mode, c->stream);
     if (st != GGQ_OK) return st;
-    e = hipMemcpy2DAsync(C, sizeof(float) * (size_t)ldc, dC, sizeof(float) * w->N, sizeof(float) * w->N, M,
-                         hipMemcpyDeviceToHost, c->stream);
+    e = ggq::launch_copy_bytes(hC, dC, c_bytes, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    return hip_status(c, e, "copy C");
+    if (e != hipSuccess) return hip_status(c, e, "copy C");
+    for (int m = 0; m < M; m++) memcpy(C + (size_t)m * ldc, hC + (size_t)m * w->N, sizeof(float) * w->N);
+    return set_status(c, GGQ_OK);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -287,6 +311,7 @@ void ggq_destroy(ggq_ctx* c) {
     if (c->part.ptr) hipFree(c->part.ptr);
     if (c->logits.ptr) hipFree(c->logits.ptr);
     if (c->attn.ptr) hipFree(c->attn.ptr);
+    if (c->pin.ptr) hipHostFree(c->pin.ptr);
     hipStreamDestroy(c->stream);
     delete c;
 }

@@ -1531,6 +1531,30 @@ hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8
     return launch_gemm_i8_multi(type, &d, 1, K, qa, sa, M, part, s);
 }
 
+// Byte copy by the shader cores, used between pinned host memory and HBM
+// for the small per-call vectors of the synchronous entry points (a copy
+// kernel's launch costs less than a DMA-engine transfer at these sizes).
+// 16-byte chunks when both ends are 16-byte aligned, then the tail.
+__global__ __launch_bounds__(256) void copy_bytes_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                         size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t n16 = n / 16;
+    if (i < n16) {
+        ((uint4*)dst)[i] = ((const uint4*)src)[i];
+    } else if (i < n16 + (n & 15)) {
+        const size_t b = n16 * 16 + (i - n16);
+        dst[b] = src[b];
+    }
+}
+
+hipError_t launch_copy_bytes(void* dst, const void* src, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (((uintptr_t)dst | (uintptr_t)src) & 15u) return hipMemcpyAsync(dst, src, n, hipMemcpyDefault, s);
+    const size_t items = n / 16 + (n & 15);
+    copy_bytes_kernel<<<(unsigned)((items + 255) / 256), 256, 0, s>>>((const uint8_t*)src, (uint8_t*)dst, n);
+    return hipGetLastError();
+}
+
 // x_eff[m][k] = q[m][k] * scale[m] (fp32) from pre-quantized activations.
 __global__ __launch_bounds__(256) void dequant_act_kernel(const int8_t* __restrict__ q, const float* __restrict__ sa,
                                                           int M, int K, float* __restrict__ x) {

@@ -83,6 +83,8 @@ hipError_t launch_argmax_rows(const float* L, int M, int N, int ld, int32_t* idx
 size_t attn_workspace_floats(int n_tok, int n_head, int head_dim, int64_t ctx_len, int64_t pos0, int n_kv);
 hipError_t launch_attn_decode(const float* Q, const float* K, const float* V, int n_tok, int n_head, int n_kv,
                               int head_dim, int64_t ctx_len, int64_t pos0, float* out, float* ws, hipStream_t s);
+// n-byte copy by a kernel (either end may be pinned host memory).
+hipError_t launch_copy_bytes(void* dst, const void* src, size_t n, hipStream_t s);
 // x[m][k] = q[m][k] * sa[m] (dense fp32 [M][K]).
 hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, float* x, hipStream_t s);
 

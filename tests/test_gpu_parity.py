@@ -309,6 +309,24 @@ def test_mul_mat_q_host_api_and_errors(ctx, orc):
     assert ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(p), 7) == gl.Status.INVALID_PARAM
 
 
+@pytest.mark.parametrize("M,N,lda,ldc", [(1, 33, 512, 33), (3, 37, 520, 41), (5, 2048, 517, 2049)])
+def test_mul_mat_q_host_strided_rows(ctx, orc, M, N, lda, ldc):
+    """Host A/C with row strides (lda > K, ldc > N) and odd N: the rows are
+    packed through the pinned staging buffer, the copy kernels handle the
+    byte tail, and C's padding columns are left untouched."""
+    t, K = 12, 512
+    raw = weights(t, N, K, seed=N)
+    rng = np.random.default_rng(M + N)
+    A = rng.standard_normal((M, lda)).astype(np.float32)
+    C = np.full((M, ldc), -7.0, np.float32)
+    p = gl.MulMatParams()
+    p.A, p.B, p.C = A.ctypes.data, raw.ctypes.data, C.ctypes.data
+    p.M, p.N, p.K, p.lda, p.ldb, p.ldc, p.n_batches, p.B_type = M, N, K, lda, K, ldc, 1, t
+    ctx.check(ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(p), 0), "mul_mat_q")
+    assert orc.rel_l2(C[:, :N], orc.mul_mat_f64(t, raw, N, K, np.ascontiguousarray(A[:, :K]), 0)) < TOL
+    assert np.all(C[:, N:] == -7.0)
+
+
 def test_weight_upload_roundtrip(ctx, orc):
     t, N, K = 23, 40, 1024
     raw = weights(t, N, K, seed=9)
