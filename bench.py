@@ -531,23 +531,33 @@ def bench_config5(torch, ctx, stream, steps=20):
 
 
 def cpu_baseline(host_layer0, budget_s=8.0):
-    """Single-core fp32 CpuRefBackend::mul_mat_q restatement (oracle, bit-exact
-    with the reference's output) on layer 0 of the decode step."""
+    """The reference's CPU path on layer 0 of the decode step, one core: the
+    compiled reference CpuRefBackend::mul_mat_q (oracle/_ref, built from the
+    reference's own sources) where that library is present ("reference"),
+    else the bit-identical restatement orc_mul_mat_cpuref_f32 ("port")."""
     from oracle import oracle as orc
+    ref = orc.ref_lib()
     rng = np.random.default_rng(0)
     work = [(m.t, raw, m.N, m.K, rng.standard_normal((1, m.K)).astype(np.float32)) for m, raw in host_layer0]
+    outs = [np.empty((1, N), np.float32) for _, _, N, _, _ in work]
     nbytes, t0, reps = 0, time.perf_counter(), 0
     while True:
-        for t, raw, N, K, A in work:
-            orc.mul_mat_cpuref_f32(t, raw, N, K, A)
+        for (t, raw, N, K, A), C in zip(work, outs):
+            if ref is not None:
+                st = ref.ref_cpuref_mul_mat(t, raw.ctypes.data, N, K, A.ctypes.data, 1, C.ctypes.data)
+                assert st == 0, st
+            else:
+                orc.mul_mat_cpuref_f32(t, raw, N, K, A)
             nbytes += gl.row_bytes(t, K) * N + 4 * (K + N)
         reps += 1
         if time.perf_counter() - t0 > budget_s:
             break
     el = time.perf_counter() - t0
-    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+    what = ("oracle/_ref CpuRefBackend::mul_mat_q (reference sources, -O3)" if ref is not None
+            else "oracle/ggq_oracle.c orc_mul_mat_cpuref_f32")
+    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "reference" if ref is not None else "port",
             "sample": f"Llama-3.2-1B layer 0 (q,k,v,o,gate,up,down; 38.8 MB Q4_K/Q6_K), batch 1, "
-                      f"{reps} passes in {el:.1f}s, oracle/ggq_oracle.c orc_mul_mat_cpuref_f32"}
+                      f"{reps} passes in {el:.1f}s, {what}"}
 
 
 def main():
