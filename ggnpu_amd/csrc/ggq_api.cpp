@@ -648,9 +648,17 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     // gate / up: rows F, K = H, activations gathered by token.
     g.N = F; g.K = H; g.X = p->x; g.ldx = H; g.x_idx = tok; g.ldy = F;
     g.type = p->gate_type; g.W = p->gate_exps; g.w_group_stride = (int64_t)F * ggq::row_bytes(p->gate_type, H); g.Y = G;
-    if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe gate");
-    g.type = p->up_type; g.W = p->up_exps; g.w_group_stride = (int64_t)F * ggq::row_bytes(p->up_type, H); g.Y = U;
-    if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe up");
+    if (p->up_type == p->gate_type && H % 32 == 0) {
+        // gate and up of each expert in one launch: each workgroup loads a
+        // token's activations once for both.
+        g.W2 = p->up_exps; g.Y2 = U; g.n1 = F; g.N = 2 * F;
+        if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe gate+up");
+        g.W2 = nullptr; g.Y2 = nullptr; g.n1 = 0;
+    } else {
+        if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe gate");
+        g.type = p->up_type; g.W = p->up_exps; g.w_group_stride = (int64_t)F * ggq::row_bytes(p->up_type, H); g.Y = U;
+        if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe up");
+    }
     if ((e = ggq::launch_swiglu(G, U, Hh, (int64_t)nk * F, s)) != hipSuccess) return hip_status(c, e, "swiglu");
     // down: rows H, K = F, activations are the sorted pair rows themselves.
     g.N = H; g.K = F; g.X = Hh; g.ldx = F; g.x_idx = nullptr; g.ldy = H; g.Y = D;
@@ -666,9 +674,15 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
         q.M = T;
         q.N = F; q.K = H; q.X = p->x; q.ldx = H; q.ldy = F;
         q.type = p->gate_type; q.W = p->gate_shexp; q.Y = SG;
-        if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared gate");
-        q.type = p->up_type; q.W = p->up_shexp; q.Y = SU;
-        if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared up");
+        if (p->up_type == p->gate_type && H % 32 == 0) {
+            q.W2 = p->up_shexp; q.Y2 = SU; q.n1 = F; q.N = 2 * F;
+            if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared gate+up");
+            q.W2 = nullptr; q.Y2 = nullptr; q.n1 = 0;
+        } else {
+            if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared gate");
+            q.type = p->up_type; q.W = p->up_shexp; q.Y = SU;
+            if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared up");
+        }
         if ((e = ggq::launch_swiglu(SG, SU, SH, (int64_t)T * F, s)) != hipSuccess) return hip_status(c, e, "shared swiglu");
         q.N = H; q.K = F; q.X = SH; q.ldx = F; q.ldy = H; q.type = p->down_type; q.W = p->down_shexp; q.Y = Dsh;
         if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared down");

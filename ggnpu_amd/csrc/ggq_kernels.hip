@@ -242,7 +242,20 @@ struct GemvArgs {
     const float* norm_w;   // [K] or null (weight 1)
     const float* R;        // residual: Y = R + result, R [M][ldr] (may alias Y)
     int ldr;
+    // Paired matrices (n1 > 0): rows [0, n1) come from W / go to Y, rows
+    // [n1, N) are rows 0.. of W2 / Y2 (same type, K, group stride and ldy):
+    // e.g. an expert's gate and up in one launch, one activation load each.
+    const uint8_t* W2;
+    float* Y2;
+    int n1;
 };
+
+// Start of weight row `row` of a (group's) matrix, or of the paired one.
+__device__ __forceinline__ const uint8_t* weight_row(const uint8_t* W, const uint8_t* W2, int n1, int64_t row_bytes,
+                                                     int row) {
+    const bool second = n1 > 0 && row >= n1;
+    return (second ? W2 : W) + (uint64_t)(uint32_t)(second ? row - n1 : row) * (uint32_t)row_bytes;
+}
 
 // Sum over aligned groups of 2^lg lanes (lg = 0..6): afterwards every lane of
 // a group of <= 32 lanes holds the group sum; for lg = 6 lane 0 holds the
@@ -266,12 +279,12 @@ __device__ __forceinline__ float group_sum(float v, int lg) {
 template <int T, int PPT, int U>
 __device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[U][PPT], const uint8_t* W, int64_t row_bytes,
                                            int it, int stride, int n_iters, int rpi, int rsub, int N, int lp, int lpr,
-                                           int P) {
+                                           int P, const uint8_t* W2 = nullptr, int n1 = 0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const int iu = it + u * stride, row = iu * rpi + rsub;
         const bool rvalid = iu < n_iters && row < N;
-        const uint8_t* wrow = W + (uint64_t)(uint32_t)(rvalid ? row : 0) * (uint32_t)row_bytes;
+        const uint8_t* wrow = weight_row(W, W2, n1, row_bytes, rvalid ? row : 0);
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = lp + i * lpr;
@@ -282,7 +295,7 @@ __device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[U][PPT]
 
 template <int T, int MB, int PPT, int U, bool F>
 __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U][PPT], const GemvArgs& a,
-                                          const uint8_t* W, int it, int stride, int n_iters, int rpi, int lp, int lpr,
+                                          const uint8_t* W, const uint8_t* W2, int it, int stride, int n_iters, int rpi, int lp, int lpr,
                                           int P, int wave, int lane, int rsub, int m0, int mc, int mcount,
                                           const float (&xr)[PPT][MB][32], const float (&xs)[PPT][MB][2],
                                           float (&red)[2][4][U * MB], int& parity) {
@@ -305,7 +318,7 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
         for (int m = 0; m < MB; m++) acc[u][m] = 0.0f;
         const int iu = it + u * stride, row = iu * rpi + rsub;
         const bool rvalid = iu < n_iters && row < a.N;
-        const uint8_t* wrow = W + (uint64_t)(uint32_t)(rvalid ? row : 0) * (uint32_t)a.row_bytes;
+        const uint8_t* wrow = weight_row(W, W2, a.n1, a.row_bytes, rvalid ? row : 0);
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = lp + i * lpr;
@@ -376,7 +389,8 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
                         if (F && a.silu) v = v / (1.0f + expf(-v));  // cpu_ref.cpp:200-209
                         const int64_t mrow = m0 + mc + m;
                         if (F && a.R) v = res[u][m] + v;
-                        a.Y[mrow * a.ldy + row] = v;
+                        if (a.n1 > 0 && row >= a.n1) a.Y2[mrow * a.ldy + (row - a.n1)] = v;
+                        else a.Y[mrow * a.ldy + row] = v;
                     }
             }
         }
@@ -465,6 +479,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
     const int rpi = 256 >> lpr_log2;
     const int P = a.K >> 5;
     const uint8_t* W = a.W + (int64_t)by * a.w_group_stride;
+    const uint8_t* W2 = a.n1 > 0 ? a.W2 + (int64_t)by * a.w_group_stride : nullptr;
     int m0 = 0, mcount = a.M;
     if (a.grp_off) {
         m0 = a.grp_off[by];
@@ -479,7 +494,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
         Raw ra[U][PPT], rb[U][PPT];
         int it = bx;
         // The first weight fetch is issued before the activations are read.
-        gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
+        gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
         float xr[PPT][MB][32];
         float xs[PPT][MB][2];
 #pragma unroll
@@ -550,24 +565,24 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
             // Fetch, then decode/multiply/reduce; latency is hidden by the
             // other resident wavefronts.
             while (true) {
-                gemv_rows<T, MB, PPT, U, F>(ra, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc,
+                gemv_rows<T, MB, PPT, U, F>(ra, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc,
                                          mcount, xr, xs, red, parity);
                 it += step;
                 if (it >= n_iters) break;
-                gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
+                gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
             }
             continue;
         }
         // Ping-pong between ra and rb: fetch the next U row-iterations, then
         // decode/multiply/reduce the current ones.
         while (it < n_iters) {
-            gemv_fetch<T, PPT, U>(rb, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
-            gemv_rows<T, MB, PPT, U, F>(ra, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
+            gemv_fetch<T, PPT, U>(rb, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
+            gemv_rows<T, MB, PPT, U, F>(ra, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
                                      xr, xs, red, parity);
             it += step;
             if (it >= n_iters) break;
-            gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P);
-            gemv_rows<T, MB, PPT, U, F>(rb, a, W, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
+            gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
+            gemv_rows<T, MB, PPT, U, F>(rb, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
                                      xr, xs, red, parity);
             it += step;
         }
@@ -786,6 +801,9 @@ static GemvPlan plan_gemv(const GemvProblem& p) {
     a.norm_w = p.norm_w;
     a.R = p.R;
     a.ldr = p.ldr;
+    a.W2 = (const uint8_t*)p.W2;
+    a.Y2 = p.Y2;
+    a.n1 = p.n1;
     g.ppt = (P + lpr - 1) / lpr;
     g.n_iters = (p.N + rpi - 1) / rpi;
     g.mrows = p.grp_off ? p.max_group_rows : p.M;
@@ -797,6 +815,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     const GemvPlan g = plan_gemv(p);
     GemvArgs a = g.a;
     const int groups = p.groups > 0 ? p.groups : 1;
+    if (p.n1 > 0 && (g.simple || fused(p) || !p.W2 || !p.Y2 || p.n1 >= p.N)) return hipErrorInvalidValue;
     if (g.simple) {
         if (p.X2 || p.rms || p.R || p.silu) return hipErrorInvalidValue;  // fused options need K % 32 == 0
         gemv_simple_kernel<T><<<dim3((p.N + 255) / 256, groups), 256, 0, s>>>(a);

@@ -45,6 +45,12 @@ struct GemvProblem {
     const float* norm_w;
     const float* R;        // Y = R + result, R [M][ldr]
     int ldr;
+    // Paired matrices (n1 > 0, N = n1 + rows of W2): rows [0, n1) from W into
+    // Y, the rest from W2 (same type, K, group stride) into Y2 (same ldy).
+    // Not with the fused options; K a multiple of 32.
+    const void* W2;
+    float* Y2;
+    int n1;
 };
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t s);
 // Several independent M = 1 problems in as few launches as possible.
