@@ -106,7 +106,11 @@ hipError_t ensure_gemm_ws(ggq_ctx* c, const ggq::GemmPlan& pl, float** part) {
     return e;
 }
 
-hipStream_t pick_stream(ggq_ctx* c, void* s) { return s ? (hipStream_t)s : c->stream; }
+// Stream of a device-pointer call: the caller's, or the HIP default (null)
+// stream for NULL, as HIP APIs treat a null stream argument.  (The context's
+// own stream is non-blocking and is used only inside the synchronous
+// entry points, which wait for it before returning.)
+hipStream_t pick_stream(ggq_ctx*, void* s) { return (hipStream_t)s; }
 
 int check_matmul_shape(ggq_ctx* c, uint32_t type, int64_t N, int64_t K, int M, int lda, int ldc,
                        int act_mode) {
@@ -323,7 +327,7 @@ int ggq_is_available(const ggq_ctx* c) { return c != nullptr; }
 
 int ggq_sync(ggq_ctx* c) {
     GGQ_GUARD(c)
-    return hip_status(c, hipStreamSynchronize(c->stream), "sync");
+    return hip_status(c, hipDeviceSynchronize(), "sync");  // every stream the calls used
     GGQ_END(c)
 }
 

@@ -314,9 +314,11 @@ template <> struct Piece<T_Q4_K> {
         const uint4 q = uint4_at(r.w + 4);
         PieceCodes o;
         o.u[0] = and4(q, 0x0F0F0F0Fu);
-        o.u[1] = and4(shr4(q, 4), 0x0F0F0F0Fu);
+        // Run 1 keeps the high nibbles in place (byte = 16 * code, no shift)
+        // and takes the 1/16 in its scale; both factors are exact.
+        o.u[1] = and4(q, 0xF0F0F0F0u);
         o.a[0] = d * (float)sc0; o.b[0] = -(dm * (float)m0);
-        o.a[1] = d * (float)sc1; o.b[1] = -(dm * (float)m1);
+        o.a[1] = (d * (float)sc1) * 0.0625f; o.b[1] = -(dm * (float)m1);
         return o;
     }
 };

@@ -324,6 +324,7 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
             const int p = lp + i * lpr;
             const bool ok = p < P;
             const PieceCodes pc = Piece<T>::decode(raw[u][i], wrow, ok ? p : 0);
+            float tp[MB];
 #pragma unroll
             for (int r = 0; r < 2; r++) {
                 float f[16];
@@ -336,10 +337,16 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
                         s0 = fmaf(xr[i][m][16 * r + j], f[j], s0);
                         s1 = fmaf(xr[i][m][16 * r + j + 1], f[j + 1], s1);
                     }
-                    const float t = fmaf(pc.a[r], s0 + s1, pc.b[r] * xs[i][m][r]);
-                    acc[u][m] += ok ? t : 0.0f;
+                    if (r == 0) {
+                        tp[m] = fmaf(pc.a[0], s0 + s1, pc.b[0] * xs[i][m][0]);
+                    } else {
+                        tp[m] = fmaf(pc.a[1], s0 + s1, tp[m]);
+                        tp[m] = fmaf(pc.b[1], xs[i][m][1], tp[m]);
+                    }
                 }
             }
+#pragma unroll
+            for (int m = 0; m < MB; m++) acc[u][m] += ok ? tp[m] : 0.0f;
         }
     }
     // A row spans at least a wavefront in the common case (K >= 2048): the

@@ -73,7 +73,8 @@ const char* ggq_last_error_message(const ggq_ctx* ctx);
 const char* ggq_name(const ggq_ctx* ctx);
 /* Backend::is_available (backend.h:157). */
 int ggq_is_available(const ggq_ctx* ctx);
-/* Backend::sync (backend.h:155): waits for all work on the context stream. */
+/* Backend::sync (backend.h:155): waits for all work queued on the context's
+ * device (the context stream and the streams passed to the *_dev calls). */
 int ggq_sync(ggq_ctx* ctx);
 
 /* ------------------------------------------------ host-pointer, synchronous */
@@ -120,7 +121,8 @@ int ggq_mul_mat(ggq_ctx* ctx, const ggq_weight* w, const float* A, int lda, floa
 
 /* --------------------------------------- device-pointer, asynchronous */
 /* All pointers below are device pointers; work is queued on `stream`
- * (a hipStream_t; NULL = the context's stream) and the call returns without
+ * (a hipStream_t; NULL = the HIP default stream, so the work is ordered
+ * with the caller's default-stream work) and the call returns without
  * waiting.  W must be 16-byte aligned and readable for 256 bytes past its
  * last block (allocations made by ggq_weight_upload are). */
 
