@@ -597,7 +597,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
 }
 
 template <int T, int MB, int PPT, int U, bool F = false>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+// Two rows per pass: held to 3 wavefronts per SIMD (168 VGPRs; Q4_K spills
+// a few registers), where the natural allocation gave 2.  That variant is
+// the MoE default (each expert sees ~2 tokens: the decoded codes are shared).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MB == 2 ? 3 : 1))) void gemv_kernel(GemvArgs a) {
     __shared__ float red[2][4][U * MB];
     if constexpr (MB > 1) {
         if (a.grp_off) {
@@ -769,7 +772,7 @@ static int env_int(const char* name, int dflt) {
 // from cache.  These knobs are read at every multi-row / grouped launch
 // (never on the single-row decode path), so a process can switch them.
 static int gemv_mb_cap() { const int v = env_int("GGQ_GEMV_MBCAP", 1); return v < 1 ? 1 : v; }
-static int moe_mb() { return env_int("GGQ_MOE_MB", 1); }
+static int moe_mb() { return env_int("GGQ_MOE_MB", 2); }
 static int moe_gx() { return env_int("GGQ_MOE_GX", 0); }
 static int moe_rounds() { const int v = env_int("GGQ_MOE_ROUNDS", 4); return v < 1 ? 1 : v; }
 
