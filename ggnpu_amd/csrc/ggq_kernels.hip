@@ -1319,6 +1319,16 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmMultiArgs a) {
             const int st = sb + d;
             if (st >= st1) break;
             const int buf = (st - st0) & 1;
+            // Formats without a min term: the epilogue of group g-1 follows
+            // the MFMA of group g, pinned by scheduling barriers, so it
+            // overlaps that MFMA and stays ahead of the stage stores and the
+            // barrier (left to itself the scheduler issues all four MFMAs
+            // and sinks every epilogue below the barrier, where the
+            // workgroup's wavefronts run them together while the MFMA pipe
+            // idles).  Two products are live at a time.
+            constexpr bool kGLag = !kMin && TM * TN == 1;
+            v16i Pq[2];
+            float dq[2];
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 v4i A[TM], B[TN];
@@ -1334,6 +1344,25 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmMultiArgs a) {
                     B[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
                     dl[j] = Bd[buf][wn + 32 * j + li][g];
                     ml[j] = Bm[buf][wn + 32 * j + li][g];
+                }
+                if constexpr (kGLag) {
+                    Pq[g & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], B[0], zero, 0, 0, 0);
+                    dq[g & 1] = dl[0];
+                    if (g > 0) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++)
+                            acc[0][0][r] = fmaf(dq[(g - 1) & 1], (float)Pq[(g - 1) & 1][r], acc[0][0][r]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (g == G - 1) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[0][0][r] = fmaf(dq[g & 1], (float)Pq[g & 1][r], acc[0][0][r]);
+                        // An opaque use of the accumulators: IR-level sinking
+                        // cannot move the epilogue below this point.
+#pragma unroll
+                        for (int r = 0; r < 16; r++) asm volatile("" : "+v"(acc[0][0][r]));
+                    }
+                    continue;
                 }
                 v16i S[TM];
                 if constexpr (kMin) {
