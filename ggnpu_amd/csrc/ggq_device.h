@@ -280,6 +280,23 @@ __device__ __forceinline__ uint32_t align2(uint32_t hi, uint32_t lo, uint32_t s)
     return __builtin_amdgcn_alignbyte(hi, lo, s);
 }
 
+// Blocks of 2-byte-aligned formats (Q8_0: 34 bytes, IQ4_NL: 18) are read as
+// a dword window from the aligned-down base b4.  Dword i of the stream that
+// starts 2 bytes after the block base is bytes 2..5 of (w[i], w[i+1]) when
+// the base is 4-aligned and w[i+1] when it is not: one v_perm_b32 with a
+// per-block selector instead of a shift and a select per dword.
+__device__ __forceinline__ uint32_t half_sel(const uint8_t* base) {
+    return ((uint32_t)(uintptr_t)base & 2u) ? 0x07060504u : 0x05040302u;
+}
+__device__ __forceinline__ uint32_t half_pick(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// The fp16 at the block base: the high half of w[0] when the base is not
+// 4-aligned, the low half when it is.
+__device__ __forceinline__ float half_d(uint32_t w0, const uint8_t* base) {
+    return h2f(w0 >> (((uint32_t)(uintptr_t)base & 2u) << 3));
+}
+
 __device__ __forceinline__ uint4 uint4_at(const uint32_t* w) { return make_uint4(w[0], w[1], w[2], w[3]); }
 
 // Dwords i..i+3 of a byte stream held as a window shifted by `s` bytes.
@@ -405,11 +422,12 @@ template <> struct Piece<T_Q8_0> {
         return r;
     }
     static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
-        const bool odd = ((uint32_t)(uintptr_t)(row + p * 34) & 2u) != 0;
-        const float d = h2f(odd ? (r.w[0] >> 16) : (r.w[0] & 0xFFFFu));
+        const uint8_t* b = row + p * 34;
+        const uint32_t sel = half_sel(b);
+        const float d = half_d(r.w[0], b);
         uint32_t q[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) q[i] = (odd ? r.w[i + 1] : align2(r.w[i + 1], r.w[i], 2)) ^ 0x80808080u;
+        for (int i = 0; i < 8; i++) q[i] = half_pick(r.w[i + 1], r.w[i], sel) ^ 0x80808080u;
         PieceCodes o;
         o.u[0] = make_uint4(q[0], q[1], q[2], q[3]);
         o.u[1] = make_uint4(q[4], q[5], q[6], q[7]);
@@ -430,11 +448,12 @@ template <> struct Piece<T_IQ4_NL> {
         return r;
     }
     static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
-        const bool odd = ((uint32_t)(uintptr_t)(row + p * 18) & 2u) != 0;
-        const float d = h2f(odd ? (r.w[0] >> 16) : (r.w[0] & 0xFFFFu));
+        const uint8_t* b = row + p * 18;
+        const uint32_t sel = half_sel(b);
+        const float d = half_d(r.w[0], b);
         uint32_t q[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) q[i] = odd ? r.w[i + 1] : align2(r.w[i + 1], r.w[i], 2);
+        for (int i = 0; i < 4; i++) q[i] = half_pick(r.w[i + 1], r.w[i], sel);
         const uint4 qq = make_uint4(q[0], q[1], q[2], q[3]);
         PieceCodes o;
         o.u[0] = lut16x4(and4(qq, 0x0F0F0F0Fu), true);

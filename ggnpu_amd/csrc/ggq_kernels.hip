@@ -1178,20 +1178,25 @@ template <int T> struct BStage {
 
 template <> struct BStage<T_Q8_0> {
     uint32_t w[9];
-    bool ok, odd;
+    const uint8_t* b;
+    bool ok;
     __device__ __forceinline__ void fetch(const uint8_t* r, int kk, bool v) {
-        const uint8_t* b = r + (kk >> 5) * 34;
+        b = r + (kk >> 5) * 34;
         ok = v;
-        odd = ((uint32_t)(uintptr_t)b & 2u) != 0;
         ld_dw<9>(align_down4(b), w);
     }
+    // A slot outside the matrix (row >= N, or k >= K) reads block 0 of a
+    // valid row; its scale is stored as 0 and its codes are left as read:
+    // they only meet zero activation codes (k >= K) or feed output columns
+    // that are never written (row >= N).
     __device__ __forceinline__ void store(int8_t* codes, float* dl, float* ml) const {
+        const uint32_t sel = half_sel(b);
         uint32_t q[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) q[i] = ok ? (odd ? w[i + 1] : align2(w[i + 1], w[i], 2)) : 0u;
+        for (int i = 0; i < 8; i++) q[i] = half_pick(w[i + 1], w[i], sel);
         *(uint4*)codes = make_uint4(q[0], q[1], q[2], q[3]);
         *(uint4*)(codes + 16) = make_uint4(q[4], q[5], q[6], q[7]);
-        *dl = ok ? h2f(odd ? (w[0] >> 16) : (w[0] & 0xFFFFu)) : 0.0f;
+        *dl = ok ? half_d(w[0], b) : 0.0f;
         *ml = 0.0f;
     }
 };
