@@ -661,6 +661,236 @@ __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     }
 }
 
+// ============================================ GEMV on the matrix cores
+// Several activation rows (M >= 2, fp32 activations): the weight codes of a
+// piece are decoded once and multiplied against up to 4*MS activation rows
+// with v_mfma_f32_4x4x4_16b_f16 instead of one fp32 FMA chain per row.
+//
+// Layout: lane = 4*blk + j (blk 0..15 per wavefront).  The 64 blocks of the
+// workgroup are piece slots; S = 2^lpr_log2 (16, 32 or 64) slots serve one
+// group of 4 weight rows, so a row-iteration covers 4*(64/S) rows.  Lane j
+// of a block owns weight row 4*group + j and activation row j (+4t) at the
+// block's pieces sg, sg+S, ... (PPT of them).  One MFMA multiplies the 4x4
+// activation slice A[m][k] (lane j supplies row m = j) by the 4x4 code slice
+// B[k][n] (lane j supplies its own row's codes); D[m][n] lands in lane j,
+// register m.  A run's 16 codes are 4 such slices of one lane, so the run's
+// scale a[r] and bias b[r] (per weight row) apply to D as in the fp32 path:
+//   sum_k x_k w_k = sum_r a[r] * D_r + b[r] * sum(x_run_r).
+// Codes are small unsigned integers (<= 255), exact in fp16.  Activations
+// are scaled per (row, piece) by a power of two that puts the piece's
+// largest magnitude in [2^14, 2^15) and split as hi + lo (both fp16, hi
+// rounded toward zero, lo = x - hi rounded toward zero): |x - hi - lo| <=
+// 2^-20 |x|, and the power of two is undone exactly in the run scale.  The
+// MFMA accumulates in fp32.
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Two codes (bytes 0,1 or 2,3 of w, by selector) as an fp16 pair: the byte
+// becomes the low mantissa byte of 1024.0 (0x64 high byte), then 1024 is
+// subtracted (exact).
+__device__ __forceinline__ uint32_t codes_f16x2(uint32_t w, uint32_t sel) {
+    const h2v v = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, w, sel));
+    const h2v off = {(_Float16)1024.0f, (_Float16)1024.0f};
+    return __builtin_bit_cast(uint32_t, v - off);
+}
+__device__ __forceinline__ h4v codes_slice(uint32_t w) {
+    return __builtin_bit_cast(h4v, make_uint2(codes_f16x2(w, 0x04010400u), codes_f16x2(w, 0x04030402u)));
+}
+__device__ __forceinline__ uint32_t u4_at(const uint4& u, int i) { return i == 0 ? u.x : i == 1 ? u.y : i == 2 ? u.z : u.w; }
+
+// Broadcast of lane m (0..3) of each 4-lane block.
+template <int M> __device__ __forceinline__ float quad_bcast(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), M * 0x55, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void quad_bcast4(float v, float (&o)[4]) {
+    o[0] = quad_bcast<0>(v); o[1] = quad_bcast<1>(v); o[2] = quad_bcast<2>(v); o[3] = quad_bcast<3>(v);
+}
+
+// ONE: a single activation row (M == 1): only row 0 of each MFMA result is
+// scaled, reduced and stored.
+template <int T, int PPT, int MS, bool ONE = false>
+__device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx, int bz, int gz,
+                                               float (&red)[2][4][2][4][4 * MS]) {
+    constexpr int NM = ONE ? 1 : 4;  // result rows per row set that are used
+    typedef typename Piece<T>::Raw Raw;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 3, blk = lane >> 2;
+    const int slot = (wave << 4) | blk;
+    const int sl2 = a.lpr_log2, S = 1 << sl2;
+    const int grp = slot >> sl2, sg = slot & (S - 1);
+    const int G = 64 >> sl2;               // row groups per iteration
+    const int wpg = S >> 4;                // wavefronts per row group
+    const int P = a.K >> 5;
+    const int n_iters = (a.N + 4 * G - 1) / (4 * G);
+    int parity = 0;
+
+    for (int mc = bz * 4 * MS; mc < a.M; mc += gz * 4 * MS) {
+        Raw ra[PPT], rb[PPT];
+        auto fetch = [&](Raw (&r)[PPT], int it) {
+            const int row = (it * G + grp) * 4 + j;
+            const bool rv = it < n_iters && row < a.N;
+            const uint8_t* wrow = a.W + (uint64_t)(uint32_t)(rv ? row : 0) * (uint32_t)a.row_bytes;
+#pragma unroll
+            for (int i = 0; i < PPT; i++) {
+                const int p = sg + i * S;
+                r[i] = Piece<T>::fetch(wrow, p < P ? p : 0);
+            }
+        };
+        int it = bx;
+        fetch(ra, it);
+
+        // Activations of this lane's row (j + 4t) at its pieces, scaled and
+        // split; run sums and inverse scales of all four rows of the block.
+        h4v xh[PPT][MS][8], xl[PPT][MS][8];
+        float xs[PPT][MS][2][4], inv[PPT][MS][4];
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int p = sg + i * S;
+            const int pc = p < P ? p : 0;
+#pragma unroll
+            for (int t = 0; t < MS; t++) {
+                const int m = mc + 4 * t + j;
+                const bool ok = p < P && m < a.M;
+                const float* xp = a.X + (int64_t)(ok ? m : 0) * a.ldx;
+                float x[32];
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const int k0 = Piece<T>::run_k(pc, r);
+                    if (a.x_vec4) {
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const float4 v = *(const float4*)(xp + k0 + 4 * q);
+                            x[16 * r + 4 * q] = v.x; x[16 * r + 4 * q + 1] = v.y;
+                            x[16 * r + 4 * q + 2] = v.z; x[16 * r + 4 * q + 3] = v.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 16; q++) x[16 * r + q] = xp[k0 + q];
+                    }
+                }
+                float amax = 0.0f, s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 32; q++) {
+                    x[q] = ok ? x[q] : 0.0f;
+                    amax = fmaxf(amax, fabsf(x[q]));
+                }
+#pragma unroll
+                for (int q = 0; q < 16; q++) { s0 += x[q]; s1 += x[16 + q]; }
+                // amax = f * 2^E, f in [0.5, 1): scale 2^(15-E) puts it in [2^14, 2^15).
+                int sh = 15 - __builtin_amdgcn_frexp_expf(amax);
+                sh = amax > 0.0f && sh < 126 ? sh : (amax > 0.0f ? 126 : 0);
+                const float scl = __builtin_amdgcn_ldexpf(1.0f, sh);
+                quad_bcast4(__builtin_amdgcn_ldexpf(1.0f, -sh), inv[i][t]);
+                quad_bcast4(s0, xs[i][t][0]);
+                quad_bcast4(s1, xs[i][t][1]);
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    float v[4], l[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = x[4 * q + e] * scl;
+                    const auto h01 = __builtin_amdgcn_cvt_pkrtz(v[0], v[1]), h23 = __builtin_amdgcn_cvt_pkrtz(v[2], v[3]);
+                    l[0] = v[0] - (float)h01[0]; l[1] = v[1] - (float)h01[1];
+                    l[2] = v[2] - (float)h23[0]; l[3] = v[3] - (float)h23[1];
+                    const auto l01 = __builtin_amdgcn_cvt_pkrtz(l[0], l[1]), l23 = __builtin_amdgcn_cvt_pkrtz(l[2], l[3]);
+                    xh[i][t][q] = __builtin_bit_cast(h4v, make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)));
+                    xl[i][t][q] = __builtin_bit_cast(h4v, make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)));
+                }
+            }
+        }
+
+        while (it < n_iters) {
+            if (it + gx < n_iters) fetch(rb, it + gx);
+            const int row = (it * G + grp) * 4 + j;
+            const uint8_t* wrow = a.W + (uint64_t)(uint32_t)(row < a.N ? row : 0) * (uint32_t)a.row_bytes;
+            float acc[MS][4];
+#pragma unroll
+            for (int t = 0; t < MS; t++)
+#pragma unroll
+                for (int m = 0; m < 4; m++) acc[t][m] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PPT; i++) {
+                const int p = sg + i * S;
+                const PieceCodes pc = Piece<T>::decode(ra[i], wrow, p < P ? p : 0);
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    h4v B[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) B[q] = codes_slice(u4_at(pc.u[r], q));
+#pragma unroll
+                    for (int t = 0; t < MS; t++) {
+                        f4v D = {0.0f, 0.0f, 0.0f, 0.0f}, E = D;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            D = __builtin_amdgcn_mfma_f32_4x4x4f16(xh[i][t][4 * r + q], B[q], D, 0, 0, 0);
+                            E = __builtin_amdgcn_mfma_f32_4x4x4f16(xl[i][t][4 * r + q], B[q], E, 0, 0, 0);
+                        }
+#pragma unroll
+                        for (int m = 0; m < NM; m++) {
+                            acc[t][m] = fmaf(pc.a[r] * inv[i][t][m], D[m] + E[m], acc[t][m]);
+                            acc[t][m] = fmaf(pc.b[r], xs[i][t][r][m], acc[t][m]);
+                        }
+                    }
+                }
+            }
+            // Sum over the wavefront's 16 blocks (lanes of equal j): rotate
+            // by 4 and 8 inside each row of 16, then xor 16; lanes 0-3 and
+            // 32-35 hold the two halves.
+#pragma unroll
+            for (int t = 0; t < MS; t++)
+#pragma unroll
+                for (int m = 0; m < NM; m++) {
+                    float v = dpp_addc<0x124>(acc[t][m]);
+                    v = dpp_addc<0x128>(v);
+                    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+                    acc[t][m] = v;
+                }
+            if ((lane & 31) < 4) {
+#pragma unroll
+                for (int t = 0; t < MS; t++)
+#pragma unroll
+                    for (int m = 0; m < NM; m++) red[parity][wave][lane >> 5][j][4 * t + m] = acc[t][m];
+            }
+            __syncthreads();
+            if (lane < 4 && (wave & (wpg - 1)) == 0 && row < a.N) {
+#pragma unroll
+                for (int t = 0; t < MS; t++)
+#pragma unroll
+                    for (int m = 0; m < NM; m++) {
+                        const int mr = mc + 4 * t + m;
+                        float s = 0.0f;
+                        for (int w = 0; w < wpg; w++) s += red[parity][wave + w][0][j][4 * t + m] + red[parity][wave + w][1][j][4 * t + m];
+                        if (mr < a.M) a.Y[(int64_t)mr * a.ldy + row] = s;
+                    }
+            }
+            parity ^= 1;
+            it += gx;
+#pragma unroll
+            for (int i = 0; i < PPT; i++) ra[i] = rb[i];
+        }
+    }
+}
+
+template <int T, int PPT, int MS, bool ONE = false>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
+    __shared__ float red[2][4][2][4][4 * MS];
+    gemv_mfma_body<T, PPT, MS, ONE>(a, blockIdx.x, gridDim.x, blockIdx.z, gridDim.z, red);
+}
+
+template <int PPT, int MS>
+__global__ __launch_bounds__(256) void gemv_mfma_multi_kernel(MultiArgs ma) {
+    __shared__ float red[2][4][2][4][4 * MS];
+    int q = 0;
+    while (q + 1 < ma.n && (int)blockIdx.x >= ma.begin[q + 1]) q++;
+    const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
+    switch (ma.type[q]) {
+#define C(TT) case TT: gemv_mfma_body<TT, PPT, MS>(ma.p[q], bx, gx, blockIdx.z, gridDim.z, red); break;
+    C(T_Q4_K) C(T_Q5_K) C(T_Q6_K) C(T_Q8_0) C(T_IQ4_NL) C(T_IQ4_XS)
+#undef C
+    default: break;
+    }
+}
+
 // Straightforward GEMV for shapes the piece kernel does not take (K not a
 // multiple of 64, i.e. an odd number of 32-value blocks): one thread per
 // (row, batch row), codes16 + group scales.
@@ -778,6 +1008,29 @@ static int moe_rounds() { const int v = env_int("GGQ_MOE_ROUNDS", 4); return v <
 
 static bool fused(const GemvProblem& p) { return p.rms || p.X2 || p.R || p.silu; }
 
+// Matrix-core GEMV (gemv_mfma_kernel) for M >= 2 plain fp32-activation
+// problems: S = 2^sl2 piece slots per group of 4 rows (16, 32 or 64), PPT
+// pieces per lane (at most 2: the split activations take 32 VGPRs per piece
+// and row set), MS row sets of 4 per pass (2 when PPT is 1 and M > 4).
+// GGQ_GEMV_MFMA=0 selects the fp32 FMA kernels instead (read at every
+// multi-row launch).
+struct MfmaPlan {
+    int sl2, ppt, ms, n_iters;
+};
+static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
+    if (env_int("GGQ_GEMV_MFMA", 1) == 0) return false;
+    if (M < (env_int("GGQ_GEMV_MFMA1", 0) ? 1 : 2) || fused(p) || p.n1 > 0 || p.grp_off || p.x_idx || (p.K % 32) != 0 || p.K <= 0) return false;
+    const int P = p.K / 32;
+    m.sl2 = P <= 16 ? 4 : (P <= 32 ? 5 : 6);
+    const int S = 1 << m.sl2;
+    m.ppt = (P + S - 1) / S;
+    if (m.ppt > 2) return false;
+    m.ms = (M > 4 && m.ppt == 1 && env_int("GGQ_GEMV_MFMA_MS", 1) >= 2) ? 2 : 1;
+    const int rows_per_iter = 4 * (64 / S);
+    m.n_iters = (p.N + rows_per_iter - 1) / rows_per_iter;
+    return true;
+}
+
 struct GemvPlan {
     GemvArgs a;
     int ppt, n_iters, mrows;
@@ -832,6 +1085,27 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         return hipGetLastError();
     }
     const int ppt = g.ppt, mrows = g.mrows;
+    {
+        MfmaPlan mp;
+        if (groups == 1 && mfma_plan(p, mrows, mp)) {
+            a.lpr_log2 = mp.sl2;
+            const int gz = (mrows + 4 * mp.ms - 1) / (4 * mp.ms);
+#define GM(PPT_, MS_, ONE_)                                                                       \
+    do {                                                                                          \
+        int gx = resident_blocks(gemv_mfma_kernel<T, PPT_, MS_, ONE_>, 0) / gz;                   \
+        gx = gx < 1 ? 1 : (gx > mp.n_iters ? mp.n_iters : gx);                                    \
+        gemv_mfma_kernel<T, PPT_, MS_, ONE_><<<dim3(gx, 1, gz), 256, 0, s>>>(a);                  \
+    } while (0)
+            if (mrows == 1) {
+                if (mp.ppt == 2) GM(2, 1, true);
+                else GM(1, 1, true);
+            } else if (mp.ppt == 2) GM(2, 1, false);
+            else if (mp.ms == 2) GM(1, 2, false);
+            else GM(1, 1, false);
+#undef GM
+            return hipGetLastError();
+        }
+    }
     // Batch rows per pass (MB) and pieces per thread (PPT) keep the
     // activation registers at 32*MB*PPT <= 128 floats.  Plain launches with
     // more rows than MB run their MB-row chunks in parallel (grid z) and
@@ -922,6 +1196,38 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
+    }
+    {
+        MfmaPlan mp[kMaxMulti];
+        bool all = M >= 2;
+        for (int i = 0; all && i < n; i++) all = mfma_plan(ps[i], M, mp[i]) && mp[i].ppt == mp[0].ppt && mp[i].ms == mp[0].ms;
+        if (all) {
+            MultiArgs mm;
+            const int ms = mp[0].ms, pp = mp[0].ppt;
+            const int gz = (M + 4 * ms - 1) / (4 * ms);
+            int tgt = pp == 2 ? resident_blocks(gemv_mfma_multi_kernel<2, 1>, 0)
+                              : (ms == 2 ? resident_blocks(gemv_mfma_multi_kernel<1, 2>, 0) : resident_blocks(gemv_mfma_multi_kernel<1, 1>, 0));
+            tgt = tgt / gz > 0 ? tgt / gz : 1;
+            int tot = 0;
+            for (int i = 0; i < n; i++) tot += mp[i].n_iters;
+            int b = 0;
+            for (int i = 0; i < n; i++) {
+                mm.p[i] = plans[i].a;
+                mm.p[i].lpr_log2 = mp[i].sl2;
+                mm.type[i] = ps[i].type;
+                mm.begin[i] = b;
+                int nb = (int)((int64_t)tgt * mp[i].n_iters / (tot > 0 ? tot : 1));
+                nb = nb < 1 ? 1 : (nb > mp[i].n_iters ? mp[i].n_iters : nb);
+                b += nb;
+            }
+            mm.begin[n] = b;
+            mm.n = n;
+            const dim3 grid(b, 1, gz);
+            if (pp == 2) gemv_mfma_multi_kernel<2, 1><<<grid, 256, 0, s>>>(mm);
+            else if (ms == 2) gemv_mfma_multi_kernel<1, 2><<<grid, 256, 0, s>>>(mm);
+            else gemv_mfma_multi_kernel<1, 1><<<grid, 256, 0, s>>>(mm);
+            return hipGetLastError();
+        }
     }
     bool any_fused = false, kq = true;
     for (int i = 0; i < n; i++) {
