@@ -709,8 +709,12 @@ __device__ __forceinline__ void quad_bcast4(float v, float (&o)[4]) {
 
 // ONE: a single activation row (M == 1): only row 0 of each MFMA result is
 // scaled, reduced and stored.
+// Grouped mode (grp_off set): workgroup row `by` serves group (expert) by,
+// whose weights start at by * w_group_stride and whose activation rows are
+// grp_off[by] .. grp_off[by+1]-1 (through x_idx when set); paired matrices
+// (n1 > 0) as in gemv_body.
 template <int T, int PPT, int MS, bool ONE = false>
-__device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx, int bz, int gz,
+__device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
                                                float (&red)[2][4][2][4][4 * MS]) {
     constexpr int NM = ONE ? 1 : 4;  // result rows per row set that are used
     typedef typename Piece<T>::Raw Raw;
@@ -723,14 +727,21 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
     const int wpg = S >> 4;                // wavefronts per row group
     const int P = a.K >> 5;
     const int n_iters = (a.N + 4 * G - 1) / (4 * G);
+    const uint8_t* const W = a.W + (int64_t)by * a.w_group_stride;
+    const uint8_t* const W2 = a.n1 > 0 ? a.W2 + (int64_t)by * a.w_group_stride : nullptr;
+    int m0 = 0, mcount = a.M;
+    if (a.grp_off) {
+        m0 = a.grp_off[by];
+        mcount = a.grp_off[by + 1] - m0;
+    }
     int parity = 0;
 
-    for (int mc = bz * 4 * MS; mc < a.M; mc += gz * 4 * MS) {
+    for (int mc = bz * 4 * MS; mc < mcount; mc += gz * 4 * MS) {
         Raw ra[PPT], rb[PPT];
         auto fetch = [&](Raw (&r)[PPT], int it) {
             const int row = (it * G + grp) * 4 + j;
             const bool rv = it < n_iters && row < a.N;
-            const uint8_t* wrow = a.W + (uint64_t)(uint32_t)(rv ? row : 0) * (uint32_t)a.row_bytes;
+            const uint8_t* wrow = weight_row(W, W2, a.n1, a.row_bytes, rv ? row : 0);
 #pragma unroll
             for (int i = 0; i < PPT; i++) {
                 const int p = sg + i * S;
@@ -751,8 +762,10 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
 #pragma unroll
             for (int t = 0; t < MS; t++) {
                 const int m = mc + 4 * t + j;
-                const bool ok = p < P && m < a.M;
-                const float* xp = a.X + (int64_t)(ok ? m : 0) * a.ldx;
+                const bool ok = p < P && m < mcount;
+                int xrow = m0 + (m < mcount ? m : 0);
+                if (a.x_idx) xrow = a.x_idx[xrow];
+                const float* xp = a.X + (int64_t)xrow * a.ldx;
                 float x[32];
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
@@ -802,7 +815,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
         while (it < n_iters) {
             if (it + gx < n_iters) fetch(rb, it + gx);
             const int row = (it * G + grp) * 4 + j;
-            const uint8_t* wrow = a.W + (uint64_t)(uint32_t)(row < a.N ? row : 0) * (uint32_t)a.row_bytes;
+            const uint8_t* wrow = weight_row(W, W2, a.n1, a.row_bytes, row < a.N ? row : 0);
             float acc[MS][4];
 #pragma unroll
             for (int t = 0; t < MS; t++)
@@ -860,7 +873,11 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
                         const int mr = mc + 4 * t + m;
                         float s = 0.0f;
                         for (int w = 0; w < wpg; w++) s += red[parity][wave + w][0][j][4 * t + m] + red[parity][wave + w][1][j][4 * t + m];
-                        if (mr < a.M) a.Y[(int64_t)mr * a.ldy + row] = s;
+                        if (mr < mcount) {
+                            const int64_t o = (int64_t)(m0 + mr) * a.ldy;
+                            if (a.n1 > 0 && row >= a.n1) a.Y2[o + (row - a.n1)] = s;
+                            else a.Y[o + row] = s;
+                        }
                     }
             }
             parity ^= 1;
@@ -874,7 +891,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
 template <int T, int PPT, int MS, bool ONE = false>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
     __shared__ float red[2][4][2][4][4 * MS];
-    gemv_mfma_body<T, PPT, MS, ONE>(a, blockIdx.x, gridDim.x, blockIdx.z, gridDim.z, red);
+    gemv_mfma_body<T, PPT, MS, ONE>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
 }
 
 template <int PPT, int MS>
@@ -884,7 +901,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_multi_kernel(MultiArgs ma) {
     while (q + 1 < ma.n && (int)blockIdx.x >= ma.begin[q + 1]) q++;
     const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
     switch (ma.type[q]) {
-#define C(TT) case TT: gemv_mfma_body<TT, PPT, MS>(ma.p[q], bx, gx, blockIdx.z, gridDim.z, red); break;
+#define C(TT) case TT: gemv_mfma_body<TT, PPT, MS>(ma.p[q], bx, gx, 0, blockIdx.z, gridDim.z, red); break;
     C(T_Q4_K) C(T_Q5_K) C(T_Q6_K) C(T_Q8_0) C(T_IQ4_NL) C(T_IQ4_XS)
 #undef C
     default: break;
@@ -1019,7 +1036,8 @@ struct MfmaPlan {
 };
 static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
     if (env_int("GGQ_GEMV_MFMA", 1) == 0) return false;
-    if (M < (env_int("GGQ_GEMV_MFMA1", 0) ? 1 : 2) || fused(p) || p.n1 > 0 || p.grp_off || p.x_idx || (p.K % 32) != 0 || p.K <= 0) return false;
+    if (M < (env_int("GGQ_GEMV_MFMA1", 0) ? 1 : 2) || fused(p) || (p.K % 32) != 0 || p.K <= 0) return false;
+    if (p.grp_off && env_int("GGQ_MOE_MFMA", 1) == 0) return false;
     const int P = p.K / 32;
     m.sl2 = P <= 16 ? 4 : (P <= 32 ? 5 : 6);
     const int S = 1 << m.sl2;
@@ -1087,14 +1105,17 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     const int ppt = g.ppt, mrows = g.mrows;
     {
         MfmaPlan mp;
-        if (groups == 1 && mfma_plan(p, mrows, mp)) {
+        if ((groups == 1 || p.grp_off) && mfma_plan(p, mrows, mp)) {
             a.lpr_log2 = mp.sl2;
-            const int gz = (mrows + 4 * mp.ms - 1) / (4 * mp.ms);
+            // Grouped: one workgroup row per group, each looping over its
+            // own row sets (as the FMA kernels' grouped launches).
+            const int gz = groups > 1 ? 1 : (mrows + 4 * mp.ms - 1) / (4 * mp.ms);
 #define GM(PPT_, MS_, ONE_)                                                                       \
     do {                                                                                          \
-        int gx = resident_blocks(gemv_mfma_kernel<T, PPT_, MS_, ONE_>, 0) / gz;                   \
+        int gx = resident_blocks(gemv_mfma_kernel<T, PPT_, MS_, ONE_>, 0) * (groups > 1 ? moe_rounds() : 1) / (gz * groups); \
+        if (groups > 1 && moe_gx() > 0) gx = moe_gx();                                            \
         gx = gx < 1 ? 1 : (gx > mp.n_iters ? mp.n_iters : gx);                                    \
-        gemv_mfma_kernel<T, PPT_, MS_, ONE_><<<dim3(gx, 1, gz), 256, 0, s>>>(a);                  \
+        gemv_mfma_kernel<T, PPT_, MS_, ONE_><<<dim3(gx, groups, gz), 256, 0, s>>>(a);             \
     } while (0)
             if (mrows == 1) {
                 if (mp.ppt == 2) GM(2, 1, true);

@@ -1,6 +1,8 @@
-"""Parity of the rows-per-pass GEMV variants that the default launch
-configuration does not select (GGQ_GEMV_MBCAP 2 / 4; GGQ_MOE_MB 1 / 4, the
-grouped default being 2).  The
+"""Parity of the GEMV variants that the default launch configuration does
+not select: the fp32 FMA kernels for several rows (GGQ_GEMV_MFMA=0) with
+GGQ_GEMV_MBCAP 2 / 4; GGQ_MOE_MB 1 / 4 (the grouped default being 2); the
+matrix-core kernel with 8 rows per pass (GGQ_GEMV_MFMA_MS=2) and for a
+single row (GGQ_GEMV_MFMA1=1).  The
 library reads these knobs at each multi-row / grouped launch, so the checks
 set them in this process and restore them afterwards."""
 import os
@@ -14,16 +16,33 @@ pytestmark = pytest.mark.gpu
 ctx = t.ctx  # module-scoped context fixture
 
 
-@pytest.fixture
-def wide_rows(request):
-    old = {k: os.environ.get(k) for k in ("GGQ_GEMV_MBCAP", "GGQ_MOE_MB")}
-    os.environ["GGQ_GEMV_MBCAP"] = os.environ["GGQ_MOE_MB"] = request.param
-    yield request.param
+def _set_env(values):
+    old = {k: os.environ.get(k) for k in values}
+    os.environ.update(values)
+    return old
+
+
+def _restore(old):
     for k, v in old.items():
         if v is None:
             os.environ.pop(k, None)
         else:
             os.environ[k] = v
+
+
+@pytest.fixture
+def wide_rows(request):
+    old = _set_env({"GGQ_GEMV_MBCAP": request.param, "GGQ_MOE_MB": request.param, "GGQ_GEMV_MFMA": "0"})
+    yield request.param
+    _restore(old)
+
+
+@pytest.fixture
+def mfma_knob(request):
+    name, value = request.param
+    old = _set_env({name: value})
+    yield request.param
+    _restore(old)
 
 
 @pytest.mark.parametrize("wide_rows", ["2", "4"], indirect=True)
@@ -36,3 +55,23 @@ def test_batched_rows_wide(ctx, orc, wide_rows, M):
 def test_moe_wide(ctx, orc, wide_rows):
     t.test_moe_small_vs_oracle(ctx, orc, True)
     t.test_moe_qwen35moe_shape_vs_oracle(ctx, orc)
+
+
+@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA_MS", "2")], indirect=True)
+@pytest.mark.parametrize("M", [5, 8, 9, 16])
+def test_mfma_eight_rows_per_pass(ctx, orc, mfma_knob, M):
+    t.test_batched_rows_gemv(ctx, orc, M)
+
+
+@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA1", "1")], indirect=True)
+@pytest.mark.parametrize("ty", [8, 12, 13, 14, 20, 23])
+def test_mfma_single_row(ctx, orc, mfma_knob, ty):
+    """One activation row through the matrix-core kernel (one and two pieces
+    per lane) against the fp64 oracle."""
+    import numpy as np
+    for K in (1024, 4096):
+        N = 333
+        raw = t.weights(ty, N, K, seed=ty + K)
+        A = np.random.default_rng(K).standard_normal((1, K)).astype(np.float32)
+        got = t.run_mm(ctx, ty, raw, N, K, A, 0)
+        assert orc.rel_l2(got, orc.mul_mat_f64(ty, raw, N, K, A, 0)) < t.TOL, (ty, K)
