@@ -751,10 +751,11 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
         int it = bx;
         fetch(ra, it);
 
-        // Activations of this lane's row (j + 4t) at its pieces, scaled and
-        // split; run sums and inverse scales of all four rows of the block.
-        h4v xh[PPT][MS][8], xl[PPT][MS][8];
-        float xs[PPT][MS][2][4], inv[PPT][MS][4];
+        // Activations of this lane's row (j + 4t) at its pieces.
+        float x[PPT][MS][32];
+        float amax[MS];
+#pragma unroll
+        for (int t = 0; t < MS; t++) amax[t] = 0.0f;
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = sg + i * S;
@@ -766,7 +767,6 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
                 int xrow = m0 + (m < mcount ? m : 0);
                 if (a.x_idx) xrow = a.x_idx[xrow];
                 const float* xp = a.X + (int64_t)xrow * a.ldx;
-                float x[32];
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
                     const int k0 = Piece<T>::run_k(pc, r);
@@ -774,34 +774,79 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             const float4 v = *(const float4*)(xp + k0 + 4 * q);
-                            x[16 * r + 4 * q] = v.x; x[16 * r + 4 * q + 1] = v.y;
-                            x[16 * r + 4 * q + 2] = v.z; x[16 * r + 4 * q + 3] = v.w;
+                            x[i][t][16 * r + 4 * q] = v.x; x[i][t][16 * r + 4 * q + 1] = v.y;
+                            x[i][t][16 * r + 4 * q + 2] = v.z; x[i][t][16 * r + 4 * q + 3] = v.w;
                         }
                     } else {
 #pragma unroll
-                        for (int q = 0; q < 16; q++) x[16 * r + q] = xp[k0 + q];
+                        for (int q = 0; q < 16; q++) x[i][t][16 * r + q] = xp[k0 + q];
                     }
                 }
-                float amax = 0.0f, s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 32; q++) {
-                    x[q] = ok ? x[q] : 0.0f;
-                    amax = fmaxf(amax, fabsf(x[q]));
+                    x[i][t][q] = ok ? x[i][t][q] : 0.0f;
+                    amax[t] = fmaxf(amax[t], fabsf(x[i][t][q]));
                 }
+            }
+        }
+        // Largest magnitude of each activation row over the workgroup's
+        // slots (all groups of a workgroup read the same rows): lanes of
+        // equal j inside the wavefront, then its two halves and the
+        // wavefronts through LDS.  Row m then gets the power of two
+        // 2^sh[m] that puts that maximum in [2^14, 2^15).
 #pragma unroll
-                for (int q = 0; q < 16; q++) { s0 += x[q]; s1 += x[16 + q]; }
-                // amax = f * 2^E, f in [0.5, 1): scale 2^(15-E) puts it in [2^14, 2^15).
-                int sh = 15 - __builtin_amdgcn_frexp_expf(amax);
-                sh = amax > 0.0f && sh < 126 ? sh : (amax > 0.0f ? 126 : 0);
-                const float scl = __builtin_amdgcn_ldexpf(1.0f, sh);
-                quad_bcast4(__builtin_amdgcn_ldexpf(1.0f, -sh), inv[i][t]);
+        for (int t = 0; t < MS; t++) {
+            float v = amax[t];
+            v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false)));
+            v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false)));
+            v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
+            if ((lane & 31) < 4) red[parity][wave][lane >> 5][j][4 * t] = v;
+        }
+        __syncthreads();
+        int sh[MS];
+        float scl[MS];
+#pragma unroll
+        for (int t = 0; t < MS; t++) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) v = fmaxf(v, fmaxf(red[parity][w][0][j][4 * t], red[parity][w][1][j][4 * t]));
+            int e = 15 - __builtin_amdgcn_frexp_expf(v);
+            e = v > 0.0f ? (e < 126 ? e : 126) : 0;
+            sh[t] = e;
+            scl[t] = __builtin_amdgcn_ldexpf(1.0f, e);
+        }
+        // The output lane of (j, m, t) = (L & 3, (L >> 2) & 3, L >> 4) needs
+        // the scale of row 4t + m: lane 4m + j' of any block holds it for
+        // j' = m.
+        const int out_t = (lane >> 4) & (MS - 1), out_m = (lane >> 2) & 3;
+        float out_inv = 1.0f;
+#pragma unroll
+        for (int t = 0; t < MS; t++) {
+            const int e = __builtin_amdgcn_ds_bpermute(4 * ((lane & ~3) | out_m), sh[t]);
+            if (t == out_t) out_inv = __builtin_amdgcn_ldexpf(1.0f, -e);
+        }
+        parity ^= 1;
+        // Split into fp16 hi + lo after the row's scale; run sums of the
+        // scaled values for the bias term, gathered for all four rows.
+        h4v xh[PPT][MS][8], xl[PPT][MS][8];
+        float xs[PPT][MS][2][4];
+#pragma unroll
+        for (int i = 0; i < PPT; i++)
+#pragma unroll
+            for (int t = 0; t < MS; t++) {
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    s0 += x[i][t][q] * scl[t];
+                    s1 += x[i][t][16 + q] * scl[t];
+                }
                 quad_bcast4(s0, xs[i][t][0]);
                 quad_bcast4(s1, xs[i][t][1]);
 #pragma unroll
                 for (int q = 0; q < 8; q++) {
                     float v[4], l[4];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) v[e] = x[4 * q + e] * scl;
+                    for (int e = 0; e < 4; e++) v[e] = x[i][t][4 * q + e] * scl[t];
                     const auto h01 = __builtin_amdgcn_cvt_pkrtz(v[0], v[1]), h23 = __builtin_amdgcn_cvt_pkrtz(v[2], v[3]);
                     l[0] = v[0] - (float)h01[0]; l[1] = v[1] - (float)h01[1];
                     l[2] = v[2] - (float)h23[0]; l[3] = v[3] - (float)h23[1];
@@ -810,7 +855,6 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
                     xl[i][t][q] = __builtin_bit_cast(h4v, make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)));
                 }
             }
-        }
 
         while (it < n_iters) {
             if (it + gx < n_iters) fetch(rb, it + gx);
@@ -832,15 +876,15 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
                     for (int q = 0; q < 4; q++) B[q] = codes_slice(u4_at(pc.u[r], q));
 #pragma unroll
                     for (int t = 0; t < MS; t++) {
-                        f4v D = {0.0f, 0.0f, 0.0f, 0.0f}, E = D;
+                        f4v D = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
                             D = __builtin_amdgcn_mfma_f32_4x4x4f16(xh[i][t][4 * r + q], B[q], D, 0, 0, 0);
-                            E = __builtin_amdgcn_mfma_f32_4x4x4f16(xl[i][t][4 * r + q], B[q], E, 0, 0, 0);
+                            D = __builtin_amdgcn_mfma_f32_4x4x4f16(xl[i][t][4 * r + q], B[q], D, 0, 0, 0);
                         }
 #pragma unroll
                         for (int m = 0; m < NM; m++) {
-                            acc[t][m] = fmaf(pc.a[r] * inv[i][t][m], D[m] + E[m], acc[t][m]);
+                            acc[t][m] = fmaf(pc.a[r], D[m], acc[t][m]);
                             acc[t][m] = fmaf(pc.b[r], xs[i][t][r][m], acc[t][m]);
                         }
                     }
@@ -865,20 +909,20 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
                     for (int m = 0; m < NM; m++) red[parity][wave][lane >> 5][j][4 * t + m] = acc[t][m];
             }
             __syncthreads();
-            if (lane < 4 && (wave & (wpg - 1)) == 0 && row < a.N) {
-#pragma unroll
-                for (int t = 0; t < MS; t++)
-#pragma unroll
-                    for (int m = 0; m < NM; m++) {
-                        const int mr = mc + 4 * t + m;
-                        float s = 0.0f;
-                        for (int w = 0; w < wpg; w++) s += red[parity][wave + w][0][j][4 * t + m] + red[parity][wave + w][1][j][4 * t + m];
-                        if (mr < mcount) {
-                            const int64_t o = (int64_t)(m0 + mr) * a.ldy;
-                            if (a.n1 > 0 && row >= a.n1) a.Y2[o + (row - a.n1)] = s;
-                            else a.Y[o + row] = s;
-                        }
-                    }
+            // Lane L of the group's first wavefront finishes output (row j =
+            // L & 3, activation row 4t + m with m = (L >> 2) & 3, t = L >> 4).
+            if ((wave & (wpg - 1)) == 0 && lane < 16 * MS && (!ONE || lane < 4)) {
+                const int orow = (it * G + grp) * 4 + (lane & 3);
+                const int mr = mc + 4 * out_t + out_m;
+                if (orow < a.N && mr < mcount) {
+                    float v = 0.0f;
+                    for (int w = 0; w < wpg; w++)
+                        v += red[parity][wave + w][0][lane & 3][4 * out_t + out_m] + red[parity][wave + w][1][lane & 3][4 * out_t + out_m];
+                    v *= out_inv;
+                    const int64_t o = (int64_t)(m0 + mr) * a.ldy;
+                    if (a.n1 > 0 && orow >= a.n1) a.Y2[o + (orow - a.n1)] = v;
+                    else a.Y[o + orow] = v;
+                }
             }
             parity ^= 1;
             it += gx;
