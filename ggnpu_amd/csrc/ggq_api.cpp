@@ -246,21 +246,20 @@ int mul_mat_host(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float
     if (M == 0) return set_status(c, GGQ_OK);
     const size_t a_bytes = sizeof(float) * (size_t)M * w->K;
     const size_t c_bytes = sizeof(float) * (size_t)M * w->N;
-    hipError_t e = ensure(c->io, align256(a_bytes) + c_bytes);
+    hipError_t e = ensure(c->io, a_bytes);
     if (e != hipSuccess) return hip_status(c, e, "io buffer");
     if ((e = ensure_pinned(c->pin, align256(a_bytes) + c_bytes)) != hipSuccess) return hip_status(c, e, "pinned buffer");
     float* dA = (float*)c->io.ptr;
-    float* dC = (float*)((char*)c->io.ptr + align256(a_bytes));
     float* hA = (float*)c->pin.ptr;
     float* hC = (float*)((char*)c->pin.ptr + align256(a_bytes));
     for (int m = 0; m < M; m++) memcpy(hA + (size_t)m * w->K, A + (size_t)m * lda, sizeof(float) * w->K);
+    // A is read by every workgroup, so it is copied to HBM first; C is
+    // written once per element, straight into the pinned buffer.
     e = ggq::launch_copy_bytes(dA, hA, a_bytes, c->stream);
     if (e != hipSuccess) return hip_status(c, e, "copy A");
-    st = mul_mat_queue(c, w->dev, w->type, w->N, w->K, dA, (int)w->K, dC, (int)w->N, M, act_mode, c->stream);
+    st = mul_mat_queue(c, w->dev, w->type, w->N, w->K, dA, (int)w->K, hC, (int)w->N, M, act_mode, c->stream);
     if (st != GGQ_OK) return st;
-    e = ggq::launch_copy_bytes(hC, dC, c_bytes, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) return hip_status(c, e, "copy C");
+    if ((e = hipStreamSynchronize(c->stream)) != hipSuccess) return hip_status(c, e, "sync");
     for (int m = 0; m < M; m++) memcpy(C + (size_t)m * ldc, hC + (size_t)m * w->N, sizeof(float) * w->N);
     return set_status(c, GGQ_OK);
 }
