@@ -2399,6 +2399,15 @@ hipError_t launch_attn_decode(const float* Q, const float* K, const float* V, in
 // in registers (E <= 1024) with a bitmask of the ones already taken; ties
 // break toward the lower expert id.  Selection j ends in lane j.
 constexpr int kRouteMaxPerLane = 16;
+// One argmax step against the lane selected by DPP control CTRL: the larger
+// value wins, ties go to the lower expert index (as the reference's scan in
+// index order).  -inf values with index 0x7FFFFFFF never win a tie.
+template <int CTRL> __device__ __forceinline__ void route_step(float& best, int& bi) {
+    const float ov = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, best), CTRL, 0xF, 0xF, false));
+    const int oi = __builtin_amdgcn_mov_dpp(bi, CTRL, 0xF, 0xF, false);
+    if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+}
+
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int E, int topk,
                                                        int32_t* __restrict__ sel, float* __restrict__ wsel) {
     const int t = blockIdx.x, lane = threadIdx.x;
@@ -2425,11 +2434,23 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
                 bi = e;
             }
         }
+        // Inside each row of 16 lanes by DPP (xor 1, xor 2, the other quad
+        // of 8, the other half of 16), then across the four rows.
+        route_step<0xB1>(best, bi);
+        route_step<0x4E>(best, bi);
+        route_step<0x141>(best, bi);
+        route_step<0x140>(best, bi);
+        {
+            float rb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, best), 0));
+            int ri = __builtin_amdgcn_readlane(bi, 0);
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(best, off, 64);
-            const int oi = __shfl_xor(bi, off, 64);
-            if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+            for (int r = 1; r < 4; r++) {
+                const float ov = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, best), 16 * r));
+                const int oi = __builtin_amdgcn_readlane(bi, 16 * r);
+                if (ov > rb || (ov == rb && oi < ri)) { rb = ov; ri = oi; }
+            }
+            best = rb;
+            bi = ri;
         }
         if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
         if (lane == j) { my_sel = bi; my_l = best; }
