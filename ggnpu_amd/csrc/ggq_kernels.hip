@@ -2533,9 +2533,75 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restri
     }
 }
 
+// The same stable counting sort for n <= 1024 pairs and E <= 256 experts
+// (decode batches): pair f is thread f, `sel` is read once, and a pair's
+// position is start[e] + (pairs of e in earlier wavefronts, from per-
+// wavefront histograms) + (pairs of e in earlier lanes of its wavefront).
+constexpr int kGroupFastE = 256;
+__global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __restrict__ sel, int n, int E,
+                                                               int topk, int32_t* __restrict__ grp_off,
+                                                               int32_t* __restrict__ tok_idx,
+                                                               int32_t* __restrict__ pos_of) {
+    __shared__ __attribute__((aligned(16))) int32_t s_sel[1024];
+    __shared__ int32_t hist[16][kGroupFastE];  // per wavefront; then exclusive prefix over wavefronts
+    __shared__ int32_t start[kGroupFastE];
+    __shared__ int32_t wsum[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e = tid < n ? sel[tid] : -1;
+    s_sel[tid] = e;
+    for (int i = tid; i < 16 * kGroupFastE; i += 1024) (&hist[0][0])[i] = 0;
+    __syncthreads();
+    if (e >= 0) atomicAdd(&hist[wave][e], 1);
+    // Pairs of e in earlier lanes of this wavefront.
+    int rank = 0;
+    const int32_t* ws = s_sel + 64 * wave;
+    for (int g = 0; g < lane; g += 4) {
+        const int4 v = *(const int4*)&ws[g];
+        rank += (v.x == e) + (g + 1 < lane && v.y == e) + (g + 2 < lane && v.z == e) + (g + 3 < lane && v.w == e);
+    }
+    __syncthreads();
+    // Thread x < E: prefix of expert x over wavefronts, its total, and an
+    // exclusive scan of the totals (four wavefronts cover 256 experts).
+    if (tid < kGroupFastE) {
+        int run = 0;
+#pragma unroll
+        for (int w = 0; w < 16; w++) {
+            const int c = hist[w][tid];
+            hist[w][tid] = run;
+            run += c;
+        }
+        int incl = run;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        start[tid] = incl - run;
+    }
+    __syncthreads();
+    if (tid < kGroupFastE) {
+        int before = 0;
+        for (int w = 0; w < wave; w++) before += wsum[w];
+        start[tid] += before;
+        if (tid < E) grp_off[tid] = start[tid];
+        if (tid == 0) grp_off[E] = n;
+    }
+    __syncthreads();
+    if (e >= 0) {
+        const int pos = start[e] + hist[wave][e] + rank;
+        tok_idx[pos] = tid / topk;
+        pos_of[tid] = pos;
+    }
+}
+
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s) {
     if (E > 1024) return hipErrorInvalidValue;
+    if (T * topk <= 1024 && E <= kGroupFastE) {
+        moe_group_small_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);
+        return hipGetLastError();
+    }
     moe_group_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);
     return hipGetLastError();
 }

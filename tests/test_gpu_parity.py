@@ -284,6 +284,18 @@ def test_moe_qwen35moe_shape_vs_oracle(ctx, orc):
     assert orc.rel_l2(out, ref) < TOL
 
 
+
+@pytest.mark.parametrize("T,E,k", [(160, 16, 8), (40, 300, 4)])
+def test_moe_large_grouping_vs_oracle(ctx, orc, T, E, k):
+    """Groupings outside the single-pass path (more than 1024 (token, expert)
+    pairs, or more than 256 experts): the chunked counting sort."""
+    H, F = 256, 256
+    (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(ctx, T, H, F, E, k, False, seed=T + E)
+    ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, 12, Wg, 12, Wu, 14, Wd, Sg, Su, Sd, sw)
+    assert np.array_equal(sel, rsel)
+    assert np.allclose(wsel, rw, rtol=1e-6)
+    assert orc.rel_l2(out, ref) < TOL
+
 # --------------------------------------------------------- host boundary
 def test_mul_mat_q_host_api_and_errors(ctx, orc):
     t, N, K, M = 14, 70, 512, 2
