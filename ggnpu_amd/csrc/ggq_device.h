@@ -296,6 +296,31 @@ __device__ __forceinline__ uint32_t half_pick(uint32_t hi, uint32_t lo, uint32_t
 __device__ __forceinline__ float half_d(uint32_t w0, const uint8_t* base) {
     return h2f(w0 >> (((uint32_t)(uintptr_t)base & 2u) << 3));
 }
+// The same two from the low address bits of the block base.
+__device__ __forceinline__ uint32_t half_sel_lo(uint32_t lo) { return (lo & 2u) ? 0x07060504u : 0x05040302u; }
+__device__ __forceinline__ float half_d_lo(uint32_t w0, uint32_t lo) { return h2f(w0 >> ((lo & 2u) << 3)); }
+
+// A weight row as a 4-aligned base and a 32-bit byte offset.  Loads at
+// base + (off + o) take the scalar-base form (64-bit SGPR base + 32-bit VGPR
+// offset) when the base is uniform over the wavefront, which saves the
+// 64-bit address arithmetic per load; one matrix (one group's matrix) must
+// stay below 4 GiB.  Alignment bits come from the offset alone.
+struct RowRef {
+    const uint8_t* base;
+    uint32_t off;
+    __device__ __forceinline__ const uint8_t* at(uint32_t o) const { return base + (uint32_t)(off + o); }
+    // The dword-aligned address at or below base + off + o.
+    __device__ __forceinline__ const uint32_t* at_al4(uint32_t o) const {
+        return (const uint32_t*)(base + ((off + o) & ~3u));
+    }
+    __device__ __forceinline__ uint32_t lo(uint32_t o) const { return off + o; }
+};
+// Row at byte offset `off` of a matrix starting at m (any alignment): the
+// misalignment of m moves into the offset.
+__device__ __forceinline__ RowRef make_row(const uint8_t* m, uint32_t off) {
+    const uint32_t mis = (uint32_t)(uintptr_t)m & 3u;
+    return RowRef{m - mis, off + mis};
+}
 
 __device__ __forceinline__ uint4 uint4_at(const uint32_t* w) { return make_uint4(w[0], w[1], w[2], w[3]); }
 
@@ -314,16 +339,16 @@ template <> struct Piece<T_Q4_K> {
     static __device__ __forceinline__ int run_k(int p, int r) {
         return (p >> 3) * 256 + ((p >> 1) & 3) * 64 + (p & 1) * 16 + 32 * r;
     }
-    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
-        const uint8_t* b = row + (p >> 3) * 144;
+    static __device__ __forceinline__ Raw fetch(RowRef row, int p) {
+        const uint32_t b = (p >> 3) * 144;
         const int c = (p >> 1) & 3, h = p & 1;
         Raw r;
-        const uint4 hd = ld16_a(b), q = ld16_a(b + 16 + 32 * c + 16 * h);
+        const uint4 hd = ld16_a(row.at(b)), q = ld16_a(row.at(b + 16 + 32 * c + 16 * h));
         r.w[0] = hd.x; r.w[1] = hd.y; r.w[2] = hd.z; r.w[3] = hd.w;
         r.w[4] = q.x; r.w[5] = q.y; r.w[6] = q.z; r.w[7] = q.w;
         return r;
     }
-    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t*, int p) {
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, RowRef, int p) {
         const int c = (p >> 1) & 3;
         const uint32_t sm = kq_pair(r.w[1], r.w[2], r.w[3], c);
         const uint32_t sc0 = sm & 0xFFu, sc1 = (sm >> 8) & 0xFFu, m0 = (sm >> 16) & 0xFFu, m1 = sm >> 24;
@@ -344,17 +369,17 @@ template <> struct Piece<T_Q4_K> {
 template <> struct Piece<T_Q5_K> {
     typedef RawW<12> Raw;
     static __device__ __forceinline__ int run_k(int p, int r) { return Piece<T_Q4_K>::run_k(p, r); }
-    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
-        const uint8_t* b = row + (p >> 3) * 176;
+    static __device__ __forceinline__ Raw fetch(RowRef row, int p) {
+        const uint32_t b = (p >> 3) * 176;
         const int c = (p >> 1) & 3, h = p & 1;
         Raw r;
-        const uint4 hd = ld16_a(b), qh = ld16_a(b + 16 + 16 * h), q = ld16_a(b + 48 + 32 * c + 16 * h);
+        const uint4 hd = ld16_a(row.at(b)), qh = ld16_a(row.at(b + 16 + 16 * h)), q = ld16_a(row.at(b + 48 + 32 * c + 16 * h));
         r.w[0] = hd.x; r.w[1] = hd.y; r.w[2] = hd.z; r.w[3] = hd.w;
         r.w[4] = qh.x; r.w[5] = qh.y; r.w[6] = qh.z; r.w[7] = qh.w;
         r.w[8] = q.x; r.w[9] = q.y; r.w[10] = q.z; r.w[11] = q.w;
         return r;
     }
-    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t*, int p) {
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, RowRef, int p) {
         const int c = (p >> 1) & 3;
         const uint32_t sm = kq_pair(r.w[1], r.w[2], r.w[3], c);
         const uint32_t sc0 = sm & 0xFFu, sc1 = (sm >> 8) & 0xFFu, m0 = (sm >> 16) & 0xFFu, m1 = sm >> 24;
@@ -381,20 +406,20 @@ template <> struct Piece<T_Q6_K> {
         return (p >> 3) * 256 + ((p >> 2) & 1) * 128 + (p & 1) * 32 + ((p >> 1) & 1) * 16 + 64 * r;
     }
     static __device__ __forceinline__ int sc_index(int p) { return 8 * ((p >> 2) & 1) + ((p >> 1) & 1) + 2 * (p & 1); }
-    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
-        const uint8_t* b = row + (p >> 3) * 210;
+    static __device__ __forceinline__ Raw fetch(RowRef row, int p) {
+        const uint32_t b = (p >> 3) * 210;
         const int n = (p >> 2) & 1, l0 = ((p >> 1) & 1) * 16, s = p & 1;
         Raw r;
-        ld_dw<5>(align_down4(b + 64 * n + 32 * s + l0), r.w);
-        ld_dw<5>(align_down4(b + 128 + 32 * n + l0), r.w + 5);
-        ld_dw<3>(align_down4(b + 192 + sc_index(p)), r.w + 10);
-        r.w[13] = ld_u16(b + 208);
+        ld_dw<5>(row.at_al4(b + 64 * n + 32 * s + l0), r.w);
+        ld_dw<5>(row.at_al4(b + 128 + 32 * n + l0), r.w + 5);
+        ld_dw<3>(row.at_al4(b + 192 + sc_index(p)), r.w + 10);
+        r.w[13] = ld_u16(row.at(b + 208));
         return r;
     }
-    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
-        const uint8_t* b = row + (p >> 3) * 210;
-        const uint32_t sh = (uint32_t)(uintptr_t)b & 3u;  // ql / qh windows (offsets are multiples of 16)
-        const uint32_t ss = (uint32_t)(uintptr_t)(b + 192 + sc_index(p)) & 3u;
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, RowRef row, int p) {
+        const uint32_t b = (p >> 3) * 210;
+        const uint32_t sh = row.lo(b) & 3u;  // ql / qh windows (offsets are multiples of 16)
+        const uint32_t ss = row.lo(b + 192 + sc_index(p)) & 3u;
         const int s = p & 1;
         const uint4 ql = realign4(r.w, sh), qh = realign4(r.w + 5, sh);
         const uint32_t sc0 = align2(r.w[11], r.w[10], ss), sc1 = align2(r.w[12], r.w[11], ss);
@@ -416,15 +441,15 @@ template <> struct Piece<T_Q6_K> {
 template <> struct Piece<T_Q8_0> {
     typedef RawW<9> Raw;
     static __device__ __forceinline__ int run_k(int p, int r) { return p * 32 + 16 * r; }
-    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
+    static __device__ __forceinline__ Raw fetch(RowRef row, int p) {
         Raw r;
-        ld_dw<9>(align_down4(row + p * 34), r.w);
+        ld_dw<9>(row.at_al4(p * 34), r.w);
         return r;
     }
-    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
-        const uint8_t* b = row + p * 34;
-        const uint32_t sel = half_sel(b);
-        const float d = half_d(r.w[0], b);
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, RowRef row, int p) {
+        const uint32_t b = row.lo(p * 34);
+        const uint32_t sel = half_sel_lo(b);
+        const float d = half_d_lo(r.w[0], b);
         uint32_t q[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = half_pick(r.w[i + 1], r.w[i], sel) ^ 0x80808080u;
@@ -442,15 +467,15 @@ template <> struct Piece<T_Q8_0> {
 template <> struct Piece<T_IQ4_NL> {
     typedef RawW<5> Raw;
     static __device__ __forceinline__ int run_k(int p, int r) { return p * 32 + 16 * r; }
-    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
+    static __device__ __forceinline__ Raw fetch(RowRef row, int p) {
         Raw r;
-        ld_dw<5>(align_down4(row + p * 18), r.w);
+        ld_dw<5>(row.at_al4(p * 18), r.w);
         return r;
     }
-    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t* row, int p) {
-        const uint8_t* b = row + p * 18;
-        const uint32_t sel = half_sel(b);
-        const float d = half_d(r.w[0], b);
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, RowRef row, int p) {
+        const uint32_t b = row.lo(p * 18);
+        const uint32_t sel = half_sel_lo(b);
+        const float d = half_d_lo(r.w[0], b);
         uint32_t q[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) q[i] = half_pick(r.w[i + 1], r.w[i], sel);
@@ -468,17 +493,17 @@ template <> struct Piece<T_IQ4_NL> {
 template <> struct Piece<T_IQ4_XS> {
     typedef RawW<6> Raw;
     static __device__ __forceinline__ int run_k(int p, int r) { return p * 32 + 16 * r; }
-    static __device__ __forceinline__ Raw fetch(const uint8_t* row, int p) {
-        const uint8_t* b = row + (p >> 3) * 136;
+    static __device__ __forceinline__ Raw fetch(RowRef row, int p) {
+        const uint32_t b = (p >> 3) * 136;
         const int ib = p & 7;
         Raw r;
-        const uint2 hd = *(const uint2*)b;
-        const uint2 lo = *(const uint2*)(b + 8 + 16 * ib);
-        const uint2 hi = *(const uint2*)(b + 16 + 16 * ib);
+        const uint2 hd = *(const uint2*)row.at(b);
+        const uint2 lo = *(const uint2*)row.at(b + 8 + 16 * ib);
+        const uint2 hi = *(const uint2*)row.at(b + 16 + 16 * ib);
         r.w[0] = hd.x; r.w[1] = hd.y; r.w[2] = lo.x; r.w[3] = lo.y; r.w[4] = hi.x; r.w[5] = hi.y;
         return r;
     }
-    static __device__ __forceinline__ PieceCodes decode(const Raw& r, const uint8_t*, int p) {
+    static __device__ __forceinline__ PieceCodes decode(const Raw& r, RowRef, int p) {
         const int ib = p & 7;
         const int ls = (int)(((r.w[1] >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15u) | (((r.w[0] >> (16 + 2 * ib)) & 3u) << 4));
         const float dl = h2f(r.w[0] & 0xFFFFu) * (float)(ls - 32);

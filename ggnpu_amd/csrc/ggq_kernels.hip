@@ -250,11 +250,11 @@ struct GemvArgs {
     int n1;
 };
 
-// Start of weight row `row` of a (group's) matrix, or of the paired one.
-__device__ __forceinline__ const uint8_t* weight_row(const uint8_t* W, const uint8_t* W2, int n1, int64_t row_bytes,
-                                                     int row) {
+// Weight row `row` of a (group's) matrix, or of the paired one.  With no
+// paired matrix (n1 == 0 known at the call) the base is the uniform W.
+__device__ __forceinline__ RowRef weight_row(const uint8_t* W, const uint8_t* W2, int n1, int64_t row_bytes, int row) {
     const bool second = n1 > 0 && row >= n1;
-    return (second ? W2 : W) + (uint64_t)(uint32_t)(second ? row - n1 : row) * (uint32_t)row_bytes;
+    return make_row(second ? W2 : W, (uint32_t)(second ? row - n1 : row) * (uint32_t)row_bytes);
 }
 
 // Sum over aligned groups of 2^lg lanes (lg = 0..6): afterwards every lane of
@@ -280,15 +280,31 @@ template <int T, int PPT, int U>
 __device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[U][PPT], const uint8_t* W, int64_t row_bytes,
                                            int it, int stride, int n_iters, int rpi, int rsub, int N, int lp, int lpr,
                                            int P, const uint8_t* W2 = nullptr, int n1 = 0) {
+    // Two copies of the loop: without a paired matrix the row base is the
+    // uniform W (scalar-base loads).
+    if (n1 > 0) {
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        const int iu = it + u * stride, row = iu * rpi + rsub;
-        const bool rvalid = iu < n_iters && row < N;
-        const uint8_t* wrow = weight_row(W, W2, n1, row_bytes, rvalid ? row : 0);
+        for (int u = 0; u < U; u++) {
+            const int iu = it + u * stride, row = iu * rpi + rsub;
+            const bool rvalid = iu < n_iters && row < N;
+            const RowRef wrow = weight_row(W, W2, n1, row_bytes, rvalid ? row : 0);
 #pragma unroll
-        for (int i = 0; i < PPT; i++) {
-            const int p = lp + i * lpr;
-            raw[u][i] = Piece<T>::fetch(wrow, p < P ? p : 0);
+            for (int i = 0; i < PPT; i++) {
+                const int p = lp + i * lpr;
+                raw[u][i] = Piece<T>::fetch(wrow, p < P ? p : 0);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int iu = it + u * stride, row = iu * rpi + rsub;
+            const bool rvalid = iu < n_iters && row < N;
+            const RowRef wrow = weight_row(W, nullptr, 0, row_bytes, rvalid ? row : 0);
+#pragma unroll
+            for (int i = 0; i < PPT; i++) {
+                const int p = lp + i * lpr;
+                raw[u][i] = Piece<T>::fetch(wrow, p < P ? p : 0);
+            }
         }
     }
 }
@@ -318,7 +334,7 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
         for (int m = 0; m < MB; m++) acc[u][m] = 0.0f;
         const int iu = it + u * stride, row = iu * rpi + rsub;
         const bool rvalid = iu < n_iters && row < a.N;
-        const uint8_t* wrow = weight_row(W, W2, a.n1, a.row_bytes, rvalid ? row : 0);
+        const RowRef wrow = weight_row(W, W2, a.n1, a.row_bytes, rvalid ? row : 0);
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = lp + i * lpr;
@@ -346,7 +362,9 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
                 }
             }
 #pragma unroll
-            for (int m = 0; m < MB; m++) acc[u][m] += ok ? tp[m] : 0.0f;
+            // Pieces past the row end (p >= P) decode piece 0 again but meet
+            // activations zeroed when they were loaded: tp is exactly 0.
+            for (int m = 0; m < MB; m++) acc[u][m] += tp[m];
         }
     }
     // A row spans at least a wavefront in the common case (K >= 2048): the
@@ -741,11 +759,20 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
         auto fetch = [&](Raw (&r)[PPT], int it) {
             const int row = (it * G + grp) * 4 + j;
             const bool rv = it < n_iters && row < a.N;
-            const uint8_t* wrow = weight_row(W, W2, a.n1, a.row_bytes, rv ? row : 0);
+            if (a.n1 > 0) {
+                const RowRef wrow = weight_row(W, W2, a.n1, a.row_bytes, rv ? row : 0);
 #pragma unroll
-            for (int i = 0; i < PPT; i++) {
-                const int p = sg + i * S;
-                r[i] = Piece<T>::fetch(wrow, p < P ? p : 0);
+                for (int i = 0; i < PPT; i++) {
+                    const int p = sg + i * S;
+                    r[i] = Piece<T>::fetch(wrow, p < P ? p : 0);
+                }
+            } else {
+                const RowRef wrow = weight_row(W, nullptr, 0, a.row_bytes, rv ? row : 0);
+#pragma unroll
+                for (int i = 0; i < PPT; i++) {
+                    const int p = sg + i * S;
+                    r[i] = Piece<T>::fetch(wrow, p < P ? p : 0);
+                }
             }
         };
         int it = bx;
@@ -859,7 +886,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
         while (it < n_iters) {
             if (it + gx < n_iters) fetch(rb, it + gx);
             const int row = (it * G + grp) * 4 + j;
-            const uint8_t* wrow = weight_row(W, W2, a.n1, a.row_bytes, row < a.N ? row : 0);
+            const RowRef wrow = weight_row(W, W2, a.n1, a.row_bytes, row < a.N ? row : 0);
             float acc[MS][4];
 #pragma unroll
             for (int t = 0; t < MS; t++)
