@@ -100,3 +100,15 @@ def test_mfma_batch_rows_mixed_types(ctx, orc, M):
     ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, descs, len(shapes), M, stream_handle()), "batch rows")
     for dC, ref in refs:
         assert orc.rel_l2(host(dC), ref) < TOL
+
+
+@pytest.mark.parametrize("ty", [12, 20, 14])
+@pytest.mark.parametrize("lda_pad,ldc_pad", [(3, 1), (1, 0)])
+def test_mfma_gemv_odd_strides(ctx, orc, ty, lda_pad, ldc_pad):
+    """Activation rows at a stride that is not a multiple of 4 floats (the
+    kernel's scalar activation loads) and padded output rows."""
+    K, N, M = 1024 if ty != 14 else 2048, 200, 6
+    raw = t.weights(ty, N, K, seed=lda_pad + ty)
+    A = np.random.default_rng(ty).standard_normal((M, K)).astype(np.float32)
+    got = t.run_mm(ctx, ty, raw, N, K, A, 0, lda=K + lda_pad, ldc=N + ldc_pad)
+    assert orc.rel_l2(got, orc.mul_mat_f64(ty, raw, N, K, A, 0)) < TOL
