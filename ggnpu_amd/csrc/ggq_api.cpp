@@ -620,16 +620,13 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     const size_t nk = (size_t)T * k;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off = align256(off + bytes); return o; };
+    // The shared expert's gate / up / SwiGLU rows follow the routed ones in
+    // the same buffers (one SwiGLU launch covers both).
+    const size_t ts = shared ? (size_t)T : 0;
     const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 1)),
-                 o_tok = take(4 * nk), o_pos = take(4 * nk), o_g = take(4 * nk * F), o_u = take(4 * nk * F),
-                 o_h = take(4 * nk * F), o_d = take(4 * nk * H);
-    size_t o_sg = 0, o_su = 0, o_sh = 0, o_sd = 0;
-    if (shared) {
-        o_sg = take(4 * (size_t)T * F);
-        o_su = take(4 * (size_t)T * F);
-        o_sh = take(4 * (size_t)T * F);
-        o_sd = take(4 * (size_t)T * H);
-    }
+                 o_tok = take(4 * nk), o_pos = take(4 * nk), o_g = take(4 * (nk + ts) * F),
+                 o_u = take(4 * (nk + ts) * F), o_h = take(4 * (nk + ts) * F), o_d = take(4 * nk * H);
+    const size_t o_sd = shared ? take(4 * (size_t)T * H) : 0;
     hipError_t e = ensure(c->ws, off);
     if (e != hipSuccess) return hip_status(c, e, "workspace");
     char* base = (char*)c->ws.ptr;
@@ -662,17 +659,11 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
         g.type = p->up_type; g.W = p->up_exps; g.w_group_stride = (int64_t)F * ggq::row_bytes(p->up_type, H); g.Y = U;
         if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe up");
     }
-    if ((e = ggq::launch_swiglu(G, U, Hh, (int64_t)nk * F, s)) != hipSuccess) return hip_status(c, e, "swiglu");
-    // down: rows H, K = F, activations are the sorted pair rows themselves.
-    g.N = H; g.K = F; g.X = Hh; g.ldx = F; g.x_idx = nullptr; g.ldy = H; g.Y = D;
-    g.type = p->down_type; g.W = p->down_exps; g.w_group_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
-    if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe down");
-
     float* Dsh = nullptr;
+    ggq::GemvProblem q{};
     if (shared) {
-        float *SG = (float*)(base + o_sg), *SU = (float*)(base + o_su), *SH = (float*)(base + o_sh);
+        float *SG = G + nk * F, *SU = U + nk * F;
         Dsh = (float*)(base + o_sd);
-        ggq::GemvProblem q{};
         q.groups = 1;
         q.M = T;
         q.N = F; q.K = H; q.X = p->x; q.ldx = H; q.ldy = F;
@@ -686,8 +677,15 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
             q.type = p->up_type; q.W = p->up_shexp; q.Y = SU;
             if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared up");
         }
-        if ((e = ggq::launch_swiglu(SG, SU, SH, (int64_t)T * F, s)) != hipSuccess) return hip_status(c, e, "shared swiglu");
-        q.N = H; q.K = F; q.X = SH; q.ldx = F; q.ldy = H; q.type = p->down_type; q.W = p->down_shexp; q.Y = Dsh;
+    }
+    // SwiGLU of the routed pair rows and the shared expert's rows together.
+    if ((e = ggq::launch_swiglu(G, U, Hh, (int64_t)(nk + ts) * F, s)) != hipSuccess) return hip_status(c, e, "swiglu");
+    // down: rows H, K = F, activations are the sorted pair rows themselves.
+    g.N = H; g.K = F; g.X = Hh; g.ldx = F; g.x_idx = nullptr; g.ldy = H; g.Y = D;
+    g.type = p->down_type; g.W = p->down_exps; g.w_group_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
+    if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe down");
+    if (shared) {
+        q.N = H; q.K = F; q.X = Hh + nk * F; q.ldx = F; q.ldy = H; q.type = p->down_type; q.W = p->down_shexp; q.Y = Dsh;
         if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared down");
     }
     if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, Dsh, p->shared_w, p->out, s)) != hipSuccess)
