@@ -131,6 +131,43 @@ __global__ __launch_bounds__(256) void quant_act_row_kernel(const float* __restr
     const int m = blockIdx.x;
     const float* a = A + (int64_t)m * lda;
     float amax = 0.0f;
+    // Rows up to 16384 values: the row is held in registers (16 float4 per
+    // thread), all loads issued before the first is used and read once.
+    constexpr int R = 16;
+    if (vec4 && K <= 1024 * R) {
+        float4 v[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 4 * threadIdx.x + 1024 * i;
+            v[i] = k < K ? *(const float4*)(a + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int i = 0; i < R; i++)
+            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i].x), fabsf(v[i].y))), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+        const float inv = __fdiv_rn(1.0f, sc);
+        if (threadIdx.x == 0 && scales) scales[m] = sc;
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 4 * threadIdx.x + 1024 * i;
+            if (k >= K) break;
+            const int8_t c0 = to_i8(__fmul_rn(v[i].x, inv)), c1 = to_i8(__fmul_rn(v[i].y, inv));
+            const int8_t c2 = to_i8(__fmul_rn(v[i].z, inv)), c3 = to_i8(__fmul_rn(v[i].w, inv));
+            if (q)
+                *(uint32_t*)(q + (int64_t)m * K + k) = (uint32_t)(uint8_t)c0 | (uint32_t)(uint8_t)c1 << 8 |
+                                                       (uint32_t)(uint8_t)c2 << 16 | (uint32_t)(uint8_t)c3 << 24;
+            if (x_eff)
+                *(float4*)(x_eff + (int64_t)m * K + k) =
+                    make_float4(__fmul_rn((float)c0, sc), __fmul_rn((float)c1, sc), __fmul_rn((float)c2, sc),
+                                __fmul_rn((float)c3, sc));
+        }
+        return;
+    }
     if (vec4) {
         for (int k = 4 * threadIdx.x; k < K; k += 1024) {
             const float4 v = *(const float4*)(a + k);

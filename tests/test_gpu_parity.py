@@ -93,7 +93,7 @@ def test_fp16_conversion_all_patterns(ctx, golden):
 
 
 @pytest.mark.parametrize("mode", [1, 2])
-@pytest.mark.parametrize("M,K", [(1, 2048), (7, 1536), (64, 8960), (3, 32)])
+@pytest.mark.parametrize("M,K", [(1, 2048), (7, 1536), (64, 8960), (3, 32), (2, 16384), (2, 20480)])
 def test_quant_act_bitexact(ctx, orc, mode, M, K):
     import torch
     rng = np.random.default_rng(M * K + mode)
