@@ -119,6 +119,9 @@ int check_matmul_shape(ggq_ctx* c, uint32_t type, int64_t N, int64_t K, int M, i
     if (K % block_elems(type)) return set_status(c, GGQ_INVALID_PARAM, "K=%lld not a multiple of the block size %d", (long long)K, block_elems(type));
     if (N > INT32_MAX || K > ggq::kGemvMaxK) return set_status(c, GGQ_INVALID_PARAM, "K=%lld exceeds the supported maximum %d", (long long)K, ggq::kGemvMaxK);
     if (lda < K || ldc < N) return set_status(c, GGQ_INVALID_PARAM, "lda/ldc smaller than K/N");
+    if (N * ggq::row_bytes(type, K) > (int64_t)0xFFFFFFFF)
+        return set_status(c, GGQ_INVALID_PARAM, "weight matrix of %lld bytes: at most 4 GiB per matrix",
+                          (long long)(N * ggq::row_bytes(type, K)));
     if (act_mode < GGQ_ACT_F32 || act_mode > GGQ_ACT_Q8_BLOCK32) return set_status(c, GGQ_INVALID_PARAM, "bad act_mode %d", act_mode);
     return GGQ_OK;
 }

@@ -1163,6 +1163,13 @@ struct GemvPlan {
     bool simple;
 };
 
+// Rows are addressed as a matrix base plus a 32-bit byte offset: each
+// matrix (each group's matrix; each of a pair) must stay below 4 GiB.
+static bool offsets_fit(const GemvProblem& p) {
+    const int64_t rows = p.n1 > 0 ? (p.n1 > p.N - p.n1 ? p.n1 : p.N - p.n1) : p.N;
+    return rows * row_bytes(p.type, p.K) <= (int64_t)0xFFFFFFFF;
+}
+
 static GemvPlan plan_gemv(const GemvProblem& p) {
     GemvPlan g;
     GemvArgs& a = g.a;
@@ -1205,6 +1212,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     GemvArgs a = g.a;
     const int groups = p.groups > 0 ? p.groups : 1;
     if (p.n1 > 0 && (g.simple || fused(p) || !p.W2 || !p.Y2 || p.n1 >= p.N)) return hipErrorInvalidValue;
+    if (!offsets_fit(p)) return hipErrorInvalidValue;
     if (g.simple) {
         if (p.X2 || p.rms || p.R || p.silu) return hipErrorInvalidValue;  // fused options need K % 32 == 0
         gemv_simple_kernel<T><<<dim3((p.N + 255) / 256, groups), 256, 0, s>>>(a);
@@ -1304,6 +1312,8 @@ static int multi_resident() {
 hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     if (n == 1) return launch_gemv(ps[0], s);  // the single-problem kernel sizes its grid for one problem
+    for (int i = 0; i < n; i++)
+        if (!offsets_fit(ps[i])) return hipErrorInvalidValue;
     MultiArgs ma;
     int ppt = -1, total_iters = 0;
     const int M = ps[0].M;

@@ -308,6 +308,12 @@ def test_mul_mat_q_host_api_and_errors(ctx, orc):
     for _ in range(2):  # second call hits the resident-weight cache
         ctx.check(ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(p), 0), "mul_mat_q")
         assert orc.rel_l2(C, orc.mul_mat_f64(t, raw, N, K, A, 0)) < TOL
+    # a matrix of 4 GiB or more is refused before any device work (rows are
+    # addressed as base + 32-bit offset)
+    big = gl.MulMatParams.from_buffer_copy(p)
+    big.N, big.K, big.lda, big.ldb, big.B_type, big.ldc = 200000, 32768, 32768, 32768, 14, 200000
+    assert ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(big), 0) == gl.Status.INVALID_PARAM
+    assert b"4 GiB" in ctx.lib.ggq_last_error_message(ctx.h)
     bad = gl.MulMatParams.from_buffer_copy(p)
     bad.A = None
     assert ctx.lib.ggq_mul_mat_q(ctx.h, ctypes.byref(bad), 0) == gl.Status.INVALID_PARAM
