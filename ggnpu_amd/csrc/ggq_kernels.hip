@@ -732,11 +732,13 @@ __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
 // scale a[r] and bias b[r] (per weight row) apply to D as in the fp32 path:
 //   sum_k x_k w_k = sum_r a[r] * D_r + b[r] * sum(x_run_r).
 // Codes are small unsigned integers (<= 255), exact in fp16.  Activations
-// are scaled per (row, piece) by a power of two that puts the piece's
-// largest magnitude in [2^14, 2^15) and split as hi + lo (both fp16, hi
-// rounded toward zero, lo = x - hi rounded toward zero): |x - hi - lo| <=
-// 2^-20 |x|, and the power of two is undone exactly in the run scale.  The
-// MFMA accumulates in fp32.
+// are scaled per row by a power of two that puts the row's largest
+// magnitude (over the workgroup's slots) in [2^14, 2^15) and split as
+// hi + lo (both fp16, hi rounded toward zero, lo = x - hi rounded toward
+// zero): |x - hi - lo| <= 2^-20 |x| for values above 2^-18 of the row
+// maximum, 2^-40 of the maximum below that; the power of two is undone
+// exactly at the store.  The MFMA accumulates in fp32; hi and lo go into
+// one accumulator per run.
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
