@@ -12,8 +12,9 @@
 //                 last_error; the non-matmul operators are not part of this
 //                 backend and report DEVICE_UNAVAILABLE, i.e. the reference's
 //                 Status::NPU_UNAVAILABLE value)
-// Inside ggnpu itself the adapter is a ggnpu::Backend subclass forwarding to
-// the same C calls; INTEGRATION.md shows that file.
+// Inside ggnpu itself the adapter is a ggnpu::Backend subclass that forwards
+// mul_mat_q to the same C calls and reports NPU_UNAVAILABLE for the other
+// operators.
 #pragma once
 
 #include <cstdint>
