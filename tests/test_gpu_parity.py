@@ -296,6 +296,20 @@ def test_moe_large_grouping_vs_oracle(ctx, orc, T, E, k):
     assert np.allclose(wsel, rw, rtol=1e-6)
     assert orc.rel_l2(out, ref) < TOL
 
+
+@pytest.mark.parametrize("tg,tu,td", [(8, 8, 8), (20, 23, 20), (23, 20, 23), (8, 13, 14)])
+def test_moe_other_formats_vs_oracle(ctx, orc, tg, tu, td):
+    """Expert weights in Q8_0 / IQ4_NL / IQ4_XS (and mixed with K-quants):
+    the grouped matrix-core path for every format, paired and unpaired
+    gate/up, with and without the shared expert."""
+    T, H, F, E, k = 24, 512, 256, 32, 4
+    for shared in (False, True):
+        (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(ctx, T, H, F, E, k, shared, seed=tg + tu + td,
+                                                                            tg=tg, tu=tu, td=td)
+        ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, tg, Wg, tu, Wu, td, Wd, Sg, Su, Sd, sw)
+        assert np.array_equal(sel, rsel)
+        assert orc.rel_l2(out, ref) < TOL, (tg, tu, td, shared)
+
 # --------------------------------------------------------- host boundary
 def test_mul_mat_q_host_api_and_errors(ctx, orc):
     t, N, K, M = 14, 70, 512, 2
