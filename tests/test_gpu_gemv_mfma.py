@@ -28,7 +28,7 @@ def _k_for(ty, pieces):
 
 @pytest.mark.parametrize("ty", TYPES)
 @pytest.mark.parametrize("pieces", [8, 24, 64, 96, 200])
-@pytest.mark.parametrize("M", [2, 4, 5, 8, 16])
+@pytest.mark.parametrize("M", [2, 4, 5, 8, 16, 64])
 def test_mfma_gemv_matches_oracle(ctx, orc, ty, pieces, M):
     K = _k_for(ty, pieces)
     N = 4 * 37 + 3  # rows that leave a partial group of 4
