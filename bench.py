@@ -281,6 +281,40 @@ def bench_decode_fused(torch, ctx, stream, steps=30):
             "GBps": round(total / gsec / 1e9, 1)}
 
 
+def bench_launch_floor(torch, n=65, reps=20):
+    """Per-launch floor of a step built from n dependent launches (the decode
+    step has 65): a HIP graph of n one-element kernels, and of n copies of
+    1 MB (1024 workgroups' worth), each launch depending on the previous one;
+    GPU time per launch from events around graph replays (no CPU launch cost
+    in the timed region)."""
+    out = {}
+    for name, nbytes in (("tiny", 4), ("copy_1MB", 1 << 20)):
+        a = torch.zeros(nbytes // 4, device="cuda")
+        b = torch.zeros_like(a)
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                for i in range(n):
+                    (b if i % 2 else a).copy_(a if i % 2 else b)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n):
+                (b if i % 2 else a).copy_(a if i % 2 else b)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(torch.cuda.current_stream())
+        for _ in range(reps):
+            g.replay()
+        e1.record(torch.cuda.current_stream())
+        e1.synchronize()
+        out[name] = {"us_per_launch": round(e0.elapsed_time(e1) * 1e3 / (reps * n), 2)}
+    out["workload"] = f"{n} dependent launches in a HIP graph: one-element copies and 1 MB copies"
+    return out
+
+
 def bench_logits(torch, ctx, stream, reps=50):
     """Output projection of configs[1] (128256x2048 Q4_K, batch 1) alone and
     with the device-side greedy token choice (ggq_logits_argmax_dev, logits
@@ -567,7 +601,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
-    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "fused", "attention", "host", "copy"],
+    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "fused", "attention", "host", "copy",
+                                       "floor"],
                     default=None,
                     help="run one workload only and print its result (profiling aid)")
     ap.add_argument("--per-matmul", action="store_true",
@@ -598,6 +633,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_per_copy": src.numel(), "copies": 4}), flush=True)
+        return
+    if args.only == "floor":
+        print(json.dumps({"only": "floor", **bench_launch_floor(torch)}), flush=True)
+        ctx.close()
         return
     if args.only in ("config1", "prefill", "config4", "moe", "logits", "fused", "attention", "host"):
         res = {"config1": bench_config1, "prefill": bench_prefill, "config4": bench_config4,
