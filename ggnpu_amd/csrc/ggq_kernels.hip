@@ -2484,14 +2484,17 @@ template <int CTRL> __device__ __forceinline__ void route_step(float& best, int&
     if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
 }
 
+// PL: logits per lane (E <= 64 * PL), so the per-step scan covers only the
+// experts that exist.
+template <int PL>
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int E, int topk,
                                                        int32_t* __restrict__ sel, float* __restrict__ wsel) {
     const int t = blockIdx.x, lane = threadIdx.x;
     const float* l = logits + (int64_t)t * E;
-    float v[kRouteMaxPerLane];
+    float v[PL];
     uint32_t taken = 0;
 #pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; i++) {
+    for (int i = 0; i < PL; i++) {
         const int e = lane + 64 * i;
         v[i] = e < E ? l[e] : -INFINITY;
         if (e >= E) taken |= 1u << i;
@@ -2502,7 +2505,7 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
         float best = -INFINITY;
         int bi = 0x7FFFFFFF;
 #pragma unroll
-        for (int i = 0; i < kRouteMaxPerLane; i++) {
+        for (int i = 0; i < PL; i++) {
             const int e = lane + 64 * i;
             const bool free = !((taken >> i) & 1u);
             if (free && (v[i] > best || (v[i] == best && e < bi))) {
@@ -2531,10 +2534,10 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
         if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
         if (lane == j) { my_sel = bi; my_l = best; }
     }
-    const float l0 = __shfl(my_l, 0, 64);
+    const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_l), 0));
     const float ex = lane < topk ? expf(my_l - l0) : 0.0f;
     float sum = 0.0f;  // in selection order, as the reference adds them
-    for (int j = 0; j < topk; j++) sum += __shfl(ex, j, 64);
+    for (int j = 0; j < topk; j++) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), j));
     if (lane < topk) {
         sel[t * topk + lane] = my_sel;
         wsel[t * topk + lane] = ex / sum;
@@ -2545,7 +2548,11 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t
                             hipStream_t s) {
     if (T == 0) return hipSuccess;
     if (E > 64 * kRouteMaxPerLane || topk > 64) return hipErrorInvalidValue;
-    moe_route_kernel<<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
+    if (E <= 64) moe_route_kernel<1><<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
+    else if (E <= 128) moe_route_kernel<2><<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
+    else if (E <= 256) moe_route_kernel<4><<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
+    else if (E <= 512) moe_route_kernel<8><<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
+    else moe_route_kernel<kRouteMaxPerLane><<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
     return hipGetLastError();
 }
 

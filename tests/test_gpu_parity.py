@@ -310,6 +310,19 @@ def test_moe_other_formats_vs_oracle(ctx, orc, tg, tu, td):
         assert np.array_equal(sel, rsel)
         assert orc.rel_l2(out, ref) < TOL, (tg, tu, td, shared)
 
+
+@pytest.mark.parametrize("E,k", [(64, 8), (100, 6), (128, 8), (500, 8), (1000, 8)])
+def test_moe_routing_expert_counts(ctx, orc, E, k):
+    """Routing for every per-lane logit count (1, 2, 4, 8, 16 experts per
+    lane): selections exactly as the oracle, weights within 1e-6, outputs
+    within the bar."""
+    T, H, F = 5, 256, 256
+    (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(ctx, T, H, F, E, k, False, seed=E)
+    ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, 12, Wg, 12, Wu, 14, Wd, Sg, Su, Sd, sw)
+    assert np.array_equal(sel, rsel)
+    assert np.allclose(wsel, rw, rtol=1e-6)
+    assert orc.rel_l2(out, ref) < TOL
+
 # --------------------------------------------------------- host boundary
 def test_mul_mat_q_host_api_and_errors(ctx, orc):
     t, N, K, M = 14, 70, 512, 2
