@@ -75,3 +75,19 @@ def test_mfma_single_row(ctx, orc, mfma_knob, ty):
         A = np.random.default_rng(K).standard_normal((1, K)).astype(np.float32)
         got = t.run_mm(ctx, ty, raw, N, K, A, 0)
         assert orc.rel_l2(got, orc.mul_mat_f64(ty, raw, N, K, A, 0)) < t.TOL, (ty, K)
+
+
+@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA", "0")], indirect=True)
+@pytest.mark.parametrize("ty", [12, 14, 20])
+def test_fma_path_batch_invariant(ctx, orc, mfma_knob, ty):
+    """On the FMA kernels every row of a batch equals the same row computed
+    alone, bit for bit."""
+    import numpy as np
+    K, N = 2048, 300
+    raw = t.weights(ty, N, K, seed=ty)
+    A = np.random.default_rng(ty).standard_normal((8, K)).astype(np.float32)
+    for M in (4, 8):
+        batch = t.run_mm(ctx, ty, raw, N, K, A[:M], 0)
+        for m in range(M):
+            alone = t.run_mm(ctx, ty, raw, N, K, A[m:m + 1], 0)
+            assert np.array_equal(batch[m].view(np.uint32), alone[0].view(np.uint32)), (M, m)
