@@ -1673,8 +1673,9 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmMultiArgs a) {
 
     __shared__ __attribute__((aligned(16))) int8_t As[2][BM][kGemmLd];
     __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN][kGemmLd];
-    __shared__ float Bd[2][BN][G];
-    __shared__ float Bm[2][BN][G];
+    __shared__ __attribute__((aligned(16))) float Bd[2][BN][G];
+    __shared__ __attribute__((aligned(16))) float Bm[2][BN][G];
+    static_assert(G % 4 == 0, "group scales are read four at a time");
 
     int q = 0;
     while (q + 1 < a.np && (int)blockIdx.x >= a.p[q + 1].tile_begin) q++;
@@ -1781,6 +1782,17 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmMultiArgs a) {
             constexpr bool kGLag = !kMin && TM * TN == 1;
             v16i Pq[2];
             float dq[2];
+            // The group-lag path reads its row's G scales up front, 16 bytes
+            // at a time: one per-group 4-byte read at a 16-byte lane stride
+            // costs an extra LDS instruction and bank conflicts per group.
+            float dg[G];
+            if constexpr (kGLag) {
+#pragma unroll
+                for (int g4 = 0; g4 < G; g4 += 4) {
+                    const float4 v = *(const float4*)&Bd[buf][wn + li][g4];
+                    dg[g4] = v.x, dg[g4 + 1] = v.y, dg[g4 + 2] = v.z, dg[g4 + 3] = v.w;
+                }
+            }
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 v4i A[TM], B[TN];
@@ -1794,12 +1806,14 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmMultiArgs a) {
                 for (int j = 0; j < TN; j++) {
                     const uint4 v = *(const uint4*)&Bs[buf][wn + 32 * j + li][32 * g + 16 * lk];
                     B[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-                    dl[j] = Bd[buf][wn + 32 * j + li][g];
-                    ml[j] = Bm[buf][wn + 32 * j + li][g];
+                    if constexpr (!kGLag) {
+                        dl[j] = Bd[buf][wn + 32 * j + li][g];
+                        ml[j] = Bm[buf][wn + 32 * j + li][g];
+                    }
                 }
                 if constexpr (kGLag) {
                     Pq[g & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0], B[0], zero, 0, 0, 0);
-                    dq[g & 1] = dl[0];
+                    dq[g & 1] = dg[g];
                     if (g > 0) {
 #pragma unroll
                         for (int r = 0; r < 16; r++)
