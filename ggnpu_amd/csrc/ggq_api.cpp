@@ -591,6 +591,20 @@ int ggq_quantize_act_dev(ggq_ctx* c, const float* A, int lda, int M, int K, int 
     GGQ_END(c)
 }
 
+int ggq_produce_quantize_act_dev(ggq_ctx* c, int producer, const float* A, const float* aux, int lda, int M, int K,
+                                 float eps, int8_t* q, float* scales, void* stream) {
+    GGQ_GUARD(c)
+    if (!A || !q || !scales || M < 0 || K <= 0 || lda < K) return set_status(c, GGQ_INVALID_PARAM, "bad arguments");
+    if (producer != GGQ_PRODUCE_RMS_NORM && producer != GGQ_PRODUCE_SWIGLU)
+        return set_status(c, GGQ_INVALID_PARAM, "producer must be GGQ_PRODUCE_RMS_NORM or GGQ_PRODUCE_SWIGLU");
+    if (producer == GGQ_PRODUCE_SWIGLU && !aux) return set_status(c, GGQ_INVALID_PARAM, "SwiGLU needs the up rows");
+    if (K > 16384 || K % 4 || lda % 4 || ((uintptr_t)A & 15u) || ((uintptr_t)aux & 15u) || ((uintptr_t)q & 3u))
+        return set_status(c, GGQ_INVALID_PARAM, "K <= 16384, K and lda multiples of 4, A and aux 16-byte aligned");
+    return hip_status(c, ggq::launch_produce_quant(producer, A, aux, lda, M, K, eps, q, scales, pick_stream(c, stream)),
+                      "produce_quant");
+    GGQ_END(c)
+}
+
 int ggq_block_dot_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const int8_t* qa, int M,
                       int32_t* out, void* stream) {
     GGQ_GUARD(c)

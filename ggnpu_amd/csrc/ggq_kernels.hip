@@ -121,6 +121,112 @@ __device__ __forceinline__ int8_t to_i8(float v) {
     return (int8_t)(int)r;
 }
 
+// Sum over the 256 threads of a workgroup (four wavefronts), in a fixed
+// order; every thread gets the total.
+__device__ __forceinline__ float wg_sum256(float v, float* red4) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
+// Producers that may run ahead of the quantization, in the same launch:
+// PROD_RMS is CpuRefBackend::rms_norm (cpu_ref.cpp:139-156), x * (1 /
+// sqrt(sum(x^2) / K + eps)) * w[k] (w null = 1), the sum of squares taken
+// over the workgroup in a fixed order; PROD_SWIGLU is silu(g) * u with
+// silu(g) = g / (1 + exp(-g)) (main.cpp:3164-3165, 3474-3477).
+enum { PROD_NONE = 0, PROD_RMS = 1, PROD_SWIGLU = 2 };
+
+// The row of up to 16384 values (K a multiple of 4, 16-byte aligned) held
+// in registers, 16 float4 per thread: all loads issued before the first is
+// used and each value read once; produced, then quantized as below.
+template <int P>
+__device__ __forceinline__ void quant_row_regs(const float* a, const float* aux, float eps, int m, int K,
+                                               int8_t* __restrict__ q, float* __restrict__ scales,
+                                               float* __restrict__ x_eff) {
+    __shared__ float wmax[4];
+    constexpr int R = 16;
+    float4 v[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int k = 4 * threadIdx.x + 1024 * i;
+        v[i] = k < K ? *(const float4*)(a + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if constexpr (P == PROD_SWIGLU) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 4 * threadIdx.x + 1024 * i;
+            if (k >= K) break;
+            const float4 u = *(const float4*)(aux + k);
+            v[i].x = (v[i].x / (1.0f + expf(-v[i].x))) * u.x;
+            v[i].y = (v[i].y / (1.0f + expf(-v[i].y))) * u.y;
+            v[i].z = (v[i].z / (1.0f + expf(-v[i].z))) * u.z;
+            v[i].w = (v[i].w / (1.0f + expf(-v[i].w))) * u.w;
+        }
+    }
+    if constexpr (P == PROD_RMS) {
+        __shared__ float wss[4];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < R; i++)
+            ss = fmaf(v[i].w, v[i].w, fmaf(v[i].z, v[i].z, fmaf(v[i].y, v[i].y, fmaf(v[i].x, v[i].x, ss))));
+        ss = wg_sum256(ss, wss);
+        // 1 / sqrt(v) with each step correctly rounded, as the reference's
+        // fp32 code computes it: the fp64 square root rounded once to fp32
+        // is the correctly rounded fp32 square root (53 >= 2 * 24 + 2 bits).
+        const float var = __fadd_rn(__fdiv_rn(ss, (float)K), eps);
+        const float is = __fdiv_rn(1.0f, (float)__dsqrt_rn((double)var));
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 4 * threadIdx.x + 1024 * i;
+            if (k >= K) break;
+            const float4 w = aux ? *(const float4*)(aux + k) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            v[i].x = __fmul_rn(__fmul_rn(v[i].x, is), w.x);
+            v[i].y = __fmul_rn(__fmul_rn(v[i].y, is), w.y);
+            v[i].z = __fmul_rn(__fmul_rn(v[i].z, is), w.z);
+            v[i].w = __fmul_rn(__fmul_rn(v[i].w, is), w.w);
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+        amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i].x), fabsf(v[i].y))), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+    const float inv = __fdiv_rn(1.0f, sc);
+    if (threadIdx.x == 0 && scales) scales[m] = sc;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int k = 4 * threadIdx.x + 1024 * i;
+        if (k >= K) break;
+        const int8_t c0 = to_i8(__fmul_rn(v[i].x, inv)), c1 = to_i8(__fmul_rn(v[i].y, inv));
+        const int8_t c2 = to_i8(__fmul_rn(v[i].z, inv)), c3 = to_i8(__fmul_rn(v[i].w, inv));
+        if (q)
+            *(uint32_t*)(q + (int64_t)m * K + k) = (uint32_t)(uint8_t)c0 | (uint32_t)(uint8_t)c1 << 8 |
+                                                   (uint32_t)(uint8_t)c2 << 16 | (uint32_t)(uint8_t)c3 << 24;
+        if (x_eff)
+            *(float4*)(x_eff + (int64_t)m * K + k) =
+                make_float4(__fmul_rn((float)c0, sc), __fmul_rn((float)c1, sc), __fmul_rn((float)c2, sc),
+                            __fmul_rn((float)c3, sc));
+    }
+}
+
+// Producer + row quantization, one workgroup per row (register path only).
+template <int P>
+__global__ __launch_bounds__(256) void produce_quant_row_kernel(const float* __restrict__ A,
+                                                                const float* __restrict__ aux, int lda, int K,
+                                                                float eps, int8_t* __restrict__ q,
+                                                                float* __restrict__ scales) {
+    const int m = blockIdx.x;
+    const float* au = P == PROD_SWIGLU ? aux + (int64_t)m * lda : aux;
+    quant_row_regs<P>(A + (int64_t)m * lda, au, eps, m, K, q, scales, nullptr);
+}
+
 // One workgroup per row: absolute maximum, then codes.  With 16-byte
 // aligned rows (lda, K multiples of 4) each thread moves float4 / 4 codes
 // at a time; the arithmetic per element is the same either way.
@@ -131,41 +237,8 @@ __global__ __launch_bounds__(256) void quant_act_row_kernel(const float* __restr
     const int m = blockIdx.x;
     const float* a = A + (int64_t)m * lda;
     float amax = 0.0f;
-    // Rows up to 16384 values: the row is held in registers (16 float4 per
-    // thread), all loads issued before the first is used and read once.
-    constexpr int R = 16;
-    if (vec4 && K <= 1024 * R) {
-        float4 v[R];
-#pragma unroll
-        for (int i = 0; i < R; i++) {
-            const int k = 4 * threadIdx.x + 1024 * i;
-            v[i] = k < K ? *(const float4*)(a + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-#pragma unroll
-        for (int i = 0; i < R; i++)
-            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i].x), fabsf(v[i].y))), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-        if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
-        __syncthreads();
-        amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-        const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
-        const float inv = __fdiv_rn(1.0f, sc);
-        if (threadIdx.x == 0 && scales) scales[m] = sc;
-#pragma unroll
-        for (int i = 0; i < R; i++) {
-            const int k = 4 * threadIdx.x + 1024 * i;
-            if (k >= K) break;
-            const int8_t c0 = to_i8(__fmul_rn(v[i].x, inv)), c1 = to_i8(__fmul_rn(v[i].y, inv));
-            const int8_t c2 = to_i8(__fmul_rn(v[i].z, inv)), c3 = to_i8(__fmul_rn(v[i].w, inv));
-            if (q)
-                *(uint32_t*)(q + (int64_t)m * K + k) = (uint32_t)(uint8_t)c0 | (uint32_t)(uint8_t)c1 << 8 |
-                                                       (uint32_t)(uint8_t)c2 << 16 | (uint32_t)(uint8_t)c3 << 24;
-            if (x_eff)
-                *(float4*)(x_eff + (int64_t)m * K + k) =
-                    make_float4(__fmul_rn((float)c0, sc), __fmul_rn((float)c1, sc), __fmul_rn((float)c2, sc),
-                                __fmul_rn((float)c3, sc));
-        }
+    if (vec4 && K <= 1024 * 16) {
+        quant_row_regs<PROD_NONE>(a, nullptr, 0.0f, m, K, q, scales, x_eff);
         return;
     }
     if (vec4) {
@@ -237,6 +310,21 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
         const int64_t n = (int64_t)M * (K / 32);
         quant_act_b32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(A, lda, M, K, q, scales, x_eff);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_produce_quant(int producer, const float* A, const float* aux, int lda, int M, int K, float eps,
+                                int8_t* q, float* scales, hipStream_t s) {
+    if (M == 0) return hipSuccess;
+    if (K <= 0 || K > 1024 * 16 || K % 4 || lda % 4 || (uintptr_t)A % 16 || (uintptr_t)aux % 16 ||
+        (uintptr_t)q % 4)
+        return hipErrorInvalidValue;
+    if (producer == PROD_RMS)
+        produce_quant_row_kernel<PROD_RMS><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales);
+    else if (producer == PROD_SWIGLU && aux)
+        produce_quant_row_kernel<PROD_SWIGLU><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

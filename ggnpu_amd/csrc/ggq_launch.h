@@ -19,6 +19,13 @@ hipError_t launch_block_dot(uint32_t type, const void* W, int N, int K, const in
 hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int8_t* q,
                             float* scales, float* x_eff, hipStream_t s);
 
+// RMSNorm (producer 1; aux = norm weight [K] or null) or SwiGLU (producer
+// 2; A = gate rows, aux = up rows, both with row stride lda) of each row,
+// then the per-row quantization of launch_quant_act mode 1.  K <= 16384,
+// K and lda multiples of 4, A and aux 16-byte aligned, q dense [M][K].
+hipError_t launch_produce_quant(int producer, const float* A, const float* aux, int lda, int M, int K, float eps,
+                                int8_t* q, float* scales, hipStream_t s);
+
 // Decode GEMV with fp32 activations: Y[y_row][n] = sum_k X[x_row][k] W[n][k].
 // Plain mode: grp_off == null, rows 0..M-1.  Grouped mode (MoE): group g uses
 // weights W + g*w_group_stride and output rows grp_off[g]..grp_off[g+1]-1,

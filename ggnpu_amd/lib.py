@@ -31,6 +31,11 @@ class GgmlType(enum.IntEnum):
     IQ4_XS = 23
 
 
+class Producer(enum.IntEnum):
+    RMS_NORM = 1
+    SWIGLU = 2
+
+
 class ActMode(enum.IntEnum):
     F32 = 0
     Q8_ROW = 1
@@ -127,6 +132,7 @@ SIGNATURES = {
     "ggq_mul_mat_q8_batch_dev": (_I, [_P, _P, _I, _U32, _I64, _P, _P, _I, _P]),
     "ggq_dequant_dev": (_I, [_P, _P, _U32, _I64, _P, _P]),
     "ggq_quantize_act_dev": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _P]),
+    "ggq_produce_quantize_act_dev": (_I, [_P, _I, _P, _P, _I, _I, _I, ctypes.c_float, _P, _P, _P]),
     "ggq_block_dot_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _P]),
     "ggq_moe_ffn_dev": (_I, [_P, ctypes.POINTER(MoeParams), _P]),
     "ggq_encode": (_I, [_U32, _P, _I64, _I64, _P]),

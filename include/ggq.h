@@ -256,6 +256,27 @@ int ggq_dequant_dev(ggq_ctx* ctx, const void* raw, uint32_t type, int64_t n_bloc
 int ggq_quantize_act_dev(ggq_ctx* ctx, const float* A, int lda, int M, int K, int act_mode,
                          int8_t* q, float* scales, void* stream);
 
+/* The producer of a prefill input and its per-row int8 quantization in one
+ * launch (no reference counterpart as a fused call), so that a caller
+ * feeding ggq_mul_mat_q8_dev / ggq_mul_mat_q8_batch_dev does not write the
+ * fp32 rows out and read them back:
+ *   GGQ_PRODUCE_RMS_NORM  x = CpuRefBackend::rms_norm of the row
+ *                         (cpu_ref.cpp:139-156): a * (1/sqrt(sum(a^2)/K +
+ *                         eps)) * aux[k]; aux = norm weight [K] or NULL (= 1);
+ *   GGQ_PRODUCE_SWIGLU    x = silu(a) * aux[m][k], silu(v) = v / (1 +
+ *                         exp(-v)) (main.cpp:3164-3165, 3474-3477); A holds
+ *                         the gate rows, aux the up rows, both with stride lda.
+ * then q[m][k], scales[m] from x as ggq_quantize_act_dev in GGQ_ACT_Q8_ROW
+ * mode (amd_xdna.cpp:598-603, 633-639, 757-771).  K <= 16384, K and lda
+ * multiples of 4, A and aux 16-byte aligned; q dense [M][K].  The result
+ * equals the unfused sequence up to the order in which the norm's sum of
+ * squares is added (and the device expf), i.e. a code may differ by one
+ * where x / scale lies within fp32 rounding of a half-integer. */
+#define GGQ_PRODUCE_RMS_NORM 1
+#define GGQ_PRODUCE_SWIGLU 2
+int ggq_produce_quantize_act_dev(ggq_ctx* ctx, int producer, const float* A, const float* aux, int lda, int M,
+                                 int K, float eps, int8_t* q, float* scales, void* stream);
+
 /* int32 dot products of the raw weight codes with int8 activations, per
  * scale group (32 values; 16 for Q6_K): out[(m*N + n)*G + g], G = K/group.
  * Codes: Q4_K nibble, Q5_K 5-bit value, Q6_K 6-bit - 32, Q8_0 int8, IQ4

@@ -699,3 +699,106 @@ def test_fused_errors(ctx):
     d[0].rms_eps = 1e-5
     assert ctx.lib.ggq_mul_mat_fused_dev(ctx.h, d, 1, 65, stream_handle()) == gl.Status.INVALID_PARAM
     ctx.check(ctx.lib.ggq_mul_mat_fused_dev(ctx.h, d, 1, 1, stream_handle()), "ok")
+
+
+def _produce_quant(ctx, producer, A, aux, eps=1e-5):
+    """ggq_produce_quantize_act_dev on dense rows; returns (codes, scales)."""
+    import torch
+    M, K = A.shape
+    dA = dev(A)
+    daux = None if aux is None else dev(aux)
+    dq = empty((M, K), torch.int8)
+    ds = empty((M,), torch.float32)
+    ctx.check(ctx.lib.ggq_produce_quantize_act_dev(ctx.h, int(producer), ptr(dA), None if daux is None else ptr(daux),
+                                                   K, M, K, eps, ptr(dq), ptr(ds), stream_handle()), "produce_quant")
+    return host(dq), host(ds)
+
+
+def _codes_agree_up_to_ties(q, s, x_ref, q_ref, s_ref):
+    """Codes equal, except by one where x / scale is within fp32 rounding of a
+    half-integer (the only freedom: the norm's summation order, the device
+    expf).  The scale carries the relative error of 1/sqrt(mean square),
+    about sqrt(K) ulps of the in-order fp32 sum at most here (2e-5); the codes
+    do not depend on it (x / scale = 127 * a w / max|a w| up to rounding)."""
+    assert np.allclose(s, s_ref, rtol=2e-5, atol=0)
+    d = q.astype(np.int32) - q_ref.astype(np.int32)
+    assert np.abs(d).max(initial=0) <= 1
+    t = x_ref.astype(np.float64) / s_ref.astype(np.float64)[:, None]
+    tie = np.abs(np.abs(t - np.floor(t)) - 0.5) <= 1e-5 * np.maximum(1.0, np.abs(t))
+    assert np.all(tie[d != 0]), f"{int((~tie[d != 0]).sum())} codes differ away from a rounding tie"
+    assert (d != 0).mean() < 1e-3
+
+
+@pytest.mark.parametrize("M,K,weighted", [(7, 1536, True), (3, 8960, True), (4, 16384, False), (2, 4, True)])
+def test_rms_quant_bitexact_on_exact_sums(ctx, orc, M, K, weighted):
+    """Rows of quarter-integers (|x| <= 4): every partial sum of squares is a
+    multiple of 1/16 below 2^22, exact in fp32 in any order, so RMSNorm and
+    the codes must be bit-exact against the in-order oracle (cpu_ref.cpp:139-156
+    then amd_xdna.cpp:633-639, 757-771)."""
+    rng = np.random.default_rng(K + M)
+    A = (rng.integers(-16, 17, size=(M, K)) / 4.0).astype(np.float32)
+    A[0] = 0.0  # zero row: inv_std = 1/sqrt(eps), scale 1
+    w = rng.standard_normal(K).astype(np.float32) if weighted else None
+    q, s = _produce_quant(ctx, gl.Producer.RMS_NORM, A, w, eps=1e-6)
+    x_ref = orc.rms_norm(A, w, eps=1e-6)
+    q_ref, s_ref = orc.quant_act(x_ref, 1)
+    assert np.array_equal(q, q_ref)
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K", [(64, 1536), (5, 8960), (3, 2048)])
+def test_rms_quant_vs_oracle(ctx, orc, M, K):
+    rng = np.random.default_rng(M * 7 + K)
+    A = (rng.standard_normal((M, K)) * np.exp(rng.uniform(-20, 20, size=(M, 1)))).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    q, s = _produce_quant(ctx, gl.Producer.RMS_NORM, A, w)
+    x_ref = orc.rms_norm(A, w)
+    q_ref, s_ref = orc.quant_act(x_ref, 1)
+    _codes_agree_up_to_ties(q, s, x_ref, q_ref, s_ref)
+
+
+@pytest.mark.parametrize("M,K", [(64, 8960), (3, 1536), (2, 12)])
+def test_swiglu_quant_vs_oracle(ctx, orc, M, K):
+    rng = np.random.default_rng(M + K)
+    g = (3.0 * rng.standard_normal((M, K))).astype(np.float32)
+    u = rng.standard_normal((M, K)).astype(np.float32)
+    g[0, :4] = [0.0, -100.0, 100.0, -0.0]
+    q, s = _produce_quant(ctx, gl.Producer.SWIGLU, g, u)
+    x_ref = (orc.silu(g) * u).astype(np.float32)
+    q_ref, s_ref = orc.quant_act(x_ref, 1)
+    _codes_agree_up_to_ties(q, s, x_ref, q_ref, s_ref)
+
+
+def test_produce_quant_feeds_q8_matmul(ctx, orc):
+    """RMSNorm+quantize, then the pre-quantized matmul: the fp64 oracle on the
+    same int8 rows (dequantized) within the fp32 bar."""
+    import torch
+    rng = np.random.default_rng(5)
+    M, K, N = 33, 1536, 96
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    raw = weights(gl.GgmlType.Q8_0, N, K, 9)
+    q, s = _produce_quant(ctx, gl.Producer.RMS_NORM, A, w)
+    dW = dev(raw)
+    dq, ds = dev(q), dev(s)
+    dC = empty((M, N), torch.float32)
+    ctx.check(ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ptr(dW), int(gl.GgmlType.Q8_0), N, K, ptr(dq), ptr(ds), M, ptr(dC), N,
+                                         stream_handle()), "mul_mat_q8")
+    x_eff = (q.astype(np.float32) * s[:, None]).astype(np.float32)
+    ref = orc.mul_mat_f64(gl.GgmlType.Q8_0, raw, N, K, x_eff, 0)
+    assert orc.rel_l2(host(dC), ref) <= 1e-4
+
+
+def test_produce_quant_rejects_bad_arguments(ctx):
+    import torch
+    A = empty((2, 20480), torch.float32)
+    q = empty((2, 20480), torch.int8)
+    s = empty((2,), torch.float32)
+    st = ctx.lib.ggq_produce_quantize_act_dev(ctx.h, 1, ptr(A), None, 20480, 2, 20480, 1e-5, ptr(q), ptr(s),
+                                              stream_handle())
+    assert st == gl.Status.INVALID_PARAM
+    assert b"16384" in ctx.lib.ggq_last_error_message(ctx.h)
+    for producer, aux in ((2, None), (3, None)):
+        st = ctx.lib.ggq_produce_quantize_act_dev(ctx.h, producer, ptr(A), aux, 1024, 2, 1024, 1e-5, ptr(q), ptr(s),
+                                                  stream_handle())
+        assert st == gl.Status.INVALID_PARAM
