@@ -525,11 +525,11 @@ def bench_config4(torch, ctx, stream, steps=10):
     return res
 
 
-def bench_config5(torch, ctx, stream, steps=20):
-    """one qwen35moe-A3B MoE FFN layer, 64 tokens, top-8 of 256
-    experts (FFN 512, Q4_K gate/up, Q6_K down) + 1 shared expert, as one
+def bench_config5(torch, ctx, stream, steps=20, T=64):
+    """one qwen35moe-A3B MoE FFN layer, 64 tokens (T), top-8 of
+    256 experts (FFN 512, Q4_K gate/up, Q6_K down) + 1 shared expert, as one
     expert-grouped ggq_moe_ffn_dev call."""
-    T, H, F, E, k = 64, 2048, 512, 256, 8
+    H, F, E, k = 2048, 512, 256, 8
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
     wg, _ = make_weight(torch, gen, Q4K, E * F, H)
@@ -558,7 +558,7 @@ def bench_config5(torch, ctx, stream, steps=20):
     hit = int(torch.unique(sel).numel())
     per_expert = 2 * gl.row_bytes(Q4K, H) * F + gl.row_bytes(Q6K, F) * H
     b = (hit + 1) * per_expert + 4 * T * H * 2 + 4 * T * E
-    return {"workload": "qwen35moe-A3B MoE FFN layer: 64 tokens, top-8 of 256 experts (FFN 512) + shared, "
+    return {"workload": f"qwen35moe-A3B MoE FFN layer: {T} tokens, top-8 of 256 experts (FFN 512) + shared, "
                         "Q4_K gate/up, Q6_K down, one grouped call", "experts_hit": hit,
             "bytes": b, "us": round(sec * 1e6, 1), "GBps": round(b / sec / 1e9, 1),
             "frac_hbm_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
@@ -605,6 +605,8 @@ def main():
                                        "floor"],
                     default=None,
                     help="run one workload only and print its result (profiling aid)")
+    ap.add_argument("--moe-tokens", type=int, default=64,
+                    help="tokens of the MoE layer for --only moe (the bench line uses 64)")
     ap.add_argument("--per-matmul", action="store_true",
                     help="one launch per matmul instead of one per dependency level")
     args = ap.parse_args()
@@ -640,7 +642,7 @@ def main():
         return
     if args.only in ("config1", "prefill", "config4", "moe", "logits", "fused", "attention", "host"):
         res = {"config1": bench_config1, "prefill": bench_prefill, "config4": bench_config4,
-               "moe": bench_config5, "logits": bench_logits, "fused": bench_decode_fused,
+               "moe": lambda *a: bench_config5(*a, T=args.moe_tokens), "logits": bench_logits, "fused": bench_decode_fused,
                "attention": bench_attention, "host": bench_host_api}[args.only](
                    torch, ctx, stream)
         print(json.dumps({"only": args.only, **res}), flush=True)

@@ -1241,7 +1241,13 @@ static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
     const int S = 1 << m.sl2;
     m.ppt = (P + S - 1) / S;
     if (m.ppt > 2) return false;
-    m.ms = (M > 4 && m.ppt == 1 && env_int("GGQ_GEMV_MFMA_MS", 1) >= 2) ? 2 : 1;
+    // 8 rows per pass (MS 2) halves the passes over each weight row but
+    // holds twice the activations: it pays off for expert groups averaging
+    // 8 rows or more (prefill-sized MoE batches), not for plain batches.
+    // GGQ_GEMV_MFMA_MS=1 / 2 forces either.
+    const int ms_env = env_int("GGQ_GEMV_MFMA_MS", 0);
+    const bool eight = ms_env ? ms_env >= 2 : (p.grp_off && p.groups > 1 && (int64_t)p.M >= 8LL * p.groups);
+    m.ms = (M > 4 && m.ppt == 1 && eight) ? 2 : 1;
     const int rows_per_iter = 4 * (64 / S);
     m.n_iters = (p.N + rows_per_iter - 1) / rows_per_iter;
     return true;
