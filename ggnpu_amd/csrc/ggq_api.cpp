@@ -640,7 +640,7 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     // The shared expert's gate / up / SwiGLU rows follow the routed ones in
     // the same buffers (one SwiGLU launch covers both).
     const size_t ts = shared ? (size_t)T : 0;
-    const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 1)), o_act = take(4 * (size_t)(E + 1)),
+    const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 1)),
                  o_tok = take(4 * nk), o_pos = take(4 * nk), o_g = take(4 * (nk + ts) * F),
                  o_u = take(4 * (nk + ts) * F), o_h = take(4 * (nk + ts) * F), o_d = take(4 * nk * H);
     const size_t o_sd = shared ? take(4 * (size_t)T * H) : 0;
@@ -655,18 +655,11 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     float *G = (float*)(base + o_g), *U = (float*)(base + o_u), *Hh = (float*)(base + o_h), *D = (float*)(base + o_d);
 
     if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
-    // Few pairs over many experts (decode): the grouped launches run their
-    // grid over the non-empty experts only (measured: 1 token 53 -> 45 us;
-    // from 8 tokens on, the larger per-expert grids cost more than the idle
-    // workgroups they replace).
-    const bool listed = ggq::moe_group_lists(T, k, E) && nk * 8 <= (size_t)E;
-    int32_t* act = listed ? (int32_t*)(base + o_act) : nullptr;
-    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, act, s)) != hipSuccess) return hip_status(c, e, "moe_group");
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s)) != hipSuccess) return hip_status(c, e, "moe_group");
 
     ggq::GemvProblem g{};
     g.groups = E;
     g.grp_off = grp;
-    g.grp_list = act;
     g.M = (int)nk;
     g.max_group_rows = T;
     // gate / up: rows F, K = H, activations gathered by token.

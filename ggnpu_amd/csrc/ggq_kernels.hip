@@ -355,7 +355,6 @@ struct GemvArgs {
     int ldy;
     int M;
     const int* grp_off;
-    const int* grp_list;  // [count, group ids...]: grid y indexes it when set
     const int* x_idx;
     int lpr_log2;
     int x_vec4;    // X rows are 16-byte aligned (float4 loads)
@@ -746,30 +745,25 @@ template <int T, int MB, int PPT, int U, bool F = false>
 // the MoE default (each expert sees ~2 tokens: the decoded codes are shared).
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MB == 2 ? 3 : 1))) void gemv_kernel(GemvArgs a) {
     __shared__ float red[2][4][U * MB];
-    int by = blockIdx.y;
-    if (a.grp_list) {  // grid y over the non-empty groups only
-        if (by >= a.grp_list[0]) return;
-        by = a.grp_list[1 + by];
-    }
     if constexpr (MB > 1) {
         if (a.grp_off) {
             // Grouped launch: each group (expert) has its own row count, so
             // the rows per pass follow it instead of the launch maximum.
-            const int cnt = a.grp_off[by + 1] - a.grp_off[by];
+            const int cnt = a.grp_off[blockIdx.y + 1] - a.grp_off[blockIdx.y];
             if (cnt <= 0) return;
             if (cnt == 1) {
-                gemv_body<T, 1, PPT, U, F>(a, blockIdx.x, gridDim.x, by, 0, 1,
+                gemv_body<T, 1, PPT, U, F>(a, blockIdx.x, gridDim.x, blockIdx.y, 0, 1,
                                         *reinterpret_cast<float(*)[2][4][U]>(&red));
                 return;
             }
             if (MB > 2 && cnt == 2) {
-                gemv_body<T, 2, PPT, U, F>(a, blockIdx.x, gridDim.x, by, 0, 1,
+                gemv_body<T, 2, PPT, U, F>(a, blockIdx.x, gridDim.x, blockIdx.y, 0, 1,
                                         *reinterpret_cast<float(*)[2][4][U * 2]>(&red));
                 return;
             }
         }
     }
-    gemv_body<T, MB, PPT, U, F>(a, blockIdx.x, gridDim.x, by, blockIdx.z, gridDim.z, red);
+    gemv_body<T, MB, PPT, U, F>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
 }
 
 // Several independent GEMV problems (any mix of formats, same pieces-per-
@@ -1095,12 +1089,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
 template <int T, int PPT, int MS, bool ONE = false>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
     __shared__ float red[2][4][2][4][4 * MS];
-    int by = blockIdx.y;
-    if (a.grp_list) {  // grid y over the non-empty groups only
-        if (by >= a.grp_list[0]) return;
-        by = a.grp_list[1 + by];
-    }
-    gemv_mfma_body<T, PPT, MS, ONE>(a, blockIdx.x, gridDim.x, by, blockIdx.z, gridDim.z, red);
+    gemv_mfma_body<T, PPT, MS, ONE>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
 }
 
 template <int PPT, int MS>
@@ -1293,7 +1282,6 @@ static GemvPlan plan_gemv(const GemvProblem& p) {
     a.Y = p.Y; a.ldy = p.ldy;
     a.M = p.M;
     a.grp_off = p.grp_off;
-    a.grp_list = g.simple ? nullptr : p.grp_list;
     a.x_idx = p.x_idx;
     a.lpr_log2 = lpr_log2;
     a.x_vec4 = ((uintptr_t)p.X % 16 == 0) && (p.ldx % 4 == 0) && ((uintptr_t)p.X2 % 16 == 0);
@@ -1327,10 +1315,6 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         return hipGetLastError();
     }
     const int ppt = g.ppt, mrows = g.mrows;
-    // With a list of the non-empty groups, grid y covers at most one group
-    // per row (a decode step's MoE call: top-k rows over hundreds of
-    // experts) and the resident capacity is shared among those.
-    const int gy = a.grp_list ? (p.M < groups ? (p.M > 0 ? p.M : 1) : groups) : groups;
     {
         MfmaPlan mp;
         if ((groups == 1 || p.grp_off) && mfma_plan(p, mrows, mp)) {
@@ -1340,10 +1324,10 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
             const int gz = groups > 1 ? 1 : (mrows + 4 * mp.ms - 1) / (4 * mp.ms);
 #define GM(PPT_, MS_, ONE_)                                                                       \
     do {                                                                                          \
-        int gx = resident_blocks(gemv_mfma_kernel<T, PPT_, MS_, ONE_>, 0) * (groups > 1 ? moe_rounds() : 1) / (gz * gy); \
+        int gx = resident_blocks(gemv_mfma_kernel<T, PPT_, MS_, ONE_>, 0) * (groups > 1 ? moe_rounds() : 1) / (gz * groups); \
         if (groups > 1 && moe_gx() > 0) gx = moe_gx();                                            \
         gx = gx < 1 ? 1 : (gx > mp.n_iters ? mp.n_iters : gx);                                    \
-        gemv_mfma_kernel<T, PPT_, MS_, ONE_><<<dim3(gx, gy, gz), 256, 0, s>>>(a);             \
+        gemv_mfma_kernel<T, PPT_, MS_, ONE_><<<dim3(gx, groups, gz), 256, 0, s>>>(a);             \
     } while (0)
             if (mrows == 1) {
                 if (mp.ppt == 2) GM(2, 1, true);
@@ -1364,10 +1348,10 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
 #define GO(MB_, PPT_, U_)                                                                        \
     do {                                                                                         \
         const int gz = groups > 1 ? 1 : (mrows + MB_ - 1) / MB_;                                 \
-        int gx = resident_blocks(gemv_kernel<T, MB_, PPT_, U_>, 0) * (groups > 1 ? moe_rounds() : 1) / (gz * gy); \
+        int gx = resident_blocks(gemv_kernel<T, MB_, PPT_, U_>, 0) * (groups > 1 ? moe_rounds() : 1) / (gz * groups); \
         if (groups > 1 && moe_gx() > 0) gx = moe_gx();                                           \
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
-        gemv_kernel<T, MB_, PPT_, U_><<<dim3(gx, gy, gz), 256, 0, s>>>(a);                   \
+        gemv_kernel<T, MB_, PPT_, U_><<<dim3(gx, groups, gz), 256, 0, s>>>(a);                   \
     } while (0)
 #define GO_F(PPT_)                                                                               \
     do {                                                                                         \
@@ -2748,11 +2732,8 @@ constexpr int kGroupFastE = 256;
 __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __restrict__ sel, int n, int E,
                                                                int topk, int32_t* __restrict__ grp_off,
                                                                int32_t* __restrict__ tok_idx,
-                                                               int32_t* __restrict__ pos_of,
-                                                               int32_t* __restrict__ active) {
+                                                               int32_t* __restrict__ pos_of) {
     __shared__ __attribute__((aligned(16))) int32_t s_sel[1024];
-    __shared__ int32_t wact[4];
-    int tot = 0;  // pairs of expert tid (tid < 256)
     __shared__ int32_t hist[16][kGroupFastE];  // per wavefront; then exclusive prefix over wavefronts
     __shared__ int32_t start[kGroupFastE];
     __shared__ int32_t wsum[4];
@@ -2780,7 +2761,6 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
             hist[w][tid] = run;
             run += c;
         }
-        tot = run;
         int incl = run;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -2799,20 +2779,6 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
         if (tid == 0) grp_off[E] = n;
     }
     __syncthreads();
-    if (active) {
-        // Ids of the non-empty experts in increasing order: wavefronts 0-3
-        // (threads 0-255) cover the experts; ballot prefix within each.
-        const bool has = tid < E && tot > 0;
-        const unsigned long long bal = __ballot(has);
-        if (tid < kGroupFastE && lane == 0) wact[wave] = __popcll(bal);
-        __syncthreads();
-        if (has) {
-            int before = 0;
-            for (int w = 0; w < wave; w++) before += wact[w];
-            active[1 + before + __popcll(bal & ((1ull << lane) - 1))] = tid;
-        }
-        if (tid == 0) active[0] = wact[0] + wact[1] + wact[2] + wact[3];
-    }
     if (e >= 0) {
         const int pos = start[e] + hist[wave][e] + rank;
         tok_idx[pos] = tid / topk;
@@ -2820,13 +2786,11 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
     }
 }
 
-bool moe_group_lists(int T, int topk, int E) { return T * topk <= 1024 && E <= kGroupFastE; }
-
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
-                            int32_t* tok_idx, int32_t* pos_of, int32_t* active, hipStream_t s) {
+                            int32_t* tok_idx, int32_t* pos_of, hipStream_t s) {
     if (E > 1024) return hipErrorInvalidValue;
-    if (moe_group_lists(T, topk, E)) {
-        moe_group_small_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of, active);
+    if (T * topk <= 1024 && E <= kGroupFastE) {
+        moe_group_small_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);
         return hipGetLastError();
     }
     moe_group_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);

@@ -42,7 +42,6 @@ struct GemvProblem {
     int M;
     int groups;
     const int* grp_off;
-    const int* grp_list;  // grouped mode, optional: [count, group ids...] of the non-empty groups
     const int* x_idx;
     int max_group_rows;  // upper bound of rows per group (grouped mode)
     // Fused neighbours (zero / null = off; plain mode only):
@@ -105,12 +104,8 @@ hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, fl
 // MoE helpers.
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel,
                             float* wsel, hipStream_t s);
-// When moe_group_lists(T, topk, E), the grouping also writes
-// active[0] = the number of non-empty experts and active[1..] their ids in
-// increasing order (active: E + 1 ints).
-bool moe_group_lists(int T, int topk, int E);
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
-                            int32_t* tok_idx, int32_t* pos_of, int32_t* active, hipStream_t s);
+                            int32_t* tok_idx, int32_t* pos_of, hipStream_t s);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int64_t n, hipStream_t s);
 hipError_t launch_moe_combine(const float* D, const int32_t* pos_of, const float* wsel, int T,
                               int topk, int H, const float* Dsh, const float* shared_w, float* out,

@@ -297,23 +297,6 @@ def test_moe_large_grouping_vs_oracle(ctx, orc, T, E, k):
     assert orc.rel_l2(out, ref) < TOL
 
 
-@pytest.mark.parametrize("T,E,k,shared,tg,td", [(1, 256, 8, True, 12, 14), (2, 256, 8, False, 12, 14),
-                                                (4, 256, 8, True, 20, 23), (1, 64, 8, False, 23, 8),
-                                                (3, 200, 4, True, 13, 14)])
-def test_moe_decode_listed_experts_vs_oracle(ctx, orc, T, E, k, shared, tg, td):
-    """Decode-sized calls (T * k * 8 <= E): the grouped launches run over the
-    list of non-empty experts that the grouping writes (paired gate+up when
-    the types match, separate launches otherwise)."""
-    H, F = 256, 256
-    tu = tg if T != 4 else 23
-    (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(ctx, T, H, F, E, k, shared, seed=7 * T + E,
-                                                                        tg=tg, tu=tu, td=td)
-    ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, tg, Wg, tu, Wu, td, Wd, Sg, Su, Sd, sw)
-    assert np.array_equal(sel, rsel)
-    assert np.allclose(wsel, rw, rtol=1e-6)
-    assert orc.rel_l2(out, ref) < TOL
-
-
 @pytest.mark.parametrize("tg,tu,td", [(8, 8, 8), (20, 23, 20), (23, 20, 23), (8, 13, 14)])
 def test_moe_other_formats_vs_oracle(ctx, orc, tg, tu, td):
     """Expert weights in Q8_0 / IQ4_NL / IQ4_XS (and mixed with K-quants):
