@@ -8,6 +8,7 @@
 // launch covers a whole matmul.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -17,6 +18,7 @@
 #include <set>
 #include <string>
 #include <tuple>
+#include <vector>
 
 #include "../../include/ggq.h"
 #include "ggq_formats.h"
@@ -36,6 +38,12 @@ struct Buffer {
     size_t size = 0;
 };
 
+// Device memory a matmul may use beyond its inputs and outputs.
+struct Work {
+    Buffer ws;    // activation quantization, MoE intermediates
+    Buffer part;  // GEMM split-K partial tiles
+};
+
 }  // namespace
 
 struct ggq_ctx {
@@ -46,12 +54,14 @@ struct ggq_ctx {
     std::string msg;
     std::map<std::tuple<const void*, uint32_t, int64_t, int64_t>, ggq_weight*> cache;
     std::set<ggq_weight*> weights;
-    Buffer ws;  // kernel workspace (activation quant, MoE intermediates)
+    Work dev;   // workspace of the *_dev entry points
+    Work host;  // workspace of the synchronous host-pointer entry points (never
+                // shared with device calls that may still run on other streams)
     Buffer io;  // staging of host A / C for the synchronous entry points
-    Buffer part;  // GEMM split-K partial tiles
     Buffer logits;  // vocab projection output when the caller does not keep it
     Buffer attn;  // attention chunk partials
     Buffer pin;   // pinned host staging of A and C for the synchronous host-pointer entry points
+    std::vector<void*> retired;  // outgrown device buffers, freed by ggq_destroy
 };
 
 namespace {
@@ -79,32 +89,65 @@ int hip_status(ggq_ctx* c, hipError_t e, const char* what) {
     return set_status(c, st, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Grows `b` to at least `need` bytes.  Work queued earlier may still use the
-// old allocation, so the device is drained before it is released.
-hipError_t ensure(Buffer& b, size_t need) {
-    if (b.size >= need) return hipSuccess;
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return e;
-    if (b.ptr) hipFree(b.ptr);
-    b.ptr = nullptr;
-    b.size = 0;
-    size_t sz = need + need / 4 + 4096;
-    e = hipMalloc(&b.ptr, sz);
-    if (e != hipSuccess) return e;
+// Grows `b` to at least `need` bytes for work queued on `s`.  An outgrown
+// allocation is not freed before ggq_destroy: work queued earlier and HIP
+// graphs captured earlier keep using its address.  Growing while `s` is being
+// captured is refused (the allocation would not be part of the graph's
+// ordering); one call outside the capture, or ggq_reserve, sizes it first.
+int grow(ggq_ctx* c, Buffer& b, size_t need, hipStream_t s, const char* what) {
+    if (b.size >= need) return GGQ_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return set_status(c, GGQ_ERROR,
+                          "%s: %zu bytes of workspace needed while the stream is being captured (%zu reserved); "
+                          "call ggq_reserve or run the call once before the capture",
+                          what, need, b.size);
+    const size_t sz = std::max(need + 4096, 2 * b.size);
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, sz);
+    if (e != hipSuccess) return hip_status(c, e, what);
+    if (b.ptr) c->retired.push_back(b.ptr);
+    b.ptr = p;
     b.size = sz;
-    return hipSuccess;
+    return GGQ_OK;
 }
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-// Split-K workspace for a GEMM plan (null when the plan does not split).
-hipError_t ensure_gemm_ws(ggq_ctx* c, const ggq::GemmPlan& pl, float** part) {
-    *part = nullptr;
-    if (pl.splits <= 1) return hipSuccess;
-    hipError_t e = ensure(c->part, sizeof(float) * pl.part_floats);
-    if (e == hipSuccess) *part = (float*)c->part.ptr;
-    return e;
-}
+// Where a call's scratch memory comes from: the growable buffers of a Work,
+// or one fixed region (activation workspace first, split-K partials after).
+struct Arena {
+    ggq_ctx* c;
+    Work* w;
+    char* fixed;
+    size_t cap;
+    hipStream_t s;
+    int get(size_t ws_bytes, size_t part_bytes, void** ws, float** part, const char* what) {
+        *ws = nullptr;
+        *part = nullptr;
+        if (w) {
+            int st;
+            if (ws_bytes && (st = grow(c, w->ws, ws_bytes, s, what)) != GGQ_OK) return st;
+            if (part_bytes && (st = grow(c, w->part, part_bytes, s, what)) != GGQ_OK) return st;
+            *ws = w->ws.ptr;
+            *part = part_bytes ? (float*)w->part.ptr : nullptr;
+            return GGQ_OK;
+        }
+        const size_t off = align256(ws_bytes);
+        if (off + part_bytes > cap)
+            return set_status(c, GGQ_INVALID_PARAM,
+                              "%s: the call needs %zu bytes of scratch; the allocation-free entry point has %zu",
+                              what, off + part_bytes, cap);
+        *ws = fixed;
+        *part = part_bytes ? (float*)(fixed + off) : nullptr;
+        return GGQ_OK;
+    }
+};
+
+Arena dev_arena(ggq_ctx* c, hipStream_t s) { return Arena{c, &c->dev, nullptr, 0, s}; }
+
+// Split-K partial bytes of a GEMM plan (0 when the plan does not split).
+size_t gemm_part_bytes(const ggq::GemmPlan& pl) { return pl.splits <= 1 ? 0 : sizeof(float) * pl.part_floats; }
 
 // Stream of a device-pointer call: the caller's, or the HIP default (null)
 // stream for NULL, as HIP APIs treat a null stream argument.  (The context's
@@ -127,10 +170,11 @@ int check_matmul_shape(ggq_ctx* c, uint32_t type, int64_t N, int64_t K, int M, i
 }
 
 // Queues C = A . W^T with the requested activation treatment.
-int mul_mat_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const float* A,
+int mul_mat_queue(ggq_ctx* c, Arena& ar, const void* W, uint32_t type, int64_t N, int64_t K, const float* A,
                   int lda, float* C, int ldc, int M, int act_mode, hipStream_t s) {
     if (M == 0) return set_status(c, GGQ_OK);
     hipError_t e;
+    int st;
     ggq::GemvProblem g{};
     g.type = type;
     g.W = W;
@@ -150,17 +194,17 @@ int mul_mat_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K
     const size_t x_off = align256(s_off + sizeof(float) * (size_t)M * (K / 32));
     const bool use_gemm = act_mode == GGQ_ACT_Q8_ROW && M > 8;
     const size_t need = use_gemm ? x_off : align256(x_off + sizeof(float) * (size_t)M * K);
-    if ((e = ensure(c->ws, need)) != hipSuccess) return hip_status(c, e, "workspace");
-    int8_t* q = (int8_t*)c->ws.ptr + q_off;
-    float* sc = (float*)((char*)c->ws.ptr + s_off);
-    float* xe = (float*)((char*)c->ws.ptr + x_off);
+    const int n32 = (int)N;
+    const size_t part_bytes = use_gemm ? gemm_part_bytes(ggq::plan_gemm_i8(type, &n32, 1, (int)K, M)) : 0;
+    void* ws;
+    float* part;
+    if ((st = ar.get(need, part_bytes, &ws, &part, "workspace")) != GGQ_OK) return st;
+    int8_t* q = (int8_t*)ws + q_off;
+    float* sc = (float*)((char*)ws + s_off);
+    float* xe = (float*)((char*)ws + x_off);
     if (use_gemm) {
         if ((e = ggq::launch_quant_act(A, lda, M, (int)K, act_mode, q, sc, nullptr, s)) != hipSuccess)
             return hip_status(c, e, "quant_act");
-        const int n32 = (int)N;
-        float* part;
-        if ((e = ensure_gemm_ws(c, ggq::plan_gemm_i8(type, &n32, 1, (int)K, M), &part)) != hipSuccess)
-            return hip_status(c, e, "workspace");
         return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, q, sc, M, C, ldc, part, s), "gemm_i8");
     }
     if ((e = ggq::launch_quant_act(A, lda, M, (int)K, act_mode, nullptr, nullptr, xe, s)) != hipSuccess)
@@ -171,19 +215,21 @@ int mul_mat_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K
 }
 
 // C = sa * (qa . W^T) from activations already quantized per row.
-int mul_mat_q8_queue(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const int8_t* qa,
+int mul_mat_q8_queue(ggq_ctx* c, Arena& ar, const void* W, uint32_t type, int64_t N, int64_t K, const int8_t* qa,
                      const float* sa, int M, float* C, int ldc, hipStream_t s) {
     if (M == 0) return set_status(c, GGQ_OK);
     hipError_t e;
+    int st;
+    void* ws;
+    float* part;
     if (M > 8) {
         const int n32 = (int)N;
-        float* part;
-        if ((e = ensure_gemm_ws(c, ggq::plan_gemm_i8(type, &n32, 1, (int)K, M), &part)) != hipSuccess)
-            return hip_status(c, e, "workspace");
+        const size_t part_bytes = gemm_part_bytes(ggq::plan_gemm_i8(type, &n32, 1, (int)K, M));
+        if ((st = ar.get(0, part_bytes, &ws, &part, "workspace")) != GGQ_OK) return st;
         return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, qa, sa, M, C, ldc, part, s), "gemm_i8");
     }
-    if ((e = ensure(c->ws, sizeof(float) * (size_t)M * K)) != hipSuccess) return hip_status(c, e, "workspace");
-    float* xe = (float*)c->ws.ptr;
+    if ((st = ar.get(sizeof(float) * (size_t)M * K, 0, &ws, &part, "workspace")) != GGQ_OK) return st;
+    float* xe = (float*)ws;
     if ((e = ggq::launch_dequant_act(qa, sa, M, (int)K, xe, s)) != hipSuccess) return hip_status(c, e, "dequant_act");
     ggq::GemvProblem g{};
     g.type = type;
@@ -249,8 +295,8 @@ int mul_mat_host(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float
     if (M == 0) return set_status(c, GGQ_OK);
     const size_t a_bytes = sizeof(float) * (size_t)M * w->K;
     const size_t c_bytes = sizeof(float) * (size_t)M * w->N;
-    hipError_t e = ensure(c->io, a_bytes);
-    if (e != hipSuccess) return hip_status(c, e, "io buffer");
+    if ((st = grow(c, c->io, a_bytes, c->stream, "io buffer")) != GGQ_OK) return st;
+    hipError_t e;
     if ((e = ensure_pinned(c->pin, align256(a_bytes) + c_bytes)) != hipSuccess) return hip_status(c, e, "pinned buffer");
     float* dA = (float*)c->io.ptr;
     float* hA = (float*)c->pin.ptr;
@@ -260,7 +306,8 @@ int mul_mat_host(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float
     // written once per element, straight into the pinned buffer.
     e = ggq::launch_copy_bytes(dA, hA, a_bytes, c->stream);
     if (e != hipSuccess) return hip_status(c, e, "copy A");
-    st = mul_mat_queue(c, w->dev, w->type, w->N, w->K, dA, (int)w->K, hC, (int)w->N, M, act_mode, c->stream);
+    Arena ar{c, &c->host, nullptr, 0, c->stream};
+    st = mul_mat_queue(c, ar, w->dev, w->type, w->N, w->K, dA, (int)w->K, hC, (int)w->N, M, act_mode, c->stream);
     if (st != GGQ_OK) return st;
     if ((e = hipStreamSynchronize(c->stream)) != hipSuccess) return hip_status(c, e, "sync");
     for (int m = 0; m < M; m++) memcpy(C + (size_t)m * ldc, hC + (size_t)m * w->N, sizeof(float) * w->N);
@@ -312,9 +359,10 @@ void ggq_destroy(ggq_ctx* c) {
         hipFree(w->dev);
         delete w;
     }
-    if (c->ws.ptr) hipFree(c->ws.ptr);
+    for (Buffer* b : {&c->dev.ws, &c->dev.part, &c->host.ws, &c->host.part})
+        if (b->ptr) hipFree(b->ptr);
+    for (void* p : c->retired) hipFree(p);
     if (c->io.ptr) hipFree(c->io.ptr);
-    if (c->part.ptr) hipFree(c->part.ptr);
     if (c->logits.ptr) hipFree(c->logits.ptr);
     if (c->attn.ptr) hipFree(c->attn.ptr);
     if (c->pin.ptr) hipHostFree(c->pin.ptr);
@@ -403,7 +451,20 @@ int ggq_mul_mat_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t
     if (!aligned16(W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
     int st = check_matmul_shape(c, type, N, K, M, lda, ldc, act_mode);
     if (st != GGQ_OK) return st;
-    return mul_mat_queue(c, W, type, N, K, A, lda, C, ldc, M, act_mode, pick_stream(c, stream));
+    const hipStream_t s = pick_stream(c, stream);
+    Arena ar = dev_arena(c, s);
+    return mul_mat_queue(c, ar, W, type, N, K, A, lda, C, ldc, M, act_mode, s);
+    GGQ_END(c)
+}
+
+int ggq_reserve(ggq_ctx* c, int64_t bytes) {
+    GGQ_GUARD(c)
+    if (bytes < 0) return set_status(c, GGQ_INVALID_PARAM, "negative size");
+    const size_t b = (size_t)bytes;
+    int st;
+    for (Buffer* buf : {&c->dev.ws, &c->dev.part, &c->logits, &c->attn})
+        if ((st = grow(c, *buf, b, c->stream, "reserve")) != GGQ_OK) return st;
+    return set_status(c, GGQ_OK);
     GGQ_END(c)
 }
 
@@ -419,11 +480,11 @@ int ggq_logits_argmax_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, i
     // does not keep them.
     const size_t part_bytes = align256(ggq::argmax_workspace_bytes(M));
     const size_t need = part_bytes + (logits ? 0 : sizeof(float) * (size_t)M * (size_t)N);
-    hipError_t e = ensure(c->logits, need);
-    if (e != hipSuccess) return hip_status(c, e, "logits workspace");
-    float* L = logits ? logits : (float*)((char*)c->logits.ptr + part_bytes);
     const hipStream_t s = pick_stream(c, stream);
-    st = mul_mat_queue(c, W, type, N, K, A, (int)K, L, (int)N, M, act_mode, s);
+    if ((st = grow(c, c->logits, need, s, "logits workspace")) != GGQ_OK) return st;
+    float* L = logits ? logits : (float*)((char*)c->logits.ptr + part_bytes);
+    Arena ar = dev_arena(c, s);
+    st = mul_mat_queue(c, ar, W, type, N, K, A, (int)K, L, (int)N, M, act_mode, s);
     if (st != GGQ_OK) return st;
     return hip_status(c, ggq::launch_argmax_rows(L, M, (int)N, (int)N, token, value, c->logits.ptr, s), "argmax");
     GGQ_END(c)
@@ -445,10 +506,11 @@ int ggq_attention_decode_dev(ggq_ctx* c, const float* Q, const float* K, const f
     if (!aligned16(Q) || !aligned16(K) || !aligned16(V))
         return set_status(c, GGQ_INVALID_PARAM, "Q, K and V must be 16-byte aligned");
     const size_t need = sizeof(float) * ggq::attn_workspace_floats(n_tok, n_head, head_dim, ctx_len, pos0, n_kv_head);
-    hipError_t e = ensure(c->attn, need);
-    if (e != hipSuccess) return hip_status(c, e, "attention workspace");
+    const hipStream_t s = pick_stream(c, stream);
+    const int st = grow(c, c->attn, need, s, "attention workspace");
+    if (st != GGQ_OK) return st;
     return hip_status(c, ggq::launch_attn_decode(Q, K, V, n_tok, n_head, n_kv_head, head_dim, ctx_len, pos0, out,
-                                                 (float*)c->attn.ptr, pick_stream(c, stream)),
+                                                 (float*)c->attn.ptr, s),
                       "attention");
     GGQ_END(c)
 }
@@ -460,7 +522,9 @@ int ggq_mul_mat_q8_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int6
     if (!aligned16(W) || ((uintptr_t)qa & 15u)) return set_status(c, GGQ_INVALID_PARAM, "W and qa must be 16-byte aligned");
     int st = check_matmul_shape(c, type, N, K, M, (int)K, ldc, GGQ_ACT_Q8_ROW);
     if (st != GGQ_OK) return st;
-    return mul_mat_q8_queue(c, W, type, N, K, qa, sa, M, C, ldc, pick_stream(c, stream));
+    const hipStream_t s = pick_stream(c, stream);
+    Arena ar = dev_arena(c, s);
+    return mul_mat_q8_queue(c, ar, W, type, N, K, qa, sa, M, C, ldc, s);
     GGQ_END(c)
 }
 
@@ -478,9 +542,10 @@ int ggq_mul_mat_q8_batch_dev(ggq_ctx* c, const ggq_gemm_desc* d, int n, uint32_t
     }
     if (M == 0) return set_status(c, GGQ_OK);
     const hipStream_t s = pick_stream(c, stream);
+    Arena ar = dev_arena(c, s);
     if (M <= 8 || type == GGQ_TYPE_Q6_K) {
         for (int i = 0; i < n; i++) {
-            const int st = mul_mat_q8_queue(c, d[i].W, type, d[i].N, K, qa, sa, M, d[i].C, d[i].ldc, s);
+            const int st = mul_mat_q8_queue(c, ar, d[i].W, type, d[i].N, K, qa, sa, M, d[i].C, d[i].ldc, s);
             if (st != GGQ_OK) return st;
         }
         return set_status(c, GGQ_OK);
@@ -491,9 +556,10 @@ int ggq_mul_mat_q8_batch_dev(ggq_ctx* c, const ggq_gemm_desc* d, int n, uint32_t
         gd[i] = ggq::GemmDesc{d[i].W, d[i].C, (int)d[i].N, d[i].ldc};
         Ns[i] = (int)d[i].N;
     }
+    void* ws;
     float* part;
-    hipError_t e = ensure_gemm_ws(c, ggq::plan_gemm_i8(type, Ns, n, (int)K, M), &part);
-    if (e != hipSuccess) return hip_status(c, e, "workspace");
+    const int st = ar.get(0, gemm_part_bytes(ggq::plan_gemm_i8(type, Ns, n, (int)K, M)), &ws, &part, "workspace");
+    if (st != GGQ_OK) return st;
     return hip_status(c, ggq::launch_gemm_i8_multi(type, gd, n, (int)K, qa, sa, M, part, s), "gemm_i8 batch");
     GGQ_END(c)
 }
@@ -644,9 +710,9 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
                  o_tok = take(4 * nk), o_pos = take(4 * nk), o_g = take(4 * (nk + ts) * F),
                  o_u = take(4 * (nk + ts) * F), o_h = take(4 * (nk + ts) * F), o_d = take(4 * nk * H);
     const size_t o_sd = shared ? take(4 * (size_t)T * H) : 0;
-    hipError_t e = ensure(c->ws, off);
-    if (e != hipSuccess) return hip_status(c, e, "workspace");
-    char* base = (char*)c->ws.ptr;
+    if ((st = grow(c, c->dev.ws, off, s, "workspace")) != GGQ_OK) return st;
+    hipError_t e;
+    char* base = (char*)c->dev.ws.ptr;
     int32_t* sel = (int32_t*)(base + o_sel);
     float* wsel = (float*)(base + o_w);
     int32_t* grp = (int32_t*)(base + o_go);

@@ -2585,7 +2585,8 @@ hipError_t launch_attn_decode(const float* Q, const float* K, const float* V, in
 constexpr int kRouteMaxPerLane = 16;
 // One argmax step against the lane selected by DPP control CTRL: the larger
 // value wins, ties go to the lower expert index (as the reference's scan in
-// index order).  -inf values with index 0x7FFFFFFF never win a tie.
+// index order).  -inf values with index 0x7FFFFFFF never win a tie; a free
+// expert always exists (topk <= E), so the final index is below E.
 template <int CTRL> __device__ __forceinline__ void route_step(float& best, int& bi) {
     const float ov = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, best), CTRL, 0xF, 0xF, false));
     const int oi = __builtin_amdgcn_mov_dpp(bi, CTRL, 0xF, 0xF, false);
@@ -2604,7 +2605,10 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
 #pragma unroll
     for (int i = 0; i < PL; i++) {
         const int e = lane + 64 * i;
-        v[i] = e < E ? l[e] : -INFINITY;
+        // A NaN logit ranks with -inf (ties to the lower id), so every
+        // selection is an expert below E whatever the logits hold.
+        const float x = e < E ? l[e] : -INFINITY;
+        v[i] = x != x ? -INFINITY : x;
         if (e >= E) taken |= 1u << i;
     }
     int my_sel = 0;
@@ -2640,8 +2644,10 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
             bi = ri;
         }
         if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == j) { my_sel = bi; my_l = best; }
+        if (lane == j) my_sel = bi;
     }
+    // The softmax takes the selected logits as given (NaN included).
+    if (lane < topk) my_l = l[my_sel];
     const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_l), 0));
     const float ex = lane < topk ? expf(my_l - l0) : 0.0f;
     float sum = 0.0f;  // in selection order, as the reference adds them
@@ -2672,6 +2678,9 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t
 // rank among earlier pairs of its expert, counted over an LDS copy of `sel`
 // (chunks of kGroupChunk pairs; `base` carries the counts of earlier chunks).
 constexpr int kGroupChunk = 8192;
+// Selections come from moe_route_kernel and are below E; the clamp keeps the
+// LDS histograms and the output positions in range regardless.
+__device__ __forceinline__ int expert_id(int e, int E) { return e < 0 ? 0 : e >= E ? E - 1 : e; }
 __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restrict__ sel, int n, int E,
                                                          int topk, int32_t* __restrict__ grp_off,
                                                          int32_t* __restrict__ tok_idx,
@@ -2682,7 +2691,7 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restri
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     base[tid] = 0;
     __syncthreads();
-    for (int f = tid; f < n; f += 1024) atomicAdd(&base[sel[f]], 1);
+    for (int f = tid; f < n; f += 1024) atomicAdd(&base[expert_id(sel[f], E)], 1);
     __syncthreads();
     // Exclusive scan of the counts: base[e] = first position of expert e.
     const int c = base[tid];
@@ -2704,7 +2713,7 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restri
     __syncthreads();
     for (int c0 = 0; c0 < n; c0 += kGroupChunk) {
         const int len = n - c0 < kGroupChunk ? n - c0 : kGroupChunk;
-        for (int f = tid; f < len; f += 1024) chunk[f] = sel[c0 + f];
+        for (int f = tid; f < len; f += 1024) chunk[f] = expert_id(sel[c0 + f], E);
         __syncthreads();
         for (int f = tid; f < len; f += 1024) {
             const int e = chunk[f];
@@ -2738,7 +2747,7 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
     __shared__ int32_t start[kGroupFastE];
     __shared__ int32_t wsum[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int e = tid < n ? sel[tid] : -1;
+    const int e = tid < n ? expert_id(sel[tid], E) : -1;
     s_sel[tid] = e;
     for (int i = tid; i < 16 * kGroupFastE; i += 1024) (&hist[0][0])[i] = 0;
     __syncthreads();

@@ -117,6 +117,7 @@ SIGNATURES = {
     "ggq_name": (ctypes.c_char_p, [_P]),
     "ggq_is_available": (_I, [_P]),
     "ggq_sync": (_I, [_P]),
+    "ggq_reserve": (_I, [_P, _I64]),
     "ggq_mul_mat_q": (_I, [_P, ctypes.POINTER(MulMatParams), _I]),
     "ggq_weight_upload": (_I, [_P, _P, _U32, _I64, _I64, ctypes.POINTER(_P)]),
     "ggq_weight_free": (_I, [_P, _P]),

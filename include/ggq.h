@@ -77,6 +77,20 @@ int ggq_is_available(const ggq_ctx* ctx);
  * device (the context stream and the streams passed to the *_dev calls). */
 int ggq_sync(ggq_ctx* ctx);
 
+/* Workspace contract.  The *_dev calls take their scratch memory (quantized
+ * activations, split-K partial tiles, MoE intermediates, logits and
+ * attention partials) from buffers the context grows on demand.  An outgrown
+ * buffer is kept until ggq_destroy, never freed earlier, so work queued
+ * before the growth and HIP graphs captured before it stay valid.  A call
+ * made while its stream is being captured never allocates: if its workspace
+ * is too small it fails with GGQ_ERROR and says so in
+ * ggq_last_error_message.  Size the workspace before a capture by running
+ * the captured calls once outside it, or with ggq_reserve.  The synchronous
+ * host-pointer calls use their own buffers.  No reference counterpart (the
+ * reference has no device workspace). */
+/* Grows each of the context's device workspaces to at least `bytes`. */
+int ggq_reserve(ggq_ctx* ctx, int64_t bytes);
+
 /* ------------------------------------------------ host-pointer, synchronous */
 
 /* MulMatParams (backend.h:21-35) with B = raw GGUF bytes; field order and

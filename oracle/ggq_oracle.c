@@ -426,27 +426,36 @@ int orc_moe_ffn_f64(const float* x, const float* logits, int T, int H, int F, in
     double* d = (double*)malloc(sizeof(double) * H);
     float* act = (float*)malloc(sizeof(float) * F);
     int* idx = (int*)malloc(sizeof(int) * E);
+    int sel_idx[64];
+    if (topk > 64) { free(g); free(u); free(d); free(act); free(idx); return 3; }
     if (!g || !u || !d || !act || !idx) { free(g); free(u); free(d); free(act); free(idx); return 5; }
     for (int t = 0; t < T; t++) {
         const float* xt = x + (size_t)t * H;
         const float* lt = logits + (size_t)t * E;
         double* ot = out + (size_t)t * H;
         for (int i = 0; i < H; i++) ot[i] = 0.0;
-        /* selection sort of the top-k by descending logit */
-        for (int e = 0; e < E; e++) idx[e] = e;
+        /* top-k by descending logit, ties to the lower expert id; a NaN
+         * logit ranks with -inf (the reference's partial_sort has no order
+         * for NaN; this rule keeps every selection a valid expert id) */
+        for (int e = 0; e < E; e++) idx[e] = 0; /* taken flags */
         for (int j = 0; j < topk; j++) {
-            int best = j;
-            for (int e = j + 1; e < E; e++)
-                if (lt[idx[e]] > lt[idx[best]]) best = e;
-            int tmp = idx[j]; idx[j] = idx[best]; idx[best] = tmp;
+            int best = -1;
+            float bv = -INFINITY;
+            for (int e = 0; e < E; e++) {
+                if (idx[e]) continue;
+                const float v = isnan(lt[e]) ? -INFINITY : lt[e];
+                if (best < 0 || v > bv) { best = e; bv = v; }
+            }
+            idx[best] = 1;
+            sel_idx[j] = best;
         }
         double wsum = 0.0, wv[64];
-        for (int j = 0; j < topk; j++) { wv[j] = exp((double)lt[idx[j]] - (double)lt[idx[0]]); wsum += wv[j]; }
+        for (int j = 0; j < topk; j++) { wv[j] = exp((double)lt[sel_idx[j]] - (double)lt[sel_idx[0]]); wsum += wv[j]; }
         for (int j = 0; j < topk + 1; j++) {
             const uint8_t *pg, *pu, *pd;
             double wj;
             if (j < topk) {
-                const int e = idx[j];
+                const int e = sel_idx[j];
                 wj = wv[j] / wsum;
                 if (sel_experts) sel_experts[t * topk + j] = e;
                 if (sel_weights) sel_weights[t * topk + j] = (float)wj;

@@ -111,6 +111,38 @@ def test_quant_act_bitexact(ctx, orc, mode, M, K):
     assert np.array_equal(host(ds).view(np.uint32), s_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("K", [64, 1536])
+def test_quant_act_rounding_rows_bitexact(ctx, orc, K):
+    """Rows with exact half-integer ties (scale 1) and rows where dividing by
+    the scale would round differently from multiplying by its reciprocal:
+    the device quantizer gives the reference's codes (exact rational
+    arithmetic) in row and block32 mode."""
+    import torch
+    from tests import quant_rows as qr
+    A = np.vstack([qr.tie_row(K), qr.reciprocal_rows(3, K, seed=K)])
+    nb = K // 32
+    B = np.vstack([np.concatenate([qr.tie_row(32), *qr.reciprocal_rows(nb - 1, 32, seed=K + 1)]),
+                   qr.reciprocal_rows(nb, 32, seed=K + 2).reshape(K)])
+    for mode, X in ((1, A), (2, B)):
+        q_ref, s_ref = orc.quant_act(X, mode)
+        M = X.shape[0]
+        dq = empty((M, K), torch.int8)
+        ds = empty(s_ref.shape, torch.float32)
+        dX = dev(X)
+        ctx.check(ctx.lib.ggq_quantize_act_dev(ctx.h, ptr(dX), K, M, K, mode, ptr(dq), ptr(ds),
+                                               stream_handle()), "quant_act")
+        q, sc = host(dq), host(ds)
+        assert np.array_equal(q, q_ref)
+        assert np.array_equal(sc.view(np.uint32), s_ref.view(np.uint32))
+        blk = K if mode == 1 else 32
+        for m in range(M):
+            for b in range(K // blk):
+                eq, es = qr.expected_codes(X[m, b * blk:(b + 1) * blk])
+                assert np.array_equal(q[m, b * blk:(b + 1) * blk], eq), (mode, m, b)
+        if mode == 1:
+            assert q[0, :10].tolist() == [127, 0, 0, 2, -2, 2, -2, 4, -4, 4]
+
+
 @pytest.mark.parametrize("M,K,lda", [(5, 1001, 1001), (4, 64, 67)])
 def test_quant_act_row_unaligned_bitexact(ctx, orc, M, K, lda):
     """Rows that are not 16-byte aligned take the scalar path; same codes."""
@@ -234,7 +266,7 @@ def test_prefill_f32_large_m(ctx, orc):
 
 
 # ------------------------------------------------------------------- MoE
-def run_moe(ctx, T, H, F, E, k, shared, seed, tg=12, tu=12, td=14):
+def run_moe(ctx, T, H, F, E, k, shared, seed, tg=12, tu=12, td=14, edit_logits=None):
     import torch
     rng = np.random.default_rng(seed)
     Wg = gl.encode(tg, (rng.standard_normal((E * F, H)) * 0.02).astype(np.float32))
@@ -248,6 +280,8 @@ def run_moe(ctx, T, H, F, E, k, shared, seed, tg=12, tu=12, td=14):
         sw = (1.0 / (1.0 + np.exp(-rng.standard_normal(T)))).astype(np.float32)
     x = rng.standard_normal((T, H)).astype(np.float32)
     logits = rng.standard_normal((T, E)).astype(np.float32)
+    if edit_logits is not None:
+        edit_logits(logits)
     keep = [dev(a) if a is not None else None for a in (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw)]
     out = empty((T, H), torch.float32)
     sel = empty((T, k), torch.int32)
@@ -322,6 +356,41 @@ def test_moe_routing_expert_counts(ctx, orc, E, k):
     assert np.array_equal(sel, rsel)
     assert np.allclose(wsel, rw, rtol=1e-6)
     assert orc.rel_l2(out, ref) < TOL
+
+def test_moe_nan_router_logits(ctx, orc):
+    """Router rows holding NaN: a NaN logit ranks with -inf, so every
+    selection is a valid expert id (an all-NaN row selects experts 0..k-1);
+    tokens with finite logits are unaffected.  Rows with tied logits select
+    the lower expert id first."""
+    T, H, F, E, k = 12, 256, 256, 64, 8
+
+    def edit(lg):
+        lg[1, :] = np.nan                 # all NaN
+        lg[3, ::2] = np.nan               # half NaN: the 32 finite ones win
+        lg[5, 60:] = np.nan               # a few NaN
+        lg[7, :] = np.nan
+        lg[7, [9, 40]] = (0.5, 0.5)       # two finite (tied), the rest NaN
+        lg[8, :] = 0.25                   # all tied
+        lg[9, :] = -np.inf
+        lg[9, 33] = np.nan
+    (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(ctx, T, H, F, E, k, True, seed=77,
+                                                                        edit_logits=edit)
+    assert sel.min() >= 0 and sel.max() < E
+    ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, 12, Wg, 12, Wu, 14, Wd, Sg, Su, Sd, sw)
+    assert np.array_equal(sel, rsel)
+    assert list(sel[1]) == list(range(k))
+    assert list(sel[7][:3]) == [9, 40, 0]
+    assert list(sel[8]) == list(range(k))
+    assert np.all(sel[3] % 2 == 1)
+    finite = np.all(np.isfinite(logits), axis=1)
+    assert finite.sum() == T - 5
+    assert np.allclose(wsel[finite], rw[finite], rtol=1e-6)
+    assert orc.rel_l2(out[finite], ref[finite]) < TOL
+    # the same finite tokens without the NaN rows in the batch give the same outputs
+    (out2, sel2, _), _ = run_moe(ctx, T, H, F, E, k, True, seed=77)
+    assert np.array_equal(sel2[finite], sel[finite])
+    assert orc.rel_l2(out[finite], out2[finite]) < 1e-6
+
 
 # --------------------------------------------------------- host boundary
 def test_mul_mat_q_host_api_and_errors(ctx, orc):

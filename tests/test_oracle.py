@@ -178,6 +178,41 @@ def test_quant_act_block32_closed_form(orc):
     assert np.array_equal(q, q_exp.reshape(3, 128))
 
 
+def test_quant_act_rounding_rules_pinned(orc):
+    """Exact ties (half to even, not half away) and rows where dividing by
+    the scale rounds differently from multiplying by its fp32 reciprocal
+    (amd_xdna.cpp:598-603, 633-639, 762-766).  Expected codes come from exact
+    rational arithmetic with explicit fp32 rounding; each wrong variant is
+    shown to disagree, so either mistake in the oracle fails this test."""
+    from tests import quant_rows as qr
+    K = 64
+    A = np.vstack([qr.tie_row(K), qr.reciprocal_rows(3, K, seed=11)])
+    q, s = orc.quant_act(A, 1)
+    for m in range(A.shape[0]):
+        eq, es = qr.expected_codes(A[m])
+        assert np.array_equal(q[m], eq), m
+        assert s[m] == es
+    assert q[0, :10].tolist() == [127, 0, 0, 2, -2, 2, -2, 4, -4, 4]
+    assert q[0, 10:13].tolist() == [126, -126, -127]
+    away = qr.variant_codes(A, divide=False, away=True)
+    div = qr.variant_codes(A, divide=True, away=False)
+    assert not np.array_equal(away[0], q[0])
+    for m in range(1, A.shape[0]):
+        assert (div[m] != q[m]).sum() >= K // 4, m
+    # block32 mode: the same rows cut into 32-value blocks, each with its own
+    # amax (the tie block's amax is 127, so its scale is exactly 1)
+    B = np.vstack([np.concatenate([qr.tie_row(32), qr.reciprocal_rows(1, 32, seed=12)[0]]),
+                   qr.reciprocal_rows(2, 32, seed=13).reshape(1, 64)])
+    qb, sb = orc.quant_act(B, 2)
+    for m in range(B.shape[0]):
+        for b in range(2):
+            eq, es = qr.expected_codes(B[m, 32 * b: 32 * b + 32])
+            assert np.array_equal(qb[m, 32 * b: 32 * b + 32], eq), (m, b)
+            assert sb[m, b] == es
+    assert not np.array_equal(qr.variant_codes(B, False, True, block=32), qb)
+    assert not np.array_equal(qr.variant_codes(B, True, False, block=32), qb)
+
+
 @pytest.mark.parametrize("name", list(TYPES))
 def test_block_dot_brute_force(orc, golden, name):
     t = TYPES[name]
@@ -236,6 +271,31 @@ def test_moe_oracle_vs_numpy_loop(orc):
             h = (g / (1 + np.exp(-g)) * u).astype(np.float32).astype(np.float64)
             ref += w[j] * (dd[e] @ h)
         assert orc.rel_l2(out[t], ref) < 1e-12
+
+
+def test_moe_oracle_routing_ties_and_nan(orc):
+    """Routing rule beyond the reference's defined cases: ties go to the
+    lower expert id (the reference's partial_sort leaves them unordered) and
+    NaN ranks with -inf, so selections are always valid ids.  Distinct finite
+    logits are ordered as std::partial_sort with `>` orders them."""
+    import ggnpu_amd.lib as gl
+    rng = np.random.default_rng(9)
+    T, H, F, E, k = 5, 256, 256, 8, 3
+    Wg = gl.encode(12, (rng.standard_normal((E * F, H)) * 0.02).astype(np.float32))
+    Wd = gl.encode(14, (rng.standard_normal((E * H, F)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    lg = np.array([[0.1, 0.9, 0.9, 0.2, 0.9, 0.0, -1.0, 0.3],        # ties at 0.9
+                   [np.nan] * 8,                                     # all NaN
+                   [np.nan, -1, np.nan, 2, np.nan, np.nan, np.nan, np.nan],
+                   [-np.inf, -np.inf, -np.inf, -np.inf, 5, -np.inf, -np.inf, np.nan],
+                   [3, 1, 4, 1.5, 9, 2.6, 5.3, 5.8]], np.float32)
+    _, sel, w = orc.moe_ffn_f64(x, lg, H, F, E, k, 12, Wg, 12, Wg, 14, Wd)
+    assert sel.tolist() == [[1, 2, 4], [0, 1, 2], [3, 1, 0], [4, 0, 1], [4, 7, 6]]
+    assert np.allclose(w[0], 1 / 3) and np.all(np.isnan(w[1]))
+    assert np.all(np.isnan(w[2]))  # a NaN among the selected makes the softmax NaN
+    assert np.allclose(w[3], [1, 0, 0])
+    e = np.exp(np.float64([9, 5.8, 5.3]) - 9)
+    assert np.allclose(w[4], e / e.sum(), rtol=1e-6)
 
 
 # ------------------------------------------- RMSNorm / silu (fused GEMV)
