@@ -386,10 +386,11 @@ def test_moe_nan_router_logits(ctx, orc):
     assert finite.sum() == T - 5
     assert np.allclose(wsel[finite], rw[finite], rtol=1e-6)
     assert orc.rel_l2(out[finite], ref[finite]) < TOL
-    # the same finite tokens without the NaN rows in the batch give the same outputs
+    # the tokens left unedited give the same outputs as in a batch without the edits
     (out2, sel2, _), _ = run_moe(ctx, T, H, F, E, k, True, seed=77)
-    assert np.array_equal(sel2[finite], sel[finite])
-    assert orc.rel_l2(out[finite], out2[finite]) < 1e-6
+    plain = np.setdiff1d(np.arange(T), [1, 3, 5, 7, 8, 9])
+    assert np.array_equal(sel2[plain], sel[plain])
+    assert orc.rel_l2(out[plain], out2[plain]) < 1e-6
 
 
 # --------------------------------------------------------- host boundary
