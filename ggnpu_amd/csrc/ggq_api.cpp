@@ -24,6 +24,8 @@
 #include "ggq_formats.h"
 #include "ggq_launch.h"
 
+static_assert(ggq::kScratchBytes == GGQ_NOALLOC_SCRATCH_BYTES, "scratch size of the header and the library differ");
+
 struct ggq_weight {
     void* dev = nullptr;
     uint32_t type = 0;
@@ -62,6 +64,7 @@ struct ggq_ctx {
     Buffer attn;  // attention chunk partials
     Buffer pin;   // pinned host staging of A and C for the synchronous host-pointer entry points
     std::vector<void*> retired;  // outgrown device buffers, freed by ggq_destroy
+    void* scratch = nullptr;     // this device's fixed scratch region (ggq_mul_mat_noalloc_dev)
 };
 
 namespace {
@@ -347,6 +350,13 @@ int ggq_create(int device, ggq_ctx** out) {
         delete c;
         return GGQ_DEVICE_UNAVAILABLE;
     }
+    // This device's copy of the fixed scratch region (looked up once per
+    // device, with the device current).
+    if (ggq::scratch_device_ptr(device, &c->scratch) != hipSuccess) {
+        hipStreamDestroy(c->stream);
+        delete c;
+        return GGQ_ERROR;
+    }
     *out = c;
     return GGQ_OK;
 }
@@ -453,6 +463,20 @@ int ggq_mul_mat_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t
     if (st != GGQ_OK) return st;
     const hipStream_t s = pick_stream(c, stream);
     Arena ar = dev_arena(c, s);
+    return mul_mat_queue(c, ar, W, type, N, K, A, lda, C, ldc, M, act_mode, s);
+    GGQ_END(c)
+}
+
+int ggq_mul_mat_noalloc_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64_t K, const float* A, int lda,
+                            float* C, int ldc, int M, int act_mode, void* stream) {
+    GGQ_GUARD(c)
+    if (!W || !A || !C) return set_status(c, GGQ_INVALID_PARAM, "null W/A/C");
+    if (!aligned16(W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
+    int st = check_matmul_shape(c, type, N, K, M, lda, ldc, act_mode);
+    if (st != GGQ_OK) return st;
+    if (!c->scratch) return set_status(c, GGQ_ERROR, "no scratch region on device %d", c->device);
+    const hipStream_t s = pick_stream(c, stream);
+    Arena ar{c, nullptr, (char*)c->scratch, ggq::kScratchBytes, s};
     return mul_mat_queue(c, ar, W, type, N, K, A, lda, C, ldc, M, act_mode, s);
     GGQ_END(c)
 }

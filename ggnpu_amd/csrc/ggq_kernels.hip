@@ -15,6 +15,9 @@
 // (src/backends/amd_xdna/amd_xdna.cpp:491-952).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <mutex>
+
 #include "ggq_device.h"
 #include "ggq_launch.h"
 
@@ -2668,6 +2671,27 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t
     else if (E <= 512) moe_route_kernel<8><<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
     else moe_route_kernel<kRouteMaxPerLane><<<T, 64, 0, s>>>(logits, E, topk, sel, wsel);
     return hipGetLastError();
+}
+
+// Scratch region of ggq_mul_mat_noalloc_dev (see kScratchBytes).  In host
+// code `scratch` names a host-side stand-in, not device memory: kernels and
+// copies get the address from scratch_device_ptr.
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+hipError_t scratch_device_ptr(int device, void** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* ptrs[kMaxDevices] = {};
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        ptrs[device] = p;
+    }
+    *out = ptrs[device];
+    return hipSuccess;
 }
 
 // Expert grouping: stable counting sort of the T*topk (token, slot) pairs by

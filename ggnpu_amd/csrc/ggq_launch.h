@@ -101,6 +101,14 @@ hipError_t launch_copy_bytes(void* dst, const void* src, size_t n, hipStream_t s
 // x[m][k] = q[m][k] * sa[m] (dense fp32 [M][K]).
 hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, float* x, hipStream_t s);
 
+// Fixed per-device scratch region of the allocation-free entry point
+// (ggq_mul_mat_noalloc_dev): kScratchBytes of device memory that every GPU the
+// library runs on holds until the process ends.  scratch_device_ptr returns
+// the current device's address of it (looked up once per device; the caller
+// makes `device` current first).
+constexpr size_t kScratchBytes = size_t(32) << 20;
+hipError_t scratch_device_ptr(int device, void** out);
+
 // MoE helpers.
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel,
                             float* wsel, hipStream_t s);

@@ -124,6 +124,7 @@ SIGNATURES = {
     "ggq_weight_device_ptr": (_P, [_P]),
     "ggq_mul_mat": (_I, [_P, _P, _P, _I, _P, _I, _I, _I]),
     "ggq_mul_mat_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _I, _I, _I, _P]),
+    "ggq_mul_mat_noalloc_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _I, _I, _I, _P]),
     "ggq_mul_mat_batch_dev": (_I, [_P, _P, _I, _P]),
     "ggq_mul_mat_batch_rows_dev": (_I, [_P, _P, _I, _I, _P]),
     "ggq_mul_mat_fused_dev": (_I, [_P, _P, _I, _I, _P]),

@@ -144,6 +144,19 @@ int ggq_mul_mat(ggq_ctx* ctx, const ggq_weight* w, const float* A, int lda, floa
 int ggq_mul_mat_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
                     const float* A, int lda, float* C, int ldc, int M, int act_mode, void* stream);
 
+/* ggq_mul_mat_dev without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Its
+ * scratch memory (quantized activations, split-K partial tiles) is one fixed
+ * region of GGQ_NOALLOC_SCRATCH_BYTES per GPU, held from library load until
+ * the process ends and shared by every context on that GPU; a call that
+ * would need more fails with GGQ_INVALID_PARAM before queuing anything.
+ * Calls that overlap on one GPU (several streams, threads or contexts) race
+ * on that region: order them.  Results equal ggq_mul_mat_dev's. */
+#define GGQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+int ggq_mul_mat_noalloc_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
+                            const float* A, int lda, float* C, int ldc, int M, int act_mode, void* stream);
+
 /* Decode GEMVs (fp32 activations, GGQ_ACT_F32 semantics) with their
  * neighbours in the same launch, for the parts of a transformer layer that
  * surround the matmuls (no reference counterpart as a fused call; each
