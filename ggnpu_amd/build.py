@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libggq_hip.so")
-SOURCES = ["ggq_kernels.hip", "ggq_api.cpp", "ggq_encode.cpp", "ggq_gguf.cpp"]
+SOURCES = ["ggq_kernels.hip", "ggq_gemv_i8.hip", "ggq_api.cpp", "ggq_encode.cpp", "ggq_gguf.cpp"]
 CXX = os.environ.get("CXX", "g++")
 # Host-only sources go through the host compiler against the HIP runtime API.
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
@@ -35,7 +35,7 @@ FLAGS = [
 
 def build(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
-    objs = []
+    objs, cmds = [], []
     for src in SOURCES:
         obj = os.path.join(LIB_DIR, os.path.splitext(src)[0] + ".o")
         if src.endswith(".hip"):
@@ -44,8 +44,18 @@ def build(verbose: bool = False) -> str:
             cmd = [CXX, *HOST_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True, stderr=None if verbose else subprocess.PIPE)
+        cmds.append(cmd)
         objs.append(obj)
+    # the translation units compile in parallel
+    procs = [subprocess.Popen(cmd, stderr=None if verbose else subprocess.PIPE) for cmd in cmds]
+    failed = []
+    for cmd, p in zip(cmds, procs):
+        _, err = p.communicate()
+        if p.returncode != 0:
+            failed.append((cmd, err))
+    if failed:
+        cmd, err = failed[0]
+        raise subprocess.CalledProcessError(1, cmd, stderr=err)
     tmp = LIB + ".tmp"
     subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
                     "-lpthread"], check=True)

@@ -192,6 +192,13 @@ int mul_mat_queue(ggq_ctx* c, Arena& ar, const void* W, uint32_t type, int64_t N
         g.ldx = lda;
         return hip_status(c, ggq::launch_gemv(g, s), "gemv");
     }
+    if (act_mode == GGQ_ACT_Q8_ROW && M <= 8) {
+        // Decode-sized: the int8 matrix-core GEMV quantizes the rows itself.
+        g.X = A;
+        g.ldx = lda;
+        if (ggq::i8_gemv_eligible(&g, 1, 1))
+            return hip_status(c, ggq::launch_i8_gemv(&g, 1, 1, nullptr, nullptr, s), "gemv_i8");
+    }
     const size_t q_off = 0;
     const size_t s_off = align256(q_off + (size_t)M * K);
     const size_t x_off = align256(s_off + sizeof(float) * (size_t)M * (K / 32));
@@ -231,20 +238,22 @@ int mul_mat_q8_queue(ggq_ctx* c, Arena& ar, const void* W, uint32_t type, int64_
         if ((st = ar.get(0, part_bytes, &ws, &part, "workspace")) != GGQ_OK) return st;
         return hip_status(c, ggq::launch_gemm_i8(type, W, (int)N, (int)K, qa, sa, M, C, ldc, part, s), "gemm_i8");
     }
-    if ((st = ar.get(sizeof(float) * (size_t)M * K, 0, &ws, &part, "workspace")) != GGQ_OK) return st;
-    float* xe = (float*)ws;
-    if ((e = ggq::launch_dequant_act(qa, sa, M, (int)K, xe, s)) != hipSuccess) return hip_status(c, e, "dequant_act");
     ggq::GemvProblem g{};
     g.type = type;
     g.W = W;
     g.N = (int)N;
     g.K = (int)K;
-    g.X = xe;
-    g.ldx = (int)K;
     g.Y = C;
     g.ldy = ldc;
     g.M = M;
     g.groups = 1;
+    if (ggq::i8_gemv_eligible(&g, 1, 2))
+        return hip_status(c, ggq::launch_i8_gemv(&g, 1, 2, qa, sa, s), "gemv_i8");
+    if ((st = ar.get(sizeof(float) * (size_t)M * K, 0, &ws, &part, "workspace")) != GGQ_OK) return st;
+    float* xe = (float*)ws;
+    if ((e = ggq::launch_dequant_act(qa, sa, M, (int)K, xe, s)) != hipSuccess) return hip_status(c, e, "dequant_act");
+    g.X = xe;
+    g.ldx = (int)K;
     return hip_status(c, ggq::launch_gemv(g, s), "gemv");
 }
 

@@ -1,0 +1,1031 @@
+// ggq_gemv_i8.hip -- decode-sized matmuls (1..8 activation rows) on the int8
+// matrix cores of gfx950 (v_mfma_i32_16x16x64_i8), straight from raw GGUF
+// blocks.
+//
+// One MFMA multiplies a 16 x 64 activation operand A by a 64 x 16 weight
+// operand B.  B's 16 columns are 16 weight rows (a "tile").  Lane l of a
+// wavefront supplies 16 bytes of B for column l%16 and of A for row l%16,
+// both for the 16 K-slots of its lane group g = l/16; the result C[i][j] =
+// sum over g and byte b of A(lane 16g+i)[b] * B(lane 16g+j)[b] lands in lane
+// 16*(i/4)+j, register i%4.  Each lane group's 16 B-bytes are the integer
+// codes (Q4_K nibble, Q5_K 5-bit value, Q6_K 6-bit value, Q8_0 int8, IQ4
+// codebook entry) of 16 consecutive values of K of one scale group, taken
+// from one 16-byte load per lane (two MFMAs per load for the nibble formats:
+// low nibbles, then high nibbles).  A lane group therefore carries one scale
+// group ("slot" s = g/2 for the 32-value groups of Q4_K, Q5_K and Q8_0, s = g
+// for Q6_K's 16-value groups and for IQ4, whose 32-value blocks span two
+// MFMAs), and each row of A is restricted to one slot by zeros in the other
+// lane groups: output lane group q holds per-group dot products and applies
+// that group's scale.  Block headers (scales, mins) are loaded by one lane
+// group and broadcast, so the loads stay at 16 bytes per lane access.
+//
+// Activations:
+//  * fp32 (CpuRefBackend::mul_mat_q semantics, cpu_ref.cpp:87-117): each row
+//    is written as fixed point X = rint(x * 2^e) with the row's largest
+//    magnitude scaled into [2^21, 2^22), i.e. |x - 2^-e X| <= 2^-22 of the
+//    row maximum, and X as three signed int8 digits, X = 65536 d0 + 256 d1 +
+//    d2.  Rows 4q, 4q+1, 4q+2 of A carry the three digits, so one MFMA gives
+//    the three digit dot products of a group in registers 0..2 of one lane;
+//    the lane forms P = 65536 C0 + 256 C1 + C2 in fp32 (relative rounding
+//    2^-24) and accumulates a*P + b*S, where a and b are the group's scale
+//    and offset (K-quant min, Q6_K's -32 code bias) and S = sum of X over the
+//    group.  Two activation rows per MFMA (one for Q6_K), more in passes.
+//  * int8 (the XDNA backend's per-row semantics, amd_xdna.cpp:598-603,
+//    633-639, 757-771): the digit is the reference's code q = clamp(rint(a *
+//    (1/scale))), computed here bit for bit, or taken as given; C is then
+//    exactly the int32 block dot product of the raw codes with q, and each
+//    lane register carries another activation row.
+//
+// Work layout: a workgroup of 16 wavefronts builds the A operand of all its
+// activation rows in LDS once (8-byte digit planes per MFMA, lane group and
+// half, plus a zero plane that inactive slots point at), then its
+// wavefronts stream weight tiles: KW wavefronts share a tile and split its K
+// into 256-value chunks (one K-quant block, or eight 32-value blocks), the
+// other wavefronts take other tiles.  Each chunk's raw bytes are fetched one
+// chunk ahead.  Partial sums of a tile are combined across lane groups by
+// swizzles and across the KW wavefronts through LDS, in a fixed order.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ggq_device.h"
+#include "ggq_launch.h"
+
+namespace ggq {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v8u __attribute__((ext_vector_type(8)));
+
+constexpr int kWaves = 16;
+constexpr int kThreads = 64 * kWaves;
+
+
+__device__ __forceinline__ v4i pack_b(uint2 lo, uint2 hi) {
+    v4i b;
+    b.x = (int)lo.x; b.y = (int)lo.y; b.z = (int)hi.x; b.w = (int)hi.y;
+    return b;
+}
+__device__ __forceinline__ uint2 and2(uint2 v, uint32_t m) { return make_uint2(v.x & m, v.y & m); }
+__device__ __forceinline__ uint2 shr2(uint2 v, int s) { return make_uint2(v.x >> s, v.y >> s); }
+__device__ __forceinline__ uint2 or2(uint2 a, uint2 b) { return make_uint2(a.x | b.x, a.y | b.y); }
+__device__ __forceinline__ uint2 shl2(uint2 v, int s) { return make_uint2(v.x << s, v.y << s); }
+
+// Byte i of w as a float (v_cvt_f32_ubyteN).
+template <int I> __device__ __forceinline__ float ubyte_f(uint32_t w) {
+    return (float)((opaque(w) >> (8 * I)) & 0xFFu);
+}
+
+// ------------------------------------------------------------ formats ----
+// IF<T>: the int8-MFMA view of a format.  A chunk is 256 values of a row
+// (4 MFMAs t = 0..3).  fetch() issues the chunk's loads for lane group g (the
+// header loads only in lane group 0), bcast() copies header words to the
+// other lane groups once the loads have landed, codes(t) gives the B operand
+// of MFMA t, coef() each MFMA's scale a[t] and offset b[t] for output slot s
+// (value = a * code + b).  kpos maps (MFMA t, lane group g) to the first of
+// its 16 consecutive values within the chunk; slot(g) is its scale group.
+template <int T> struct IF;
+
+// Weight loads go through a buffer resource over the matrix: offsets are
+// 32-bit, and a lane whose offset is out of range (kOOB and above) reads
+// zeros without a memory access, so lanes that do not own a load and
+// fetches past the last chunk cost no memory traffic and need no branch
+// (branches around loads make the compiler wait for every load in flight).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr uint32_t kOOB = 0xC0000000u;
+__device__ __forceinline__ Rsrc make_rsrc(const uint8_t* W, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4u bl16(Rsrc rs, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0); }
+__device__ __forceinline__ uint32_t bl4(Rsrc rs, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0); }
+__device__ __forceinline__ uint32_t bl2(Rsrc rs, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0); }
+__device__ __forceinline__ uint32_t own(bool mine, uint32_t off) { return mine ? off : kOOB; }
+
+__device__ __forceinline__ uint32_t lane_bcast(uint32_t v, int src) { return (uint32_t)__shfl((int)v, src, 64); }
+__device__ __forceinline__ v4i nib_lo(v4u w) {
+    v4i r; r.x = (int)(w.x & 0x0F0F0F0Fu); r.y = (int)(w.y & 0x0F0F0F0Fu); r.z = (int)(w.z & 0x0F0F0F0Fu); r.w = (int)(w.w & 0x0F0F0F0Fu);
+    return r;
+}
+__device__ __forceinline__ v4i nib_hi(v4u w) {
+    v4i r; r.x = (int)((w.x >> 4) & 0x0F0F0F0Fu); r.y = (int)((w.y >> 4) & 0x0F0F0F0Fu);
+    r.z = (int)((w.z >> 4) & 0x0F0F0F0Fu); r.w = (int)((w.w >> 4) & 0x0F0F0F0Fu);
+    return r;
+}
+
+// Q4_K (kquant.h:9-13, 133-151): qs[128] at 16; 32-byte run c holds
+// sub-block 2c (low nibbles) and 2c+1 (high nibbles).  Lane group g loads
+// qs[16g, +16) and qs[64+16g, +16): runs 2u + (g>>1), values 16(g&1).. of
+// them.  MFMA t = 2u + h takes the low (h = 0) or high (h = 1) nibbles, so
+// slot s = g>>1 is sub-block 4u + 2s + h.
+template <> struct IF<T_Q4_K> {
+    static constexpr int G = 2, CHUNK = 144;
+    static constexpr bool BIAS = true;
+    struct Raw { v4u q0, q1, hd; };
+    static __device__ __forceinline__ Raw fetch(Rsrc rs, uint32_t off, int g, int) {
+        Raw r;
+        r.q0 = bl16(rs, off + 16 + 16 * g);
+        r.q1 = bl16(rs, off + 80 + 16 * g);
+        r.hd = bl16(rs, own(g == 0, off));
+        return r;
+    }
+    static __device__ __forceinline__ void bcast(Raw& r, int col) {
+        r.hd.x = lane_bcast(r.hd.x, col); r.hd.y = lane_bcast(r.hd.y, col);
+        r.hd.z = lane_bcast(r.hd.z, col); r.hd.w = lane_bcast(r.hd.w, col);
+    }
+    static __device__ __forceinline__ v4i codes(const Raw& r, int t, int) {
+        const v4u w = (t >> 1) ? r.q1 : r.q0;
+        return (t & 1) ? nib_hi(w) : nib_lo(w);
+    }
+    // scale / min of sub-blocks 2s, 2s+1 (t = 0, 1) and 4+2s, 5+2s (t = 2,
+    // 3), kquant.h:56-64, as the pairs s and 2+s of kq_pair.
+    static __device__ __forceinline__ void coef(const Raw& r, int s, float (&a)[4], float (&b)[4]) {
+        const float d = h2f(r.hd.x & 0xFFFFu), dm = h2f(r.hd.x >> 16);
+        const uint32_t b2 = 2u * (uint32_t)s;
+        const uint32_t A = __builtin_amdgcn_perm(r.hd.z, r.hd.y, b2 | (b2 + 1) << 8 | (b2 + 4) << 16 | (b2 + 5) << 24);
+        const uint32_t Q = __builtin_amdgcn_perm(r.hd.w, r.hd.w, b2 | (b2 + 1) << 8 | b2 << 16 | (b2 + 1) << 24);
+        const uint32_t lo = A & 0x3F3F3F3Fu;  // sc(2s), sc(2s+1), m(2s), m(2s+1)
+        const uint32_t hi = ((A >> 2) & 0x30303030u) | (Q & 0x00000F0Fu) | ((Q >> 4) & 0x0F0F0000u);
+        a[0] = d * ubyte_f<0>(lo); a[1] = d * ubyte_f<1>(lo);
+        b[0] = -(dm * ubyte_f<2>(lo)); b[1] = -(dm * ubyte_f<3>(lo));
+        a[2] = d * ubyte_f<0>(hi); a[3] = d * ubyte_f<1>(hi);
+        b[2] = -(dm * ubyte_f<2>(hi)); b[3] = -(dm * ubyte_f<3>(hi));
+    }
+    static __device__ __forceinline__ int slot(int g) { return g >> 1; }
+    static __device__ __forceinline__ int kpos(int t, int g) { return 128 * (t >> 1) + 64 * (g >> 1) + 32 * (t & 1) + 16 * (g & 1); }
+    static __device__ __forceinline__ void inv(int x, int& t, int& g) { t = 2 * (x >> 3) + ((x >> 1) & 1); g = 2 * ((x >> 2) & 1) + (x & 1); }
+};
+
+// Q5_K (kquant.h:157-179): as Q4_K with qs at 48 and the fifth bits in
+// qh[32] at 16: bit 2c of qh[p] for sub-block 2c, bit 2c+1 for 2c+1.  Lane
+// groups 0 and 1 load qh[16(g&1), +16) for 2 and 3 as well.
+template <> struct IF<T_Q5_K> {
+    static constexpr int G = 2, CHUNK = 176;
+    static constexpr bool BIAS = true;
+    struct Raw { v4u q0, q1, qh, hd; };
+    static __device__ __forceinline__ Raw fetch(Rsrc rs, uint32_t off, int g, int) {
+        Raw r;
+        r.q0 = bl16(rs, off + 48 + 16 * g);
+        r.q1 = bl16(rs, off + 112 + 16 * g);
+        r.qh = bl16(rs, own(g < 2, off + 16 + 16 * g));
+        r.hd = bl16(rs, own(g == 0, off));
+        return r;
+    }
+    static __device__ __forceinline__ void bcast(Raw& r, int col) {
+        IF<T_Q4_K>::Raw h{r.q0, r.q1, r.hd};
+        IF<T_Q4_K>::bcast(h, col);
+        r.hd = h.hd;
+        const int src = (int)(threadIdx.x & 31);
+        r.qh.x = lane_bcast(r.qh.x, src); r.qh.y = lane_bcast(r.qh.y, src);
+        r.qh.z = lane_bcast(r.qh.z, src); r.qh.w = lane_bcast(r.qh.w, src);
+    }
+    static __device__ __forceinline__ v4i codes(const Raw& r, int t, int g) {
+        const v4u w = (t >> 1) ? r.q1 : r.q0;
+        v4i c = (t & 1) ? nib_hi(w) : nib_lo(w);
+        // bit 2c + h of qh, c = 2u + (g>>1): moved to bit 4 of each byte
+        const int sh = 4 * (t >> 1) + 2 * (g >> 1) + (t & 1);
+        c.x |= (int)(((r.qh.x >> sh) & 0x01010101u) << 4); c.y |= (int)(((r.qh.y >> sh) & 0x01010101u) << 4);
+        c.z |= (int)(((r.qh.z >> sh) & 0x01010101u) << 4); c.w |= (int)(((r.qh.w >> sh) & 0x01010101u) << 4);
+        return c;
+    }
+    static __device__ __forceinline__ void coef(const Raw& r, int s, float (&a)[4], float (&b)[4]) {
+        IF<T_Q4_K>::coef(IF<T_Q4_K>::Raw{r.q0, r.q1, r.hd}, s, a, b);
+    }
+    static __device__ __forceinline__ int slot(int g) { return g >> 1; }
+    static __device__ __forceinline__ int kpos(int t, int g) { return IF<T_Q4_K>::kpos(t, g); }
+    static __device__ __forceinline__ void inv(int x, int& t, int& g) { IF<T_Q4_K>::inv(x, t, g); }
+};
+
+// Q6_K (kquant.h:182-202): half n of the block: ql[64n + 16g, +16) for lane
+// group g; low nibbles (MFMA t = 2n) are values 128n + 16g.., high nibbles
+// (t = 2n+1) values 128n + 64 + 16g..; the top two bits come from qh[32n +
+// 16(g&1) + b], bits 2(g>>1) (+4 for the high nibbles).  Codes stay unsigned
+// (0..63) and the -32 goes into b.  Slot s = g: scale sc[4t + s].  Lane
+// groups 0 and 1 load qh for 2 and 3; lane group 0 loads sc and d.
+template <> struct IF<T_Q6_K> {
+    static constexpr int G = 4, CHUNK = 210;
+    static constexpr bool BIAS = true;
+    struct Raw { v4u ql0, ql1, qh0, qh1, sc; uint32_t d; };
+    static __device__ __forceinline__ Raw fetch(Rsrc rs, uint32_t off, int g, int) {
+        Raw r;
+        r.ql0 = bl16(rs, off + 16 * g);
+        r.ql1 = bl16(rs, off + 64 + 16 * g);
+        r.qh0 = bl16(rs, own(g < 2, off + 128 + 16 * g));
+        r.qh1 = bl16(rs, own(g < 2, off + 160 + 16 * g));
+        r.sc = bl16(rs, own(g == 0, off + 192));
+        r.d = bl2(rs, own(g == 0, off + 208));
+        return r;
+    }
+    static __device__ __forceinline__ void bcast(Raw& r, int col) {
+        const int src = (int)(threadIdx.x & 31);
+        r.qh0.x = lane_bcast(r.qh0.x, src); r.qh0.y = lane_bcast(r.qh0.y, src);
+        r.qh0.z = lane_bcast(r.qh0.z, src); r.qh0.w = lane_bcast(r.qh0.w, src);
+        r.qh1.x = lane_bcast(r.qh1.x, src); r.qh1.y = lane_bcast(r.qh1.y, src);
+        r.qh1.z = lane_bcast(r.qh1.z, src); r.qh1.w = lane_bcast(r.qh1.w, src);
+        r.sc.x = lane_bcast(r.sc.x, col); r.sc.y = lane_bcast(r.sc.y, col);
+        r.sc.z = lane_bcast(r.sc.z, col); r.sc.w = lane_bcast(r.sc.w, col);
+        r.d = lane_bcast(r.d, col);
+    }
+    static __device__ __forceinline__ v4i codes(const Raw& r, int t, int g) {
+        const v4u w = (t >> 1) ? r.ql1 : r.ql0;
+        const v4u qh = (t >> 1) ? r.qh1 : r.qh0;
+        v4i c = (t & 1) ? nib_hi(w) : nib_lo(w);
+        const int sh = 4 * (t & 1) + 2 * (g >> 1);
+        c.x |= (int)(((qh.x >> sh) & 0x03030303u) << 4); c.y |= (int)(((qh.y >> sh) & 0x03030303u) << 4);
+        c.z |= (int)(((qh.z >> sh) & 0x03030303u) << 4); c.w |= (int)(((qh.w >> sh) & 0x03030303u) << 4);
+        return c;
+    }
+    static __device__ __forceinline__ void coef(const Raw& r, int s, float (&a)[4], float (&b)[4]) {
+        const float d = h2f(r.d);
+        const uint32_t w[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            a[t] = d * (float)(int)(int8_t)((w[t] >> (8 * s)) & 0xFFu);
+            b[t] = -32.0f * a[t];
+        }
+    }
+    static __device__ __forceinline__ int slot(int g) { return g; }
+    static __device__ __forceinline__ int kpos(int t, int g) { return 128 * (t >> 1) + 64 * (t & 1) + 16 * g; }
+    static __device__ __forceinline__ void inv(int x, int& t, int& g) { t = 2 * (x >> 3) + ((x >> 2) & 1); g = x & 3; }
+};
+
+// Q8_0 (q8_0.cpp:19-25): a chunk is 8 blocks of 34 bytes; MFMA t takes
+// blocks 2t + (g>>1), codes 16(g&1)..+15 (signed, as they are); slot
+// s = g>>1.  Each output lane loads the d of its own slot's blocks.
+template <> struct IF<T_Q8_0> {
+    static constexpr int G = 2, CHUNK = 272;
+    static constexpr bool BIAS = false;
+    struct Raw { v4u q0, q1, q2, q3; uint32_t d01, d23; };
+    static __device__ __forceinline__ Raw fetch(Rsrc rs, uint32_t off, int g, int s) {
+        Raw r;
+        const uint32_t o = off + 34 * (g >> 1) + 2 + 16 * (g & 1);
+        r.q0 = bl16(rs, o); r.q1 = bl16(rs, o + 68); r.q2 = bl16(rs, o + 136); r.q3 = bl16(rs, o + 204);
+        const uint32_t od = off + 34 * s;
+        r.d01 = bl2(rs, od) | bl2(rs, od + 68) << 16;
+        r.d23 = bl2(rs, od + 136) | bl2(rs, od + 204) << 16;
+        return r;
+    }
+    static __device__ __forceinline__ void bcast(Raw&, int) {}
+    static __device__ __forceinline__ v4i codes(const Raw& r, int t, int) {
+        const v4u w = t == 0 ? r.q0 : t == 1 ? r.q1 : t == 2 ? r.q2 : r.q3;
+        v4i c; c.x = (int)w.x; c.y = (int)w.y; c.z = (int)w.z; c.w = (int)w.w;
+        return c;
+    }
+    static __device__ __forceinline__ void coef(const Raw& r, int, float (&a)[4], float (&b)[4]) {
+        a[0] = h2f(r.d01 & 0xFFFFu); a[1] = h2f(r.d01 >> 16); a[2] = h2f(r.d23 & 0xFFFFu); a[3] = h2f(r.d23 >> 16);
+        b[0] = b[1] = b[2] = b[3] = 0.0f;
+    }
+    static __device__ __forceinline__ int slot(int g) { return g >> 1; }
+    static __device__ __forceinline__ int kpos(int t, int g) { return 64 * t + 16 * g; }
+    static __device__ __forceinline__ void inv(int x, int& t, int& g) { t = x >> 2; g = x & 3; }
+};
+
+// Codebook entries of four nibbles (one per byte), signed: v_perm picks from
+// the two 8-entry halves of the table, and bit 3 of each nibble (moved to
+// the byte's sign bit and replicated by v_perm's sign selectors) chooses.
+__device__ __forceinline__ uint32_t iq4_lut(uint32_t nib) {
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(GGQ_IQ4S1, GGQ_IQ4S0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(GGQ_IQ4S3, GGQ_IQ4S2, sel);
+    const uint32_t x = nib << 4;
+    const uint32_t msk = __builtin_amdgcn_perm(x << 8, x, 0x090B080Au);
+    return (hi & msk) | (lo & ~msk);
+}
+__device__ __forceinline__ v4i iq4_codes(v4u w, int hi) {
+    const v4i n = hi ? nib_hi(w) : nib_lo(w);
+    v4i c;
+    c.x = (int)iq4_lut((uint32_t)n.x); c.y = (int)iq4_lut((uint32_t)n.y);
+    c.z = (int)iq4_lut((uint32_t)n.z); c.w = (int)iq4_lut((uint32_t)n.w);
+    return c;
+}
+
+// IQ4_NL (iq4_nl.cpp:16-31): 8 blocks of 18 bytes per chunk; value j < 16 is
+// the low nibble of qs[j], value j+16 the high nibble.  Lane group g loads
+// the 16 qs bytes of blocks g and 4+g; MFMA t = 2w + h takes nibbles h of
+// blocks 4w + g: slot s = g (block 4w + s).
+template <> struct IF<T_IQ4_NL> {
+    static constexpr int G = 4, CHUNK = 144;
+    static constexpr bool BIAS = false;
+    struct Raw { v4u q0, q1; uint32_t d0, d1; };
+    static __device__ __forceinline__ Raw fetch(Rsrc rs, uint32_t off, int g, int s) {
+        Raw r;
+        r.q0 = bl16(rs, off + 18 * g + 2);
+        r.q1 = bl16(rs, off + 18 * (4 + g) + 2);
+        r.d0 = bl2(rs, off + 18 * s);
+        r.d1 = bl2(rs, off + 18 * (4 + s));
+        return r;
+    }
+    static __device__ __forceinline__ void bcast(Raw&, int) {}
+    static __device__ __forceinline__ v4i codes(const Raw& r, int t, int) { return iq4_codes((t >> 1) ? r.q1 : r.q0, t & 1); }
+    static __device__ __forceinline__ void coef(const Raw& r, int, float (&a)[4], float (&b)[4]) {
+        a[0] = a[1] = h2f(r.d0); a[2] = a[3] = h2f(r.d1);
+        b[0] = b[1] = b[2] = b[3] = 0.0f;
+    }
+    static __device__ __forceinline__ int slot(int g) { return g; }
+    static __device__ __forceinline__ int kpos(int t, int g) { return 128 * (t >> 1) + 32 * g + 16 * (t & 1); }
+    static __device__ __forceinline__ void inv(int x, int& t, int& g) { t = 2 * (x >> 3) + (x & 1); g = (x >> 1) & 3; }
+};
+
+// IQ4_XS (iq4_xs.cpp:21-38): sub-block j of the block: qs[16j, +16), low
+// nibbles values 32j.., high 32j+16..; scale d * (ls - 32) with the 6-bit ls
+// from scales_l / scales_h.  Lane group g loads sub-blocks g and 4+g; lane
+// group 0 the 8-byte header.
+template <> struct IF<T_IQ4_XS> {
+    static constexpr int G = 4, CHUNK = 136;
+    static constexpr bool BIAS = false;
+    struct Raw { v4u q0, q1; uint32_t h0, h1; };
+    static __device__ __forceinline__ Raw fetch(Rsrc rs, uint32_t off, int g, int) {
+        Raw r;
+        r.q0 = bl16(rs, off + 8 + 16 * g);
+        r.q1 = bl16(rs, off + 72 + 16 * g);
+        r.h0 = bl4(rs, own(g == 0, off));
+        r.h1 = bl4(rs, own(g == 0, off + 4));
+        return r;
+    }
+    static __device__ __forceinline__ void bcast(Raw& r, int col) {
+        r.h0 = lane_bcast(r.h0, col);
+        r.h1 = lane_bcast(r.h1, col);
+    }
+    static __device__ __forceinline__ v4i codes(const Raw& r, int t, int) { return iq4_codes((t >> 1) ? r.q1 : r.q0, t & 1); }
+    static __device__ __forceinline__ void coef(const Raw& r, int s, float (&a)[4], float (&b)[4]) {
+        const float d = h2f(r.h0 & 0xFFFFu);
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            const int ib = 4 * w + s;
+            const int ls = (int)(((r.h1 >> (4 * ib)) & 15u) | (((r.h0 >> (16 + 2 * ib)) & 3u) << 4));
+            a[2 * w] = a[2 * w + 1] = __fmul_rn(d, (float)(ls - 32));
+        }
+        b[0] = b[1] = b[2] = b[3] = 0.0f;
+    }
+    static __device__ __forceinline__ int slot(int g) { return g; }
+    static __device__ __forceinline__ int kpos(int t, int g) { return IF<T_IQ4_NL>::kpos(t, g); }
+    static __device__ __forceinline__ void inv(int x, int& t, int& g) { IF<T_IQ4_NL>::inv(x, t, g); }
+};
+
+// ------------------------------------------------------------- launch ----
+struct I8Prob {
+    const uint8_t* W;
+    uint32_t row_bytes;
+    uint32_t type;
+    int N, K;
+    const float* X;     // fp32 activations [M][ldx] (modes 0, 1)
+    int ldx;
+    const int8_t* QA;   // given int8 activations [M][K] and row scales (mode 2)
+    const float* SA;
+    float* Y;
+    int ldy;
+    int kw_log2;        // wavefronts per tile
+    int x_vec4;         // X rows 16-byte aligned
+};
+
+constexpr int kMaxProbs = 8;
+struct I8Args {
+    I8Prob p[kMaxProbs];
+    int begin[kMaxProbs + 1];
+    int n;
+    int M;
+    int mode;  // 0: fp32 -> 3 digits; 1: fp32 -> per-row int8 codes; 2: given int8 codes
+};
+
+// Geometry of one launch instantiation.
+template <int T, int D, int NE, int NP> struct Geo {
+    static constexpr int G = IF<T>::G;
+    static constexpr int RG = 4 / G;                     // activation row groups per pass (lane groups)
+    static constexpr int RP = RG * (D == 1 ? NE : 1);    // activation rows per pass
+    static constexpr int MT = RP * NP;                   // most rows of a launch
+};
+
+// LDS carve (bytes) for K values and M activation rows:
+//  * A entries, 16 bytes each, per (MFMA t, lane group g): entry d*M + m =
+//    digit plane d of row m at that lane group's 16 values, and a zero entry
+//    last: E = D*M + 1 per (t, g);
+//  * group sums S[chunk][slot s][row m][mfma t] (floats);
+//  * per-row scale and exponent; the reduction buffer (two tiles' worth, by
+//    parity); the per-wavefront row maxima.
+__host__ __device__ inline int i8_entries(int D, int M) { return D * M + 1; }
+__host__ __device__ inline int i8_lds_a(int K, int D, int M) { return (K / 64) * 4 * i8_entries(D, M) * 16; }
+__host__ __device__ inline int i8_lds_s(int K, int G, int M) { return (K / 256) * G * M * 4 * 4; }
+__host__ __device__ inline int i8_lds_red(int MT) { return 2 * kWaves * MT * 16 * 4; }
+__host__ __device__ inline int i8_lds_total(int K, int G, int D, int M, int MT) {
+    return i8_lds_a(K, D, M) + (D == 3 ? 2 : 1) * i8_lds_s(K, G, M) + M * 8 + i8_lds_red(MT) + kWaves * M * 4;
+}
+
+// Fixed-point digits of one value: X = rint(x 2^e) + 0x808080 as bytes
+// (offset binary); the digits are those bytes xor 0x80.
+__device__ __forceinline__ uint32_t fixed_u(float x, int e) {
+    const float f = __fadd_rn(ldexpf(x, e), 12582912.0f);  // 1.5 * 2^23: rounds to an integer (ties to even)
+    return __builtin_bit_cast(uint32_t, f) - 0x4B400000u + 0x808080u;
+}
+
+// Four values' digit bytes: byte k of plane dword = digit of value k.
+// Plane 0 is the most significant digit (byte 2 of u), plane 2 the least.
+__device__ __forceinline__ void digit_planes4(const uint32_t* v, uint32_t& p0, uint32_t& p1, uint32_t& p2) {
+    const uint32_t a01 = __builtin_amdgcn_perm(v[1], v[0], 0x05010400u);  // v0.b0 v1.b0 v0.b1 v1.b1
+    const uint32_t a23 = __builtin_amdgcn_perm(v[3], v[2], 0x05010400u);
+    const uint32_t c01 = __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0602u);  // v0.b2 v1.b2
+    const uint32_t c23 = __builtin_amdgcn_perm(v[3], v[2], 0x0c0c0602u);
+    p2 = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;  // byte 0 of each
+    p1 = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;  // byte 1
+    p0 = __builtin_amdgcn_perm(c23, c01, 0x05040100u) ^ 0x80808080u;  // byte 2
+}
+
+__device__ __forceinline__ int8_t code_i8(float v) {
+    float r = __builtin_rintf(v);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    return (int8_t)(int)r;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int T, int D, int NE, int NP>
+__device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx, uint8_t* lds) {
+    typedef Geo<T, D, NE, NP> GEO;
+    constexpr int G = GEO::G, RG = GEO::RG, RP = GEO::RP, MT = GEO::MT;
+    typedef typename IF<T>::Raw Raw;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, col = lane & 15;
+    const int M = args.M, K = a.K, N = a.N;
+    const int NC = K >> 8;
+    const int KW = 1 << a.kw_log2, TPI = kWaves >> a.kw_log2;
+    const int kp = w & (KW - 1), slot_t = w >> a.kw_log2;
+    const int tiles = (N + 15) >> 4;
+    const int n_it = (tiles + TPI - 1) / TPI;
+    const int nmy = (NC - kp + KW - 1) >> a.kw_log2;
+    // scale-group slot and row group of this lane's outputs
+    const int s_out = g % G, rg_out = g / G;
+    const int E = i8_entries(D, M);
+    const uint32_t TS = 64u * (uint32_t)E;  // A bytes per MFMA
+
+    uint8_t* lds_a = lds;
+    float* lds_s = (float*)(lds + i8_lds_a(K, D, M));
+    float* lds_sc = (float*)((uint8_t*)lds_s + i8_lds_s(K, G, M));  // fp32 mode: group scales
+    float* row_rs = (float*)((uint8_t*)lds_s + (D == 3 ? 2 : 1) * i8_lds_s(K, G, M));
+    int* row_re = (int*)(row_rs + M);
+    float* red = (float*)(row_re + M);
+    float* wmax = red + i8_lds_red(MT) / 4;
+    // outputs of this workgroup's tiles, stored to Y after the main loop
+    // (stores inside it would make the compiler wait for the weight loads
+    // in flight): [row m][local output row]
+    const int iters_wg = (n_it - bx + gx - 1) / gx;
+    const int ROWS = iters_wg * TPI * 16;
+    float* outl = wmax + kWaves * M;
+
+    const Rsrc rs = make_rsrc(a.W, (uint32_t)N * a.row_bytes);
+    // Chunk offset of a (tile iteration, chunk) position: rows past N read
+    // row N-1 (their results are dropped), positions past the last
+    // iteration read nothing (out-of-range offset).
+    auto chunk_off = [&](int it, int i) __attribute__((always_inline)) {
+        int n = (it * TPI + slot_t) * 16 + col;
+        n = n < N ? n : N - 1;
+        const uint32_t o = (uint32_t)n * a.row_bytes + (uint32_t)(kp + KW * i) * IF<T>::CHUNK;
+        return it < n_it ? o : kOOB;
+    };
+    // (tile iteration, chunk) positions: compute position and the position
+    // of the next fetch, two chunks ahead.
+    int it = bx, i = 0;
+    int itf = bx, jf = 0;
+    auto adv = [&](int& pit, int& pi) __attribute__((always_inline)) {
+        if (++pi >= nmy) { pi = 0; pit += gx; }
+    };
+    // The first chunk's loads go out before the activation set-up, the
+    // second's right after it.
+    // ---- activation set-up, per hexad (16 consecutive values of K).  The
+    // thread's first hexad of row 0 is loaded before anything else
+    // (its latency then overlaps the first weight fetch); others are read
+    // when needed.
+    const int n_hex = K >> 4;
+    const int mode = args.mode;
+    constexpr int KR = 1;
+    float xk[KR][16];
+    auto load_hex = [&](int m, int x, float (&v)[16]) __attribute__((always_inline)) {
+        const float* xr = a.X + (int64_t)m * a.ldx + 16 * x;
+        if (a.x_vec4) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 f = *(const float4*)(xr + 4 * q);
+                v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = xr[k];
+        }
+    };
+    if (mode != 2 && tid < n_hex) {
+#pragma unroll
+        for (int m = 0; m < KR; m++)
+            if (m < M) load_hex(m, tid, xk[m]);
+    }
+    auto get_hex = [&](int m, int x, float (&v)[16]) __attribute__((always_inline)) {
+        if (x == tid && m < KR) {
+#pragma unroll
+            for (int r = 0; r < KR; r++)
+                if (r == m) {
+#pragma unroll
+                    for (int k = 0; k < 16; k++) v[k] = xk[r][k];
+                }
+        } else {
+            load_hex(m, x, v);
+        }
+    };
+    Raw r0, r1, r2;
+    r0 = IF<T>::fetch(rs, chunk_off(itf, jf), g, s_out);
+    adv(itf, jf);
+
+    // phase 1 (int8 codes only): row maxima, the reference's per-row scale
+    if (mode == 1) {
+        for (int m = 0; m < M; m++) {
+            float mx = 0.0f;
+            for (int x = tid; x < n_hex; x += kThreads) {
+                float v[16];
+                get_hex(m, x, v);
+#pragma unroll
+                for (int k = 0; k < 16; k++) mx = fmaxf(mx, fabsf(v[k]));
+            }
+            mx = wave_max(mx);
+            if (lane == 0) wmax[w * M + m] = mx;
+        }
+        __syncthreads();
+    }
+    // phase 2: A entries and group sums (fp32 mode: each scale group gets its
+    // own power of two, from its largest magnitude; int8 modes: per-row
+    // scale and codes)
+    for (int m = 0; m < M; m++) {
+        float rs_m = 1.0f, inv = 0.0f;
+        if (mode == 2) {
+            rs_m = a.SA[m];
+        } else if (mode == 1) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kWaves; k++) amax = fmaxf(amax, wmax[k * M + m]);
+            rs_m = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+            inv = __fdiv_rn(1.0f, rs_m);
+        }
+        if (tid == 0) { row_rs[m] = rs_m; row_re[m] = 0; }
+        for (int x = tid; x < n_hex; x += kThreads) {
+            int tl, hg;
+            IF<T>::inv(x & 15, tl, hg);
+            const int t = 4 * (x >> 4) + tl;
+            uint4 pl[3];
+            float gsum = 0.0f, gscale = 1.0f;
+            if (mode == 2) {
+                const uint4 q = *(const uint4*)(a.QA + (int64_t)m * K + 16 * x);
+                pl[0] = q;
+                const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+                int sum = 0;
+#pragma unroll
+                for (int k = 0; k < 16; k++) sum += (int)(int8_t)(qq[k >> 2] >> (8 * (k & 3)));
+                if (G == 2) sum += __shfl_xor(sum, 1, 64);
+                gsum = (float)sum;
+            } else {
+                float v[16];
+                get_hex(m, x, v);
+                if (mode == 0) {
+                    // the group's power of two: its largest magnitude in [2^21, 2^22)
+                    float mx = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 16; k++) mx = fmaxf(mx, fabsf(v[k]));
+                    if (G == 2) mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+                    int Ex = 0;
+                    frexpf(mx, &Ex);
+                    const int e = mx > 0.0f ? 22 - Ex : 0;
+                    gscale = ldexpf(1.0f, -e);
+                    int sum = 0;
+                    uint32_t p0[4], p1[4], p2[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        uint32_t u[4];
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            u[k] = fixed_u(v[4 * q + k], e);
+                            sum += (int)(u[k] - 0x808080u);
+                        }
+                        digit_planes4(u, p0[q], p1[q], p2[q]);
+                    }
+                    if (G == 2) sum += __shfl_xor(sum, 1, 64);
+                    gsum = ldexpf((float)sum, -e);  // the group sum of the fixed-point values
+                    pl[0] = make_uint4(p0[0], p0[1], p0[2], p0[3]);
+                    pl[1] = make_uint4(p1[0], p1[1], p1[2], p1[3]);
+                    pl[2] = make_uint4(p2[0], p2[1], p2[2], p2[3]);
+                } else {
+                    uint32_t c[4] = {0u, 0u, 0u, 0u};
+                    int sum = 0;
+#pragma unroll
+                    for (int k = 0; k < 16; k++) {
+                        const int8_t cq = code_i8(__fmul_rn(v[k], inv));
+                        sum += cq;
+                        c[k >> 2] |= (uint32_t)(uint8_t)cq << (8 * (k & 3));
+                    }
+                    if (G == 2) sum += __shfl_xor(sum, 1, 64);
+                    gsum = (float)sum;
+                    pl[0] = make_uint4(c[0], c[1], c[2], c[3]);
+                }
+            }
+            uint4* ent = (uint4*)(lds_a + (size_t)t * TS) + hg * E;
+#pragma unroll
+            for (int d = 0; d < D; d++) ent[d * M + m] = pl[d];
+            if (m == 0) ent[E - 1] = make_uint4(0u, 0u, 0u, 0u);  // the zero entry
+            // a 32-value group is two consecutive hexads: the first writes
+            if (G == 4 || (x & 1) == 0) {
+                const int sl = IF<T>::slot(hg);
+                const int si = (((x >> 4) * G + sl) * M + m) * 4 + tl;
+                lds_s[si] = gsum;
+                if (D == 3) lds_sc[si] = gscale;
+            }
+        }
+    }
+    __syncthreads();
+    r1 = IF<T>::fetch(rs, chunk_off(itf, jf), g, s_out);
+    adv(itf, jf);
+
+    // ---- per-lane A entry offsets (bytes within one MFMA's entries)
+    const int ai = lane & 15, ae = ai & 3, aq = ai >> 2;
+    const int as = aq % G, arg = aq / G;
+    uint32_t aoff[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        int entry = E - 1;  // zero
+        if (IF<T>::slot(g) == as) {
+            if (D == 3) {
+                const int m = p * RP + arg;
+                if (ae < 3 && m < M) entry = ae * M + m;
+            } else {
+                const int m = p * RP + arg * NE + ae;
+                if (ae < NE && m < M) entry = m;
+            }
+        }
+        aoff[p] = 16u * (uint32_t)(g * E + entry);
+    }
+    constexpr int NS = D == 3 ? 1 : NE;  // rows per lane register set
+    int srow[NP][NS];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int e2 = 0; e2 < NS; e2++) {
+            const int m = p * RP + (D == 3 ? rg_out : rg_out * NE + e2);
+            srow[p][e2] = m < M ? m : M - 1;
+        }
+
+    constexpr int NACC = NP * NS;
+    float acc[NACC];
+#pragma unroll
+    for (int k = 0; k < NACC; k++) acc[k] = 0.0f;
+
+    auto compute = [&](const Raw& r_in, int c) __attribute__((always_inline)) {
+        Raw r = r_in;
+        IF<T>::bcast(r, col);
+        float ca[4], cb[4];
+        IF<T>::coef(r, s_out, ca, cb);
+        const uint8_t* abase = lds_a + (size_t)c * 4 * TS;
+        float sv[NP][NS][4], sc[NP][4];
+        if (IF<T>::BIAS) {
+#pragma unroll
+            for (int p = 0; p < NP; p++)
+#pragma unroll
+                for (int e2 = 0; e2 < NS; e2++) {
+                    const float4 v = *(const float4*)(lds_s + ((c * G + s_out) * M + srow[p][e2]) * 4);
+                    sv[p][e2][0] = v.x; sv[p][e2][1] = v.y; sv[p][e2][2] = v.z; sv[p][e2][3] = v.w;
+                }
+        }
+        if (D == 3) {
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                const float4 v = *(const float4*)(lds_sc + ((c * G + s_out) * M + srow[p][0]) * 4);
+                sc[p][0] = v.x; sc[p][1] = v.y; sc[p][2] = v.z; sc[p][3] = v.w;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const v4i B = IF<T>::codes(r, t, g);
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                const v4i A = *(const v4i*)(abase + t * TS + aoff[p]);
+                const v4i Z = {0, 0, 0, 0};
+                const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, Z, 0, 0, 0);
+                if constexpr (D == 3) {
+                    const int hi2 = (int)(((uint32_t)C.x << 8) + (uint32_t)C.y);
+                    const float P = fmaf((float)hi2, 256.0f, (float)C.z);
+                    acc[p] = fmaf(ca[t] * sc[p][t], P, acc[p]);
+                    if (IF<T>::BIAS) acc[p] = fmaf(cb[t], sv[p][0][t], acc[p]);
+                } else {
+                    const int cc[4] = {C.x, C.y, C.z, C.w};
+#pragma unroll
+                    for (int e2 = 0; e2 < NE; e2++) {
+                        acc[p * NE + e2] = fmaf(ca[t], (float)cc[e2], acc[p * NE + e2]);
+                        if (IF<T>::BIAS) acc[p * NE + e2] = fmaf(cb[t], sv[p][e2][t], acc[p * NE + e2]);
+                    }
+                }
+            }
+        }
+    };
+
+    // Tile end: lane groups of one output row are added (they differ in the
+    // scale-group slot), then the KW wavefronts of the tile through LDS in
+    // wavefront order; the first of them stores.
+    int parity = 0;
+    auto finish = [&](int fit) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < NACC; k++) {
+            float v = acc[k];
+            v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));  // lane ^ 16
+            if (G == 4) v += __shfl_xor(v, 32, 64);
+            acc[k] = v;
+        }
+        const int rl = ((fit - bx) / gx * TPI + slot_t) * 16 + col;  // local output row
+        const bool holder = G == 2 ? ((g & 1) == 0) : (g == 0);
+        auto store = [&](int k, float v) __attribute__((always_inline)) {
+            const int p = k / NS, e2 = k % NS;
+            const int m = p * RP + (D == 3 ? rg_out : rg_out * NE + e2);
+            if (m < M) outl[m * ROWS + rl] = ldexpf(v * row_rs[m], row_re[m]);
+        };
+        if (KW == 1) {
+            if (holder) {
+#pragma unroll
+                for (int k = 0; k < NACC; k++) store(k, acc[k]);
+            }
+        } else {
+            float* rb_ = red + parity * (kWaves * MT * 16);
+            if (holder) {
+#pragma unroll
+                for (int k = 0; k < NACC; k++) rb_[(w * NACC + k) * (RG * 16) + rg_out * 16 + col] = acc[k];
+            }
+            __syncthreads();
+            if (kp == 0 && holder) {
+#pragma unroll
+                for (int k = 0; k < NACC; k++) {
+                    float v = 0.0f;
+                    for (int q = 0; q < KW; q++) v += rb_[((w + q) * NACC + k) * (RG * 16) + rg_out * 16 + col];
+                    store(k, v);
+                }
+            }
+            parity ^= 1;
+        }
+#pragma unroll
+        for (int k = 0; k < NACC; k++) acc[k] = 0.0f;
+    };
+
+    // ---- main loop: three register sets in rotation; each step issues the
+    // fetch two chunks ahead before computing the current one.
+#define GGQ_I8_STEP(CUR, NXT)                                                   \
+    {                                                                           \
+        NXT = IF<T>::fetch(rs, chunk_off(itf, jf), g, s_out);                 \
+        adv(itf, jf);                                                           \
+        __builtin_amdgcn_sched_barrier(0);                                      \
+        compute(CUR, kp + KW * i);                                              \
+        if (i == nmy - 1) finish(it);                                           \
+        adv(it, i);                                                             \
+        if (it >= n_it) break;                                                  \
+    }
+    if (it < n_it) {
+        while (true) {
+            GGQ_I8_STEP(r0, r2)
+            GGQ_I8_STEP(r1, r0)
+            GGQ_I8_STEP(r2, r1)
+        }
+    }
+#undef GGQ_I8_STEP
+    __syncthreads();
+    // this workgroup's outputs: tile iterations bx, bx + gx, ... of TPI tiles
+    for (int idx = tid; idx < M * ROWS; idx += kThreads) {
+        const int m = idx / ROWS, rl = idx % ROWS;
+        const int j = rl / (TPI * 16), tr = rl % (TPI * 16);
+        const int n = (bx + j * gx) * TPI * 16 + tr;
+        if (n < N) a.Y[(int64_t)m * a.ldy + n] = outl[idx];
+    }
+}
+
+// Format sets a kernel is compiled for (the register allocation is the
+// largest over its formats).
+enum : int {
+    FS_Q4K = 1 << 0, FS_Q5K = 1 << 1, FS_Q6K = 1 << 2, FS_Q80 = 1 << 3, FS_IQ4NL = 1 << 4, FS_IQ4XS = 1 << 5,
+    FS_ALL = 63,
+};
+__host__ __device__ constexpr int fs_bit(uint32_t t) {
+    return t == T_Q4_K ? FS_Q4K : t == T_Q5_K ? FS_Q5K : t == T_Q6_K ? FS_Q6K : t == T_Q8_0 ? FS_Q80
+         : t == T_IQ4_NL ? FS_IQ4NL : t == T_IQ4_XS ? FS_IQ4XS : 0;
+}
+
+template <int D, int NE, int NP, int FS>
+__global__ __launch_bounds__(kThreads) void i8_gemv_kernel(I8Args args) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int q = 0;
+    while (q + 1 < args.n && (int)blockIdx.x >= args.begin[q + 1]) q++;
+    const int bx = blockIdx.x - args.begin[q], gx = args.begin[q + 1] - args.begin[q];
+    const I8Prob& a = args.p[q];
+    switch (a.type) {
+    case T_Q4_K: if constexpr ((FS & FS_Q4K) != 0) i8_gemv_body<T_Q4_K, D, NE, NP>(args, a, bx, gx, lds); break;
+    case T_Q5_K: if constexpr ((FS & FS_Q5K) != 0) i8_gemv_body<T_Q5_K, D, NE, NP>(args, a, bx, gx, lds); break;
+    case T_Q6_K: if constexpr ((FS & FS_Q6K) != 0) i8_gemv_body<T_Q6_K, D, NE, NP>(args, a, bx, gx, lds); break;
+    case T_Q8_0: if constexpr ((FS & FS_Q80) != 0) i8_gemv_body<T_Q8_0, D, NE, NP>(args, a, bx, gx, lds); break;
+    case T_IQ4_NL: if constexpr ((FS & FS_IQ4NL) != 0) i8_gemv_body<T_IQ4_NL, D, NE, NP>(args, a, bx, gx, lds); break;
+    case T_IQ4_XS: if constexpr ((FS & FS_IQ4XS) != 0) i8_gemv_body<T_IQ4_XS, D, NE, NP>(args, a, bx, gx, lds); break;
+    default: break;
+    }
+}
+
+int env_i8(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e && *e ? atoi(e) : dflt;
+}
+
+int cu_count() {
+    static int v = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    return v;
+}
+
+// Formats with four scale slots per MFMA (one row per pass in fp32 mode).
+bool g4_format(uint32_t t) { return t == T_Q6_K || t == T_IQ4_NL || t == T_IQ4_XS; }
+
+// Instantiation choice for M rows: (D, NE, NP) and the rows per pass.
+struct I8Shape { int D, NE, NP; };
+bool i8_shape(int M, int mode, bool has_q6, I8Shape& sh) {  // has_q6: a format with four slots per MFMA
+    if (M < 1 || M > 8) return false;
+    if (mode == 0) {
+        // two rows per pass (one for Q6_K)
+        const int rp = has_q6 ? 1 : 2;
+        const int np = (M + rp - 1) / rp;
+        if (np > 2) return false;  // more passes hold more accumulators than fit without spills
+        sh = {3, 1, np};
+        return true;
+    }
+    // int8 codes: rows in registers; NE rows per lane group
+    const int rg = has_q6 ? 1 : 2;
+    int ne = (M + rg - 1) / rg;
+    if (ne <= 1) ne = 1;
+    else if (ne <= 2) ne = 2;
+    else ne = 4;
+    const int np = (M + rg * ne - 1) / (rg * ne);
+    if (np > 1) return false;
+    sh = {1, ne, np};
+    return true;
+}
+
+int i8_lds_bytes(int K, int M, bool q6, const I8Shape& sh) {
+    const int G = q6 ? 4 : 2;
+    const int mt = (4 / G) * (sh.D == 1 ? sh.NE : 1) * sh.NP;
+    return i8_lds_total(K, G, sh.D, M, mt);
+}
+
+constexpr int kMaxLds = 150 * 1024;
+
+// Wavefronts per tile and workgroups per problem of a launch (one
+// 1024-thread workgroup per CU), and the LDS it needs: lds_need (set-up and
+// reduction) plus each workgroup's output rows.
+struct I8Grid { int kw_log2[kMaxProbs], gx[kMaxProbs]; int lds; };
+I8Grid i8_grid(const GemvProblem* ps, int n, const int* lds_need, int M) {
+    I8Grid gr{};
+    const int resident = cu_count();
+    const int resident_waves = resident * kWaves;
+    // wavefronts per tile: split K so the launch fills the resident waves
+    int tiles_total = 0;
+    for (int i = 0; i < n; i++) tiles_total += (ps[i].N + 15) / 16;
+    const int kw_env = env_i8("GGQ_I8_KW", 0);
+    int want[kMaxProbs];
+    int want_total = 0;
+    for (int i = 0; i < n; i++) {
+        const GemvProblem& p = ps[i];
+        const int nc = p.K / 256, tiles = (p.N + 15) / 16;
+        int kw = 1;
+        while (kw < 16 && 2 * kw <= nc && tiles_total * 2 * kw <= resident_waves) kw *= 2;
+        if (kw_env > 0) {
+            kw = 1;
+            while (2 * kw <= kw_env && 2 * kw <= nc && kw < 16) kw *= 2;
+        }
+        gr.kw_log2[i] = __builtin_ctz(kw);
+        const int tpi = kWaves / kw;
+        want[i] = (tiles + tpi - 1) / tpi;
+        want_total += want[i];
+    }
+    // workgroups per problem: all it can use when the launch fits the
+    // resident capacity, else in proportion
+    gr.lds = 0;
+    for (int i = 0; i < n; i++) {
+        int gxi = want[i];
+        if (want_total > resident) {
+            gxi = (int)((int64_t)want[i] * resident / want_total);
+            gxi = gxi < 1 ? 1 : gxi;
+        }
+        gr.gx[i] = gxi;
+        const int tpi = kWaves >> gr.kw_log2[i];
+        const int rows = (want[i] + gxi - 1) / gxi * tpi * 16;
+        const int need = lds_need[i] + rows * M * 4;
+        gr.lds = need > gr.lds ? need : gr.lds;
+    }
+    return gr;
+}
+
+template <int D, int NE, int NP, int FS>
+hipError_t i8_run(I8Args& args, const I8Grid& gr, int n, hipStream_t s) {
+    auto kern = i8_gemv_kernel<D, NE, NP, FS>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        attr_set = true;
+    }
+    const int lds = gr.lds;
+    args.begin[0] = 0;
+    for (int i = 0; i < n; i++) {
+        args.p[i].kw_log2 = gr.kw_log2[i];
+        args.begin[i + 1] = args.begin[i] + gr.gx[i];
+    }
+    args.n = n;
+    kern<<<args.begin[n], kThreads, lds, s>>>(args);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool i8_gemv_eligible(const GemvProblem* ps, int n, int mode) {
+    // GGQ_GEMV_MFMA=0 keeps every GEMV on the fp32 FMA kernels
+    if (env_i8("GGQ_GEMV_I8", 1) == 0 || env_i8("GGQ_GEMV_MFMA", 1) == 0 || n < 1 || n > kMaxProbs) return false;
+    bool q6 = false;
+    for (int i = 0; i < n; i++) q6 = q6 || g4_format(ps[i].type);
+    I8Shape sh;
+    if (!i8_shape(ps[0].M, mode, q6, sh)) return false;
+    for (int i = 0; i < n; i++) {
+        const GemvProblem& p = ps[i];
+        if (p.M != ps[0].M || !supported(p.type)) return false;
+        if (p.grp_off || p.W2 || p.n1 > 0 || p.X2 || p.rms || p.R || p.silu) return false;
+        if (p.K % 256 != 0 || p.K <= 0 || p.N <= 0 || p.groups > 1) return false;
+        if (p.N * row_bytes(p.type, p.K) >= (int64_t)kOOB) return false;  // buffer offsets below kOOB
+    }
+    if (mode == 0) {
+        // fp32 activations: the matrix-core kernel pays a fixed set-up (the
+        // activation digits in LDS, 1024-thread workgroups, one per tile
+        // group) that only launches moving enough weight bytes amortize;
+        // smaller ones stay on the fp32 kernels (GGQ_I8_MIN_BYTES, bytes).
+        int64_t bytes = 0;
+        for (int i = 0; i < n; i++) bytes += (int64_t)ps[i].N * row_bytes(ps[i].type, ps[i].K);
+        if (bytes < (int64_t)env_i8("GGQ_I8_MIN_BYTES", 16 << 20)) return false;
+    }
+    int lds_need[kMaxProbs];
+    for (int i = 0; i < n; i++) lds_need[i] = i8_lds_bytes(ps[i].K, ps[i].M, g4_format(ps[i].type), sh);
+    return i8_grid(ps, n, lds_need, ps[0].M).lds <= kMaxLds;
+}
+
+hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* qa, const float* sa, hipStream_t s) {
+    if (n < 1 || n > kMaxProbs) return hipErrorInvalidValue;
+    const int M = ps[0].M;
+    bool q6 = false;
+    for (int i = 0; i < n; i++) {
+        if (ps[i].M != M) return hipErrorInvalidValue;
+        q6 = q6 || g4_format(ps[i].type);
+    }
+    I8Shape sh;
+    if (!i8_shape(M, mode, q6, sh)) return hipErrorInvalidValue;
+    I8Args args{};
+    args.M = M;
+    args.mode = mode;
+    int lds_need[kMaxProbs];
+    for (int i = 0; i < n; i++) {
+        const GemvProblem& g = ps[i];
+        I8Prob& p = args.p[i];
+        p.W = (const uint8_t*)g.W;
+        p.row_bytes = (uint32_t)row_bytes(g.type, g.K);
+        p.type = g.type;
+        p.N = g.N;
+        p.K = g.K;
+        p.X = g.X;
+        p.ldx = g.ldx;
+        p.QA = qa;
+        p.SA = sa;
+        p.Y = g.Y;
+        p.ldy = g.ldy;
+        p.x_vec4 = g.X && ((uintptr_t)g.X % 16 == 0) && (g.ldx % 4 == 0);
+        lds_need[i] = i8_lds_bytes(g.K, M, g4_format(g.type), sh);  // each format's own geometry
+        if (lds_need[i] > kMaxLds) return hipErrorInvalidValue;
+    }
+    int fs = 0;
+    for (int i = 0; i < n; i++) fs |= fs_bit(ps[i].type);
+    // one format, or the Q4_K_M pair (Q4_K and Q6_K), each get their own
+    // kernel; other mixes the kernel compiled for all formats
+    const I8Grid gr = i8_grid(ps, n, lds_need, M);
+    if (gr.lds > kMaxLds) return hipErrorInvalidValue;
+#define R(D_, NE_, NP_)                                                                          \
+    switch (fs) {                                                                                \
+    case FS_Q4K: return i8_run<D_, NE_, NP_, FS_Q4K>(args, gr, n, s);                      \
+    case FS_Q6K: return i8_run<D_, NE_, NP_, FS_Q6K>(args, gr, n, s);                      \
+    case FS_Q4K | FS_Q6K: return i8_run<D_, NE_, NP_, FS_Q4K | FS_Q6K>(args, gr, n, s);    \
+    case FS_Q80: return i8_run<D_, NE_, NP_, FS_Q80>(args, gr, n, s);                      \
+    default: return i8_run<D_, NE_, NP_, FS_ALL>(args, gr, n, s);                          \
+    }
+    if (sh.D == 3) {
+        if (sh.NP == 1) R(3, 1, 1);
+        R(3, 1, 2);
+    }
+    switch (sh.NE) {
+    case 1: R(1, 1, 1);
+    case 2: R(1, 2, 1);
+    default: R(1, 4, 1);
+    }
+#undef R
+}
+
+}  // namespace ggq

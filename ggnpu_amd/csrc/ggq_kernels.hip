@@ -1413,6 +1413,9 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     if (n == 1) return launch_gemv(ps[0], s);  // the single-problem kernel sizes its grid for one problem
     for (int i = 0; i < n; i++)
         if (!offsets_fit(ps[i])) return hipErrorInvalidValue;
+    {
+        if (i8_gemv_eligible(ps, n, 0)) return launch_i8_gemv(ps, n, 0, nullptr, nullptr, s);
+    }
     MultiArgs ma;
     int ppt = -1, total_iters = 0;
     const int M = ps[0].M;
@@ -1528,6 +1531,7 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
 
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t s) {
     if (p.N == 0 || p.M == 0) return hipSuccess;
+    if (offsets_fit(p) && i8_gemv_eligible(&p, 1, 0)) return launch_i8_gemv(&p, 1, 0, nullptr, nullptr, s);
 #define L(TT) return launch_gemv_t<TT>(p, s)
     GGQ_DISPATCH_TYPE(p.type, L)
 #undef L

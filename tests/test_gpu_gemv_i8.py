@@ -1,0 +1,131 @@
+"""The decode GEMV on the int8 matrix cores (ggq_gemv_i8.hip), reached
+through the C ABI for 1..8 activation rows and K a multiple of 256:
+
+* fp32 activations (exact 3-digit fixed point): every format, 1..4 rows,
+  ragged N, long K, strided and unaligned activation rows, extreme and mixed
+  magnitudes, against the fp64 oracle (rel-L2 <= 1e-4);
+* GGQ_ACT_Q8_ROW (codes quantized per row inside the kernel) and the
+  pre-quantized entry point (ggq_mul_mat_q8_dev), 1..8 rows: the two agree
+  bit for bit and meet the bar against the oracle's Q8_ROW treatment;
+* several problems of mixed formats in one launch (ggq_mul_mat_batch_dev);
+* every split of a tile's K over wavefronts (GGQ_I8_KW, read per launch).
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import ggnpu_amd.lib as gl
+from tests.gpu_util import dev, empty, host, ptr, stream_handle
+from tests.test_gpu_parity import TYPES, TOL, ctx, run_mm, weights  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _every_size(monkeypatch):
+    # fp32 launches of any size take the matrix-core path here
+    monkeypatch.setenv("GGQ_I8_MIN_BYTES", "0")
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_i8_gemv_f32_all_formats(ctx, orc, name, M):
+    t = TYPES[name]
+    for N, K in ((700, 256), (33, 2048), (16, 1024)):
+        raw = weights(t, N, K, seed=N + K + t)
+        A = np.random.default_rng(M * 7 + t).standard_normal((M, K)).astype(np.float32)
+        got = run_mm(ctx, t, raw, N, K, A, 0)
+        err = orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 0))
+        assert err < TOL, (name, M, N, K, err)
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q8_0"])
+def test_i8_gemv_long_k_and_strides(ctx, orc, name):
+    t = TYPES[name]
+    N, K = 300, 8960 if name == "Q8_0" else 8192
+    raw = weights(t, N, K, seed=3 + t)
+    A = np.random.default_rng(t).standard_normal((2, K)).astype(np.float32)
+    for lda, ldc in ((K, N), (K + 3, N + 5)):  # unaligned rows take the scalar loads
+        got = run_mm(ctx, t, raw, N, K, A, 0, lda=lda, ldc=ldc)
+        assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 0)) < TOL, (lda, ldc)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_i8_gemv_magnitudes(ctx, orc, name):
+    """Rows of 1e-30, 1e30, mixed magnitudes inside one row, a zero row and a
+    row with one non-zero value: the per-row power of two keeps 22 bits
+    relative to the row maximum."""
+    t = TYPES[name]
+    N, K = 64, 512
+    raw = weights(t, N, K, seed=9)
+    rng = np.random.default_rng(9)
+    rows = [rng.standard_normal(K) * 1e-30, rng.standard_normal(K) * 1e30,
+            rng.standard_normal(K) * np.where(rng.random(K) < 0.5, 1e-3, 1e3), np.zeros(K)]
+    one = np.zeros(K); one[77] = -3.5
+    rows.append(one)
+    for r in rows:
+        A = r[None, :].astype(np.float32)
+        got = run_mm(ctx, t, raw, N, K, A, 0)
+        ref = orc.mul_mat_f64(t, raw, N, K, A, 0)
+        if not np.any(ref):
+            assert not np.any(got)
+        else:
+            assert orc.rel_l2(got, ref) < TOL
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("M", [1, 2, 5, 8])
+def test_i8_gemv_q8_row_and_prequantized(ctx, orc, name, M):
+    import torch
+    t = TYPES[name]
+    if t == 14 and M > 4:
+        pytest.skip("Q6_K: up to 4 rows per launch on this path (more take the fp32 route)")
+    N, K = 200, 1536 if name in ("Q8_0", "IQ4_NL") else 2048
+    raw = weights(t, N, K, seed=M + t)
+    A = np.random.default_rng(M + 100 * t).standard_normal((M, K)).astype(np.float32)
+    got = run_mm(ctx, t, raw, N, K, A, 1)
+    assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL
+    # quantize, then the pre-quantized entry point: the same codes, the same sums
+    dA, dW = dev(A), dev(raw)
+    q = empty((M, K), torch.int8)
+    sa = empty((M,), torch.float32)
+    ctx.check(ctx.lib.ggq_quantize_act_dev(ctx.h, ptr(dA), K, M, K, 1, ptr(q), ptr(sa), stream_handle()), "quant")
+    C = empty((M, N), torch.float32)
+    ctx.check(ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ptr(dW), t, N, K, ptr(q), ptr(sa), M, ptr(C), N, stream_handle()),
+              "q8_dev")
+    assert np.array_equal(host(C).view(np.uint32), got.view(np.uint32))
+
+
+def test_i8_gemv_batch_mixed_formats(ctx, orc):
+    """One launch over problems of different formats, K and N (the decode
+    step's q/k/v level shape, plus IQ4 / Q5_K / Q8_0 members)."""
+    import torch
+    specs = [(12, 2048, 2048), (12, 512, 2048), (14, 512, 2048), (23, 100, 1024), (13, 70, 512), (8, 333, 1536)]
+    for M in (1, 2):
+        rng = np.random.default_rng(M)
+        keep, descs, ref = [], (gl.GemvDesc * len(specs))(), []
+        for i, (t, N, K) in enumerate(specs):
+            raw = weights(t, N, K, seed=50 + i)
+            A = rng.standard_normal((M, K)).astype(np.float32)
+            dW, dA = dev(raw), dev(A)
+            dC = torch.full((M, N), float("nan"), device="cuda")
+            keep += [dW, dA, dC]
+            descs[i].W, descs[i].type, descs[i].N, descs[i].K = dW.data_ptr(), t, N, K
+            descs[i].A, descs[i].C = dA.data_ptr(), dC.data_ptr()
+            ref.append((t, raw, N, K, A, dC))
+        ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, descs, len(specs), M, stream_handle()), "batch")
+        for t, raw, N, K, A, dC in ref:
+            assert orc.rel_l2(host(dC), orc.mul_mat_f64(t, raw, N, K, A, 0)) < TOL, (t, N, K, M)
+
+
+@pytest.mark.parametrize("kw", ["1", "2", "4", "16"])
+def test_i8_gemv_k_splits(ctx, orc, kw, monkeypatch):
+    monkeypatch.setenv("GGQ_I8_KW", kw)
+    for t, N, K in ((12, 2048, 8192), (14, 96, 4096), (8, 40, 2560)):
+        raw = weights(t, N, K, seed=int(kw) + t)
+        A = np.random.default_rng(int(kw)).standard_normal((2, K)).astype(np.float32)
+        for mode in (0, 1):
+            got = run_mm(ctx, t, raw, N, K, A, mode)
+            assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, mode)) < TOL, (kw, t, mode)
