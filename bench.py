@@ -134,7 +134,7 @@ def back_to_back_times(torch, fns, reps):
     return out
 
 
-def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream, fuse_levels=True):
+def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream, fuse_levels=True, probe_levels=True):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
     mats, host_layer0 = [], []
@@ -194,13 +194,16 @@ def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream, fuse_levels=
         return lambda: launch_batch(ctx, lv, stream)
 
     # Per-level breakdown of layer 0 and the output projection (diagnostic).
+    if not probe_levels:
+        return levels, host_layer0, sec, gpu_sec, step_bytes, []
     probe = levels[:4] + [levels[-1]]
     kt = back_to_back_times(torch, [level_fn(lv) for lv in probe], reps=10)
     return levels, host_layer0, sec, gpu_sec, step_bytes, list(zip(probe, kt))
 
 
-def bench_config1(torch, ctx, stream, reps=200):
-    """Single Q4_K GEMV 8192x2048; 32 distinct HBM copies rotated."""
+def bench_config1(torch, ctx, stream, reps=200, act_mode=0):
+    """Single Q4_K GEMV 8192x2048; 32 distinct HBM copies rotated.  act_mode
+    0 = fp32 activations, 1 = per-row int8 activations (GGQ_ACT_Q8_ROW)."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1)
     dev, _ = make_weight(torch, gen, Q4K, 8192, 2048)
@@ -210,15 +213,40 @@ def bench_config1(torch, ctx, stream, reps=200):
 
     def run():
         for m in mats:
-            launch(ctx, m, 0, stream)
+            launch(ctx, m, act_mode, stream)
 
     sec, gsec = time_steps(torch, run, max(1, reps // 32), 2, gpu_time=True)
     sec /= len(mats)
     kmean = gsec / len(mats)
     b = mats[0].bytes()
-    return {"workload": "Q4_K GEMV 8192x2048 batch 1 fp32 (32 rotated copies)", "bytes_per_call": b,
+    act = "fp32" if act_mode == 0 else "per-row int8 (GGQ_ACT_Q8_ROW)"
+    return {"workload": f"Q4_K GEMV 8192x2048 batch 1, {act} activations (32 rotated copies)", "bytes_per_call": b,
             "us_per_call_wall": sec * 1e6, "us_per_call_gpu_event": kmean * 1e6,
             "GBps": b / kmean / 1e9, "frac_hbm_peak": b / kmean / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_decode_levels(torch, ctx, levels, stream, act_mode, steps=30):
+    """The decode step's levels again with another activation treatment:
+    one ggq_mul_mat_batch_act_dev call per dependency level."""
+    calls = []
+    for lv in levels:
+        descs = (gl.GemvDesc * len(lv))()
+        for i, m in enumerate(lv):
+            descs[i].W, descs[i].type, descs[i].N, descs[i].K = m.w.data_ptr(), m.t, m.N, m.K
+            descs[i].A, descs[i].C = m.x.data_ptr(), m.y.data_ptr()
+        calls.append((descs, len(lv)))
+
+    def run():
+        for descs, n in calls:
+            st = ctx.lib.ggq_mul_mat_batch_act_dev(ctx.h, descs, n, 1, act_mode, stream)
+            if st != 0:
+                ctx.check(st, "mul_mat_batch_act_dev")
+
+    sec, gsec = time_steps(torch, run, steps, 3, gpu_time=True)
+    b = sum(m.bytes() for lv in levels for m in lv)
+    return {"workload": "configs[1] decode step, per-row int8 activations (GGQ_ACT_Q8_ROW), one call per level",
+            "ms_per_step": round(sec * 1e3, 4), "GBps": round(b / sec / 1e9, 1),
+            "kernel_us_per_step": round(gsec * 1e6, 1), "frac_hbm_peak": round(b / gsec / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def bench_decode_fused(torch, ctx, stream, steps=30):
@@ -564,34 +592,218 @@ def bench_config5(torch, ctx, stream, steps=20, T=64):
             "frac_hbm_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def cpu_baseline(host_layer0, budget_s=8.0):
-    """The reference's CPU path on layer 0 of the decode step, one core: the
-    compiled reference CpuRefBackend::mul_mat_q (oracle/_ref, built from the
-    reference's own sources) where that library is present ("reference"),
-    else the bit-identical restatement orc_mul_mat_cpuref_f32 ("port")."""
-    from oracle import oracle as orc
-    ref = orc.ref_lib()
+def host_cpu():
+    """Host CPU model and core counts for the cpu_baseline records."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"host_cpu": model, "host_cores_total": os.cpu_count(),
+            "host_cores_usable": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
+
+
+class CpuPath:
+    """The reference's CPU arithmetic, one core: the compiled reference
+    sources (oracle/_ref, "reference") where present, else the oracle's
+    bit-identical restatements ("port").
+      cpuref(t, W, N, K, A)  CpuRefBackend::mul_mat_q (cpu_ref.cpp:87-117;
+                             Q4_K / Q6_K, the types it takes)
+      rowdot(t, W, N, K, A)  the CLI's dequantize-row + fp32 dot for weights
+                             no backend takes (main.cpp:317-326, :1380-1386)"""
+
+    def __init__(self):
+        from oracle import oracle as orc
+        self.orc = orc
+        self.ref = orc.ref_lib()
+        self.kind = "reference" if self.ref is not None else "port"
+
+    def _run(self, fn_ref, fn_orc, t, W, N, K, A):
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        if self.ref is None:
+            return fn_orc(t, W, N, K, A)
+        C = np.empty((A.shape[0], N), np.float32)
+        st = fn_ref(t, W.ctypes.data, N, K, A.ctypes.data, A.shape[0], C.ctypes.data)
+        assert st == 0, st
+        return C
+
+    def cpuref(self, t, W, N, K, A):
+        return self._run(self.ref and self.ref.ref_cpuref_mul_mat, self.orc.mul_mat_cpuref_f32, t, W, N, K, A)
+
+    def rowdot(self, t, W, N, K, A):
+        return self._run(self.ref and self.ref.ref_rowdot_mul_mat, self.orc.mul_mat_rowdot_f32, t, W, N, K, A)
+
+    def what(self, fn):
+        src = {"cpuref": ("oracle/_ref CpuRefBackend::mul_mat_q (reference sources, -O3)",
+                          "oracle/ggq_oracle.c orc_mul_mat_cpuref_f32"),
+               "rowdot": ("oracle/_ref reference block decoders + main.cpp:317-326 row-dot loop",
+                          "oracle/ggq_oracle.c orc_mul_mat_rowdot_f32")}[fn]
+        return src[0] if self.ref is not None else src[1]
+
+
+def _timed(budget_s, body):
+    """Repeat body() until budget_s has passed; (passes, seconds)."""
+    t0, n = time.perf_counter(), 0
+    while True:
+        body()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s:
+            return n, el
+
+
+def _host_weight(rng, t, N, K):
+    return gl.encode(t, (rng.standard_normal((N, K), dtype=np.float32) * 0.02))
+
+
+def _cpu_record(cp, value, unit, sample, **kw):
+    return {"value": round(value, 4), "unit": unit, "cores": 1, "kind": cp.kind, "sample": sample, **host_cpu(), **kw}
+
+
+def cpu_baseline(host_layer0, budget_s=6.0):
+    """configs[1]: CpuRefBackend::mul_mat_q over layer 0 of the decode step."""
+    cp = CpuPath()
     rng = np.random.default_rng(0)
     work = [(m.t, raw, m.N, m.K, rng.standard_normal((1, m.K)).astype(np.float32)) for m, raw in host_layer0]
-    outs = [np.empty((1, N), np.float32) for _, _, N, _, _ in work]
-    nbytes, t0, reps = 0, time.perf_counter(), 0
-    while True:
-        for (t, raw, N, K, A), C in zip(work, outs):
-            if ref is not None:
-                st = ref.ref_cpuref_mul_mat(t, raw.ctypes.data, N, K, A.ctypes.data, 1, C.ctypes.data)
-                assert st == 0, st
-            else:
-                orc.mul_mat_cpuref_f32(t, raw, N, K, A)
-            nbytes += gl.row_bytes(t, K) * N + 4 * (K + N)
-        reps += 1
+    nbytes = sum(gl.row_bytes(t, K) * N + 4 * (K + N) for t, _, N, K, _ in work)
+    reps, el = _timed(budget_s, lambda: [cp.cpuref(t, raw, N, K, A) for t, raw, N, K, A in work])
+    return _cpu_record(cp, reps * nbytes / el / 1e9, "GB/s",
+                       f"Llama-3.2-1B layer 0 (q,k,v,o,gate,up,down; {nbytes / 1e6:.1f} MB Q4_K/Q6_K), batch 1, "
+                       f"{reps} passes in {el:.1f}s, {cp.what('cpuref')}")
+
+
+def cpu_baseline_config0(budget_s=3.0):
+    """configs[0]: CpuRefBackend::mul_mat_q on the 8192x2048 Q4_K GEMV."""
+    cp = CpuPath()
+    rng = np.random.default_rng(1)
+    W = _host_weight(rng, Q4K, 8192, 2048)
+    A = rng.standard_normal((1, 2048)).astype(np.float32)
+    nbytes = W.size + 4 * (2048 + 8192)
+    reps, el = _timed(budget_s, lambda: cp.cpuref(Q4K, W, 8192, 2048, A))
+    return _cpu_record(cp, reps * nbytes / el / 1e9, "GB/s",
+                       f"the whole workload (Q4_K 8192x2048, batch 1), {reps} calls in {el:.1f}s, {cp.what('cpuref')}",
+                       us_per_call=round(el / reps * 1e6, 1))
+
+
+def cpu_baseline_config2(budget_s=4.0, rows=32):
+    """the reference on the CPU for Q8_0 weights is the
+    dequantize-row + fp32 dot loop (CpuRefBackend takes no Q8_0,
+    main.cpp:317-326); timed on the first `rows` rows of each layer-0 weight
+    for all 512 tokens and scaled to the 28-layer step.  The accelerator
+    route's host preparation is timed beside it: the per-row int8 activation
+    quantization (amd_xdna.cpp:598-603, per step) and the per-row int8 weight
+    requantization decode_q8_0_for_npu (q8_0.cpp:30-77, once per weight)."""
+    cp = CpuPath()
+    rng = np.random.default_rng(2)
+    T = PREFILL_TOKENS
+    mats = [(name, _host_weight(rng, Q8_0, rows, K), K) for name, _, _, K in QWEN_LAYER]
+    acts = {K: rng.standard_normal((T, K)).astype(np.float32) for K in (1536, 8960)}
+    sample_ops = sum(2 * T * rows * K for _, _, K in mats)
+    reps, el = _timed(budget_s, lambda: [cp.rowdot(Q8_0, W, rows, K, acts[K]) for _, W, K in mats])
+    sec_per_op = el / reps / sample_ops
+    step_ops = QWEN_LAYERS * sum(2 * T * N * K for _, _, N, K in QWEN_LAYER)
+    # host prep of the int8 route: four activation quantizations per layer
+    # (port: the reference's quantizer lives in the accelerator backend) and
+    # the weight requantization (reference decode_q8_0_for_npu where built)
+    t0 = time.perf_counter()
+    for K in (1536, 1536, 1536, 8960):
+        cp.orc.quant_act(acts[K], 1)
+    act_quant_ms = (time.perf_counter() - t0) * 1e3 * QWEN_LAYERS
+    req_rows = sum(rows for _ in mats)
+    t0 = time.perf_counter()
+    for _, W, K in mats:
+        if cp.ref is not None:
+            q = np.empty((rows, K), np.int8)
+            sc = np.empty(rows, np.float32)
+            assert cp.ref.ref_decode_for_npu(Q8_0, W.ctypes.data, W.size, rows, K, q.ctypes.data, sc.ctypes.data) == 0
+    req_s = time.perf_counter() - t0
+    model_elems = QWEN_LAYERS * sum(N * K for _, _, N, K in QWEN_LAYER)
+    req_elems = sum(rows * K for _, _, K in mats)
+    step_s = sec_per_op * step_ops + act_quant_ms / 1e3
+    out = _cpu_record(cp, step_ops / step_s / 1e12, "TOPS",
+                      f"first {rows} rows of each Qwen2.5-1.5B layer-0 Q8_0 weight x {T} tokens ({reps} passes in "
+                      f"{el:.1f}s, {cp.what('rowdot')}), scaled to the 28-layer step; plus the per-row int8 "
+                      "activation quantization of the step's 112 inputs (oracle port, single core)",
+                      ms_per_step=round(step_s * 1e3, 1), act_quant_ms_per_step=round(act_quant_ms, 1))
+    if cp.ref is not None:
+        out["weight_requant_s_once"] = round(req_s / req_elems * model_elems, 2)
+        out["weight_requant_note"] = ("reference decode_q8_0_for_npu (q8_0.cpp:30-77) on the same rows, scaled to "
+                                      "the model's 28 layers; paid once per weight (WeightCache), not per step")
+    return out
+
+
+def cpu_baseline_config3(budget_s=2.0):
+    """IQ4_NL / IQ4_XS / Q5_K weights take the dequantize-row +
+    fp32 dot loop (main.cpp:317-326) on the CPU; layer 0 at batch 1 and 8."""
+    cp = CpuPath()
+    rng = np.random.default_rng(3)
+    cycle = [IQ4NL, IQ4XS, Q5K]
+    mats = [(cycle[i % 3], _host_weight(rng, cycle[i % 3], N, K), N, K) for i, (_, N, K) in enumerate(QWEN3_SHAPES)]
+    res = {}
+    for M in (1, 8):
+        acts = {K: rng.standard_normal((M, K)).astype(np.float32) for K in (1024, 2048, 3072)}
+        nbytes = sum(W.size + 4 * M * (K + N) for _, W, N, K in mats)
+        reps, el = _timed(budget_s, lambda: [cp.rowdot(t, W, N, K, acts[K]) for t, W, N, K in mats])
+        res[M] = (reps * nbytes / el / 1e9, reps, el, el / reps * QWEN3_LAYERS * 1e6)
+    g1, reps, el, us1 = res[1]
+    return _cpu_record(cp, g1, "GB/s",
+                       f"Qwen3-0.6B layer 0 (7 weights, IQ4_NL/IQ4_XS/Q5_K), batch 1: {reps} passes in {el:.1f}s, "
+                       f"{cp.what('rowdot')}", us_per_step_batch1=round(us1, 1),
+                       batch8={"GBps": round(res[8][0], 3), "us_per_step": round(res[8][3], 1)})
+
+
+def cpu_baseline_config4(budget_s=6.0, T=64):
+    """the reference's per-token MoE loop (main.cpp:3110-3193):
+    per token top-8 of 256 router logits, softmax over the selected, then
+    for each selected expert and the shared one gate / up (Q4_K 512x2048)
+    and down (Q6_K 2048x512) through CpuRefBackend::mul_mat_q, silu(gate) *
+    up, weighted sum.  The 256 experts occupy distinct host memory (16
+    encoded experts copied over the 256 slots: the timing does not depend on
+    the values)."""
+    cp = CpuPath()
+    H, F, E, k = 2048, 512, 256, 8
+    rng = np.random.default_rng(5)
+    pool = [(_host_weight(rng, Q4K, F, H), _host_weight(rng, Q4K, F, H), _host_weight(rng, Q6K, H, F)) for _ in range(16)]
+    experts = [tuple(a.copy() for a in pool[e % 16]) for e in range(E)]
+    shared = pool[0]
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    sw = 1.0 / (1.0 + np.exp(-rng.standard_normal(T).astype(np.float32)))
+
+    def expert(ws, xt):
+        g = cp.cpuref(Q4K, ws[0], F, H, xt)
+        u = cp.cpuref(Q4K, ws[1], F, H, xt)
+        a = (g / (1.0 + np.exp(-g))) * u
+        return cp.cpuref(Q6K, ws[2], H, F, a)
+
+    t0, done, hit = time.perf_counter(), 0, set()
+    for t in range(T):
+        xt = x[t: t + 1]
+        sel = np.argsort(-logits[t], kind="stable")[:k]
+        w = np.exp(logits[t, sel] - logits[t, sel[0]])
+        w /= w.sum()
+        out = np.zeros((1, H), np.float32)
+        for e, we in zip(sel, w):
+            out += we * expert(experts[e], xt)
+            hit.add(int(e))
+        out += sw[t] * expert(shared, xt)
+        done += 1
         if time.perf_counter() - t0 > budget_s:
             break
     el = time.perf_counter() - t0
-    what = ("oracle/_ref CpuRefBackend::mul_mat_q (reference sources, -O3)" if ref is not None
-            else "oracle/ggq_oracle.c orc_mul_mat_cpuref_f32")
-    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "reference" if ref is not None else "port",
-            "sample": f"Llama-3.2-1B layer 0 (q,k,v,o,gate,up,down; 38.8 MB Q4_K/Q6_K), batch 1, "
-                      f"{reps} passes in {el:.1f}s, {what}"}
+    layer_s = el / done * T
+    per_expert = 2 * gl.row_bytes(Q4K, H) * F + gl.row_bytes(Q6K, F) * H
+    # the same algorithmic bytes as the GPU line (each hit expert once)
+    sel_all = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    nbytes = (len(np.unique(sel_all)) + 1) * per_expert + 4 * T * H * 2 + 4 * T * E
+    return _cpu_record(cp, nbytes / layer_s / 1e9, "GB/s",
+                       f"{done} of {T} tokens through the per-token loop in {el:.1f}s, scaled to the {T}-token layer; "
+                       f"GB/s over the GPU line's algorithmic bytes; {cp.what('cpuref')}",
+                       us_per_layer=round(layer_s * 1e6, 1))
 
 
 def main():
@@ -601,7 +813,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
-    ap.add_argument("--only", choices=["decode", "config1", "prefill", "config4", "moe", "logits", "fused", "attention", "host", "copy",
+    ap.add_argument("--only", choices=["decode", "config1", "config1_q8", "prefill", "config4", "moe", "logits", "fused", "attention", "host", "copy",
                                        "floor"],
                     default=None,
                     help="run one workload only and print its result (profiling aid)")
@@ -640,8 +852,9 @@ def main():
         print(json.dumps({"only": "floor", **bench_launch_floor(torch)}), flush=True)
         ctx.close()
         return
-    if args.only in ("config1", "prefill", "config4", "moe", "logits", "fused", "attention", "host"):
-        res = {"config1": bench_config1, "prefill": bench_prefill, "config4": bench_config4,
+    if args.only in ("config1", "config1_q8", "prefill", "config4", "moe", "logits", "fused", "attention", "host"):
+        res = {"config1": bench_config1, "config1_q8": lambda t, c, st: bench_config1(t, c, st, act_mode=1),
+               "prefill": bench_prefill, "config4": bench_config4,
                "moe": lambda *a: bench_config5(*a, T=args.moe_tokens), "logits": bench_logits, "fused": bench_decode_fused,
                "attention": bench_attention, "host": bench_host_api}[args.only](
                    torch, ctx, stream)
@@ -649,7 +862,7 @@ def main():
         ctx.close()
         return
     levels, host_layer0, sec, gpu_sec, step_bytes, per_level = bench_decode_step(
-        torch, ctx, args.steps, args.warmup, args.graph, stream, not args.per_matmul)
+        torch, ctx, args.steps, args.warmup, args.graph, stream, not args.per_matmul, args.only != "decode")
     value = step_bytes / sec / 1e9
     achieved = step_bytes / gpu_sec / 1e9
     out = {
@@ -684,18 +897,28 @@ def main():
     if os.path.exists(tpath) and not args.per_matmul:
         with open(tpath) as f:
             t = json.load(f)
-        out["roofline"]["traffic"] = round(1024 * (t["fetch_kib_per_step_raw"] * t["fetch_scale"]
-                                                   + t["write_kib_per_step_raw"] * t["write_scale"]))
+        out["roofline"]["traffic"] = t.get("traffic_bytes_per_step")
         out["roofline"]["traffic_unit"] = "HBM bytes per step (rocprofv3 FETCH_SIZE + WRITE_SIZE, " + t["source"] + ")"
-    if not args.no_extra:
-        out["extra"] = {"config1": bench_config1(torch, ctx, stream)}
-        for key, fn in (("config3_prefill", bench_prefill), ("config4_iq4_q5k", bench_config4),
-                        ("config5_moe", bench_config5), ("logits_argmax", bench_logits), ("attention_decode", bench_attention), ("host_api_decode", bench_host_api),
-                        ("decode_fused", bench_decode_fused)):
+    if not args.no_extra and args.only != "decode":
+        # Every BASELINE config beside the headline, each with its own CPU
+        # baseline (configs[0] in both activation treatments; configs[1]'s
+        # CPU baseline is the top-level one).
+        out["extra"] = {}
+        for key, fn, cpu in (
+                ("config1", bench_config1, cpu_baseline_config0),
+                ("config1_q8_row", lambda t, c, st: bench_config1(t, c, st, act_mode=1), None),
+                ("config2_q8_row", lambda t, c, st: bench_decode_levels(t, c, levels, st, 1), None),
+                ("config3_prefill", bench_prefill, cpu_baseline_config2),
+                ("config4_iq4_q5k", bench_config4, cpu_baseline_config3),
+                ("config5_moe", bench_config5, cpu_baseline_config4),
+                ("logits_argmax", bench_logits, None), ("attention_decode", bench_attention, None),
+                ("host_api_decode", bench_host_api, None), ("decode_fused", bench_decode_fused, None)):
             try:
                 out["extra"][key] = fn(torch, ctx, stream)
             except Exception as e:  # reported, never silently replaced
                 out["extra"][key] = {"error": str(e)}
+            if cpu is not None:
+                out["extra"][key]["cpu_baseline"] = cpu()
         out["cpu_baseline"] = cpu_baseline(host_layer0)
     per = {"method": "HIP events around 10 back-to-back launches of the level (small weights partly cache-warm)"}
     for lv, d in per_level:

@@ -669,6 +669,45 @@ int ggq_mul_mat_batch_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, void* strea
     return ggq_mul_mat_batch_rows_dev(c, d, n, 1, stream);
 }
 
+int ggq_mul_mat_batch_act_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, int M, int act_mode, void* stream) {
+    if (act_mode == GGQ_ACT_F32) return ggq_mul_mat_batch_rows_dev(c, d, n, M, stream);
+    GGQ_GUARD(c)
+    if (!d || n < 1 || n > GGQ_MAX_BATCH) return set_status(c, GGQ_INVALID_PARAM, "need 1..%d descriptors", GGQ_MAX_BATCH);
+    if (M < 0 || M > GGQ_MAX_BATCH_ROWS) return set_status(c, GGQ_INVALID_PARAM, "M=%d outside 0..%d", M, GGQ_MAX_BATCH_ROWS);
+    ggq::GemvProblem ps[GGQ_MAX_BATCH];
+    for (int i = 0; i < n; i++) {
+        if (!d[i].W || !d[i].A || !d[i].C) return set_status(c, GGQ_INVALID_PARAM, "null pointer in entry %d", i);
+        if (!aligned16(d[i].W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
+        int st = check_matmul_shape(c, d[i].type, d[i].N, d[i].K, M, (int)d[i].K, (int)d[i].N, act_mode);
+        if (st != GGQ_OK) return st;
+        ps[i] = ggq::GemvProblem{};
+        ps[i].type = d[i].type;
+        ps[i].W = d[i].W;
+        ps[i].N = (int)d[i].N;
+        ps[i].K = (int)d[i].K;
+        ps[i].X = d[i].A;
+        ps[i].ldx = (int)d[i].K;
+        ps[i].Y = d[i].C;
+        ps[i].ldy = (int)d[i].N;
+        ps[i].M = M;
+        ps[i].groups = 1;
+    }
+    if (M == 0) return set_status(c, GGQ_OK);
+    hipStream_t s = pick_stream(c, stream);
+    // Per-row int8 decode rows: one matrix-core launch quantizes and
+    // multiplies every entry; otherwise one queued matmul per entry.
+    if (act_mode == GGQ_ACT_Q8_ROW && M <= 8 && ggq::i8_gemv_eligible(ps, n, 1))
+        return hip_status(c, ggq::launch_i8_gemv(ps, n, 1, nullptr, nullptr, s), "gemv_i8 batch");
+    Arena ar = dev_arena(c, s);
+    for (int i = 0; i < n; i++) {
+        int st = mul_mat_queue(c, ar, d[i].W, d[i].type, d[i].N, d[i].K, d[i].A, (int)d[i].K, d[i].C, (int)d[i].N, M,
+                               act_mode, s);
+        if (st != GGQ_OK) return st;
+    }
+    return set_status(c, GGQ_OK);
+    GGQ_END(c)
+}
+
 int ggq_dequant_dev(ggq_ctx* c, const void* raw, uint32_t type, int64_t n_blocks, float* out, void* stream) {
     GGQ_GUARD(c)
     if (!raw || !out || n_blocks < 0) return set_status(c, GGQ_INVALID_PARAM, "bad arguments");

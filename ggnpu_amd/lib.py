@@ -127,6 +127,7 @@ SIGNATURES = {
     "ggq_mul_mat_noalloc_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _I, _I, _I, _P]),
     "ggq_mul_mat_batch_dev": (_I, [_P, _P, _I, _P]),
     "ggq_mul_mat_batch_rows_dev": (_I, [_P, _P, _I, _I, _P]),
+    "ggq_mul_mat_batch_act_dev": (_I, [_P, _P, _I, _I, _I, _P]),
     "ggq_mul_mat_fused_dev": (_I, [_P, _P, _I, _I, _P]),
     "ggq_mul_mat_q8_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _P, _I, _P, _I, _P]),
     "ggq_logits_argmax_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _I, _P, _P, _P, _P]),

@@ -2,11 +2,20 @@
 
     python -m ggnpu_amd.profile_summary stats <results.db> [name-filter]
     python -m ggnpu_amd.profile_summary pmc   <results.db> [name-filter]
+    python -m ggnpu_amd.profile_summary traffic <fetch.db> <write.db> <copy_fetch.db>
+            <copy_write.db> <steps> <copy_bytes> <algorithmic_bytes_per_step> <out.json> [name-filter]
 
 `stats`: per kernel (and grid size): dispatches, mean / min / max duration.
 `pmc`:   per kernel (and grid size): mean counter value per dispatch for
          every collected counter (FETCH_SIZE / WRITE_SIZE are in KiB).
+`traffic`: HBM bytes per step of a profiled run of `steps` steps: the sum of
+         FETCH_SIZE and of WRITE_SIZE over the matching kernels' dispatches,
+         each scaled by the factor that makes the same counter read the known
+         size of a device copy (copy_bytes read and written per copy), divided
+         by `steps`.  Prints the tables and the derivation, and writes the one
+         figure (with its inputs) to out.json.
 """
+import json
 import sqlite3
 import sys
 
@@ -41,7 +50,50 @@ def pmc(db, pat):
         print("%-64s %7d %-14s %6d %14.1f" % (name[:64], wgs, cn, n, v))
 
 
+def _counter_sum(db, counter, pat):
+    """(sum of counter over all matching dispatches in KiB, dispatches)."""
+    c = sqlite3.connect(db)
+    row = c.execute("select sum(counter_value), count(distinct dispatch_id) from pmc_events "
+                    "where name like ? and counter_name = ?", (pat, counter)).fetchone()
+    return float(row[0] or 0.0), int(row[1] or 0)
+
+
+def traffic(fdb, wdb, cfdb, cwdb, steps, copy_bytes, alg_bytes, out_json, pat="%ggq%"):
+    steps, copy_bytes, alg_bytes = int(steps), int(copy_bytes), int(alg_bytes)
+    copy_kib = copy_bytes / 1024
+    cf, nf = _counter_sum(cfdb, "FETCH_SIZE", "%copyBuffer%")
+    cw, nw = _counter_sum(cwdb, "WRITE_SIZE", "%copyBuffer%")
+    fscale = copy_kib / (cf / nf)
+    wscale = copy_kib / (cw / nw)
+    f, df = _counter_sum(fdb, "FETCH_SIZE", pat)
+    w, dw = _counter_sum(wdb, "WRITE_SIZE", pat)
+    fetch = f * fscale / steps * 1024
+    write = w * wscale / steps * 1024
+    tot = round(fetch + write)
+    print("# per kernel, FETCH_SIZE run:")
+    pmc(fdb, pat)
+    print("# per kernel, WRITE_SIZE run:")
+    pmc(wdb, pat)
+    print(f"# calibration copy ({copy_kib:.0f} KiB read + written): FETCH_SIZE {cf / nf:.1f} KiB -> x {fscale:.3f}, "
+          f"WRITE_SIZE {cw / nw:.1f} KiB -> x {wscale:.3f}")
+    print(f"# {df} / {dw} matching dispatches over {steps} steps")
+    print(f"# per step: fetch {f / steps:.1f} KiB raw x {fscale:.3f} = {fetch / 1e6:.1f} MB; "
+          f"write {w / steps:.1f} KiB raw x {wscale:.3f} = {write / 1e6:.2f} MB")
+    print(f"# traffic = {tot} bytes per step vs {alg_bytes} algorithmic ({tot / alg_bytes:.3f}x)")
+    with open(out_json, "w") as fh:
+        json.dump({"source": "ggnpu_amd/profile_summary.py traffic over the FETCH_SIZE / WRITE_SIZE runs",
+                   "traffic_bytes_per_step": tot, "algorithmic_bytes_per_step": alg_bytes,
+                   "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4),
+                   "fetch_kib_per_step_raw": round(f / steps, 1), "write_kib_per_step_raw": round(w / steps, 1),
+                   "steps_profiled": steps}, fh)
+        fh.write("\n")
+
+
 if __name__ == "__main__":
-    mode, db = sys.argv[1], sys.argv[2]
-    pat = sys.argv[3] if len(sys.argv) > 3 else "%"
-    {"stats": stats, "pmc": pmc}[mode](db, pat)
+    mode = sys.argv[1]
+    if mode == "traffic":
+        traffic(*sys.argv[2:])
+    else:
+        db = sys.argv[2]
+        pat = sys.argv[3] if len(sys.argv) > 3 else "%"
+        {"stats": stats, "pmc": pmc}[mode](db, pat)

@@ -271,6 +271,14 @@ int ggq_mul_mat_batch_dev(ggq_ctx* ctx, const ggq_gemv_desc* descs, int n, void*
 #define GGQ_MAX_BATCH_ROWS 64
 int ggq_mul_mat_batch_rows_dev(ggq_ctx* ctx, const ggq_gemv_desc* descs, int n, int M, void* stream);
 
+/* ggq_mul_mat_batch_rows_dev with an activation treatment (act_mode as for
+ * ggq_mul_mat_dev): same result as one ggq_mul_mat_dev call per entry with
+ * that act_mode.  GGQ_ACT_Q8_ROW with M <= 8 quantizes each entry's rows as
+ * amd_xdna.cpp:598-603 and runs all entries in one int8 launch where the
+ * shapes allow.  No reference counterpart as a batched call (the reference
+ * issues one mul_mat_q per weight, main.cpp:3256-3267). */
+int ggq_mul_mat_batch_act_dev(ggq_ctx* ctx, const ggq_gemv_desc* descs, int n, int M, int act_mode, void* stream);
+
 /* Bit-exact fp32 dequant of n_blocks consecutive blocks, equal to the
  * reference's dequant_*_block functions (kquant.h:133-202, q8_0.cpp:19-25,
  * iq4_nl.cpp:24-31, iq4_xs.cpp:21-38). */

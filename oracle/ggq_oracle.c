@@ -21,6 +21,10 @@
  *   orc_mul_mat_f64       vs the compiled CpuRefBackend::mul_mat_q (Q4_K, Q6_K)
  *                         and vs numpy float64 matmul of the dequantized rows
  *   orc_moe_ffn_f64       vs a per-token numpy loop over orc_mul_mat_f64 rows
+ *   orc_mul_mat_rowdot_f32  bit-identical to the reference decoders + the same
+ *                         loop (oracle/_ref ref_rowdot_mul_mat) and to a numpy
+ *                         float32 sequential cumsum over the dequantized row
+ *                         (a per-block partial sum would differ in the bits)
  */
 #include "ggq_oracle.h"
 
@@ -401,6 +405,29 @@ int orc_mul_mat_cpuref_f32(uint32_t t, const uint8_t* W, int64_t N, int64_t K,
                 C[(size_t)m * ldc + n] += sum;
             }
         }
+    return 0;
+}
+
+/* ---- dequantize-row + fp32 dot: main.cpp:317-326 and :1380-1386 -----------
+ * The CLI's loop for weights no backend takes: the whole row is decoded
+ * (dequant_tensor_row, main.cpp:36-...), then one running fp32 sum over k. */
+int orc_mul_mat_rowdot_f32(uint32_t t, const uint8_t* W, int64_t N, int64_t K,
+                           const float* A, int lda, int M, float* C, int ldc) {
+    const int be = orc_block_elems(t), bb = orc_block_bytes(t);
+    if (!be || t == ORC_F32 || K % be) return 3;
+    const int64_t nb = K / be;
+    float* row = (float*)malloc((size_t)K * sizeof(float));
+    if (!row) return 2;
+    for (int64_t n = 0; n < N; n++) {
+        orc_dequant_blocks(t, W + n * nb * bb, nb, row);
+        for (int m = 0; m < M; m++) {
+            const float* am = A + (size_t)m * lda;
+            float acc = 0.0f;
+            for (int64_t k = 0; k < K; k++) acc += am[k] * row[k];
+            C[(size_t)m * ldc + n] = acc;
+        }
+    }
+    free(row);
     return 0;
 }
 

@@ -81,6 +81,9 @@ int    orc_mul_mat_cpuref_f32(uint32_t type, const uint8_t* W, int64_t N, int64_
 /* RMSNorm, restating CpuRefBackend::rms_norm (cpu_ref.cpp:139-156) in its
  * fp32 order: sum of squares in index order, / n, + eps, 1/sqrt, then
  * out[i] = x[i] * inv * w[i] (w NULL = 1). */
+/* main.cpp:317-326 dequant-row + fp32 dot (weights no backend takes) */
+int    orc_mul_mat_rowdot_f32(uint32_t type, const uint8_t* W, int64_t N, int64_t K,
+                              const float* A, int lda, int M, float* C, int ldc);
 void   orc_rms_norm(const float* x, int n, const float* w, float eps, float* out);
 /* silu, restating CpuRefBackend::silu (cpu_ref.cpp:200-209):
  * out[i] = x[i] / (1 + expf(-x[i])) in fp32. */

@@ -29,6 +29,7 @@ _ORC_SIGS = {
     "orc_block_dot": (_I, [_U32, _P, _I64, _I64, _P, _I, _P]),
     "orc_mul_mat_f64": (_I, [_U32, _P, _I64, _I64, _P, _I, _I, _I, _P, _I]),
     "orc_mul_mat_cpuref_f32": (_I, [_U32, _P, _I64, _I64, _P, _I, _I, _P, _I]),
+    "orc_mul_mat_rowdot_f32": (_I, [_U32, _P, _I64, _I64, _P, _I, _I, _P, _I]),
     "orc_moe_ffn_f64": (_I, [_P, _P, _I, _I, _I, _I, _I, _U32, _P, _U32, _P, _U32, _P,
                              _P, _P, _P, _P, _P, _P, _P]),
     "orc_rms_norm": (None, [_P, _I, _P, ctypes.c_float, _P]),
@@ -45,6 +46,7 @@ _REF_SIGS = {
     "ref_blck_size": (ctypes.c_uint64, [_U32]),
     "ref_decode_for_npu": (_I, [_U32, _P, ctypes.c_uint64, _I64, _I64, _P, _P]),
     "ref_cpuref_mul_mat": (_I, [_U32, _P, _I, _I, _P, _I, _P]),
+    "ref_rowdot_mul_mat": (_I, [_U32, _P, _I, _I, _P, _I, _P]),
     "ref_rms_norm": (_I, [_P, _I, _P, ctypes.c_float, _P]),
     "ref_silu": (_I, [_P, _I, _P]),
     "ref_flash_attn": (_I, [_P, _P, _P, _I, _I, _I64, _I64, _P]),
@@ -149,6 +151,14 @@ def mul_mat_cpuref_f32(t, W, N, K, A):
     M = A.shape[0]
     C = np.empty((M, N), dtype=np.float32)
     assert lib().orc_mul_mat_cpuref_f32(int(t), _ptr(W), N, K, _ptr(A), K, M, _ptr(C), N) == 0
+    return C
+
+
+def mul_mat_rowdot_f32(t, W, N, K, A):
+    A = np.ascontiguousarray(A, dtype=np.float32)
+    M = A.shape[0]
+    C = np.empty((M, N), dtype=np.float32)
+    assert lib().orc_mul_mat_rowdot_f32(int(t), _ptr(W), N, K, _ptr(A), K, M, _ptr(C), N) == 0
     return C
 
 

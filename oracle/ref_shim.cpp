@@ -70,6 +70,28 @@ int ref_cpuref_mul_mat(uint32_t type, const void* W, int N, int K, const float* 
     return static_cast<int>(be->mul_mat_q(p));
 }
 
+// The dequantize-row + fp32 dot loop the CLI runs where no backend takes the
+// weight type (main.cpp:317-326, :1380-1386): whole row through the
+// reference's block decoders, then one running fp32 sum over k per row of A.
+int ref_rowdot_mul_mat(uint32_t type, const uint8_t* W, int N, int K, const float* A, int M, float* C) {
+    const size_t be = ggml_blck_size(static_cast<GgmlType>(type));
+    const size_t bs = ggml_type_size(static_cast<GgmlType>(type));
+    if (be == 0 || K % be) return 3;
+    const size_t nb = K / be;
+    std::vector<float> row(static_cast<size_t>(K));
+    for (int n = 0; n < N; n++) {
+        int st = ref_dequant_blocks(type, W + static_cast<size_t>(n) * nb * bs, static_cast<int64_t>(nb), row.data());
+        if (st) return st;
+        for (int m = 0; m < M; m++) {
+            const float* a = A + static_cast<size_t>(m) * K;
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) acc += a[k] * row[k];
+            C[static_cast<size_t>(m) * N + n] = acc;
+        }
+    }
+    return 0;
+}
+
 // CpuRefBackend::rms_norm (cpu_ref.cpp:139-156) and silu (:200-209).
 int ref_rms_norm(const float* x, int n, const float* w, float eps, float* out) {
     auto be = create_cpu_ref_backend();

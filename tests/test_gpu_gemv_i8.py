@@ -129,3 +129,32 @@ def test_i8_gemv_k_splits(ctx, orc, kw, monkeypatch):
         for mode in (0, 1):
             got = run_mm(ctx, t, raw, N, K, A, mode)
             assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, mode)) < TOL, (kw, t, mode)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_batch_act_q8_row(ctx, orc, M):
+    """ggq_mul_mat_batch_act_dev in GGQ_ACT_Q8_ROW: each entry meets the bar
+    against the oracle's per-row int8 treatment, whether the level runs as
+    one int8 launch or (a Q6_K entry above 4 rows, K not a multiple of 256)
+    entry by entry; and it equals ggq_mul_mat_batch_rows_dev in GGQ_ACT_F32."""
+    import torch
+    specs = [(12, 2048, 2048), (14, 512, 2048), (20, 300, 1024), (8, 96, 96)]
+    rng = np.random.default_rng(M)
+    keep, descs, ref = [], (gl.GemvDesc * len(specs))(), []
+    for i, (t, N, K) in enumerate(specs):
+        raw = weights(t, N, K, seed=70 + i)
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        dW, dA = dev(raw), dev(A)
+        dC = torch.full((M, N), float("nan"), device="cuda")
+        keep += [dW, dA, dC]
+        descs[i].W, descs[i].type, descs[i].N, descs[i].K = dW.data_ptr(), t, N, K
+        descs[i].A, descs[i].C = dA.data_ptr(), dC.data_ptr()
+        ref.append((t, raw, N, K, A, dC))
+    for mode in (1, 0):
+        ctx.check(ctx.lib.ggq_mul_mat_batch_act_dev(ctx.h, descs, len(specs), M, mode, stream_handle()), "batch act")
+        for t, raw, N, K, A, dC in ref:
+            assert orc.rel_l2(host(dC), orc.mul_mat_f64(t, raw, N, K, A, mode)) < TOL, (t, N, K, M, mode)
+    f32 = [host(r[5]).copy() for r in ref]
+    ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, descs, len(specs), M, stream_handle()), "batch rows")
+    for r, y in zip(ref, f32):
+        assert np.array_equal(host(r[5]).view(np.uint32), y.view(np.uint32))

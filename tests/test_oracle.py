@@ -103,6 +103,35 @@ def test_f64_oracle_vs_reference_cpuref(orc, golden, name):
     assert np.array_equal(got32, C)
 
 
+@pytest.mark.parametrize("name", list(TYPES))
+def test_rowdot_oracle_pinned(orc, golden, name):
+    """orc_mul_mat_rowdot_f32 (main.cpp:317-326): a running fp32 sum over the
+    dequantized row -- bitwise a numpy float32 sequential cumsum, bitwise the
+    reference decoders + loop where oracle/_ref is built, and not equal to a
+    per-block partial-sum order."""
+    t = TYPES[name]
+    raw = golden[f"{name}_raw"]
+    be, bb = orc.block_elems(t), orc.block_bytes(t)
+    K = 512 if be == 256 else 128
+    N = raw.size // bb // (K // be)
+    W = np.ascontiguousarray(raw[: N * (K // be) * bb])
+    A = np.random.default_rng(t).standard_normal((3, K)).astype(np.float32)
+    got = orc.mul_mat_rowdot_f32(t, W, N, K, A)
+    rows = orc.dequant(t, W).reshape(N, K)
+    exp = np.cumsum(A[:, None, :] * rows[None, :, :], axis=2, dtype=np.float32)[:, :, -1]
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+    blockwise = np.zeros((3, N), np.float32)
+    for b in range(K // be):
+        sl = slice(b * be, (b + 1) * be)
+        blockwise += np.cumsum(A[:, None, sl] * rows[None, :, sl], axis=2, dtype=np.float32)[:, :, -1]
+    assert not np.array_equal(got, blockwise)
+    ref = orc.ref_lib()
+    if ref is not None:
+        out = np.empty((3, N), np.float32)
+        assert ref.ref_rowdot_mul_mat(t, W.ctypes.data, N, K, A.ctypes.data, 3, out.ctypes.data) == 0
+        assert np.array_equal(got.view(np.uint32), out.view(np.uint32))
+
+
 # ------------------------------------------------------------ closed forms
 def test_iq4_nl_closed_form(orc, golden):
     raw = golden["IQ4_NL_raw"].reshape(-1, 18)
