@@ -361,6 +361,7 @@ struct GemvArgs {
     const int* x_idx;
     int lpr_log2;
     int x_vec4;    // X rows are 16-byte aligned (float4 loads)
+    uint32_t p_div; // ceil(2^32 / P), P = K / 32: s / P == umulhi(s, p_div) for s < 8 P
     int prefetch;  // fetch the next row-iteration while computing the current one
     // Fused neighbours of the matmul (all off when zero / null):
     const float* X2;       // elementwise product input: the activation is X * X2 (X2 like X)
@@ -622,9 +623,10 @@ __device__ __forceinline__ void gemv_rms_norm(const GemvArgs& a, float (&xr)[PPT
 // bz, bz + gz, ... of its activation rows.
 // F: compiled with the fused options (RMSNorm, product input, silu,
 // residual); the plain instantiations carry none of their code.
-template <int T, int MB, int PPT, int U, bool F>
+template <int T, int MB, int PPT, int U, bool F, bool XL = false>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
                                           float (&red)[2][4][U * MB]) {
+    static_assert(!XL || (MB == 1 && !F), "LDS-staged activations: one plain activation row per pass");
     typedef typename Piece<T>::Raw Raw;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lpr_log2 = a.lpr_log2;
@@ -650,6 +652,34 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
         gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
         float xr[PPT][MB][32];
         float xs[PPT][MB][2];
+        if constexpr (XL) {
+            // The activation row is read from memory once per workgroup and
+            // staged in LDS as float4 slots s = 8 p' + ... transposed to
+            // s = j P + p (j = 4 r + quad of run r of piece p): the stores
+            // and each lane's reads of its pieces are consecutive 16-byte
+            // words across lanes (no bank conflicts).
+            extern __shared__ float4 xl[];
+            if (mc != bz * MB) __syncthreads();  // the previous chunk's row is read by every wavefront
+            const float* xp = a.X + (int64_t)(m0 + mc) * a.ldx;
+            for (int sl = tid; sl < 8 * P; sl += 256) {
+                const int j = (int)__umulhi((uint32_t)sl, a.p_div);
+                const int p = sl - j * P;
+                xl[sl] = *(const float4*)(xp + Piece<T>::run_k(p, j >> 2) + 4 * (j & 3));
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < PPT; i++) {
+                const int p = lp + i * lpr;
+                const int pc = p < P ? p : 0;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float4 v = xl[j * P + pc];
+                    const bool ok = p < P;
+                    xr[i][0][4 * j + 0] = ok ? v.x : 0.0f; xr[i][0][4 * j + 1] = ok ? v.y : 0.0f;
+                    xr[i][0][4 * j + 2] = ok ? v.z : 0.0f; xr[i][0][4 * j + 3] = ok ? v.w : 0.0f;
+                }
+            }
+        } else
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = lp + i * lpr;
@@ -742,7 +772,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
     }
 }
 
-template <int T, int MB, int PPT, int U, bool F = false>
+template <int T, int MB, int PPT, int U, bool F = false, bool XL = false>
 // Two rows per pass: held to 3 wavefronts per SIMD (168 VGPRs; Q4_K spills
 // a few registers), where the natural allocation gave 2.  That variant is
 // the MoE default (each expert sees ~2 tokens: the decoded codes are shared).
@@ -766,7 +796,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MB == 2 ? 3
             }
         }
     }
-    gemv_body<T, MB, PPT, U, F>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
+    gemv_body<T, MB, PPT, U, F, XL>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
 }
 
 // Several independent GEMV problems (any mix of formats, same pieces-per-
@@ -784,7 +814,7 @@ struct MultiArgs {
 // KQ: compiled for Q4_K and Q6_K only (the Q4_K_M decode levels), so the
 // register budget is not set by the other formats' decoders (Q5_K's needs
 // one more wavefront's worth of VGPRs than Q4_K's).
-template <int MB, int PPT, int U, bool F = false, bool KQ = false>
+template <int MB, int PPT, int U, bool F = false, bool KQ = false, bool XL = false>
 __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     __shared__ float red[2][4][U * MB];
     int q = 0;
@@ -792,17 +822,17 @@ __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
     const int bz = blockIdx.z, gz = gridDim.z;
     if constexpr (KQ) {
-        if (ma.type[q] == T_Q4_K) gemv_body<T_Q4_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red);
-        else gemv_body<T_Q6_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red);
+        if (ma.type[q] == T_Q4_K) gemv_body<T_Q4_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red);
+        else gemv_body<T_Q6_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red);
         return;
     }
     switch (ma.type[q]) {
-    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U, F>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
     default: break;
     }
 }
@@ -1198,6 +1228,19 @@ static int gemv_prefetch() {
     return v;
 }
 
+static bool fused(const GemvProblem& p) { return p.rms || p.X2 || p.R || p.silu; }
+
+// Single-row launches stage the activation row in LDS once per workgroup
+// (K <= 8192, 16-byte aligned rows) instead of every wavefront reading it
+// from memory; GGQ_GEMV_XLDS=0 selects the per-wavefront loads.
+static bool gemv_xlds(const GemvProblem& p, const GemvArgs& a) {
+    static int v = [] {
+        const char* e = getenv("GGQ_GEMV_XLDS");
+        return e && *e ? atoi(e) : 1;
+    }();
+    return v != 0 && p.M <= 1 && !p.grp_off && !p.x_idx && !fused(p) && a.x_vec4 && a.lpr_log2 < 8 && p.K >= 64 && p.K <= 8192 && p.K % 32 == 0;
+}
+
 static int gemv_max_lpr() {
     static int v = [] {
         const char* e = getenv("GGQ_GEMV_MAXLPR");
@@ -1224,7 +1267,6 @@ static int moe_mb() { return env_int("GGQ_MOE_MB", 2); }
 static int moe_gx() { return env_int("GGQ_MOE_GX", 0); }
 static int moe_rounds() { const int v = env_int("GGQ_MOE_ROUNDS", 4); return v < 1 ? 1 : v; }
 
-static bool fused(const GemvProblem& p) { return p.rms || p.X2 || p.R || p.silu; }
 
 // Matrix-core GEMV (gemv_mfma_kernel) for M >= 2 plain fp32-activation
 // problems: S = 2^sl2 piece slots per group of 4 rows (16, 32 or 64), PPT
@@ -1288,6 +1330,7 @@ static GemvPlan plan_gemv(const GemvProblem& p) {
     a.x_idx = p.x_idx;
     a.lpr_log2 = lpr_log2;
     a.x_vec4 = ((uintptr_t)p.X % 16 == 0) && (p.ldx % 4 == 0) && ((uintptr_t)p.X2 % 16 == 0);
+    a.p_div = (uint32_t)((0x100000000ull + P - 1) / P);
     a.prefetch = gemv_prefetch();
     a.X2 = p.X2;
     a.silu = p.silu;
@@ -1364,6 +1407,21 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         gemv_kernel<T, 1, PPT_, 1, true><<<dim3(gx, 1, gz), 256, 0, s>>>(a);                     \
     } while (0)
     const int u = gemv_rows_per_iter();
+#define GO_X(PPT_)                                                                               \
+    do {                                                                                         \
+        const size_t lds = (size_t)p.K * sizeof(float);                                          \
+        int gx = resident_blocks(gemv_kernel<T, 1, PPT_, 1, false, true>, lds);                  \
+        gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
+        gemv_kernel<T, 1, PPT_, 1, false, true><<<dim3(gx, 1, 1), 256, lds, s>>>(a);             \
+    } while (0)
+    if (groups == 1 && u == 1 && gemv_xlds(p, a)) {
+        if (ppt == 1) GO_X(1);
+        else if (ppt == 2) GO_X(2);
+        else if (ppt <= 4) GO_X(4);
+        else return hipErrorInvalidValue;
+#undef GO_X
+        return hipGetLastError();
+    }
     if (fused(p)) {  // one activation row per pass, the fused options compiled in
         if (groups > 1) return hipErrorInvalidValue;
         if (ppt == 1) GO_F(1);
@@ -1470,17 +1528,26 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
             return hipGetLastError();
         }
     }
-    bool any_fused = false, kq = true;
+    bool any_fused = false, kq = true, xl = true;
+    int kmax = 0;
     for (int i = 0; i < n; i++) {
         any_fused = any_fused || fused(ps[i]);
         kq = kq && (ps[i].type == T_Q4_K || ps[i].type == T_Q6_K);
+        xl = xl && gemv_xlds(ps[i], plans[i].a);
+        kmax = ps[i].K > kmax ? ps[i].K : kmax;
     }
     const int u = any_fused ? 1 : gemv_rows_per_iter();
     const int mb = any_fused ? 1 : multi_mb(ppt, M);
     const int gz = (M + mb - 1) / mb;
     kq = kq && ppt == 1 && mb == 1 && u == 1;  // the variants compiled with KQ
+    xl = xl && !any_fused && mb == 1 && u == 1 && M == 1;
+    const size_t lds = xl ? (size_t)kmax * sizeof(float) : 0;
     int target;
-    if (any_fused) {
+    if (xl) {
+        target = kq ? resident_blocks(gemv_multi_kernel<1, 1, 1, false, true, true>, lds)
+                    : ppt == 1 ? resident_blocks(gemv_multi_kernel<1, 1, 1, false, false, true>, lds)
+                               : resident_blocks(gemv_multi_kernel<1, 2, 1, false, false, true>, lds);
+    } else if (any_fused) {
         target = ppt == 1 ? (kq ? multi_resident<1, 1, 1, true, true>() : multi_resident<1, 1, 1, true>())
                           : multi_resident<1, 2, 1, true>();
     } else if (kq) {
@@ -1506,7 +1573,11 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     ma.begin[n] = b;
     ma.n = n;
     const dim3 grid(b, 1, gz);
-    if (any_fused) {
+    if (xl) {
+        if (kq) gemv_multi_kernel<1, 1, 1, false, true, true><<<grid, 256, lds, s>>>(ma);
+        else if (ppt == 1) gemv_multi_kernel<1, 1, 1, false, false, true><<<grid, 256, lds, s>>>(ma);
+        else gemv_multi_kernel<1, 2, 1, false, false, true><<<grid, 256, lds, s>>>(ma);
+    } else if (any_fused) {
         if (kq) gemv_multi_kernel<1, 1, 1, true, true><<<grid, 256, 0, s>>>(ma);
         else if (ppt == 1) gemv_multi_kernel<1, 1, 1, true><<<grid, 256, 0, s>>>(ma);
         else gemv_multi_kernel<1, 2, 1, true><<<grid, 256, 0, s>>>(ma);
