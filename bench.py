@@ -553,10 +553,11 @@ def bench_config4(torch, ctx, stream, steps=10):
     return res
 
 
-def bench_config5(torch, ctx, stream, steps=20, T=64):
+def bench_config5(torch, ctx, stream, steps=20, T=64, act_mode=0):
     """one qwen35moe-A3B MoE FFN layer, 64 tokens (T), top-8 of
     256 experts (FFN 512, Q4_K gate/up, Q6_K down) + 1 shared expert, as one
-    expert-grouped ggq_moe_ffn_dev call."""
+    expert-grouped ggq_moe_ffn_act_dev call (act_mode 0: fp32 activations,
+    1: per-row int8 activations, the grouped int8 GEMM)."""
     H, F, E, k = 2048, 512, 256, 8
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
@@ -580,14 +581,15 @@ def bench_config5(torch, ctx, stream, steps=20, T=64):
     p.shared_w, p.out, p.sel_experts = sw.data_ptr(), out.data_ptr(), sel.data_ptr()
 
     def run():
-        ctx.check(ctx.lib.ggq_moe_ffn_dev(ctx.h, ctypes.byref(p), stream), "moe_ffn")
+        ctx.check(ctx.lib.ggq_moe_ffn_act_dev(ctx.h, ctypes.byref(p), act_mode, stream), "moe_ffn")
 
     sec = time_steps(torch, run, steps, 2)
     hit = int(torch.unique(sel).numel())
     per_expert = 2 * gl.row_bytes(Q4K, H) * F + gl.row_bytes(Q6K, F) * H
     b = (hit + 1) * per_expert + 4 * T * H * 2 + 4 * T * E
+    act = "fp32" if act_mode == 0 else "per-row int8 (GGQ_ACT_Q8_ROW)"
     return {"workload": f"qwen35moe-A3B MoE FFN layer: {T} tokens, top-8 of 256 experts (FFN 512) + shared, "
-                        "Q4_K gate/up, Q6_K down, one grouped call", "experts_hit": hit,
+                        f"Q4_K gate/up, Q6_K down, {act} activations, one grouped call", "experts_hit": hit,
             "bytes": b, "us": round(sec * 1e6, 1), "GBps": round(b / sec / 1e9, 1),
             "frac_hbm_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
 
@@ -819,6 +821,8 @@ def main():
                     help="run one workload only and print its result (profiling aid)")
     ap.add_argument("--moe-tokens", type=int, default=64,
                     help="tokens of the MoE layer for --only moe (the bench line uses 64)")
+    ap.add_argument("--moe-act", type=int, default=0, choices=[0, 1],
+                    help="activation treatment of --only moe: 0 fp32, 1 per-row int8")
     ap.add_argument("--per-matmul", action="store_true",
                     help="one launch per matmul instead of one per dependency level")
     args = ap.parse_args()
@@ -855,7 +859,7 @@ def main():
     if args.only in ("config1", "config1_q8", "prefill", "config4", "moe", "logits", "fused", "attention", "host"):
         res = {"config1": bench_config1, "config1_q8": lambda t, c, st: bench_config1(t, c, st, act_mode=1),
                "prefill": bench_prefill, "config4": bench_config4,
-               "moe": lambda *a: bench_config5(*a, T=args.moe_tokens), "logits": bench_logits, "fused": bench_decode_fused,
+               "moe": lambda *a: bench_config5(*a, T=args.moe_tokens, act_mode=args.moe_act), "logits": bench_logits, "fused": bench_decode_fused,
                "attention": bench_attention, "host": bench_host_api}[args.only](
                    torch, ctx, stream)
         print(json.dumps({"only": args.only, **res}), flush=True)
@@ -911,6 +915,8 @@ def main():
                 ("config3_prefill", bench_prefill, cpu_baseline_config2),
                 ("config4_iq4_q5k", bench_config4, cpu_baseline_config3),
                 ("config5_moe", bench_config5, cpu_baseline_config4),
+                ("config5_moe_q8_row", lambda t, c, st: bench_config5(t, c, st, act_mode=1), None),
+                ("config5_moe_512_q8_row", lambda t, c, st: bench_config5(t, c, st, steps=10, T=512, act_mode=1), None),
                 ("logits_argmax", bench_logits, None), ("attention_decode", bench_attention, None),
                 ("host_api_decode", bench_host_api, None), ("decode_fused", bench_decode_fused, None)):
             try:

@@ -754,6 +754,106 @@ int ggq_block_dot_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64
     GGQ_END(c)
 }
 
+// MoE layer with per-row int8 activations (GGQ_ACT_Q8_ROW): route, group,
+// quantize the token rows once, one grouped int8 GEMM for every expert's
+// gate and up (and the shared expert's, as group E), SwiGLU fused into the
+// row quantization of the pair rows, one grouped GEMM for down, combine.
+static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
+    const int T = p->T, H = p->H, F = p->F, E = p->E, k = p->top_k;
+    const bool shared = p->gate_shexp != nullptr;
+    const size_t nk = (size_t)T * k, ts = shared ? (size_t)T : 0, rows = nk + ts;
+    const int max_tiles = (int)((rows + ggq::kMoeTileRows - 1) / ggq::kMoeTileRows) + E + 1;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off = align256(off + bytes); return o; };
+    const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 2)),
+                 o_tok = take(4 * rows), o_pos = take(4 * nk), o_qx = take((size_t)T * H), o_sx = take(4 * (size_t)T),
+                 o_g = take(4 * rows * F), o_u = take(4 * rows * F), o_qh = take(rows * F), o_sh = take(4 * rows),
+                 o_d = take(4 * rows * H), o_tl = take(8 * (size_t)max_tiles), o_nt = take(4);
+    int st;
+    if ((st = grow(c, c->dev.ws, off, s, "workspace")) != GGQ_OK) return st;
+    hipError_t e;
+    char* base = (char*)c->dev.ws.ptr;
+    int32_t* sel = (int32_t*)(base + o_sel);
+    float* wsel = (float*)(base + o_w);
+    int32_t* grp = (int32_t*)(base + o_go);
+    int32_t* tok = (int32_t*)(base + o_tok);
+    int32_t* pos = (int32_t*)(base + o_pos);
+    int8_t* qx = (int8_t*)(base + o_qx);
+    float* sx = (float*)(base + o_sx);
+    float *G = (float*)(base + o_g), *U = (float*)(base + o_u), *D = (float*)(base + o_d);
+    int8_t* qh = (int8_t*)(base + o_qh);
+    float* sh = (float*)(base + o_sh);
+    void* tiles = base + o_tl;
+    int32_t* ntiles = (int32_t*)(base + o_nt);
+
+    if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s)) != hipSuccess) return hip_status(c, e, "moe_group");
+    if ((e = ggq::launch_moe_tiles(grp, tok, E, (int)ts, (int2*)tiles, ntiles, s)) != hipSuccess)
+        return hip_status(c, e, "moe_tiles");
+    if ((e = ggq::launch_quant_act(p->x, H, T, H, GGQ_ACT_Q8_ROW, qx, sx, nullptr, s)) != hipSuccess)
+        return hip_status(c, e, "quant x");
+    ggq::MoeGemm g{};
+    g.E = E; g.grp = grp; g.tiles = tiles; g.n_tiles = ntiles; g.max_tiles = max_tiles;
+    // gate and up: K = H, token rows gathered through tok; paired when the
+    // types match, else two launches.
+    g.K = H; g.QA = qx; g.sa = sx; g.x_idx = tok; g.ldc = F;
+    g.w_stride = (int64_t)F * ggq::row_bytes(p->gate_type, H);
+    if (p->up_type == p->gate_type) {
+        g.W = p->gate_exps; g.W2 = p->up_exps; g.Wsh = p->gate_shexp; g.W2sh = p->up_shexp;
+        g.N = 2 * F; g.n1 = F; g.C = G; g.C2 = U;
+        if ((e = ggq::launch_moe_gemm(p->gate_type, g, s)) != hipSuccess) return hip_status(c, e, "moe gate+up");
+    } else {
+        g.W = p->gate_exps; g.W2 = nullptr; g.Wsh = p->gate_shexp; g.W2sh = nullptr;
+        g.N = F; g.n1 = F; g.C = G; g.C2 = nullptr;
+        if ((e = ggq::launch_moe_gemm(p->gate_type, g, s)) != hipSuccess) return hip_status(c, e, "moe gate");
+        g.W = p->up_exps; g.Wsh = p->up_shexp; g.C = U;
+        g.w_stride = (int64_t)F * ggq::row_bytes(p->up_type, H);
+        if ((e = ggq::launch_moe_gemm(p->up_type, g, s)) != hipSuccess) return hip_status(c, e, "moe up");
+    }
+    // SwiGLU of every pair row (routed and shared) and its int8 row codes.
+    if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s)) != hipSuccess)
+        return hip_status(c, e, "swiglu quant");
+    // down: K = F, the pair rows themselves.
+    g.K = F; g.QA = qh; g.sa = sh; g.x_idx = nullptr; g.ldc = H;
+    g.W = p->down_exps; g.W2 = nullptr; g.Wsh = p->down_shexp; g.W2sh = nullptr;
+    g.w_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
+    g.N = H; g.n1 = H; g.C = D; g.C2 = nullptr;
+    if ((e = ggq::launch_moe_gemm(p->down_type, g, s)) != hipSuccess) return hip_status(c, e, "moe down");
+    if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, shared ? D + nk * H : nullptr, p->shared_w, p->out, s)) !=
+        hipSuccess)
+        return hip_status(c, e, "moe combine");
+    if (p->sel_experts && (e = hipMemcpyAsync(p->sel_experts, sel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_status(c, e, "copy selection");
+    if (p->sel_weights && (e = hipMemcpyAsync(p->sel_weights, wsel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_status(c, e, "copy weights");
+    return set_status(c, GGQ_OK);
+}
+
+int ggq_moe_ffn_act_dev(ggq_ctx* c, const ggq_moe_params* p, int act_mode, void* stream) {
+    if (act_mode == GGQ_ACT_F32) return ggq_moe_ffn_dev(c, p, stream);
+    GGQ_GUARD(c)
+    if (act_mode != GGQ_ACT_Q8_ROW) return set_status(c, GGQ_INVALID_PARAM, "act_mode must be F32 or Q8_ROW");
+    if (!p || !p->x || !p->router_logits || !p->gate_exps || !p->up_exps || !p->down_exps || !p->out)
+        return set_status(c, GGQ_INVALID_PARAM, "null pointer");
+    const int T = p->T, H = p->H, F = p->F, E = p->E, k = p->top_k;
+    if (T < 0 || H <= 0 || F <= 0 || E <= 0 || E > 1023 || k <= 0 || k > 64 || k > E || (int64_t)T * k > 65536)
+        return set_status(c, GGQ_INVALID_PARAM, "bad MoE shape");
+    int st;
+    if ((st = check_matmul_shape(c, p->gate_type, F, H, T, H, F, 0)) != GGQ_OK) return st;
+    if ((st = check_matmul_shape(c, p->up_type, F, H, T, H, F, 0)) != GGQ_OK) return st;
+    if ((st = check_matmul_shape(c, p->down_type, H, F, T, F, H, 0)) != GGQ_OK) return st;
+    if (H % 32 || F % 32 || H > 16384 || F > 16384 || H % 4 || F % 4)
+        return set_status(c, GGQ_INVALID_PARAM, "Q8_ROW MoE needs H and F multiples of 32, at most 16384");
+    const bool shared = p->gate_shexp != nullptr;
+    if (shared && (!p->up_shexp || !p->down_shexp)) return set_status(c, GGQ_INVALID_PARAM, "partial shared expert");
+    for (const void* w : {p->gate_exps, p->up_exps, p->down_exps, p->gate_shexp, p->up_shexp, p->down_shexp})
+        if (w && !aligned16(w)) return set_status(c, GGQ_INVALID_PARAM, "weights must be 16-byte aligned");
+    if (((uintptr_t)p->x & 15u)) return set_status(c, GGQ_INVALID_PARAM, "x must be 16-byte aligned");
+    if (T == 0) return set_status(c, GGQ_OK);
+    return moe_ffn_q8(c, p, pick_stream(c, stream));
+    GGQ_END(c)
+}
+
 int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     GGQ_GUARD(c)
     if (!p || !p->x || !p->router_logits || !p->gate_exps || !p->up_exps || !p->down_exps || !p->out)

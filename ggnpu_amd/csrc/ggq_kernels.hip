@@ -2059,6 +2059,304 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmMultiArgs a) {
         }
 }
 
+// ------------------------------------------ expert-grouped int8 GEMM (MoE)
+// Prefill-sized MoE batches (tens of tokens per expert) with per-row int8
+// activations: one launch multiplies every expert's weight matrix by the
+// token rows routed to it.  A tile is (expert e, 32 consecutive pair rows
+// of e's group, 128 weight rows); the tile list over all experts (and the
+// shared expert as group E) is built on the device (moe_tiles_kernel) from
+// the group offsets, so the grid is sized by an upper bound and the
+// workgroups past the list end exit.  Per K-step (128 values) the
+// workgroup gathers its 32 activation rows (token rows through x_idx) and
+// decodes 128 weight rows' codes into LDS once; four wavefronts each take
+// 32 weight rows with v_mfma_i32_32x32x32_i8 per 32-value scale group
+// (Q6_K's 16-value groups: two MFMAs, each with the other half of the lane
+// groups' activation codes zeroed), and the exact per-group epilogue
+// acc += dl * P (- ml * S for the K-quant mins, S from an MFMA against
+// ones).  Weight rows [0, n1) come from W and go to C, rows [n1, N) from W2
+// to C2 (an expert's gate and up in one pass); the shared expert's
+// matrices replace W / W2 for group E.
+struct MoeGemmArgs {
+    const uint8_t* W;
+    const uint8_t* W2;
+    const uint8_t* Wsh;
+    const uint8_t* W2sh;
+    int64_t w_stride;  // bytes per expert matrix
+    int64_t row_bytes;
+    int N, K, n1, E;
+    const int8_t* QA;        // activation codes, rows of K
+    const float* sa;         // activation row scales
+    const int32_t* x_idx;    // pair row -> activation row (null: the pair row itself)
+    const int32_t* grp;      // [E + 2] first pair row of each group (E: shared expert)
+    const int2* tiles;       // (group, first pair row)
+    const int32_t* n_tiles;  // tile count
+    float* C;
+    float* C2;
+    int ldc;
+};
+constexpr int kMoeBM = kMoeTileRows, kMoeBN = 128;
+
+// Weight staging of the grouped GEMM: fetch() issues plain loads of one
+// (row, 32-value group) slot's raw bytes into registers, store() decodes
+// them into LDS codes and scales one K-step later, so the loads of step
+// k+1 are in flight during step k.  Q4_K: the block header and the 32 qs
+// bytes holding the group's nibbles (16-byte aligned loads).  Q6_K
+// (2-byte-aligned 210-byte blocks): aligned dword windows over the group's
+// ql and qh bytes, realigned when stored, plus its two 16-value scales and
+// d.  Other formats stage through BStage.
+template <int T> struct MStage : BStage<T> {
+    __device__ __forceinline__ void store2(int8_t* codes, float* dl, float* ml) const { this->store(codes, dl, ml); }
+};
+template <> struct MStage<T_Q4_K> {
+    uint4 hd, q0, q1;
+    int j;
+    bool ok;
+    __device__ __forceinline__ void fetch(const uint8_t* row, int k, bool v) {
+        const uint8_t* b = row + (k >> 8) * 144;
+        j = (k & 255) >> 5;
+        ok = v;
+        hd = ld16_a(b);
+        q0 = ld16_a(b + 16 + 32 * (j >> 1));
+        q1 = ld16_a(b + 32 + 32 * (j >> 1));
+    }
+    __device__ __forceinline__ void store2(int8_t* codes, float* dl, float* ml) const {
+        const uint32_t sh = 4 * (j & 1);
+        *(uint4*)codes = and4(shr4(q0, sh), 0x0F0F0F0Fu);
+        *(uint4*)(codes + 16) = and4(shr4(q1, sh), 0x0F0F0F0Fu);
+        uint32_t sc, m;
+        kq_scale_min(hd.y, hd.z, hd.w, j, sc, m);
+        *dl = ok ? __fmul_rn(h2f(hd.x & 0xFFFFu), (float)sc) : 0.0f;
+        *ml = ok ? __fmul_rn(h2f(hd.x >> 16), (float)m) : 0.0f;
+    }
+};
+template <> struct MStage<T_Q6_K> {
+    uint32_t ql[9], qh[9], sc, d;
+    uint32_t sel;
+    int qd;
+    bool ok;
+    __device__ __forceinline__ void fetch(const uint8_t* row, int k, bool v) {
+        const uint8_t* b = row + (k >> 8) * 210;
+        const int kk = k & 255, h = kk >> 7;
+        qd = (kk & 127) >> 5;
+        ok = v;
+        // the ql and qh runs start at b + (multiple of 4): dword i of a run
+        // is w[i] (b 4-aligned) or bytes 2..5 of (w[i], w[i+1])
+        sel = ((uint32_t)(uintptr_t)b & 2u) ? 0x05040302u : 0x03020100u;
+        ld_dw<9>(align_down4(b + 64 * h + 32 * (qd & 1)), ql);
+        ld_dw<9>(align_down4(b + 128 + 32 * h), qh);
+        sc = ld_u16(b + 192 + (kk >> 4));
+        d = ld_u16(b + 208);
+    }
+    // writes the scales of both 16-value groups: dl[0], dl[1]
+    __device__ __forceinline__ void store2(int8_t* codes, float* dl, float*) const {
+        uint32_t c[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t l = half_pick(ql[i + 1], ql[i], sel), hh = half_pick(qh[i + 1], qh[i], sel);
+            c[i] = six_to_s8(((l >> (4 * (qd >> 1))) & 0x0F0F0F0Fu) | (((hh >> (2 * qd)) & 0x03030303u) << 4));
+        }
+        *(uint4*)codes = make_uint4(c[0], c[1], c[2], c[3]);
+        *(uint4*)(codes + 16) = make_uint4(c[4], c[5], c[6], c[7]);
+        const float df = h2f(d);
+        dl[0] = ok ? __fmul_rn(df, (float)(int8_t)(sc & 0xFFu)) : 0.0f;
+        dl[1] = ok ? __fmul_rn(df, (float)(int8_t)(sc >> 8)) : 0.0f;
+    }
+};
+
+template <int T>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
+    constexpr bool kMin = T == T_Q4_K || T == T_Q5_K;
+    constexpr bool kQ6 = T == T_Q6_K;
+    constexpr int G = kGemmBK / 32;                // 32-value groups per K-step
+    constexpr int GS = kQ6 ? 2 * G : G;            // scales per row and step
+    __shared__ __attribute__((aligned(16))) int8_t As[2][kMoeBM][kGemmLd];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[2][kMoeBN][kGemmLd];
+    __shared__ __attribute__((aligned(16))) float Bd[2][kMoeBN][GS];
+    __shared__ __attribute__((aligned(16))) float Bm[2][kMoeBN][G];
+
+    const int tile = blockIdx.y;
+    if (tile >= *a.n_tiles) return;
+    const int2 te = a.tiles[tile];
+    const int e = te.x, p0 = te.y, p_end = a.grp[e + 1];
+    const uint8_t* const W1 = e == a.E ? a.Wsh : a.W + (int64_t)e * a.w_stride;
+    const uint8_t* const W2 = e == a.E ? a.W2sh : (a.W2 ? a.W2 + (int64_t)e * a.w_stride : nullptr);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lk = lane >> 5;
+    const int n_tile = blockIdx.x * kMoeBN;
+    const int nsteps = (a.K + kGemmBK - 1) / kGemmBK;
+
+    // Activations: 32 rows x 128 bytes per step, one 16-byte chunk per thread.
+    const int ar = tid >> 3, akc = (tid & 7) * 16;
+    const int pa = p0 + ar;
+    const bool arow_ok = pa < p_end;
+    const int arow = a.x_idx ? a.x_idx[arow_ok ? pa : p0] : (arow_ok ? pa : p0);
+    const int8_t* const aptr = a.QA + (int64_t)arow * a.K + akc;
+    // Weights: 128 rows x 4 groups per step, two (row, group) slots per thread.
+    const uint8_t* bptr[2];
+    bool brow_ok[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int sl = tid + 256 * i, n = n_tile + sl / G;
+        brow_ok[i] = n < a.N;
+        const int nn = brow_ok[i] ? n : 0;
+        bptr[i] = nn < a.n1 ? W1 + (int64_t)nn * a.row_bytes : W2 + (int64_t)(nn - a.n1) * a.row_bytes;
+    }
+
+    uint4 areg;
+    MStage<T> breg[2];
+    auto fetch = [&](int st) {
+        const int k0 = st * kGemmBK;
+        areg = arow_ok && k0 + akc < a.K ? *(const uint4*)(aptr + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int k = k0 + 32 * ((tid + 256 * i) % G);
+            const bool ok = brow_ok[i] && k < a.K;
+            breg[i].fetch(bptr[i], ok ? k : 0, ok);
+        }
+    };
+    auto store = [&](int buf) {
+        *(uint4*)&As[buf][ar][akc] = areg;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int sl = tid + 256 * i, r = sl / G, g = sl % G;
+            if constexpr (kQ6) breg[i].store2(&Bs[buf][r][32 * g], &Bd[buf][r][2 * g], nullptr);
+            else breg[i].store2(&Bs[buf][r][32 * g], &Bd[buf][r][g], &Bm[buf][r][g]);
+        }
+    };
+
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    const v16i zero = {};
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    const int wn = 32 * wave;
+
+    fetch(0);
+    store(0);
+    if (nsteps > 1) fetch(1);
+    __syncthreads();
+    for (int st = 0; st < nsteps; st++) {
+        const int buf = st & 1;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const uint4 av = *(const uint4*)&As[buf][li][32 * g + 16 * lk];
+            const uint4 bv = *(const uint4*)&Bs[buf][wn + li][32 * g + 16 * lk];
+            const v4i A = v4i{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+            const v4i B = v4i{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
+            if constexpr (kQ6) {
+                // lane group lk holds values 16 lk.. of the 32: group 2g + lk
+                const v4i A0 = lk == 0 ? A : v4i{0, 0, 0, 0};
+                const v4i A1 = lk == 1 ? A : v4i{0, 0, 0, 0};
+                const v16i P0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B, zero, 0, 0, 0);
+                const v16i P1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B, zero, 0, 0, 0);
+                const float d0 = Bd[buf][wn + li][2 * g], d1 = Bd[buf][wn + li][2 * g + 1];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    acc[r] = fmaf(d0, (float)P0[r], acc[r]);
+                    acc[r] = fmaf(d1, (float)P1[r], acc[r]);
+                }
+            } else {
+                const v16i P = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, zero, 0, 0, 0);
+                const float dl = Bd[buf][wn + li][g];
+                if constexpr (kMin) {
+                    const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, ones, zero, 0, 0, 0);
+                    const float ml = Bm[buf][wn + li][g];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        acc[r] = fmaf(dl, (float)P[r], acc[r]);
+                        acc[r] = fmaf(-ml, (float)S[r], acc[r]);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[r] = fmaf(dl, (float)P[r], acc[r]);
+                }
+            }
+        }
+        if (st + 1 < nsteps) {
+            store(buf ^ 1);
+            if (st + 2 < nsteps) fetch(st + 2);
+            __syncthreads();
+        }
+    }
+
+    // Lane (li, lk) holds weight row n = n_tile + wn + li and pair rows
+    // p0 + 8 (r >> 2) + 4 lk + (r & 3).
+    const int n = n_tile + wn + li;
+    if (n >= a.N) return;
+    float* const Cb = n < a.n1 ? a.C + n : a.C2 + (n - a.n1);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int p = p0 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (p < p_end) Cb[(int64_t)p * a.ldc] = acc[r] * a.sa[a.x_idx ? a.x_idx[p] : p];
+    }
+}
+
+// The tile list of the grouped GEMM: group e (experts 0..E-1, then the
+// shared expert as group E with T_sh rows after the routed ones) covers
+// ceil(rows / 32) tiles.  One workgroup: a prefix sum over the groups.
+// Also completes the shared group's entries: grp[E + 1] and the token of
+// each shared row (x_idx[grp[E] + t] = t).
+__global__ __launch_bounds__(1024) void moe_tiles_kernel(int32_t* __restrict__ grp, int32_t* __restrict__ x_idx,
+                                                         int E, int T_sh, int2* __restrict__ tiles,
+                                                         int32_t* __restrict__ n_tiles) {
+    __shared__ int cnt[1024 + 1];
+    const int tid = threadIdx.x;
+    const int base = grp[E];  // routed rows end (all pair rows are sorted by expert)
+    if (tid == 0) grp[E + 1] = base + T_sh;
+    for (int t = tid; t < T_sh; t += 1024) x_idx[base + t] = t;
+    const int G = E + 1;
+    int mine = 0;
+    if (tid < G) {
+        const int rows = tid < E ? grp[tid + 1] - grp[tid] : T_sh;
+        mine = (rows + kMoeBM - 1) / kMoeBM;
+    }
+    cnt[tid] = mine;
+    __syncthreads();
+    // inclusive scan (Hillis-Steele over 1024 entries)
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int v = tid >= off ? cnt[tid - off] : 0;
+        __syncthreads();
+        cnt[tid] += v;
+        __syncthreads();
+    }
+    if (tid < G) {
+        const int first = cnt[tid] - mine;
+        const int p0 = tid < E ? grp[tid] : base;
+        for (int i = 0; i < mine; i++) tiles[first + i] = make_int2(tid, p0 + kMoeBM * i);
+    }
+    if (tid == 1023) *n_tiles = cnt[1023];
+}
+
+hipError_t launch_moe_tiles(int32_t* grp, int32_t* x_idx, int E, int T_sh, int2* tiles, int32_t* n_tiles, hipStream_t s) {
+    if (E + 1 > 1024) return hipErrorInvalidValue;
+    moe_tiles_kernel<<<1, 1024, 0, s>>>(grp, x_idx, E, T_sh, tiles, n_tiles);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s) {
+    MoeGemmArgs a;
+    a.W = (const uint8_t*)g.W; a.W2 = (const uint8_t*)g.W2;
+    a.Wsh = (const uint8_t*)g.Wsh; a.W2sh = (const uint8_t*)g.W2sh;
+    a.w_stride = g.w_stride;
+    a.row_bytes = row_bytes(type, g.K);
+    a.N = g.N; a.K = g.K; a.n1 = g.n1 > 0 ? g.n1 : g.N; a.E = g.E;
+    a.QA = g.QA; a.sa = g.sa; a.x_idx = g.x_idx; a.grp = g.grp;
+    a.tiles = (const int2*)g.tiles; a.n_tiles = g.n_tiles;
+    a.C = g.C; a.C2 = g.C2; a.ldc = g.ldc;
+    const dim3 grid((g.N + kMoeBN - 1) / kMoeBN, g.max_tiles);
+    if (g.max_tiles <= 0) return hipSuccess;
+    switch (type) {
+    case T_Q4_K: moe_gemm_kernel<T_Q4_K><<<grid, 256, 0, s>>>(a); break;
+    case T_Q5_K: moe_gemm_kernel<T_Q5_K><<<grid, 256, 0, s>>>(a); break;
+    case T_Q6_K: moe_gemm_kernel<T_Q6_K><<<grid, 256, 0, s>>>(a); break;
+    case T_Q8_0: moe_gemm_kernel<T_Q8_0><<<grid, 256, 0, s>>>(a); break;
+    case T_IQ4_NL: moe_gemm_kernel<T_IQ4_NL><<<grid, 256, 0, s>>>(a); break;
+    case T_IQ4_XS: moe_gemm_kernel<T_IQ4_XS><<<grid, 256, 0, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // C = sa * (slice 0 + slice 1 + ...) for each output tile, with the (m, n)
 // of each register element as in gemm_i8_lds_kernel.  Workgroup (x, y, z)
 // covers tile (x, y) and register elements [4z, 4z + 4) of every thread, so
@@ -2832,10 +3130,12 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restri
     }
 }
 
-// The same stable counting sort for n <= 1024 pairs and E <= 256 experts
-// (decode batches): pair f is thread f, `sel` is read once, and a pair's
-// position is start[e] + (pairs of e in earlier wavefronts, from per-
-// wavefront histograms) + (pairs of e in earlier lanes of its wavefront).
+// The same stable counting sort for E <= 256 experts and any number of
+// pairs, in rounds of 1024 (one pair per thread): a histogram of all pairs
+// gives each expert's start; within a round a pair's position is start[e]
+// + (pairs of e in earlier rounds) + (pairs of e in earlier wavefronts of
+// the round, from per-wavefront histograms) + (pairs of e in earlier lanes
+// of its wavefront).
 constexpr int kGroupFastE = 256;
 __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __restrict__ sel, int n, int E,
                                                                int topk, int32_t* __restrict__ grp_off,
@@ -2843,61 +3143,76 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
                                                                int32_t* __restrict__ pos_of) {
     __shared__ __attribute__((aligned(16))) int32_t s_sel[1024];
     __shared__ int32_t hist[16][kGroupFastE];  // per wavefront; then exclusive prefix over wavefronts
-    __shared__ int32_t start[kGroupFastE];
+    __shared__ int32_t start[kGroupFastE];     // first position of each expert, advanced by each round
     __shared__ int32_t wsum[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int e = tid < n ? expert_id(sel[tid], E) : -1;
-    s_sel[tid] = e;
-    for (int i = tid; i < 16 * kGroupFastE; i += 1024) (&hist[0][0])[i] = 0;
+    // Totals of all pairs, then their exclusive scan (four wavefronts cover
+    // 256 experts).
+    if (tid < kGroupFastE) start[tid] = 0;
     __syncthreads();
-    if (e >= 0) atomicAdd(&hist[wave][e], 1);
-    // Pairs of e in earlier lanes of this wavefront.
-    int rank = 0;
-    const int32_t* ws = s_sel + 64 * wave;
-    for (int g = 0; g < lane; g += 4) {
-        const int4 v = *(const int4*)&ws[g];
-        rank += (v.x == e) + (g + 1 < lane && v.y == e) + (g + 2 < lane && v.z == e) + (g + 3 < lane && v.w == e);
-    }
+    for (int f = tid; f < n; f += 1024) atomicAdd(&start[expert_id(sel[f], E)], 1);
     __syncthreads();
-    // Thread x < E: prefix of expert x over wavefronts, its total, and an
-    // exclusive scan of the totals (four wavefronts cover 256 experts).
     if (tid < kGroupFastE) {
-        int run = 0;
-#pragma unroll
-        for (int w = 0; w < 16; w++) {
-            const int c = hist[w][tid];
-            hist[w][tid] = run;
-            run += c;
-        }
-        int incl = run;
+        const int c = start[tid];
+        int incl = c;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const int o = __shfl_up(incl, off, 64);
             if (lane >= off) incl += o;
         }
         if (lane == 63) wsum[wave] = incl;
-        start[tid] = incl - run;
+        hist[0][tid] = incl - c;  // staged: wsum is not complete yet
     }
     __syncthreads();
     if (tid < kGroupFastE) {
         int before = 0;
         for (int w = 0; w < wave; w++) before += wsum[w];
-        start[tid] += before;
+        start[tid] = hist[0][tid] + before;
         if (tid < E) grp_off[tid] = start[tid];
         if (tid == 0) grp_off[E] = n;
     }
     __syncthreads();
-    if (e >= 0) {
-        const int pos = start[e] + hist[wave][e] + rank;
-        tok_idx[pos] = tid / topk;
-        pos_of[tid] = pos;
+    for (int r0 = 0; r0 < n; r0 += 1024) {
+        const int f = r0 + tid;
+        const int e = f < n ? expert_id(sel[f], E) : -1;
+        s_sel[tid] = e;
+        for (int i = tid; i < 16 * kGroupFastE; i += 1024) (&hist[0][0])[i] = 0;
+        __syncthreads();
+        if (e >= 0) atomicAdd(&hist[wave][e], 1);
+        // Pairs of e in earlier lanes of this wavefront.
+        int rank = 0;
+        const int32_t* ws = s_sel + 64 * wave;
+        for (int g = 0; g < lane; g += 4) {
+            const int4 v = *(const int4*)&ws[g];
+            rank += (v.x == e) + (g + 1 < lane && v.y == e) + (g + 2 < lane && v.z == e) + (g + 3 < lane && v.w == e);
+        }
+        __syncthreads();
+        // Thread x < 256: prefix of expert x over the round's wavefronts.
+        int total = 0;
+        if (tid < kGroupFastE) {
+#pragma unroll
+            for (int w = 0; w < 16; w++) {
+                const int c = hist[w][tid];
+                hist[w][tid] = total;
+                total += c;
+            }
+        }
+        __syncthreads();
+        if (e >= 0) {
+            const int pos = start[e] + hist[wave][e] + rank;
+            tok_idx[pos] = f / topk;
+            pos_of[f] = pos;
+        }
+        __syncthreads();
+        if (tid < kGroupFastE) start[tid] += total;
+        __syncthreads();
     }
 }
 
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s) {
     if (E > 1024) return hipErrorInvalidValue;
-    if (T * topk <= 1024 && E <= kGroupFastE) {
+    if (E <= kGroupFastE) {
         moe_group_small_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);
         return hipGetLastError();
     }

@@ -122,6 +122,30 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t
                             float* wsel, hipStream_t s);
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s);
+// Expert-grouped int8 GEMM over a device-built tile list (see
+// moe_gemm_kernel): C[p] = sa[row(p)] * codes(p) . W_e^T for every pair row
+// p of group e; rows [n1, N) of the output come from W2 into C2.
+struct MoeGemm {
+    const void* W;
+    const void* W2;   // paired matrix (rows [n1, N)) or null
+    const void* Wsh;  // shared expert (group E) matrices
+    const void* W2sh;
+    int64_t w_stride;
+    int N, K, n1, E;
+    const int8_t* QA;
+    const float* sa;
+    const int32_t* x_idx;
+    const int32_t* grp;
+    const void* tiles;
+    const int32_t* n_tiles;
+    int max_tiles;
+    float* C;
+    float* C2;
+    int ldc;
+};
+constexpr int kMoeTileRows = 32;  // pair rows per grouped-GEMM tile
+hipError_t launch_moe_tiles(int32_t* grp, int32_t* x_idx, int E, int T_sh, int2* tiles, int32_t* n_tiles, hipStream_t s);
+hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int64_t n, hipStream_t s);
 hipError_t launch_moe_combine(const float* D, const int32_t* pos_of, const float* wsel, int T,
                               int topk, int H, const float* Dsh, const float* shared_w, float* out,

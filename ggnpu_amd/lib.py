@@ -138,6 +138,7 @@ SIGNATURES = {
     "ggq_produce_quantize_act_dev": (_I, [_P, _I, _P, _P, _I, _I, _I, ctypes.c_float, _P, _P, _P]),
     "ggq_block_dot_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _P]),
     "ggq_moe_ffn_dev": (_I, [_P, ctypes.POINTER(MoeParams), _P]),
+    "ggq_moe_ffn_act_dev": (_I, [_P, ctypes.POINTER(MoeParams), _I, _P]),
     "ggq_encode": (_I, [_U32, _P, _I64, _I64, _P]),
     "ggq_row_bytes": (_I64, [_U32, _I64]),
 }

@@ -346,6 +346,16 @@ typedef struct {
 } ggq_moe_params;
 int ggq_moe_ffn_dev(ggq_ctx* ctx, const ggq_moe_params* p, void* stream);
 
+/* ggq_moe_ffn_dev with the activation treatment of the expert matmuls:
+ * GGQ_ACT_F32 is ggq_moe_ffn_dev; GGQ_ACT_Q8_ROW quantizes each expert
+ * matmul's input per row as the XDNA backend does for every mul_mat_q call
+ * of the per-token loop (amd_xdna.cpp:598-603): the token row for gate and
+ * up, the SwiGLU row (fp32) for down.  That mode runs each expert's matmuls
+ * for all its tokens as one grouped int8 GEMM (weights decoded once per 32
+ * token rows) -- the prefill-sized path.  Extra requirements in that mode:
+ * H and F multiples of 32 and at most 16384, E <= 1023, x 16-byte aligned. */
+int ggq_moe_ffn_act_dev(ggq_ctx* ctx, const ggq_moe_params* p, int act_mode, void* stream);
+
 /* ------------------------------------------------------- synthetic data */
 
 /* Host-side encoder float -> GGUF blocks for seeded synthetic weights (the

@@ -445,6 +445,22 @@ int orc_moe_ffn_f64(const float* x, const float* logits, int T, int H, int F, in
                     const uint8_t* Sg, const uint8_t* Su, const uint8_t* Sd,
                     const float* shared_w, double* out,
                     int32_t* sel_experts, float* sel_weights) {
+    return orc_moe_ffn_act_f64(x, logits, T, H, F, E, topk, tg, Wg, tu, Wu, td, Wd, Sg, Su, Sd, shared_w,
+                               ORC_ACT_F32, out, sel_experts, sel_weights);
+}
+
+/* The same with each expert matmul under an activation treatment
+ * (act_mode as orc_mul_mat_f64): with ORC_ACT_Q8_ROW the token row is
+ * quantized per row for gate / up and the SwiGLU row, rounded to fp32 as
+ * the reference holds it (main.cpp:3164-3165), is quantized per row for
+ * down -- each mul_mat_weight call of the per-token loop quantizing its own
+ * input (amd_xdna.cpp:598-603). */
+int orc_moe_ffn_act_f64(const float* x, const float* logits, int T, int H, int F, int E, int topk,
+                        uint32_t tg, const uint8_t* Wg, uint32_t tu, const uint8_t* Wu,
+                        uint32_t td, const uint8_t* Wd,
+                        const uint8_t* Sg, const uint8_t* Su, const uint8_t* Sd,
+                        const float* shared_w, int act_mode, double* out,
+                        int32_t* sel_experts, float* sel_weights) {
     const size_t gbytes = (size_t)F * (H / orc_block_elems(tg)) * orc_block_bytes(tg);
     const size_t ubytes = (size_t)F * (H / orc_block_elems(tu)) * orc_block_bytes(tu);
     const size_t dbytes = (size_t)H * (F / orc_block_elems(td)) * orc_block_bytes(td);
@@ -492,10 +508,10 @@ int orc_moe_ffn_f64(const float* x, const float* logits, int T, int H, int F, in
                 wj = shared_w ? (double)shared_w[t] : 1.0;
                 pg = Sg; pu = Su; pd = Sd;
             }
-            orc_mul_mat_f64(tg, pg, F, H, xt, H, 1, ORC_ACT_F32, g, F);
-            orc_mul_mat_f64(tu, pu, F, H, xt, H, 1, ORC_ACT_F32, u, F);
+            orc_mul_mat_f64(tg, pg, F, H, xt, H, 1, act_mode, g, F);
+            orc_mul_mat_f64(tu, pu, F, H, xt, H, 1, act_mode, u, F);
             for (int i = 0; i < F; i++) act[i] = (float)(orc_silu_f64(g[i]) * u[i]);
-            orc_mul_mat_f64(td, pd, H, F, act, F, 1, ORC_ACT_F32, d, H);
+            orc_mul_mat_f64(td, pd, H, F, act, F, 1, act_mode, d, H);
             for (int i = 0; i < H; i++) ot[i] += wj * d[i];
         }
     }

@@ -112,6 +112,14 @@ int    orc_moe_ffn_f64(const float* x, const float* logits, int T, int H, int F,
                        const uint8_t* Sg, const uint8_t* Su, const uint8_t* Sd,
                        const float* shared_w, double* out,
                        int32_t* sel_experts, float* sel_weights);
+/* orc_moe_ffn_f64 with each expert matmul under act_mode (ORC_ACT_F32 or
+ * ORC_ACT_Q8_ROW; the SwiGLU row is rounded to fp32 before it is quantized). */
+int    orc_moe_ffn_act_f64(const float* x, const float* logits, int T, int H, int F, int E, int topk,
+                           uint32_t tg, const uint8_t* Wg, uint32_t tu, const uint8_t* Wu,
+                           uint32_t td, const uint8_t* Wd,
+                           const uint8_t* Sg, const uint8_t* Su, const uint8_t* Sd,
+                           const float* shared_w, int act_mode, double* out,
+                           int32_t* sel_experts, float* sel_weights);
 
 #ifdef __cplusplus
 }

@@ -32,6 +32,8 @@ _ORC_SIGS = {
     "orc_mul_mat_rowdot_f32": (_I, [_U32, _P, _I64, _I64, _P, _I, _I, _P, _I]),
     "orc_moe_ffn_f64": (_I, [_P, _P, _I, _I, _I, _I, _I, _U32, _P, _U32, _P, _U32, _P,
                              _P, _P, _P, _P, _P, _P, _P]),
+    "orc_moe_ffn_act_f64": (_I, [_P, _P, _I, _I, _I, _I, _I, _U32, _P, _U32, _P, _U32, _P,
+                                 _P, _P, _P, _P, _I, _P, _P, _P]),
     "orc_rms_norm": (None, [_P, _I, _P, ctypes.c_float, _P]),
     "orc_silu": (None, [_P, _I, _P]),
     "orc_flash_attn": (None, [_P, _P, _P, _I, _I, _I64, _I64, _P]),
@@ -163,7 +165,7 @@ def mul_mat_rowdot_f32(t, W, N, K, A):
 
 
 def moe_ffn_f64(x, logits, H, F, E, topk, tg, Wg, tu, Wu, td, Wd, Sg=None, Su=None, Sd=None,
-                shared_w=None):
+                shared_w=None, act_mode=0):
     x = np.ascontiguousarray(x, dtype=np.float32)
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     T = x.shape[0]
@@ -171,11 +173,11 @@ def moe_ffn_f64(x, logits, H, F, E, topk, tg, Wg, tu, Wu, td, Wd, Sg=None, Su=No
     sel = np.empty((T, topk), dtype=np.int32)
     wsel = np.empty((T, topk), dtype=np.float32)
     sw = None if shared_w is None else np.ascontiguousarray(shared_w, dtype=np.float32)
-    st = lib().orc_moe_ffn_f64(_ptr(x), _ptr(logits), T, H, F, E, topk, int(tg), _ptr(Wg), int(tu), _ptr(Wu),
-                               int(td), _ptr(Wd),
-                               None if Sg is None else _ptr(Sg), None if Su is None else _ptr(Su),
-                               None if Sd is None else _ptr(Sd), None if sw is None else _ptr(sw),
-                               _ptr(out), _ptr(sel), _ptr(wsel))
+    st = lib().orc_moe_ffn_act_f64(_ptr(x), _ptr(logits), T, H, F, E, topk, int(tg), _ptr(Wg), int(tu), _ptr(Wu),
+                                   int(td), _ptr(Wd),
+                                   None if Sg is None else _ptr(Sg), None if Su is None else _ptr(Su),
+                                   None if Sd is None else _ptr(Sd), None if sw is None else _ptr(sw),
+                                   int(act_mode), _ptr(out), _ptr(sel), _ptr(wsel))
     assert st == 0
     return out, sel, wsel
 

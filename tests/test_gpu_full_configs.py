@@ -173,11 +173,14 @@ def test_prefill_layer_as_benchmarked(ctx, orc):
         check_rows(orc, m["t"], m["raw"], m["N"], m["K"], A, C[rows], 1, 1024, len(name), name)
 
 
-@pytest.mark.parametrize("T", [64])
-def test_moe_layer_as_benchmarked(ctx, orc, T):
+@pytest.mark.parametrize("T,act_mode,n_check", [(64, 0, 64), (512, 1, 128), (64, 1, 64)])
+def test_moe_layer_as_benchmarked(ctx, orc, T, act_mode, n_check):
     """the qwen35moe-A3B MoE layer at the benchmark's 64 tokens
     (E 256, FFN 512, top-8, Q4_K gate/up, Q6_K down, sigmoid-weighted shared
-    expert), one ggq_moe_ffn_dev call, every token against the oracle."""
+    expert), one ggq_moe_ffn_dev call, every token against the oracle; and
+    the prefill-sized batch of 512 tokens with per-row int8 activations (the
+    grouped int8 GEMM path), a seeded sample of its tokens against the
+    oracle's per-token loop in the same mode (tokens are independent)."""
     import torch
     H, F, E, k = 2048, 512, 256, 8
     Wg, Wu, Wd = make(Q4K, E * F, H, 51), make(Q4K, E * F, H, 52), make(Q6K, E * H, F, 53)
@@ -196,13 +199,19 @@ def test_moe_layer_as_benchmarked(ctx, orc, T):
     p.gate_exps, p.up_exps, p.down_exps = keep[2].data_ptr(), keep[3].data_ptr(), keep[4].data_ptr()
     p.gate_shexp, p.up_shexp, p.down_shexp = keep[5].data_ptr(), keep[6].data_ptr(), keep[7].data_ptr()
     p.shared_w, p.out, p.sel_experts = keep[8].data_ptr(), out.data_ptr(), sel.data_ptr()
-    ctx.check(ctx.lib.ggq_moe_ffn_dev(ctx.h, ctypes.byref(p), stream_handle()), "moe")
+    ctx.check(ctx.lib.ggq_moe_ffn_act_dev(ctx.h, ctypes.byref(p), act_mode, stream_handle()), "moe")
     got, gsel = host(out), host(sel)
-    ref, rsel, _ = orc.moe_ffn_f64(x, logits, H, F, E, k, Q4K, Wg, Q4K, Wu, Q6K, Wd, Sg, Su, Sd, sw)
-    assert np.array_equal(gsel, rsel)
     counts = np.bincount(gsel.reshape(-1), minlength=E)
     assert counts.max() > 4, "expected an expert with a second pass of token rows"
-    err = orc.rel_l2(got, ref)
+    rows = np.sort(np.random.default_rng(T).choice(T, n_check, replace=False))
+    ref, rsel, _ = orc.moe_ffn_f64(x[rows], logits[rows], H, F, E, k, Q4K, Wg, Q4K, Wu, Q6K, Wd, Sg, Su, Sd, sw[rows],
+                                   act_mode=act_mode)
+    assert np.array_equal(gsel[rows], rsel)
+    if act_mode == 1:  # two quantized stages: see assert_q8_moe_close
+        from tests.test_gpu_parity import assert_q8_moe_close
+        assert_q8_moe_close(orc, got[rows], ref)
+        return
+    err = orc.rel_l2(got[rows], ref)
     assert err < TOL, err
-    for t in range(T):
-        assert orc.rel_l2(got[t], ref[t]) < TOL, t
+    for i, t in enumerate(rows):
+        assert orc.rel_l2(got[t], ref[i]) < TOL, t

@@ -302,6 +302,51 @@ def test_moe_oracle_vs_numpy_loop(orc):
         assert orc.rel_l2(out[t], ref) < 1e-12
 
 
+def test_moe_oracle_q8_row_vs_numpy_loop(orc):
+    """orc_moe_ffn_act_f64 in GGQ_ACT_Q8_ROW: each expert matmul quantizes
+    its own input row (the token row for gate / up, the fp32 SwiGLU row for
+    down) with the pinned per-row quantizer, and the result differs from the
+    fp32-activation layer (so the mode is not silently ignored)."""
+    import ggnpu_amd.lib as gl
+    rng = np.random.default_rng(6)
+    T, H, F, E, k = 3, 256, 256, 6, 2
+    Wg = gl.encode(12, (rng.standard_normal((E * F, H)) * 0.02).astype(np.float32))
+    Wu = gl.encode(12, (rng.standard_normal((E * F, H)) * 0.02).astype(np.float32))
+    Wd = gl.encode(14, (rng.standard_normal((E * H, F)) * 0.02).astype(np.float32))
+    Sg = gl.encode(12, (rng.standard_normal((F, H)) * 0.02).astype(np.float32))
+    Su = gl.encode(12, (rng.standard_normal((F, H)) * 0.02).astype(np.float32))
+    Sd = gl.encode(14, (rng.standard_normal((H, F)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    sw = rng.random(T).astype(np.float32)
+    out, sel, _ = orc.moe_ffn_f64(x, logits, H, F, E, k, 12, Wg, 12, Wu, 14, Wd, Sg, Su, Sd, sw, act_mode=1)
+    out32, _, _ = orc.moe_ffn_f64(x, logits, H, F, E, k, 12, Wg, 12, Wu, 14, Wd, Sg, Su, Sd, sw, act_mode=0)
+    dg = orc.dequant(12, Wg).astype(np.float64).reshape(E, F, H)
+    du = orc.dequant(12, Wu).astype(np.float64).reshape(E, F, H)
+    dd = orc.dequant(14, Wd).astype(np.float64).reshape(E, H, F)
+    sg = orc.dequant(12, Sg).astype(np.float64).reshape(F, H)
+    su = orc.dequant(12, Su).astype(np.float64).reshape(F, H)
+    sd = orc.dequant(14, Sd).astype(np.float64).reshape(H, F)
+
+    def q8(row):
+        q, s = orc.quant_act(row[None, :].astype(np.float32), 1)
+        return q[0].astype(np.float64) * float(s[0])
+
+    for t in range(T):
+        order = np.argsort(-logits[t], kind="stable")[:k]
+        assert list(sel[t]) == list(order)
+        w = np.exp(logits[t, order].astype(np.float64) - logits[t, order[0]])
+        w /= w.sum()
+        xa = q8(x[t])
+        ref = np.zeros(H)
+        for wj, (G, U, D) in [(w[j], (dg[e], du[e], dd[e])) for j, e in enumerate(order)] + [(float(sw[t]), (sg, su, sd))]:
+            g, u = G @ xa, U @ xa
+            h = (g / (1 + np.exp(-g)) * u).astype(np.float32)
+            ref += wj * (D @ q8(h))
+        assert orc.rel_l2(out[t], ref) < 1e-12
+    assert orc.rel_l2(out, out32) > 1e-4
+
+
 def test_moe_oracle_routing_ties_and_nan(orc):
     """Routing rule beyond the reference's defined cases: ties go to the
     lower expert id (the reference's partial_sort leaves them unordered) and
