@@ -2,7 +2,9 @@
 not select: the fp32 FMA kernels for several rows (GGQ_GEMV_MFMA=0) with
 GGQ_GEMV_MBCAP 2 / 4; GGQ_MOE_MB 1 / 4 (the grouped default being 2); the
 matrix-core kernel with 8 rows per pass (GGQ_GEMV_MFMA_MS=2) and for a
-single row (GGQ_GEMV_MFMA1=1).  The
+single row (GGQ_GEMV_MFMA1=1); per-row int8 decode without the int8
+matrix-core GEMV (GGQ_GEMV_I8=0: quantize, dequantize, fp32 kernel) and
+fp32 launches of every size on it (GGQ_I8_MIN_BYTES=0).  The
 library reads these knobs at each multi-row / grouped launch, so the checks
 set them in this process and restore them afterwards."""
 import os
@@ -91,3 +93,11 @@ def test_fma_path_batch_invariant(ctx, orc, mfma_knob, ty):
         for m in range(M):
             alone = t.run_mm(ctx, ty, raw, N, K, A[m:m + 1], 0)
             assert np.array_equal(batch[m].view(np.uint32), alone[0].view(np.uint32)), (M, m)
+
+
+@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_I8", "0"), ("GGQ_I8_MIN_BYTES", "0")], indirect=True)
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q8_0", "IQ4_XS"])
+def test_i8_gemv_switches(ctx, orc, mfma_knob, name):
+    for M in (1, 3):
+        t.test_gemv_f32_vs_oracle(ctx, orc, name, M)
+    t.test_gemv_q8_act_vs_oracle(ctx, orc, name, 1)
