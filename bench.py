@@ -514,7 +514,7 @@ QWEN3_SHAPES = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1
 QWEN3_LAYERS = 28
 
 
-def bench_config4(torch, ctx, stream, steps=10):
+def bench_config4(torch, ctx, stream, steps=40):
     """28 Qwen3-0.6B layers of IQ4_NL / IQ4_XS / Q5_K matmuls with
     batch 1, 4 and 8 fp32 activation rows; one launch per dependency level
     (q/k/v, o, gate/up, down) through ggq_mul_mat_batch_rows_dev."""

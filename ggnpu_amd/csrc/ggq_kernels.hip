@@ -627,6 +627,14 @@ template <int T, int MB, int PPT, int U, bool F, bool XL = false>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
                                           float (&red)[2][4][U * MB]) {
     static_assert(!XL || (MB == 1 && !F), "LDS-staged activations: one plain activation row per pass");
+    if constexpr (XL) {
+        // Every kernel argument the launch reads, in one round of scalar
+        // loads: left to itself the compiler loads them next to their first
+        // use, three dependent rounds before the first weight fetch.
+        asm volatile("" ::"s"(a.W), "s"(a.w_group_stride), "s"(a.row_bytes), "s"(a.N), "s"(a.K), "s"(a.X),
+                     "s"(a.ldx), "s"(a.Y), "s"(a.ldy), "s"(a.M), "s"(a.lpr_log2), "s"(a.p_div), "s"(a.prefetch),
+                     "s"(a.W2), "s"(a.n1));
+    }
     typedef typename Piece<T>::Raw Raw;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lpr_log2 = a.lpr_log2;
@@ -636,7 +644,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
     const uint8_t* W = a.W + (int64_t)by * a.w_group_stride;
     const uint8_t* W2 = a.n1 > 0 ? a.W2 + (int64_t)by * a.w_group_stride : nullptr;
     int m0 = 0, mcount = a.M;
-    if (a.grp_off) {
+    // (The LDS-staged launches are never grouped: no dependent read of the
+    // group offsets before the first weight fetch.)
+    if (!XL && a.grp_off) {
         m0 = a.grp_off[by];
         mcount = a.grp_off[by + 1] - m0;
     }
