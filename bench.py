@@ -594,6 +594,175 @@ def bench_config5(torch, ctx, stream, steps=20, T=64, act_mode=0):
             "frac_hbm_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_decode_token(torch, ctx, stream, n_tok=24, start=512, n_ctx=1024):
+    """A whole Llama-3.2-1B decode token (16 layers, hidden 2048, 32 q / 8 kv
+    heads of 64, FFN 8192, vocab 128256) from a GGUF file: a synthetic
+    Q4_K_M model (q/k/o/gate/up/output and the token embedding Q4_K, v and
+    down Q6_K, F32 norms; seeded N(0, 0.02) weights, one matrix per shape
+    repeated over the layers) is written to a temporary file, opened with
+    ggq_gguf_open and uploaded unchanged with ggq_gguf_upload.  Per token:
+    the embedding row decoded on the device (ggq_dequant_dev); per layer
+    q/k/v with the attention RMSNorm fused in (v written straight into the
+    layer's KV-cache slot), RoPE on q and k together by the caller (torch, as
+    the reference keeps RoPE with its caller) and k copied into the cache,
+    ggq_attention_decode_dev over the
+    start + t positions, o with the residual, gate (silu) / up with the FFN
+    norm, down on silu(gate) * up with the residual; then the output norm
+    (torch) and ggq_logits_argmax_dev, whose token is read back and fed to
+    the next token's embedding (one host round trip per token, as a decode
+    loop has).  The cache holds `start` synthetic positions before the
+    first timed token."""
+    import tempfile
+    from ggnpu_amd import gguf_writer as gw
+    L, H, NH, NKV, HD, F, V = 16, 2048, 32, 8, 64, 8192, 128256
+    EPS, BASE = 1e-5, 500000.0
+    rng = np.random.default_rng(7)
+    enc = {}
+
+    def weight(t, N, K):
+        key = (t, N, K)
+        if key not in enc:
+            enc[key] = gl.encode(t, (rng.standard_normal((N, K), dtype=np.float32) * 0.02)).tobytes()
+        return enc[key]
+
+    def norm_bytes():
+        return (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32).tobytes()
+
+    shapes = {"attn_q": (Q4K, NH * HD, H), "attn_k": (Q4K, NKV * HD, H), "attn_v": (Q6K, NKV * HD, H),
+              "attn_output": (Q4K, H, NH * HD), "ffn_gate": (Q4K, F, H), "ffn_up": (Q4K, F, H),
+              "ffn_down": (Q6K, H, F)}
+    tensors = [("token_embd.weight", Q4K, [H, V], gl.row_bytes(Q4K, H) * V, lambda: weight(Q4K, V, H))]
+    for li in range(L):
+        tensors.append((f"blk.{li}.attn_norm.weight", 0, [H], 4 * H, norm_bytes))
+        tensors.append((f"blk.{li}.ffn_norm.weight", 0, [H], 4 * H, norm_bytes))
+        for name, (t, N, K) in shapes.items():
+            tensors.append((f"blk.{li}.{name}.weight", t, [K, N], gl.row_bytes(t, K) * N,
+                            (lambda t=t, N=N, K=K: weight(t, N, K))))
+    tensors.append(("output_norm.weight", 0, [H], 4 * H, norm_bytes))
+    tensors.append(("output.weight", Q4K, [H, V], gl.row_bytes(Q4K, H) * V, lambda: weight(Q4K, V, H)))
+    kvs = [("general.architecture", gw.STRING, "llama"), ("llama.block_count", gw.UINT32, L),
+           ("llama.embedding_length", gw.UINT32, H), ("llama.feed_forward_length", gw.UINT32, F),
+           ("llama.attention.head_count", gw.UINT32, NH), ("llama.attention.head_count_kv", gw.UINT32, NKV),
+           ("llama.attention.layer_norm_rms_epsilon", gw.FLOAT32, EPS), ("llama.rope.freq_base", gw.FLOAT32, BASE)]
+    lib = ctx.lib
+    t0 = time.time()
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "llama-3.2-1b-synthetic-q4_k_m.gguf")
+        gw.write_stream(path, kvs, tensors)
+        fbytes = os.path.getsize(path)
+        enc.clear()
+        dev, handles = {}, []
+        with gl.GgufFile(path) as g:
+            assert (g.kv("llama.block_count"), g.kv("llama.attention.head_count_kv")) == (L, NKV)
+            eps = g.kv("llama.attention.layer_norm_rms_epsilon")
+            base = g.kv("llama.rope.freq_base")
+            for name, info in g.tensors.items():
+                if info["type"] == 0:
+                    dev[name] = torch.from_numpy(np.frombuffer(g.tensor_bytes(name), np.float32).copy()).cuda()
+                else:
+                    w = ctypes.c_void_p()
+                    ctx.check(g.lib.ggq_gguf_upload(ctx.h, g.h, name.encode(), ctypes.byref(w)), name)
+                    handles.append(w)
+                    dims = info["dims"]
+                    dev[name] = (lib.ggq_weight_device_ptr(w), info["type"], int(np.prod(dims[1:])), dims[0])
+    setup_s = time.time() - t0
+    weight_bytes = sum(gl.row_bytes(v[1], v[3]) * v[2] for v in dev.values() if isinstance(v, tuple))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(8)
+    Kc = torch.randn((L, n_ctx, NKV, HD), device="cuda", generator=gen)
+    Vc = torch.randn((L, n_ctx, NKV, HD), device="cuda", generator=gen)
+    half = HD // 2
+    theta = torch.arange(n_ctx, dtype=torch.float64, device="cuda")[:, None] * \
+        base ** (-2.0 * torch.arange(half, dtype=torch.float64, device="cuda") / HD)
+    cos_t, sin_t = torch.cos(theta).float(), torch.sin(theta).float()
+    qk = torch.empty((NH + NKV, HD), device="cuda")  # q and k next to each other: one RoPE for both
+    q, kbuf = qk[:NH], qk[NH:]
+    att = torch.empty((1, NH * HD), device="cuda")
+    gb, ub = torch.empty((1, F), device="cuda"), torch.empty((1, F), device="cuda")
+    x = torch.empty((1, H), device="cuda")
+    logits = torch.empty((1, V), device="cuda")
+    tok = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    emb = dev["token_embd.weight"]
+    emb_row = gl.row_bytes(Q4K, H)
+
+    def descs(entries):
+        arr = (gl.GemvFusedDesc * len(entries))()
+        for d, e in zip(arr, entries):
+            d.W, d.type, d.N, d.K = dev[e["w"]]
+            d.A, d.C = e["A"], e["C"]
+            if "up" in e:
+                d.A_up = e["up"]
+            if e.get("res"):
+                d.residual = e["C"]
+            if "norm" in e:
+                d.rms_norm, d.rms_eps, d.rms_w = 1, eps, dev[e["norm"]].data_ptr()
+            d.silu = int(e.get("silu", False))
+        return arr, len(entries)
+
+    # the launches' descriptors, built once (per token only the k / v cache
+    # slots of the q/k/v entries change)
+    plan = []
+    for li in range(L):
+        p = f"blk.{li}."
+        plan.append((descs([{"w": p + "attn_q.weight", "A": x.data_ptr(), "C": q.data_ptr(), "norm": p + "attn_norm.weight"},
+                            {"w": p + "attn_k.weight", "A": x.data_ptr(), "C": kbuf.data_ptr(), "norm": p + "attn_norm.weight"},
+                            {"w": p + "attn_v.weight", "A": x.data_ptr(), "C": 0, "norm": p + "attn_norm.weight"}]),
+                     descs([{"w": p + "attn_output.weight", "A": att.data_ptr(), "C": x.data_ptr(), "res": True}]),
+                     descs([{"w": p + "ffn_gate.weight", "A": x.data_ptr(), "C": gb.data_ptr(),
+                             "norm": p + "ffn_norm.weight", "silu": True},
+                            {"w": p + "ffn_up.weight", "A": x.data_ptr(), "C": ub.data_ptr(), "norm": p + "ffn_norm.weight"}]),
+                     descs([{"w": p + "ffn_down.weight", "A": gb.data_ptr(), "up": ub.data_ptr(), "C": x.data_ptr(),
+                             "res": True}])))
+
+    def fused(dn):
+        ctx.check(lib.ggq_mul_mat_fused_dev(ctx.h, dn[0], dn[1], 1, stream), "fused")
+
+    def rope(v, n, pos):
+        v = v.view(n, HD)
+        a, b = v[:, :half].clone(), v[:, half:]
+        c, s = cos_t[pos], sin_t[pos]
+        v[:, :half] = a * c - b * s
+        v[:, half:] = a * s + b * c
+
+    def token(t, pos):
+        ctx.check(lib.ggq_dequant_dev(ctx.h, ctypes.c_void_p(emb[0] + t * emb_row), Q4K, H // 256,
+                                      ctypes.c_void_p(x.data_ptr()), stream), "embedding")
+        for li in range(L):
+            qkv, o, gu, down = plan[li]
+            kslot, vslot = Kc[li, pos], Vc[li, pos]
+            qkv[0][2].C = vslot.data_ptr()
+            fused(qkv)
+            rope(qk, NH + NKV, pos)
+            kslot.copy_(kbuf)
+            ctx.check(lib.ggq_attention_decode_dev(ctx.h, q.data_ptr(), Kc[li].data_ptr(), Vc[li].data_ptr(), 1, NH, NKV,
+                                                   HD, pos + 1, pos, att.data_ptr(), stream), "attention")
+            fused(o)
+            fused(gu)
+            fused(down)
+        xo = x * torch.rsqrt((x * x).mean() + eps) * dev["output_norm.weight"]
+        wo = dev["output.weight"]
+        ctx.check(lib.ggq_logits_argmax_dev(ctx.h, wo[0], wo[1], wo[2], wo[3], xo.data_ptr(), 1, 0, logits.data_ptr(),
+                                            tok.data_ptr(), None, stream), "logits")
+        return int(tok.item())  # the decode loop's host round trip
+
+    t = 1
+    for i in range(4):  # warm-up tokens
+        t = token(t, start - 4 + i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n_tok):
+        t = token(t, start + i)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / n_tok
+    for w in handles:
+        ctx.check(lib.ggq_weight_free(ctx.h, w), "free")
+    return {"workload": f"Llama-3.2-1B decode token from a GGUF file (synthetic Q4_K_M, {fbytes / 1e6:.0f} MB): 16 layers "
+                        f"with RMSNorm / SwiGLU / residual fused, RoPE by the caller (torch), attention over "
+                        f"{start}..{start + n_tok - 1} positions, output norm, logits + greedy token, token read back",
+            "tokens": n_tok, "ms_per_token": round(sec * 1e3, 3), "tokens_per_s": round(1.0 / sec, 1),
+            "weight_GBps": round(weight_bytes / sec / 1e9, 1), "setup_s": round(setup_s, 1)}
+
+
 def host_cpu():
     """Host CPU model and core counts for the cpu_baseline records."""
     model = "unknown"
@@ -815,7 +984,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--graph", action="store_true", help="replay the step as a HIP graph")
     ap.add_argument("--no-extra", action="store_true", help="skip config 1 / config 3 / CPU baseline")
-    ap.add_argument("--only", choices=["decode", "config1", "config1_q8", "prefill", "config4", "moe", "logits", "fused", "attention", "host", "copy",
+    ap.add_argument("--only", choices=["decode", "token", "config1", "config1_q8", "prefill", "config4", "moe", "logits", "fused", "attention", "host", "copy",
                                        "floor"],
                     default=None,
                     help="run one workload only and print its result (profiling aid)")
@@ -856,8 +1025,8 @@ def main():
         print(json.dumps({"only": "floor", **bench_launch_floor(torch)}), flush=True)
         ctx.close()
         return
-    if args.only in ("config1", "config1_q8", "prefill", "config4", "moe", "logits", "fused", "attention", "host"):
-        res = {"config1": bench_config1, "config1_q8": lambda t, c, st: bench_config1(t, c, st, act_mode=1),
+    if args.only in ("token", "config1", "config1_q8", "prefill", "config4", "moe", "logits", "fused", "attention", "host"):
+        res = {"token": bench_decode_token, "config1": bench_config1, "config1_q8": lambda t, c, st: bench_config1(t, c, st, act_mode=1),
                "prefill": bench_prefill, "config4": bench_config4,
                "moe": lambda *a: bench_config5(*a, T=args.moe_tokens, act_mode=args.moe_act), "logits": bench_logits, "fused": bench_decode_fused,
                "attention": bench_attention, "host": bench_host_api}[args.only](
@@ -918,7 +1087,8 @@ def main():
                 ("config5_moe_q8_row", lambda t, c, st: bench_config5(t, c, st, act_mode=1), None),
                 ("config5_moe_512_q8_row", lambda t, c, st: bench_config5(t, c, st, steps=10, T=512, act_mode=1), None),
                 ("logits_argmax", bench_logits, None), ("attention_decode", bench_attention, None),
-                ("host_api_decode", bench_host_api, None), ("decode_fused", bench_decode_fused, None)):
+                ("host_api_decode", bench_host_api, None), ("decode_fused", bench_decode_fused, None),
+                ("decode_token_gguf", bench_decode_token, None)):
             try:
                 out["extra"][key] = fn(torch, ctx, stream)
             except Exception as e:  # reported, never silently replaced

@@ -1,6 +1,7 @@
-"""Minimal GGUF v3 writer for the tests (test infrastructure, not the
-product): header, typed metadata, tensor infos, padding to the alignment,
-tensor data.  Written from the format description in include/ggq_gguf.h."""
+"""Minimal GGUF v3 writer: header, typed metadata, tensor infos, padding to
+the alignment, tensor data -- for synthetic models (the tests' files and the
+benchmark's full-size decode model).  Written from the format description in
+include/ggq_gguf.h; the reader is ggq_gguf_* (ggnpu_amd/csrc/ggq_gguf.cpp)."""
 import struct
 
 import numpy as np
@@ -53,6 +54,28 @@ def write(path, kvs, tensors, **kw):
     with open(path, "wb") as f:
         f.write(blob)
     return offsets
+
+
+def write_stream(path, kvs, tensors, alignment=32):
+    """The layout of build(), written tensor by tensor: tensors is a list of
+    (name, ggml_type, dims, nbytes, produce) where produce() returns the
+    tensor's bytes when its turn comes (large synthetic models never hold
+    the whole file in memory)."""
+    head = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kvs)))
+    for key, t, v in kvs:
+        head += _str(key) + struct.pack("<I", t) + _value(t, v)
+    off = 0
+    for name, gt, dims, nbytes, _ in tensors:
+        head += _str(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<IQ", gt, off)
+        off += (nbytes + alignment - 1) // alignment * alignment
+    with open(path, "wb") as f:
+        f.write(bytes(head) + b"\0" * ((-len(head)) % alignment))
+        for name, gt, dims, nbytes, produce in tensors:
+            raw = produce()
+            assert len(raw) == nbytes, name
+            f.write(raw)
+            f.write(b"\0" * ((-nbytes) % alignment))
 
 
 def raw_bytes(a):

@@ -1,4 +1,4 @@
-"""GGUF v3 reader (include/ggq_gguf.h) on files written by tests/gguf_writer.py:
+"""GGUF v3 reader (include/ggq_gguf.h) on files written by ggnpu_amd/gguf_writer.py:
 every metadata type, tensor infos and data read in place, alignment, and
 malformed files rejected with a message.  CPU only.  The type table is
 pinned by the reference's own table for the six path types (golden
@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import ggnpu_amd.lib as gl
-from tests import gguf_writer as gw
+from ggnpu_amd import gguf_writer as gw
 
 Q8, Q4K, Q6K, IQ4XS, F32, F16 = 8, 12, 14, 23, 0, 1
 

@@ -1,7 +1,7 @@
 """A few decode tokens of a small Llama-style model read from a GGUF file,
 run through the device entry points only, against an fp64 restatement.
 
-The file (tests/gguf_writer.py) carries the tensor names and metadata of a
+The file (ggnpu_amd/gguf_writer.py) carries the tensor names and metadata of a
 llama GGUF: Q4_K q/k/o/gate/up/output, Q6_K v/down, F32 norms and
 embedding.  The weights go to HBM with ggq_gguf_upload; per token and layer
 the GPU path is
@@ -24,11 +24,11 @@ import numpy as np
 import pytest
 
 import ggnpu_amd.lib as gl
-from tests import gguf_writer as gw
+from ggnpu_amd import gguf_writer as gw
 
 pytestmark = pytest.mark.gpu
 
-L, H, NH, NKV, HD, F, V = 2, 256, 4, 2, 64, 512, 1024
+H, NH, NKV, HD, F, V = 256, 4, 2, 64, 512, 1024
 EPS, ROPE_BASE = 1e-5, 10000.0
 Q4K, Q6K, F32 = 12, 14, 0
 TOL = 1e-4
@@ -43,7 +43,7 @@ def ctx():
     c.close()
 
 
-def _model(seed=0):
+def _model(L, seed=0):
     rng = np.random.default_rng(seed)
     mats = {}
 
@@ -68,7 +68,7 @@ def _model(seed=0):
     return mats, norms, embd
 
 
-def _write(path, mats, norms, embd):
+def _write(path, mats, norms, embd, L):
     kvs = [("general.architecture", gw.STRING, "llama"), ("llama.block_count", gw.UINT32, L),
            ("llama.embedding_length", gw.UINT32, H), ("llama.feed_forward_length", gw.UINT32, F),
            ("llama.attention.head_count", gw.UINT32, NH), ("llama.attention.head_count_kv", gw.UINT32, NKV),
@@ -93,7 +93,7 @@ def _rms_np(x, w):
     return x / np.sqrt(np.mean(x * x) + EPS) * w
 
 
-def _reference(orc, mats, norms, embd, tokens):
+def _reference(orc, mats, norms, embd, tokens, L):
     W = {n: orc.dequant(t, raw).reshape(N, K).astype(np.float64) for n, (t, N, K, raw) in mats.items()}
     nw = {n: w.astype(np.float64) for n, w in norms.items()}
     Kc = np.zeros((L, len(tokens), NKV, HD))
@@ -124,13 +124,15 @@ def _reference(orc, mats, norms, embd, tokens):
     return out
 
 
-def test_llama_decode_tokens_from_gguf(ctx, orc, tmp_path):
+@pytest.mark.parametrize("L", [2, 16])
+def test_llama_decode_tokens_from_gguf(ctx, orc, tmp_path, L):
+    """2 layers, and the 16 layers of Llama-3.2-1B (at small widths)."""
     import torch
-    mats, norms, embd = _model()
+    mats, norms, embd = _model(L)
     path = tmp_path / "tiny-llama.gguf"
-    _write(path, mats, norms, embd)
+    _write(path, mats, norms, embd, L)
     tokens = [3, 17, 999, 3, 512, 77]
-    ref = _reference(orc, mats, norms, embd, tokens)
+    ref = _reference(orc, mats, norms, embd, tokens, L)
 
     lib = ctx.lib
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import ggnpu_amd.lib as gl
-from tests import gguf_writer as gw
+from ggnpu_amd import gguf_writer as gw
 from tests.gpu_util import empty, host, stream_handle
 
 pytestmark = pytest.mark.gpu
