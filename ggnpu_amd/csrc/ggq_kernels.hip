@@ -626,7 +626,7 @@ __device__ __forceinline__ void gemv_rms_norm(const GemvArgs& a, float (&xr)[PPT
 template <int T, int MB, int PPT, int U, bool F, bool XL = false>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
                                           float (&red)[2][4][U * MB]) {
-    static_assert(!XL || (MB == 1 && !F), "LDS-staged activations: one plain activation row per pass");
+    static_assert(!XL || MB == 1, "LDS-staged activations: one activation row per pass");
     if constexpr (XL) {
         // Every kernel argument the launch reads, in one round of scalar
         // loads: left to itself the compiler loads them next to their first
@@ -674,7 +674,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
             for (int sl = tid; sl < 8 * P; sl += 256) {
                 const int j = (int)__umulhi((uint32_t)sl, a.p_div);
                 const int p = sl - j * P;
-                xl[sl] = *(const float4*)(xp + Piece<T>::run_k(p, j >> 2) + 4 * (j & 3));
+                const int k = Piece<T>::run_k(p, j >> 2) + 4 * (j & 3);
+                float4 v = *(const float4*)(xp + k);
+                if (F && a.X2) {  // SwiGLU's product: silu(gate) (already applied) * up, main.cpp:3474-3477
+                    const float4 u = *(const float4*)(a.X2 + (int64_t)(m0 + mc) * a.ldx + k);
+                    v = make_float4(__fmul_rn(v.x, u.x), __fmul_rn(v.y, u.y), __fmul_rn(v.z, u.z), __fmul_rn(v.w, u.w));
+                }
+                xl[sl] = v;
             }
             __syncthreads();
 #pragma unroll
@@ -1248,7 +1254,7 @@ static bool gemv_xlds(const GemvProblem& p, const GemvArgs& a) {
         const char* e = getenv("GGQ_GEMV_XLDS");
         return e && *e ? atoi(e) : 1;
     }();
-    return v != 0 && p.M <= 1 && !p.grp_off && !p.x_idx && !fused(p) && a.x_vec4 && a.lpr_log2 < 8 && p.K >= 64 && p.K <= 8192 && p.K % 32 == 0;
+    return v != 0 && p.M <= 1 && !p.grp_off && !p.x_idx && a.x_vec4 && a.lpr_log2 < 8 && p.K >= 64 && p.K <= 8192 && p.K % 32 == 0;
 }
 
 static int gemv_max_lpr() {
@@ -1424,7 +1430,22 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
         gemv_kernel<T, 1, PPT_, 1, false, true><<<dim3(gx, 1, 1), 256, lds, s>>>(a);             \
     } while (0)
-    if (groups == 1 && u == 1 && gemv_xlds(p, a)) {
+#define GO_FX(PPT_)                                                                              \
+    do {                                                                                         \
+        const size_t lds = (size_t)p.K * sizeof(float);                                          \
+        int gx = resident_blocks(gemv_kernel<T, 1, PPT_, 1, true, true>, lds);                   \
+        gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
+        gemv_kernel<T, 1, PPT_, 1, true, true><<<dim3(gx, 1, 1), 256, lds, s>>>(a);              \
+    } while (0)
+    if (groups == 1 && fused(p) && gemv_xlds(p, a)) {
+        if (ppt == 1) GO_FX(1);
+        else if (ppt == 2) GO_FX(2);
+        else if (ppt <= 4) GO_FX(4);
+        else return hipErrorInvalidValue;
+#undef GO_FX
+        return hipGetLastError();
+    }
+    if (groups == 1 && u == 1 && !fused(p) && gemv_xlds(p, a)) {
         if (ppt == 1) GO_X(1);
         else if (ppt == 2) GO_X(2);
         else if (ppt <= 4) GO_X(4);
@@ -1550,10 +1571,14 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     const int mb = any_fused ? 1 : multi_mb(ppt, M);
     const int gz = (M + mb - 1) / mb;
     kq = kq && ppt == 1 && mb == 1 && u == 1;  // the variants compiled with KQ
-    xl = xl && !any_fused && mb == 1 && u == 1 && M == 1;
+    xl = xl && mb == 1 && u == 1 && M == 1;
     const size_t lds = xl ? (size_t)kmax * sizeof(float) : 0;
     int target;
-    if (xl) {
+    if (xl && any_fused) {
+        target = ppt == 1 ? (kq ? resident_blocks(gemv_multi_kernel<1, 1, 1, true, true, true>, lds)
+                                : resident_blocks(gemv_multi_kernel<1, 1, 1, true, false, true>, lds))
+                          : resident_blocks(gemv_multi_kernel<1, 2, 1, true, false, true>, lds);
+    } else if (xl) {
         target = kq ? resident_blocks(gemv_multi_kernel<1, 1, 1, false, true, true>, lds)
                     : ppt == 1 ? resident_blocks(gemv_multi_kernel<1, 1, 1, false, false, true>, lds)
                                : resident_blocks(gemv_multi_kernel<1, 2, 1, false, false, true>, lds);
@@ -1583,7 +1608,11 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     ma.begin[n] = b;
     ma.n = n;
     const dim3 grid(b, 1, gz);
-    if (xl) {
+    if (xl && any_fused) {
+        if (kq) gemv_multi_kernel<1, 1, 1, true, true, true><<<grid, 256, lds, s>>>(ma);
+        else if (ppt == 1) gemv_multi_kernel<1, 1, 1, true, false, true><<<grid, 256, lds, s>>>(ma);
+        else gemv_multi_kernel<1, 2, 1, true, false, true><<<grid, 256, lds, s>>>(ma);
+    } else if (xl) {
         if (kq) gemv_multi_kernel<1, 1, 1, false, true, true><<<grid, 256, lds, s>>>(ma);
         else if (ppt == 1) gemv_multi_kernel<1, 1, 1, false, false, true><<<grid, 256, lds, s>>>(ma);
         else gemv_multi_kernel<1, 2, 1, false, false, true><<<grid, 256, lds, s>>>(ma);
