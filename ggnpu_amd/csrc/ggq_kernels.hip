@@ -907,7 +907,7 @@ __device__ __forceinline__ void quad_bcast4(float v, float (&o)[4]) {
 // whose weights start at by * w_group_stride and whose activation rows are
 // grp_off[by] .. grp_off[by+1]-1 (through x_idx when set); paired matrices
 // (n1 > 0) as in gemv_body.
-template <int T, int PPT, int MS, bool ONE = false>
+template <int T, int PPT, int MS, bool ONE = false, bool X32 = false, bool XL = false>
 __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
                                                float (&red)[2][4][2][4][4 * MS]) {
     constexpr int NM = ONE ? 1 : 4;  // result rows per row set that are used
@@ -959,6 +959,45 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
         float amax[MS];
 #pragma unroll
         for (int t = 0; t < MS; t++) amax[t] = 0.0f;
+        if constexpr (XL) {
+            // The workgroup's 4 MS activation rows are read from memory once
+            // (16-byte words, consecutive k across lanes) and staged in LDS
+            // as float4 slot (j8, p, m) at j8 (4 MS P + 1) + 4 MS p + m, with
+            // j8 = 4 r + quad of run r of piece p: each lane's reads of its
+            // (piece, row) are consecutive slots across the wavefront.
+            extern __shared__ float4 xls[];
+            constexpr int R4 = 4 * MS;
+            const int pstride = R4 * P + 1;
+            if (mc != bz * 4 * MS) __syncthreads();  // every wavefront has read the previous rows
+            for (int sl = tid; sl < 8 * R4 * P; sl += 256) {
+                const int j8 = sl & 7, rest = sl >> 3;
+                const int mrow = (int)__umulhi((uint32_t)rest, a.p_div);
+                const int p = rest - mrow * P;
+                const int k = Piece<T>::run_k(p, j8 >> 2) + 4 * (j8 & 3);
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (mc + mrow < mcount) v = *(const float4*)(a.X + (int64_t)(mc + mrow) * a.ldx + k);
+                xls[j8 * pstride + p * R4 + mrow] = v;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < PPT; i++) {
+                const int p = sg + i * S;
+                const bool ok = p < P;
+                const int pc = ok ? p : 0;
+#pragma unroll
+                for (int t = 0; t < MS; t++)
+#pragma unroll
+                    for (int j8 = 0; j8 < 8; j8++) {
+                        const float4 v = xls[j8 * pstride + pc * R4 + 4 * t + j];
+                        x[i][t][4 * j8] = ok ? v.x : 0.0f; x[i][t][4 * j8 + 1] = ok ? v.y : 0.0f;
+                        x[i][t][4 * j8 + 2] = ok ? v.z : 0.0f; x[i][t][4 * j8 + 3] = ok ? v.w : 0.0f;
+                    }
+#pragma unroll
+                for (int t = 0; t < MS; t++)
+#pragma unroll
+                    for (int q = 0; q < 32; q++) amax[t] = fmaxf(amax[t], fabsf(x[i][t][q]));
+            }
+        } else
 #pragma unroll
         for (int i = 0; i < PPT; i++) {
             const int p = sg + i * S;
@@ -992,6 +1031,28 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
                 }
             }
         }
+        // X32: the fp32 activations go into the fp32 matrix-core product as
+        // they are (4x4x1 steps, one value of k per step); only the run sums
+        // of the bias term are formed here.
+        float xs[PPT][MS][2][4];
+        h4v xh[PPT][MS][X32 ? 1 : 8], xl[PPT][MS][X32 ? 1 : 8];
+        float out_inv = 1.0f;
+        const int out_t = (lane >> 4) & (MS - 1), out_m = (lane >> 2) & 3;
+        if constexpr (X32) {
+#pragma unroll
+            for (int i = 0; i < PPT; i++)
+#pragma unroll
+                for (int t = 0; t < MS; t++) {
+                    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 16; q++) {
+                        s0 += x[i][t][q];
+                        s1 += x[i][t][16 + q];
+                    }
+                    quad_bcast4(s0, xs[i][t][0]);
+                    quad_bcast4(s1, xs[i][t][1]);
+                }
+        } else {
         // Largest magnitude of each activation row over the workgroup's
         // slots (all groups of a workgroup read the same rows): lanes of
         // equal j inside the wavefront, then its two halves and the
@@ -1021,8 +1082,6 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
         // The output lane of (j, m, t) = (L & 3, (L >> 2) & 3, L >> 4) needs
         // the scale of row 4t + m: lane 4m + j' of any block holds it for
         // j' = m.
-        const int out_t = (lane >> 4) & (MS - 1), out_m = (lane >> 2) & 3;
-        float out_inv = 1.0f;
 #pragma unroll
         for (int t = 0; t < MS; t++) {
             const int e = __builtin_amdgcn_ds_bpermute(4 * ((lane & ~3) | out_m), sh[t]);
@@ -1031,8 +1090,6 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
         parity ^= 1;
         // Split into fp16 hi + lo after the row's scale; run sums of the
         // scaled values for the bias term, gathered for all four rows.
-        h4v xh[PPT][MS][8], xl[PPT][MS][8];
-        float xs[PPT][MS][2][4];
 #pragma unroll
         for (int i = 0; i < PPT; i++)
 #pragma unroll
@@ -1058,6 +1115,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
                     xl[i][t][q] = __builtin_bit_cast(h4v, make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)));
                 }
             }
+        }
 
         while (it < n_iters) {
             if (it + gx < n_iters) fetch(rb, it + gx);
@@ -1075,15 +1133,26 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
                     h4v B[4];
+                    float Bf[16];
+                    if constexpr (X32) {
 #pragma unroll
-                    for (int q = 0; q < 4; q++) B[q] = codes_slice(u4_at(pc.u[r], q));
+                        for (int q = 0; q < 16; q++) Bf[q] = (float)((u4_at(pc.u[r], q >> 2) >> (8 * (q & 3))) & 0xFFu);
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; q++) B[q] = codes_slice(u4_at(pc.u[r], q));
+                    }
 #pragma unroll
                     for (int t = 0; t < MS; t++) {
                         f4v D = {0.0f, 0.0f, 0.0f, 0.0f};
+                        if constexpr (X32) {
 #pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            D = __builtin_amdgcn_mfma_f32_4x4x4f16(xh[i][t][4 * r + q], B[q], D, 0, 0, 0);
-                            D = __builtin_amdgcn_mfma_f32_4x4x4f16(xl[i][t][4 * r + q], B[q], D, 0, 0, 0);
+                            for (int q = 0; q < 16; q++) D = __builtin_amdgcn_mfma_f32_4x4x1f32(x[i][t][16 * r + q], Bf[q], D, 0, 0, 0);
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                D = __builtin_amdgcn_mfma_f32_4x4x4f16(xh[i][t][4 * r + q], B[q], D, 0, 0, 0);
+                                D = __builtin_amdgcn_mfma_f32_4x4x4f16(xl[i][t][4 * r + q], B[q], D, 0, 0, 0);
+                            }
                         }
 #pragma unroll
                         for (int m = 0; m < NM; m++) {
@@ -1135,20 +1204,20 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
     }
 }
 
-template <int T, int PPT, int MS, bool ONE = false>
+template <int T, int PPT, int MS, bool ONE = false, bool X32 = false, bool XL = false>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
     __shared__ float red[2][4][2][4][4 * MS];
-    gemv_mfma_body<T, PPT, MS, ONE>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
+    gemv_mfma_body<T, PPT, MS, ONE, X32, XL>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
 }
 
-template <int PPT, int MS>
+template <int PPT, int MS, bool X32 = false, bool XL = false>
 __global__ __launch_bounds__(256) void gemv_mfma_multi_kernel(MultiArgs ma) {
     __shared__ float red[2][4][2][4][4 * MS];
     int q = 0;
     while (q + 1 < ma.n && (int)blockIdx.x >= ma.begin[q + 1]) q++;
     const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
     switch (ma.type[q]) {
-#define C(TT) case TT: gemv_mfma_body<TT, PPT, MS>(ma.p[q], bx, gx, 0, blockIdx.z, gridDim.z, red); break;
+#define C(TT) case TT: gemv_mfma_body<TT, PPT, MS, false, X32, XL>(ma.p[q], bx, gx, 0, blockIdx.z, gridDim.z, red); break;
     C(T_Q4_K) C(T_Q5_K) C(T_Q6_K) C(T_Q8_0) C(T_IQ4_NL) C(T_IQ4_XS)
 #undef C
     default: break;
@@ -1292,7 +1361,11 @@ static int moe_rounds() { const int v = env_int("GGQ_MOE_ROUNDS", 4); return v <
 // multi-row launch).
 struct MfmaPlan {
     int sl2, ppt, ms, n_iters;
+    bool x32, xl;
 };
+// LDS bytes of the staged activation rows (8 float4 slots per piece and row,
+// one pad slot per run quad).
+static size_t mfma_xl_bytes(int K, int ms) { return (size_t)8 * (4 * ms * (K / 32) + 1) * 16; }
 static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
     if (env_int("GGQ_GEMV_MFMA", 1) == 0) return false;
     if (M < (env_int("GGQ_GEMV_MFMA1", 0) ? 1 : 2) || fused(p) || (p.K % 32) != 0 || p.K <= 0) return false;
@@ -1309,6 +1382,16 @@ static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
     const int ms_env = env_int("GGQ_GEMV_MFMA_MS", 0);
     const bool eight = ms_env ? ms_env >= 2 : (p.grp_off && p.groups > 1 && (int64_t)p.M >= 8LL * p.groups);
     m.ms = (M > 4 && m.ppt == 1 && eight) ? 2 : 1;
+    // Plain batches: fp32 activations straight into 4x4x1 fp32 products.
+    // Grouped (expert) launches: the fp16 hi + lo split into 4x4x4 fp16
+    // products, faster there.  GGQ_GEMV_MFMA32=0 / 1 forces either.
+    m.x32 = env_int("GGQ_GEMV_MFMA32", p.grp_off ? 0 : 1) != 0;
+    // Rows staged in LDS once per workgroup when two or more row groups of
+    // the workgroup would read the same activations (K <= 1024);
+    // GGQ_GEMV_MFMA_XL=0 / 2 never / always (where the layout allows).
+    const int xl_env = env_int("GGQ_GEMV_MFMA_XL", 1);
+    m.xl = xl_env != 0 && (xl_env == 2 || m.sl2 <= 5) && !p.grp_off && !p.x_idx && (uintptr_t)p.X % 16 == 0 &&
+           p.ldx % 4 == 0 && P >= 2 && mfma_xl_bytes(p.K, m.ms) <= 60 * 1024;
     const int rows_per_iter = 4 * (64 / S);
     m.n_iters = (p.N + rows_per_iter - 1) / rows_per_iter;
     return true;
@@ -1364,6 +1447,25 @@ static GemvPlan plan_gemv(const GemvProblem& p) {
     return g;
 }
 
+template <int T, int PPT, int MS, bool ONE>
+static void launch_mfma_one(const GemvArgs& a, const MfmaPlan& mp, int K, int groups, int gz, hipStream_t s) {
+    void (*k)(GemvArgs) = mp.x32 ? (mp.xl ? gemv_mfma_kernel<T, PPT, MS, ONE, true, true> : gemv_mfma_kernel<T, PPT, MS, ONE, true, false>)
+                                 : (mp.xl ? gemv_mfma_kernel<T, PPT, MS, ONE, false, true> : gemv_mfma_kernel<T, PPT, MS, ONE, false, false>);
+    const size_t lds = mp.xl ? mfma_xl_bytes(K, MS) : 0;
+    int gx = resident_blocks(k, lds) * (groups > 1 ? moe_rounds() : 1) / (gz * groups);
+    if (groups > 1 && moe_gx() > 0) gx = moe_gx();
+    gx = gx < 1 ? 1 : (gx > mp.n_iters ? mp.n_iters : gx);
+    hipLaunchKernelGGL(k, dim3(gx, groups, gz), dim3(256), lds, s, a);
+}
+
+template <int PPT, int MS>
+static void launch_mfma_multi(const MultiArgs& mm, const MfmaPlan* mp, int n, int kmax, int gz, hipStream_t s) {
+    void (*k)(MultiArgs) = mp[0].x32 ? (mp[0].xl ? gemv_mfma_multi_kernel<PPT, MS, true, true> : gemv_mfma_multi_kernel<PPT, MS, true, false>)
+                                     : (mp[0].xl ? gemv_mfma_multi_kernel<PPT, MS, false, true> : gemv_mfma_multi_kernel<PPT, MS, false, false>);
+    const size_t lds = mp[0].xl ? mfma_xl_bytes(kmax, MS) : 0;
+    hipLaunchKernelGGL(k, dim3(mm.begin[n], 1, gz), dim3(256), lds, s, mm);
+}
+
 template <int T>
 static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
     const GemvPlan g = plan_gemv(p);
@@ -1384,20 +1486,12 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
             // Grouped: one workgroup row per group, each looping over its
             // own row sets (as the FMA kernels' grouped launches).
             const int gz = groups > 1 ? 1 : (mrows + 4 * mp.ms - 1) / (4 * mp.ms);
-#define GM(PPT_, MS_, ONE_)                                                                       \
-    do {                                                                                          \
-        int gx = resident_blocks(gemv_mfma_kernel<T, PPT_, MS_, ONE_>, 0) * (groups > 1 ? moe_rounds() : 1) / (gz * groups); \
-        if (groups > 1 && moe_gx() > 0) gx = moe_gx();                                            \
-        gx = gx < 1 ? 1 : (gx > mp.n_iters ? mp.n_iters : gx);                                    \
-        gemv_mfma_kernel<T, PPT_, MS_, ONE_><<<dim3(gx, groups, gz), 256, 0, s>>>(a);             \
-    } while (0)
             if (mrows == 1) {
-                if (mp.ppt == 2) GM(2, 1, true);
-                else GM(1, 1, true);
-            } else if (mp.ppt == 2) GM(2, 1, false);
-            else if (mp.ms == 2) GM(1, 2, false);
-            else GM(1, 1, false);
-#undef GM
+                if (mp.ppt == 2) launch_mfma_one<T, 2, 1, true>(a, mp, p.K, groups, gz, s);
+                else launch_mfma_one<T, 1, 1, true>(a, mp, p.K, groups, gz, s);
+            } else if (mp.ppt == 2) launch_mfma_one<T, 2, 1, false>(a, mp, p.K, groups, gz, s);
+            else if (mp.ms == 2) launch_mfma_one<T, 1, 2, false>(a, mp, p.K, groups, gz, s);
+            else launch_mfma_one<T, 1, 1, false>(a, mp, p.K, groups, gz, s);
             return hipGetLastError();
         }
     }
@@ -1531,12 +1625,18 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
         MfmaPlan mp[kMaxMulti];
         bool all = M >= 2;
         for (int i = 0; all && i < n; i++) all = mfma_plan(ps[i], M, mp[i]) && mp[i].ppt == mp[0].ppt && mp[i].ms == mp[0].ms;
+        int kmax = 0;
+        for (int i = 0; all && i < n; i++) {
+            mp[0].xl = mp[0].xl && mp[i].xl;
+            kmax = ps[i].K > kmax ? ps[i].K : kmax;
+        }
         if (all) {
             MultiArgs mm;
             const int ms = mp[0].ms, pp = mp[0].ppt;
             const int gz = (M + 4 * ms - 1) / (4 * ms);
-            int tgt = pp == 2 ? resident_blocks(gemv_mfma_multi_kernel<2, 1>, 0)
-                              : (ms == 2 ? resident_blocks(gemv_mfma_multi_kernel<1, 2>, 0) : resident_blocks(gemv_mfma_multi_kernel<1, 1>, 0));
+            const size_t lds = mp[0].xl ? mfma_xl_bytes(kmax, ms) : 0;
+            int tgt = pp == 2 ? resident_blocks(gemv_mfma_multi_kernel<2, 1>, lds)
+                              : (ms == 2 ? resident_blocks(gemv_mfma_multi_kernel<1, 2>, lds) : resident_blocks(gemv_mfma_multi_kernel<1, 1>, lds));
             tgt = tgt / gz > 0 ? tgt / gz : 1;
             int tot = 0;
             for (int i = 0; i < n; i++) tot += mp[i].n_iters;
@@ -1552,10 +1652,9 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
             }
             mm.begin[n] = b;
             mm.n = n;
-            const dim3 grid(b, 1, gz);
-            if (pp == 2) gemv_mfma_multi_kernel<2, 1><<<grid, 256, 0, s>>>(mm);
-            else if (ms == 2) gemv_mfma_multi_kernel<1, 2><<<grid, 256, 0, s>>>(mm);
-            else gemv_mfma_multi_kernel<1, 1><<<grid, 256, 0, s>>>(mm);
+            if (pp == 2) launch_mfma_multi<2, 1>(mm, mp, n, kmax, gz, s);
+            else if (ms == 2) launch_mfma_multi<1, 2>(mm, mp, n, kmax, gz, s);
+            else launch_mfma_multi<1, 1>(mm, mp, n, kmax, gz, s);
             return hipGetLastError();
         }
     }
