@@ -658,8 +658,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
     for (int mc = bz * MB; mc < mcount; mc += gz * MB) {
         Raw ra[U][PPT], rb[U][PPT];
         int it = bx;
-        // The first weight fetch is issued before the activations are read.
-        gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
+        // Without staging the first weight fetch is issued before the
+        // activations are read.
+        if constexpr (!XL) gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
         float xr[PPT][MB][32];
         float xs[PPT][MB][2];
         if constexpr (XL) {
@@ -667,20 +668,41 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
             // staged in LDS as float4 slots s = 8 p' + ... transposed to
             // s = j P + p (j = 4 r + quad of run r of piece p): the stores
             // and each lane's reads of its pieces are consecutive 16-byte
-            // words across lanes (no bank conflicts).
+            // words across lanes (no bank conflicts).  Its loads (8 P <= 1024
+            // slots, at most 4 per thread) are all issued before the weight
+            // fetch: loads complete in issue order, so the LDS stores wait
+            // only for the (cache-resident) activations, not for the weights.
             extern __shared__ float4 xl[];
             if (mc != bz * MB) __syncthreads();  // the previous chunk's row is read by every wavefront
             const float* xp = a.X + (int64_t)(m0 + mc) * a.ldx;
-            for (int sl = tid; sl < 8 * P; sl += 256) {
-                const int j = (int)__umulhi((uint32_t)sl, a.p_div);
-                const int p = sl - j * P;
-                const int k = Piece<T>::run_k(p, j >> 2) + 4 * (j & 3);
-                float4 v = *(const float4*)(xp + k);
-                if (F && a.X2) {  // SwiGLU's product: silu(gate) (already applied) * up, main.cpp:3474-3477
-                    const float4 u = *(const float4*)(a.X2 + (int64_t)(m0 + mc) * a.ldx + k);
-                    v = make_float4(__fmul_rn(v.x, u.x), __fmul_rn(v.y, u.y), __fmul_rn(v.z, u.z), __fmul_rn(v.w, u.w));
+            // (Unconditional loads, slots past the row reading slot 0: a
+            // branch around a load makes the compiler wait for every load
+            // in flight.)
+            float4 xv[4], uv[4];
+            const int nq = (8 * P + 255) >> 8;  // (uniform)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                if (q == 0 || q < nq) {
+                    const int sl = tid + 256 * q < 8 * P ? tid + 256 * q : 0;
+                    const int j = (int)__umulhi((uint32_t)sl, a.p_div);
+                    const int p = sl - j * P;
+                    const int k = Piece<T>::run_k(p, j >> 2) + 4 * (j & 3);
+                    xv[q] = *(const float4*)(xp + k);
+                    if (F && a.X2) uv[q] = *(const float4*)(a.X2 + (int64_t)(m0 + mc) * a.ldx + k);
                 }
-                xl[sl] = v;
+            }
+            gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int sl = tid + 256 * q;
+                if (sl < 8 * P) {
+                    float4 v = xv[q];
+                    if (F && a.X2) {  // SwiGLU's product: silu(gate) (already applied) * up, main.cpp:3474-3477
+                        const float4 u = uv[q];
+                        v = make_float4(__fmul_rn(v.x, u.x), __fmul_rn(v.y, u.y), __fmul_rn(v.z, u.z), __fmul_rn(v.w, u.w));
+                    }
+                    xl[sl] = v;
+                }
             }
             __syncthreads();
 #pragma unroll
@@ -952,7 +974,7 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
             }
         };
         int it = bx;
-        fetch(ra, it);
+        if constexpr (!XL) fetch(ra, it);
 
         // Activations of this lane's row (j + 4t) at its pieces.
         float x[PPT][MS][32];
@@ -965,18 +987,31 @@ __device__ __forceinline__ void gemv_mfma_body(const GemvArgs& a, int bx, int gx
             // as float4 slot (j8, p, m) at j8 (4 MS P + 1) + 4 MS p + m, with
             // j8 = 4 r + quad of run r of piece p: each lane's reads of its
             // (piece, row) are consecutive slots across the wavefront.
+            // P <= 32: at most 4 MS slots per thread, all loaded (rows past
+            // the batch and slots past the rows reading row 0 / slot 0,
+            // without a branch) before the weight fetch, so that the LDS
+            // stores wait only for them (loads complete in issue order).
             extern __shared__ float4 xls[];
             constexpr int R4 = 4 * MS;
             const int pstride = R4 * P + 1;
             if (mc != bz * 4 * MS) __syncthreads();  // every wavefront has read the previous rows
-            for (int sl = tid; sl < 8 * R4 * P; sl += 256) {
-                const int j8 = sl & 7, rest = sl >> 3;
+            float4 xv[R4];
+#pragma unroll
+            for (int q = 0; q < R4; q++) {
+                const int sl = tid + 256 * q < 8 * R4 * P ? tid + 256 * q : 0, rest = sl >> 3;
                 const int mrow = (int)__umulhi((uint32_t)rest, a.p_div);
                 const int p = rest - mrow * P;
-                const int k = Piece<T>::run_k(p, j8 >> 2) + 4 * (j8 & 3);
-                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (mc + mrow < mcount) v = *(const float4*)(a.X + (int64_t)(mc + mrow) * a.ldx + k);
-                xls[j8 * pstride + p * R4 + mrow] = v;
+                const int k = Piece<T>::run_k(p, (sl & 7) >> 2) + 4 * (sl & 3);
+                xv[q] = *(const float4*)(a.X + (int64_t)(mc + mrow < mcount ? mc + mrow : 0) * a.ldx + k);
+            }
+            fetch(ra, it);
+#pragma unroll
+            for (int q = 0; q < R4; q++) {
+                const int sl = tid + 256 * q, rest = sl >> 3;
+                const int mrow = (int)__umulhi((uint32_t)rest, a.p_div);
+                const int p = rest - mrow * P;
+                if (sl < 8 * R4 * P)
+                    xls[(sl & 7) * pstride + p * R4 + mrow] = mc + mrow < mcount ? xv[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
             __syncthreads();
 #pragma unroll
@@ -1388,10 +1423,9 @@ static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
     m.x32 = env_int("GGQ_GEMV_MFMA32", p.grp_off ? 0 : 1) != 0;
     // Rows staged in LDS once per workgroup when two or more row groups of
     // the workgroup would read the same activations (K <= 1024);
-    // GGQ_GEMV_MFMA_XL=0 / 2 never / always (where the layout allows).
-    const int xl_env = env_int("GGQ_GEMV_MFMA_XL", 1);
-    m.xl = xl_env != 0 && (xl_env == 2 || m.sl2 <= 5) && !p.grp_off && !p.x_idx && (uintptr_t)p.X % 16 == 0 &&
-           p.ldx % 4 == 0 && P >= 2 && mfma_xl_bytes(p.K, m.ms) <= 60 * 1024;
+    // GGQ_GEMV_MFMA_XL=0 never.
+    m.xl = env_int("GGQ_GEMV_MFMA_XL", 1) != 0 && P >= 2 && P <= 32 && !p.grp_off && !p.x_idx && (uintptr_t)p.X % 16 == 0 &&
+           p.ldx % 4 == 0;
     const int rows_per_iter = 4 * (64 / S);
     m.n_iters = (p.N + rows_per_iter - 1) / rows_per_iter;
     return true;

@@ -4,8 +4,8 @@ GGQ_GEMV_MBCAP 2 / 4; GGQ_MOE_MB 1 / 4 (the grouped default being 2); the
 matrix-core kernel with 8 rows per pass (GGQ_GEMV_MFMA_MS=2) and for a
 single row (GGQ_GEMV_MFMA1=1); its fp16 hi + lo products for plain batches
 and fp32 products for expert groups (GGQ_GEMV_MFMA32=0 / 1), and its
-activation rows read per wavefront or staged in LDS at every K
-(GGQ_GEMV_MFMA_XL=0 / 2); per-row int8 decode without the int8
+activation rows read per wavefront instead of staged in LDS
+(GGQ_GEMV_MFMA_XL=0); per-row int8 decode without the int8
 matrix-core GEMV (GGQ_GEMV_I8=0: quantize, dequantize, fp32 kernel) and
 fp32 launches of every size on it (GGQ_I8_MIN_BYTES=0).  The
 library reads these knobs at each multi-row / grouped launch, so the checks
@@ -68,7 +68,7 @@ def test_mfma_eight_rows_per_pass(ctx, orc, mfma_knob, M):
     t.test_batched_rows_gemv(ctx, orc, M)
 
 
-@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA32", "0"), ("GGQ_GEMV_MFMA_XL", "0"), ("GGQ_GEMV_MFMA_XL", "2")],
+@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA32", "0"), ("GGQ_GEMV_MFMA_XL", "0")],
                          indirect=True)
 @pytest.mark.parametrize("M", [2, 5, 8, 16])
 def test_mfma_product_and_staging(ctx, orc, mfma_knob, M):
