@@ -374,7 +374,18 @@ struct I8Prob {
     float* Y;
     int ldy;
     int kw_log2;        // wavefronts per tile
-    int x_vec4;         // X rows 16-byte aligned
+    int x_vec4;         // X (and X2) rows 16-byte aligned
+    // Fused neighbours (modes 0 and 1; zero / null = off), as the fp32
+    // kernels apply them: the activation is X * X2, then RMSNorm'd
+    // (x * (1 / sqrt(sum(x^2) / K + eps)) * norm_w); the output is
+    // silu(result), then R + result.
+    const float* X2;
+    const float* norm_w;
+    const float* R;
+    int ldr;
+    int rms, silu;
+    float eps;
+    int nw_vec4;        // norm_w 16-byte aligned
 };
 
 constexpr int kMaxProbs = 8;
@@ -400,13 +411,14 @@ template <int T, int D, int NE, int NP> struct Geo {
 //    last: E = D*M + 1 per (t, g);
 //  * group sums S[chunk][slot s][row m][mfma t] (floats);
 //  * per-row scale and exponent; the reduction buffer (two tiles' worth, by
-//    parity); the per-wavefront row maxima.
+//    parity); the per-wavefront row maxima and sums of squares; the per-row
+//    RMSNorm factor.
 __host__ __device__ inline int i8_entries(int D, int M) { return D * M + 1; }
 __host__ __device__ inline int i8_lds_a(int K, int D, int M) { return (K / 64) * 4 * i8_entries(D, M) * 16; }
 __host__ __device__ inline int i8_lds_s(int K, int G, int M) { return (K / 256) * G * M * 4 * 4; }
 __host__ __device__ inline int i8_lds_red(int MT) { return 2 * kWaves * MT * 16 * 4; }
 __host__ __device__ inline int i8_lds_total(int K, int G, int D, int M, int MT) {
-    return i8_lds_a(K, D, M) + (D == 3 ? 2 : 1) * i8_lds_s(K, G, M) + M * 8 + i8_lds_red(MT) + kWaves * M * 4;
+    return i8_lds_a(K, D, M) + (D == 3 ? 2 : 1) * i8_lds_s(K, G, M) + M * 8 + i8_lds_red(MT) + 2 * kWaves * M * 4 + M * 4;
 }
 
 // Fixed-point digits of one value: X = rint(x 2^e) + 0x808080 as bytes
@@ -432,6 +444,12 @@ __device__ __forceinline__ int8_t code_i8(float v) {
     float r = __builtin_rintf(v);
     r = fminf(fmaxf(r, -128.0f), 127.0f);
     return (int8_t)(int)r;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -471,7 +489,9 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
     // in flight): [row m][local output row]
     const int iters_wg = (n_it - bx + gx - 1) / gx;
     const int ROWS = iters_wg * TPI * 16;
-    float* outl = wmax + kWaves * M;
+    float* wss = wmax + kWaves * M;      // per-wavefront sums of squares (RMSNorm)
+    float* row_is = wss + kWaves * M;    // per-row RMSNorm factor
+    float* outl = row_is + M;
 
     const Rsrc rs = make_rsrc(a.W, (uint32_t)N * a.row_bytes);
     // Chunk offset of a (tile iteration, chunk) position: rows past N read
@@ -530,9 +550,68 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
             load_hex(m, x, v);
         }
     };
+    // Fused inputs: the product with X2, then (norm = true) the RMSNorm
+    // factor and weights, rounded as the fp32 kernels round them.
+    auto load16 = [&](const float* p, bool vec, float (&u)[16]) __attribute__((always_inline)) {
+        if (vec) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 f = *(const float4*)(p + 4 * q);
+                u[4 * q] = f.x; u[4 * q + 1] = f.y; u[4 * q + 2] = f.z; u[4 * q + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; k++) u[k] = p[k];
+        }
+    };
+    auto fuse_in = [&](int m, int x, float (&v)[16], bool norm) __attribute__((always_inline)) {
+        if (a.X2) {
+            float u[16];
+            load16(a.X2 + (int64_t)m * a.ldx + 16 * x, a.x_vec4, u);
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = __fmul_rn(v[k], u[k]);
+        }
+        if (norm && a.rms) {
+            const float is = row_is[m];
+            float u[16];
+            if (a.norm_w) {
+                load16(a.norm_w + 16 * x, a.nw_vec4, u);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 16; k++) u[k] = 1.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = __fmul_rn(__fmul_rn(v[k], is), u[k]);
+        }
+    };
     Raw r0, r1, r2;
     r0 = IF<T>::fetch(rs, chunk_off(itf, jf), g, s_out);
     adv(itf, jf);
+
+    // phase 0 (RMSNorm): each row's sum of squares over the workgroup, then
+    // its factor 1 / sqrt(sum / K + eps) (cpu_ref.cpp:139-156)
+    if (a.rms) {
+        for (int m = 0; m < M; m++) {
+            float ss = 0.0f;
+            for (int x = tid; x < n_hex; x += kThreads) {
+                float v[16];
+                get_hex(m, x, v);
+                fuse_in(m, x, v, false);
+#pragma unroll
+                for (int k = 0; k < 16; k++) ss = fmaf(v[k], v[k], ss);
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) wss[w * M + m] = ss;
+        }
+        __syncthreads();
+        if (tid < M) {
+            float t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kWaves; k++) t += wss[k * M + tid];
+            row_is[tid] = 1.0f / sqrtf(t / (float)K + a.eps);
+        }
+        __syncthreads();
+    }
 
     // phase 1 (int8 codes only): row maxima, the reference's per-row scale
     if (mode == 1) {
@@ -541,6 +620,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
             for (int x = tid; x < n_hex; x += kThreads) {
                 float v[16];
                 get_hex(m, x, v);
+                fuse_in(m, x, v, true);
 #pragma unroll
                 for (int k = 0; k < 16; k++) mx = fmaxf(mx, fabsf(v[k]));
             }
@@ -582,6 +662,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
             } else {
                 float v[16];
                 get_hex(m, x, v);
+                fuse_in(m, x, v, true);
                 if (mode == 0) {
                     // the group's power of two: its largest magnitude in [2^21, 2^22)
                     float mx = 0.0f;
@@ -792,7 +873,12 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
         const int m = idx / ROWS, rl = idx % ROWS;
         const int j = rl / (TPI * 16), tr = rl % (TPI * 16);
         const int n = (bx + j * gx) * TPI * 16 + tr;
-        if (n < N) a.Y[(int64_t)m * a.ldy + n] = outl[idx];
+        if (n < N) {
+            float v = outl[idx];
+            if (a.silu) v = v / (1.0f + expf(-v));  // cpu_ref.cpp:200-209
+            if (a.R) v = a.R[(int64_t)m * a.ldr + n] + v;
+            a.Y[(int64_t)m * a.ldy + n] = v;
+        }
     }
 }
 
@@ -952,7 +1038,8 @@ bool i8_gemv_eligible(const GemvProblem* ps, int n, int mode) {
     for (int i = 0; i < n; i++) {
         const GemvProblem& p = ps[i];
         if (p.M != ps[0].M || !supported(p.type)) return false;
-        if (p.grp_off || p.W2 || p.n1 > 0 || p.X2 || p.rms || p.R || p.silu) return false;
+        if (p.grp_off || p.W2 || p.n1 > 0) return false;
+        if (mode == 2 && (p.X2 || p.rms || p.R || p.silu)) return false;  // fused options apply to fp32 inputs
         if (p.K % 256 != 0 || p.K <= 0 || p.N <= 0 || p.groups > 1) return false;
         if (p.N * row_bytes(p.type, p.K) >= (int64_t)kOOB) return false;  // buffer offsets below kOOB
     }
@@ -998,7 +1085,15 @@ hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* 
         p.SA = sa;
         p.Y = g.Y;
         p.ldy = g.ldy;
-        p.x_vec4 = g.X && ((uintptr_t)g.X % 16 == 0) && (g.ldx % 4 == 0);
+        p.x_vec4 = g.X && ((uintptr_t)g.X % 16 == 0) && (g.ldx % 4 == 0) && ((uintptr_t)g.X2 % 16 == 0);
+        p.X2 = g.X2;
+        p.norm_w = g.norm_w;
+        p.nw_vec4 = (uintptr_t)g.norm_w % 16 == 0;
+        p.R = g.R;
+        p.ldr = g.ldr;
+        p.rms = g.rms;
+        p.silu = g.silu;
+        p.eps = g.eps;
         lds_need[i] = i8_lds_bytes(g.K, M, g4_format(g.type), sh);  // each format's own geometry
         if (lds_need[i] > kMaxLds) return hipErrorInvalidValue;
     }

@@ -62,8 +62,9 @@ struct GemvProblem {
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t s);
 // Several independent M = 1 problems in as few launches as possible.
 hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s);
-// Decode-sized matmuls (1..8 activation rows, K a multiple of 256, no
-// fused options, no grouping) on the int8 matrix cores (ggq_gemv_i8.hip).
+// Decode-sized matmuls (1..8 activation rows, K a multiple of 256, the
+// fused options in modes 0 and 1, no grouping, no pairs) on the int8
+// matrix cores (ggq_gemv_i8.hip).
 // mode 0: fp32 activations X (exact fixed-point digits); mode 1: X
 // quantized per row to int8 in the kernel (GGQ_ACT_Q8_ROW semantics);
 // mode 2: given int8 codes qa [M][K] with row scales sa.  Several problems

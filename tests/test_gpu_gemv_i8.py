@@ -8,7 +8,9 @@ through the C ABI for 1..8 activation rows and K a multiple of 256:
   pre-quantized entry point (ggq_mul_mat_q8_dev), 1..8 rows: the two agree
   bit for bit and meet the bar against the oracle's Q8_ROW treatment;
 * several problems of mixed formats in one launch (ggq_mul_mat_batch_dev);
-* every split of a tile's K over wavefronts (GGQ_I8_KW, read per launch).
+* every split of a tile's K over wavefronts (GGQ_I8_KW, read per launch);
+* the fused options (RMSNorm prologue, product input, silu epilogue,
+  residual add) through ggq_mul_mat_fused_dev.
 """
 import ctypes
 import os
@@ -158,3 +160,51 @@ def test_batch_act_q8_row(ctx, orc, M):
     ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, descs, len(specs), M, stream_handle()), "batch rows")
     for r, y in zip(ref, f32):
         assert np.array_equal(host(r[5]).view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [1, 2, 3])
+@pytest.mark.parametrize("K", [1024, 2048, 8192])
+def test_i8_fused_rmsnorm_and_residual(ctx, orc, M, K):
+    """The fused options on the int8 matrix-core GEMV (every launch of any
+    size takes it here): RMSNorm prologue (one row's sum of squares over the
+    workgroup) on q/k/v-like entries and a residual add in place."""
+    from tests.test_gpu_parity import test_fused_rmsnorm_qkv_and_residual
+    test_fused_rmsnorm_qkv_and_residual(ctx, orc, M, K)
+
+
+@pytest.mark.parametrize("t,K", [(14, 8192), (23, 1024), (13, 3072), (12, 2048)])
+def test_i8_fused_swiglu(ctx, orc, t, K):
+    """silu epilogue next to a plain entry, then the product input with and
+    without the residual, on the int8 matrix-core GEMV."""
+    from tests.test_gpu_parity import test_fused_swiglu
+    test_fused_swiglu(ctx, orc, t, K)
+
+
+def test_i8_fused_unaligned_and_default_norm(ctx, orc):
+    """RMSNorm without weights (norm_w null) and with weights, on activation
+    rows that are not 16-byte aligned (the scalar loads), against the
+    oracle."""
+    import torch
+    from tests.test_gpu_parity import _fused_ref
+    M, N, K = 2, 200, 2048
+    rng = np.random.default_rng(5)
+    A = (rng.standard_normal((M, K)) * 3.0).astype(np.float32)
+    raw = weights(12, N, K, seed=5)
+    nw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    dW = dev(raw)
+    Abuf = torch.zeros(M * K + 1, device="cuda")
+    Av = Abuf[1:].view(M, K)
+    Av.copy_(torch.from_numpy(A))
+    nbuf = torch.from_numpy(nw).cuda()
+    for norm in (None, nbuf):
+        d = (gl.GemvFusedDesc * 1)()
+        C = torch.full((M, N), float("nan"), device="cuda")
+        d[0].W, d[0].type, d[0].N, d[0].K = dW.data_ptr(), 12, N, K
+        d[0].A, d[0].C = Av.data_ptr(), C.data_ptr()
+        d[0].rms_norm, d[0].rms_eps = 1, 1e-5
+        if norm is not None:
+            d[0].rms_w = norm.data_ptr()
+        ctx.check(ctx.lib.ggq_mul_mat_fused_dev(ctx.h, d, 1, M, stream_handle()), "fused")
+        ref = _fused_ref(orc, dict(A=A, type=12, W=raw, N=N, K=K, rms=True, eps=1e-5,
+                                   rms_w=None if norm is None else nw), M)
+        assert orc.rel_l2(host(C), ref) < TOL
