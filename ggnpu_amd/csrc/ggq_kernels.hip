@@ -678,7 +678,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
             // (Unconditional loads, slots past the row reading slot 0: a
             // branch around a load makes the compiler wait for every load
             // in flight.)
-            float4 xv[4], uv[4];
+            float4 xv[4], uv[F ? 4 : 1];
             const int nq = (8 * P + 255) >> 8;  // (uniform)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -688,7 +688,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
                     const int p = sl - j * P;
                     const int k = Piece<T>::run_k(p, j >> 2) + 4 * (j & 3);
                     xv[q] = *(const float4*)(xp + k);
-                    if (F && a.X2) uv[q] = *(const float4*)(a.X2 + (int64_t)(m0 + mc) * a.ldx + k);
+                    if (F && a.X2) uv[F ? q : 0] = *(const float4*)(a.X2 + (int64_t)(m0 + mc) * a.ldx + k);
                 }
             }
             gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
@@ -698,7 +698,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
                 if (sl < 8 * P) {
                     float4 v = xv[q];
                     if (F && a.X2) {  // SwiGLU's product: silu(gate) (already applied) * up, main.cpp:3474-3477
-                        const float4 u = uv[q];
+                        const float4 u = uv[F ? q : 0];
                         v = make_float4(__fmul_rn(v.x, u.x), __fmul_rn(v.y, u.y), __fmul_rn(v.z, u.z), __fmul_rn(v.w, u.w));
                     }
                     xl[sl] = v;
@@ -1351,14 +1351,15 @@ static int gemv_prefetch() {
 static bool fused(const GemvProblem& p) { return p.rms || p.X2 || p.R || p.silu; }
 
 // Single-row launches stage the activation row in LDS once per workgroup
-// (K <= 8192, 16-byte aligned rows) instead of every wavefront reading it
-// from memory; GGQ_GEMV_XLDS=0 selects the per-wavefront loads.
+// (K <= 4096, at most 4 slots per thread; 16-byte aligned rows) instead of
+// every wavefront reading it from memory; GGQ_GEMV_XLDS=0 selects the
+// per-wavefront loads.
 static bool gemv_xlds(const GemvProblem& p, const GemvArgs& a) {
     static int v = [] {
         const char* e = getenv("GGQ_GEMV_XLDS");
         return e && *e ? atoi(e) : 1;
     }();
-    return v != 0 && p.M <= 1 && !p.grp_off && !p.x_idx && a.x_vec4 && a.lpr_log2 < 8 && p.K >= 64 && p.K <= 8192 && p.K % 32 == 0;
+    return v != 0 && p.M <= 1 && !p.grp_off && !p.x_idx && a.x_vec4 && a.lpr_log2 < 8 && p.K >= 64 && p.K <= 4096 && p.K % 32 == 0;
 }
 
 static int gemv_max_lpr() {
