@@ -193,9 +193,15 @@ int mul_mat_queue(ggq_ctx* c, Arena& ar, const void* W, uint32_t type, int64_t N
         return hip_status(c, ggq::launch_gemv(g, s), "gemv");
     }
     if (act_mode == GGQ_ACT_Q8_ROW && M <= 8) {
-        // Decode-sized: the int8 matrix-core GEMV quantizes the rows itself.
+        // Decode-sized: one row below 16 MB of weights on the LDS-staged fp32
+        // kernel with the row quantized in its staging; otherwise the int8
+        // matrix-core GEMV quantizes the rows itself.
         g.X = A;
         g.ldx = lda;
+        if (ggq::gemv_q8row_eligible(&g, 1)) {
+            g.q8row = 1;
+            return hip_status(c, ggq::launch_gemv(g, s), "gemv_q8row");
+        }
         if (ggq::i8_gemv_eligible(&g, 1, 1))
             return hip_status(c, ggq::launch_i8_gemv(&g, 1, 1, nullptr, nullptr, s), "gemv_i8");
     }
@@ -696,6 +702,10 @@ int ggq_mul_mat_batch_act_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, int M, 
     hipStream_t s = pick_stream(c, stream);
     // Per-row int8 decode rows: one matrix-core launch quantizes and
     // multiplies every entry; otherwise one queued matmul per entry.
+    if (act_mode == GGQ_ACT_Q8_ROW && M == 1 && ggq::gemv_q8row_eligible(ps, n)) {
+        for (int i = 0; i < n; i++) ps[i].q8row = 1;
+        return hip_status(c, ggq::launch_gemv_multi(ps, n, s), "gemv_q8row batch");
+    }
     if (act_mode == GGQ_ACT_Q8_ROW && M <= 8 && ggq::i8_gemv_eligible(ps, n, 1))
         return hip_status(c, ggq::launch_i8_gemv(ps, n, 1, nullptr, nullptr, s), "gemv_i8 batch");
     Arena ar = dev_arena(c, s);

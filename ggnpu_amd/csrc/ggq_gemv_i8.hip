@@ -1038,7 +1038,7 @@ bool i8_gemv_eligible(const GemvProblem* ps, int n, int mode) {
     for (int i = 0; i < n; i++) {
         const GemvProblem& p = ps[i];
         if (p.M != ps[0].M || !supported(p.type)) return false;
-        if (p.grp_off || p.W2 || p.n1 > 0) return false;
+        if (p.grp_off || p.W2 || p.n1 > 0 || p.q8row) return false;
         if (mode == 2 && (p.X2 || p.rms || p.R || p.silu)) return false;  // fused options apply to fp32 inputs
         if (p.K % 256 != 0 || p.K <= 0 || p.N <= 0 || p.groups > 1) return false;
         if (p.N * row_bytes(p.type, p.K) >= (int64_t)kOOB) return false;  // buffer offsets below kOOB

@@ -377,6 +377,10 @@ struct GemvArgs {
     const uint8_t* W2;
     float* Y2;
     int n1;
+    // Per-row int8 activations (GGQ_ACT_Q8_ROW, LDS-staged single-row
+    // launches): the staging replaces the row by its codes q = clamp(rint(x /
+    // s)), s = max|x| / 127, and the outputs are scaled by s.
+    int q8row;
 };
 
 // Weight row `row` of a (group's) matrix, or of the paired one.  With no
@@ -400,6 +404,20 @@ __device__ __forceinline__ float group_sum(float v, int lg) {
     if (lg >= 5) v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));  // xor 16
     if (lg >= 6) v += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
     return v;
+}
+
+// Largest value over the wavefront (lane 0 holds it), the steps of
+// group_sum with max.
+template <int CTRL> __device__ __forceinline__ float dpp_maxc(float v) {
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ float wave_max_lane0(float v) {
+    v = dpp_maxc<0xB1>(v);
+    v = dpp_maxc<0x4E>(v);
+    v = dpp_maxc<0x141>(v);
+    v = dpp_maxc<0x140>(v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)));
 }
 
 // Fetches are unconditional: out-of-range rows / pieces read row 0 / piece 0
@@ -443,7 +461,7 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
                                           const uint8_t* W, const uint8_t* W2, int it, int stride, int n_iters, int rpi, int lp, int lpr,
                                           int P, int wave, int lane, int rsub, int m0, int mc, int mcount,
                                           const float (&xr)[PPT][MB][32], const float (&xs)[PPT][MB][2],
-                                          float (&red)[2][4][U * MB], int& parity) {
+                                          float (&red)[2][4][U * MB], int& parity, float q8s) {
     float acc[U][MB];
     // The writer lane reads its residual values first, so their latency
     // overlaps the row's decode and reduction.
@@ -540,6 +558,7 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
                 for (int m = 0; m < MB; m++)
                     if (mc + m < mcount) {
                         float v = acc[u][m];
+                        if (!F && a.q8row) v = v * q8s;  // the row's int8 scale
                         if (F && a.silu) v = v / (1.0f + expf(-v));  // cpu_ref.cpp:200-209
                         const int64_t mrow = m0 + mc + m;
                         if (F && a.R) v = res[u][m] + v;
@@ -654,6 +673,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
     const int stride = gx;
     const int step = U * stride;
     int parity = 0;
+    float q8s = 1.0f;  // per-row int8 activations: the row's scale
 
     for (int mc = bz * MB; mc < mcount; mc += gz * MB) {
         Raw ra[U][PPT], rb[U][PPT];
@@ -692,11 +712,33 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
                 }
             }
             gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
+            float q8inv = 0.0f;
+            if (!F && a.q8row) {
+                // The row's largest magnitude over the workgroup, then the
+                // reference's per-row scale and codes (amd_xdna.cpp:598-603,
+                // 633-639): s = max / 127, q = clamp(rint(x * (1 / s))).
+                __shared__ float q8max[4];
+                float mx = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if ((q == 0 || q < nq) && tid + 256 * q < 8 * P)
+                        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[q].x), fabsf(xv[q].y)), fmaxf(fabsf(xv[q].z), fabsf(xv[q].w))));
+                mx = wave_max_lane0(mx);
+                if (lane == 0) q8max[wave] = mx;
+                __syncthreads();
+                const float amax = fmaxf(fmaxf(q8max[0], q8max[1]), fmaxf(q8max[2], q8max[3]));
+                q8s = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+                q8inv = __fdiv_rn(1.0f, q8s);
+            }
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int sl = tid + 256 * q;
                 if (sl < 8 * P) {
                     float4 v = xv[q];
+                    if (!F && a.q8row) {
+                        auto code = [&](float x) { return fminf(fmaxf(__builtin_rintf(__fmul_rn(x, q8inv)), -128.0f), 127.0f); };
+                        v = make_float4(code(v.x), code(v.y), code(v.z), code(v.w));
+                    }
                     if (F && a.X2) {  // SwiGLU's product: silu(gate) (already applied) * up, main.cpp:3474-3477
                         const float4 u = uv[F ? q : 0];
                         v = make_float4(__fmul_rn(v.x, u.x), __fmul_rn(v.y, u.y), __fmul_rn(v.z, u.z), __fmul_rn(v.w, u.w));
@@ -787,7 +829,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
             // other resident wavefronts.
             while (true) {
                 gemv_rows<T, MB, PPT, U, F>(ra, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc,
-                                         mcount, xr, xs, red, parity);
+                                         mcount, xr, xs, red, parity, q8s);
                 it += step;
                 if (it >= n_iters) break;
                 gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
@@ -799,12 +841,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
         while (it < n_iters) {
             gemv_fetch<T, PPT, U>(rb, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
             gemv_rows<T, MB, PPT, U, F>(ra, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
-                                     xr, xs, red, parity);
+                                     xr, xs, red, parity, q8s);
             it += step;
             if (it >= n_iters) break;
             gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
             gemv_rows<T, MB, PPT, U, F>(rb, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
-                                     xr, xs, red, parity);
+                                     xr, xs, red, parity, q8s);
             it += step;
         }
     }
@@ -1403,7 +1445,7 @@ struct MfmaPlan {
 // one pad slot per run quad).
 static size_t mfma_xl_bytes(int K, int ms) { return (size_t)8 * (4 * ms * (K / 32) + 1) * 16; }
 static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
-    if (env_int("GGQ_GEMV_MFMA", 1) == 0) return false;
+    if (env_int("GGQ_GEMV_MFMA", 1) == 0 || p.q8row) return false;
     if (M < (env_int("GGQ_GEMV_MFMA1", 0) ? 1 : 2) || fused(p) || (p.K % 32) != 0 || p.K <= 0) return false;
     if (p.grp_off && env_int("GGQ_MOE_MFMA", 1) == 0) return false;
     const int P = p.K / 32;
@@ -1476,6 +1518,7 @@ static GemvPlan plan_gemv(const GemvProblem& p) {
     a.W2 = (const uint8_t*)p.W2;
     a.Y2 = p.Y2;
     a.n1 = p.n1;
+    a.q8row = p.q8row;
     g.ppt = (P + lpr - 1) / lpr;
     g.n_iters = (p.N + rpi - 1) / rpi;
     g.mrows = p.grp_off ? p.max_group_rows : p.M;
@@ -1566,6 +1609,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
         gemv_kernel<T, 1, PPT_, 1, true, true><<<dim3(gx, 1, 1), 256, lds, s>>>(a);              \
     } while (0)
+    if (p.q8row && !(groups == 1 && u == 1 && !fused(p) && gemv_xlds(p, a))) return hipErrorInvalidValue;
     if (groups == 1 && fused(p) && gemv_xlds(p, a)) {
         if (ppt == 1) GO_FX(1);
         else if (ppt == 2) GO_FX(2);
@@ -1706,6 +1750,8 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     const int gz = (M + mb - 1) / mb;
     kq = kq && ppt == 1 && mb == 1 && u == 1;  // the variants compiled with KQ
     xl = xl && mb == 1 && u == 1 && M == 1;
+    for (int i = 0; i < n; i++)
+        if (ps[i].q8row && (!xl || any_fused)) return hipErrorInvalidValue;  // quantized in the LDS staging only
     const size_t lds = xl ? (size_t)kmax * sizeof(float) : 0;
     int target;
     if (xl && any_fused) {
@@ -1771,6 +1817,27 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
         else gemv_multi_kernel<2, 2, 1><<<grid, 256, 0, s>>>(ma);
     }
     return hipGetLastError();
+}
+
+// Single-row GGQ_ACT_Q8_ROW problems that the LDS-staged fp32 kernels take
+// with the row quantized in the staging (GemvArgs::q8row): K <= 4096 and a
+// multiple of 32, aligned rows, no fused options or grouping, and together
+// fewer weight bytes than the int8 matrix-core GEMV's threshold (its fixed
+// set-up only pays off above it).
+bool gemv_q8row_eligible(const GemvProblem* ps, int n) {
+    if (n < 1 || n > kMaxMulti || gemv_rows_per_iter() != 1) return false;
+    int64_t bytes = 0;
+    for (int i = 0; i < n; i++) {
+        const GemvProblem& p = ps[i];
+        if (p.M != 1 || !supported(p.type) || fused(p) || p.grp_off || p.x_idx || p.groups > 1 || p.n1 > 0 || p.W2)
+            return false;
+        GemvProblem q = p;
+        q.q8row = 1;
+        const GemvPlan g = plan_gemv(q);
+        if (g.simple || !offsets_fit(p) || !gemv_xlds(p, g.a)) return false;
+        bytes += (int64_t)p.N * row_bytes(p.type, p.K);
+    }
+    return bytes < (int64_t)env_int("GGQ_I8_MIN_BYTES", 16 << 20) && env_int("GGQ_GEMV_Q8XL", 1) != 0;
 }
 
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t s) {

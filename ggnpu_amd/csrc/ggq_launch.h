@@ -58,6 +58,10 @@ struct GemvProblem {
     const void* W2;
     float* Y2;
     int n1;
+    // Single-row GGQ_ACT_Q8_ROW on the LDS-staged fp32 kernels: the row is
+    // replaced by its per-row int8 codes in the staging and the outputs are
+    // scaled back (gemv_q8row_eligible problems only).
+    int q8row;
 };
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t s);
 // Several independent M = 1 problems in as few launches as possible.
@@ -70,6 +74,7 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s);
 // mode 2: given int8 codes qa [M][K] with row scales sa.  Several problems
 // (same M) run as one launch.
 bool i8_gemv_eligible(const GemvProblem* ps, int n, int mode);
+bool gemv_q8row_eligible(const GemvProblem* ps, int n);
 hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* qa, const float* sa, hipStream_t s);
 // Largest K the register-resident GEMV supports.
 constexpr int kGemvMaxK = 32768;

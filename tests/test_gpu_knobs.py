@@ -7,7 +7,9 @@ and fp32 products for expert groups (GGQ_GEMV_MFMA32=0 / 1), and its
 activation rows read per wavefront instead of staged in LDS
 (GGQ_GEMV_MFMA_XL=0); per-row int8 decode without the int8
 matrix-core GEMV (GGQ_GEMV_I8=0: quantize, dequantize, fp32 kernel) and
-fp32 launches of every size on it (GGQ_I8_MIN_BYTES=0).  The
+fp32 launches of every size on it (GGQ_I8_MIN_BYTES=0); single per-row
+int8 rows on it rather than quantized in the fp32 kernel's staging
+(GGQ_GEMV_Q8XL=0).  The
 library reads these knobs at each multi-row / grouped launch, so the checks
 set them in this process and restore them afterwards."""
 import os
@@ -111,7 +113,8 @@ def test_fma_path_batch_invariant(ctx, orc, mfma_knob, ty):
             assert np.array_equal(batch[m].view(np.uint32), alone[0].view(np.uint32)), (M, m)
 
 
-@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_I8", "0"), ("GGQ_I8_MIN_BYTES", "0")], indirect=True)
+@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_I8", "0"), ("GGQ_I8_MIN_BYTES", "0"), ("GGQ_GEMV_Q8XL", "0")],
+                         indirect=True)
 @pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q8_0", "IQ4_XS"])
 def test_i8_gemv_switches(ctx, orc, mfma_knob, name):
     for M in (1, 3):
