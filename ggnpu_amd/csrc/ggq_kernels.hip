@@ -1460,10 +1460,11 @@ static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
     const int ms_env = env_int("GGQ_GEMV_MFMA_MS", 0);
     const bool eight = ms_env ? ms_env >= 2 : (p.grp_off && p.groups > 1 && (int64_t)p.M >= 8LL * p.groups);
     m.ms = (M > 4 && m.ppt == 1 && eight) ? 2 : 1;
-    // Plain batches: fp32 activations straight into 4x4x1 fp32 products.
-    // Grouped (expert) launches: the fp16 hi + lo split into 4x4x4 fp16
-    // products, faster there.  GGQ_GEMV_MFMA32=0 / 1 forces either.
-    m.x32 = env_int("GGQ_GEMV_MFMA32", p.grp_off ? 0 : 1) != 0;
+    // Plain batches of up to 8 rows: fp32 activations straight into 4x4x1
+    // fp32 products.  Grouped (expert) launches and larger batches: the fp16
+    // hi + lo split into 4x4x4 fp16 products (half the MFMA issues per row
+    // set), faster there.  GGQ_GEMV_MFMA32=0 / 1 forces either.
+    m.x32 = env_int("GGQ_GEMV_MFMA32", p.grp_off || M > 8 ? 0 : 1) != 0;
     // Rows staged in LDS once per workgroup when two or more row groups of
     // the workgroup would read the same activations (K <= 1024);
     // GGQ_GEMV_MFMA_XL=0 never.
