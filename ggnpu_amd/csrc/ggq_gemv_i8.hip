@@ -458,7 +458,7 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-template <int T, int D, int NE, int NP>
+template <int T, int D, int NE, int NP, bool FU>
 __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx, uint8_t* lds) {
     typedef Geo<T, D, NE, NP> GEO;
     constexpr int G = GEO::G, RG = GEO::RG, RP = GEO::RP, MT = GEO::MT;
@@ -590,13 +590,13 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
 
     // phase 0 (RMSNorm): each row's sum of squares over the workgroup, then
     // its factor 1 / sqrt(sum / K + eps) (cpu_ref.cpp:139-156)
-    if (a.rms) {
+    if (FU && a.rms) {
         for (int m = 0; m < M; m++) {
             float ss = 0.0f;
             for (int x = tid; x < n_hex; x += kThreads) {
                 float v[16];
                 get_hex(m, x, v);
-                fuse_in(m, x, v, false);
+                if constexpr (FU) fuse_in(m, x, v, false);
 #pragma unroll
                 for (int k = 0; k < 16; k++) ss = fmaf(v[k], v[k], ss);
             }
@@ -620,7 +620,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
             for (int x = tid; x < n_hex; x += kThreads) {
                 float v[16];
                 get_hex(m, x, v);
-                fuse_in(m, x, v, true);
+                if constexpr (FU) fuse_in(m, x, v, true);
 #pragma unroll
                 for (int k = 0; k < 16; k++) mx = fmaxf(mx, fabsf(v[k]));
             }
@@ -662,7 +662,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
             } else {
                 float v[16];
                 get_hex(m, x, v);
-                fuse_in(m, x, v, true);
+                if constexpr (FU) fuse_in(m, x, v, true);
                 if (mode == 0) {
                     // the group's power of two: its largest magnitude in [2^21, 2^22)
                     float mx = 0.0f;
@@ -875,8 +875,8 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
         const int n = (bx + j * gx) * TPI * 16 + tr;
         if (n < N) {
             float v = outl[idx];
-            if (a.silu) v = v / (1.0f + expf(-v));  // cpu_ref.cpp:200-209
-            if (a.R) v = a.R[(int64_t)m * a.ldr + n] + v;
+            if (FU && a.silu) v = v / (1.0f + expf(-v));  // cpu_ref.cpp:200-209
+            if (FU && a.R) v = a.R[(int64_t)m * a.ldr + n] + v;
             a.Y[(int64_t)m * a.ldy + n] = v;
         }
     }
@@ -887,6 +887,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
 enum : int {
     FS_Q4K = 1 << 0, FS_Q5K = 1 << 1, FS_Q6K = 1 << 2, FS_Q80 = 1 << 3, FS_IQ4NL = 1 << 4, FS_IQ4XS = 1 << 5,
     FS_ALL = 63,
+    FS_FUSED = 64,  // compiled with the fused options (fp32 mode)
 };
 __host__ __device__ constexpr int fs_bit(uint32_t t) {
     return t == T_Q4_K ? FS_Q4K : t == T_Q5_K ? FS_Q5K : t == T_Q6_K ? FS_Q6K : t == T_Q8_0 ? FS_Q80
@@ -901,12 +902,12 @@ __global__ __launch_bounds__(kThreads) void i8_gemv_kernel(I8Args args) {
     const int bx = blockIdx.x - args.begin[q], gx = args.begin[q + 1] - args.begin[q];
     const I8Prob& a = args.p[q];
     switch (a.type) {
-    case T_Q4_K: if constexpr ((FS & FS_Q4K) != 0) i8_gemv_body<T_Q4_K, D, NE, NP>(args, a, bx, gx, lds); break;
-    case T_Q5_K: if constexpr ((FS & FS_Q5K) != 0) i8_gemv_body<T_Q5_K, D, NE, NP>(args, a, bx, gx, lds); break;
-    case T_Q6_K: if constexpr ((FS & FS_Q6K) != 0) i8_gemv_body<T_Q6_K, D, NE, NP>(args, a, bx, gx, lds); break;
-    case T_Q8_0: if constexpr ((FS & FS_Q80) != 0) i8_gemv_body<T_Q8_0, D, NE, NP>(args, a, bx, gx, lds); break;
-    case T_IQ4_NL: if constexpr ((FS & FS_IQ4NL) != 0) i8_gemv_body<T_IQ4_NL, D, NE, NP>(args, a, bx, gx, lds); break;
-    case T_IQ4_XS: if constexpr ((FS & FS_IQ4XS) != 0) i8_gemv_body<T_IQ4_XS, D, NE, NP>(args, a, bx, gx, lds); break;
+    case T_Q4_K: if constexpr ((FS & FS_Q4K) != 0) i8_gemv_body<T_Q4_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
+    case T_Q5_K: if constexpr ((FS & FS_Q5K) != 0) i8_gemv_body<T_Q5_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
+    case T_Q6_K: if constexpr ((FS & FS_Q6K) != 0) i8_gemv_body<T_Q6_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
+    case T_Q8_0: if constexpr ((FS & FS_Q80) != 0) i8_gemv_body<T_Q8_0, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
+    case T_IQ4_NL: if constexpr ((FS & FS_IQ4NL) != 0) i8_gemv_body<T_IQ4_NL, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
+    case T_IQ4_XS: if constexpr ((FS & FS_IQ4XS) != 0) i8_gemv_body<T_IQ4_XS, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
     default: break;
     }
 }
@@ -1039,7 +1040,7 @@ bool i8_gemv_eligible(const GemvProblem* ps, int n, int mode) {
         const GemvProblem& p = ps[i];
         if (p.M != ps[0].M || !supported(p.type)) return false;
         if (p.grp_off || p.W2 || p.n1 > 0 || p.q8row) return false;
-        if (mode == 2 && (p.X2 || p.rms || p.R || p.silu)) return false;  // fused options apply to fp32 inputs
+        if (mode != 0 && (p.X2 || p.rms || p.R || p.silu)) return false;  // fused options: fp32 mode only
         if (p.K % 256 != 0 || p.K <= 0 || p.N <= 0 || p.groups > 1) return false;
         if (p.N * row_bytes(p.type, p.K) >= (int64_t)kOOB) return false;  // buffer offsets below kOOB
     }
@@ -1110,6 +1111,21 @@ hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* 
     case FS_Q4K | FS_Q6K: return i8_run<D_, NE_, NP_, FS_Q4K | FS_Q6K>(args, gr, n, s);    \
     case FS_Q80: return i8_run<D_, NE_, NP_, FS_Q80>(args, gr, n, s);                      \
     default: return i8_run<D_, NE_, NP_, FS_ALL>(args, gr, n, s);                          \
+    }
+    bool fused = false;
+    for (int i = 0; i < n; i++) fused = fused || ps[i].X2 || ps[i].rms || ps[i].R || ps[i].silu;
+    if (fused) {
+        if (sh.D != 3) return hipErrorInvalidValue;
+#define RF(NP_)                                                                                    \
+    switch (fs) {                                                                                  \
+    case FS_Q4K: return i8_run<3, 1, NP_, FS_Q4K | FS_FUSED>(args, gr, n, s);                    \
+    case FS_Q6K: return i8_run<3, 1, NP_, FS_Q6K | FS_FUSED>(args, gr, n, s);                    \
+    case FS_Q4K | FS_Q6K: return i8_run<3, 1, NP_, FS_Q4K | FS_Q6K | FS_FUSED>(args, gr, n, s);  \
+    default: return i8_run<3, 1, NP_, FS_ALL | FS_FUSED>(args, gr, n, s);                        \
+    }
+        if (sh.NP == 1) RF(1);
+        RF(2);
+#undef RF
     }
     if (sh.D == 3) {
         if (sh.NP == 1) R(3, 1, 1);

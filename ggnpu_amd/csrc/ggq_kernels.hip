@@ -17,6 +17,7 @@
 #include <stdint.h>
 
 #include <mutex>
+#include <vector>
 
 #include "ggq_device.h"
 #include "ggq_launch.h"
@@ -456,7 +457,7 @@ __device__ __forceinline__ void gemv_fetch(typename Piece<T>::Raw (&raw)[U][PPT]
     }
 }
 
-template <int T, int MB, int PPT, int U, bool F>
+template <int T, int MB, int PPT, int U, bool F, bool Q8 = false>
 __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U][PPT], const GemvArgs& a,
                                           const uint8_t* W, const uint8_t* W2, int it, int stride, int n_iters, int rpi, int lp, int lpr,
                                           int P, int wave, int lane, int rsub, int m0, int mc, int mcount,
@@ -558,7 +559,7 @@ __device__ __forceinline__ void gemv_rows(const typename Piece<T>::Raw (&raw)[U]
                 for (int m = 0; m < MB; m++)
                     if (mc + m < mcount) {
                         float v = acc[u][m];
-                        if (!F && a.q8row) v = v * q8s;  // the row's int8 scale
+                        if constexpr (Q8) v = v * q8s;  // the row's int8 scale
                         if (F && a.silu) v = v / (1.0f + expf(-v));  // cpu_ref.cpp:200-209
                         const int64_t mrow = m0 + mc + m;
                         if (F && a.R) v = res[u][m] + v;
@@ -642,10 +643,11 @@ __device__ __forceinline__ void gemv_rms_norm(const GemvArgs& a, float (&xr)[PPT
 // bz, bz + gz, ... of its activation rows.
 // F: compiled with the fused options (RMSNorm, product input, silu,
 // residual); the plain instantiations carry none of their code.
-template <int T, int MB, int PPT, int U, bool F, bool XL = false>
+template <int T, int MB, int PPT, int U, bool F, bool XL = false, bool Q8 = false>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
                                           float (&red)[2][4][U * MB]) {
     static_assert(!XL || MB == 1, "LDS-staged activations: one activation row per pass");
+    static_assert(!Q8 || (XL && !F), "per-row int8 codes are formed in the LDS staging of the plain kernels");
     if constexpr (XL) {
         // Every kernel argument the launch reads, in one round of scalar
         // loads: left to itself the compiler loads them next to their first
@@ -713,7 +715,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
             }
             gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
             float q8inv = 0.0f;
-            if (!F && a.q8row) {
+            if constexpr (Q8) {
                 // The row's largest magnitude over the workgroup, then the
                 // reference's per-row scale and codes (amd_xdna.cpp:598-603,
                 // 633-639): s = max / 127, q = clamp(rint(x * (1 / s))).
@@ -735,7 +737,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
                 const int sl = tid + 256 * q;
                 if (sl < 8 * P) {
                     float4 v = xv[q];
-                    if (!F && a.q8row) {
+                    if constexpr (Q8) {
                         auto code = [&](float x) { return fminf(fmaxf(__builtin_rintf(__fmul_rn(x, q8inv)), -128.0f), 127.0f); };
                         v = make_float4(code(v.x), code(v.y), code(v.z), code(v.w));
                     }
@@ -828,7 +830,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
             // Fetch, then decode/multiply/reduce; latency is hidden by the
             // other resident wavefronts.
             while (true) {
-                gemv_rows<T, MB, PPT, U, F>(ra, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc,
+                gemv_rows<T, MB, PPT, U, F, Q8>(ra, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc,
                                          mcount, xr, xs, red, parity, q8s);
                 it += step;
                 if (it >= n_iters) break;
@@ -840,19 +842,19 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
         // decode/multiply/reduce the current ones.
         while (it < n_iters) {
             gemv_fetch<T, PPT, U>(rb, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
-            gemv_rows<T, MB, PPT, U, F>(ra, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
+            gemv_rows<T, MB, PPT, U, F, Q8>(ra, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
                                      xr, xs, red, parity, q8s);
             it += step;
             if (it >= n_iters) break;
             gemv_fetch<T, PPT, U>(ra, W, a.row_bytes, it + step, stride, n_iters, rpi, rsub, a.N, lp, lpr, P, W2, a.n1);
-            gemv_rows<T, MB, PPT, U, F>(rb, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
+            gemv_rows<T, MB, PPT, U, F, Q8>(rb, a, W, W2, it, stride, n_iters, rpi, lp, lpr, P, wave, lane, rsub, m0, mc, mcount,
                                      xr, xs, red, parity, q8s);
             it += step;
         }
     }
 }
 
-template <int T, int MB, int PPT, int U, bool F = false, bool XL = false>
+template <int T, int MB, int PPT, int U, bool F = false, bool XL = false, bool Q8 = false>
 // Two rows per pass: held to 3 wavefronts per SIMD (168 VGPRs; Q4_K spills
 // a few registers), where the natural allocation gave 2.  That variant is
 // the MoE default (each expert sees ~2 tokens: the decoded codes are shared).
@@ -876,7 +878,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MB == 2 ? 3
             }
         }
     }
-    gemv_body<T, MB, PPT, U, F, XL>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
+    gemv_body<T, MB, PPT, U, F, XL, Q8>(a, blockIdx.x, gridDim.x, blockIdx.y, blockIdx.z, gridDim.z, red);
 }
 
 // Several independent GEMV problems (any mix of formats, same pieces-per-
@@ -894,7 +896,7 @@ struct MultiArgs {
 // KQ: compiled for Q4_K and Q6_K only (the Q4_K_M decode levels), so the
 // register budget is not set by the other formats' decoders (Q5_K's needs
 // one more wavefront's worth of VGPRs than Q4_K's).
-template <int MB, int PPT, int U, bool F = false, bool KQ = false, bool XL = false>
+template <int MB, int PPT, int U, bool F = false, bool KQ = false, bool XL = false, bool Q8 = false>
 __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     __shared__ float red[2][4][U * MB];
     int q = 0;
@@ -902,17 +904,17 @@ __global__ __launch_bounds__(256) void gemv_multi_kernel(MultiArgs ma) {
     const int bx = blockIdx.x - ma.begin[q], gx = ma.begin[q + 1] - ma.begin[q];
     const int bz = blockIdx.z, gz = gridDim.z;
     if constexpr (KQ) {
-        if (ma.type[q] == T_Q4_K) gemv_body<T_Q4_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red);
-        else gemv_body<T_Q6_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red);
+        if (ma.type[q] == T_Q4_K) gemv_body<T_Q4_K, MB, PPT, U, F, XL, Q8>(ma.p[q], bx, gx, 0, bz, gz, red);
+        else gemv_body<T_Q6_K, MB, PPT, U, F, XL, Q8>(ma.p[q], bx, gx, 0, bz, gz, red);
         return;
     }
     switch (ma.type[q]) {
-    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
-    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U, F, XL>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q4_K: gemv_body<T_Q4_K, MB, PPT, U, F, XL, Q8>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q5_K: gemv_body<T_Q5_K, MB, PPT, U, F, XL, Q8>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q6_K: gemv_body<T_Q6_K, MB, PPT, U, F, XL, Q8>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_Q8_0: gemv_body<T_Q8_0, MB, PPT, U, F, XL, Q8>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_IQ4_NL: gemv_body<T_IQ4_NL, MB, PPT, U, F, XL, Q8>(ma.p[q], bx, gx, 0, bz, gz, red); break;
+    case T_IQ4_XS: gemv_body<T_IQ4_XS, MB, PPT, U, F, XL, Q8>(ma.p[q], bx, gx, 0, bz, gz, red); break;
     default: break;
     }
 }
@@ -1363,12 +1365,24 @@ static int device_cus() {
     return v;
 }
 
+// Resident 256-thread workgroups per CU of a kernel at an LDS size, asked
+// of the runtime once per (kernel, LDS size) and thread: the occupancy query
+// costs about as much host time as a launch.
+static int occupancy_per_cu(const void* kernel, size_t lds) {
+    struct Entry { const void* k; size_t lds; int v; };
+    thread_local std::vector<Entry> cache;
+    for (const Entry& e : cache)
+        if (e.k == kernel && e.lds == lds) return e.v;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) != hipSuccess || per_cu <= 0) per_cu = 1;
+    cache.push_back({kernel, lds, per_cu});
+    return per_cu;
+}
+
 template <typename K>
 static int resident_blocks(K kernel, size_t lds) {
     if (gemv_blocks_override() > 0) return gemv_blocks_override();
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds) != hipSuccess || per_cu <= 0) per_cu = 1;
-    return per_cu * device_cus();
+    return occupancy_per_cu((const void*)kernel, lds) * device_cus();
 }
 
 // Row-iterations processed together per wavefront (their loads are issued
@@ -1599,9 +1613,10 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
 #define GO_X(PPT_)                                                                               \
     do {                                                                                         \
         const size_t lds = (size_t)p.K * sizeof(float);                                          \
-        int gx = resident_blocks(gemv_kernel<T, 1, PPT_, 1, false, true>, lds);                  \
+        void (*k_)(GemvArgs) = p.q8row ? gemv_kernel<T, 1, PPT_, 1, false, true, true> : gemv_kernel<T, 1, PPT_, 1, false, true>; \
+        int gx = resident_blocks(k_, lds);                                                       \
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
-        gemv_kernel<T, 1, PPT_, 1, false, true><<<dim3(gx, 1, 1), 256, lds, s>>>(a);             \
+        hipLaunchKernelGGL(k_, dim3(gx, 1, 1), dim3(256), lds, s, a);                            \
     } while (0)
 #define GO_FX(PPT_)                                                                              \
     do {                                                                                         \
@@ -1751,8 +1766,9 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     const int gz = (M + mb - 1) / mb;
     kq = kq && ppt == 1 && mb == 1 && u == 1;  // the variants compiled with KQ
     xl = xl && mb == 1 && u == 1 && M == 1;
+    const bool q8 = ps[0].q8row != 0;
     for (int i = 0; i < n; i++)
-        if (ps[i].q8row && (!xl || any_fused)) return hipErrorInvalidValue;  // quantized in the LDS staging only
+        if ((ps[i].q8row != 0) != q8 || (q8 && (!xl || any_fused))) return hipErrorInvalidValue;  // quantized in the LDS staging only
     const size_t lds = xl ? (size_t)kmax * sizeof(float) : 0;
     int target;
     if (xl && any_fused) {
@@ -1793,6 +1809,10 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
         if (kq) gemv_multi_kernel<1, 1, 1, true, true, true><<<grid, 256, lds, s>>>(ma);
         else if (ppt == 1) gemv_multi_kernel<1, 1, 1, true, false, true><<<grid, 256, lds, s>>>(ma);
         else gemv_multi_kernel<1, 2, 1, true, false, true><<<grid, 256, lds, s>>>(ma);
+    } else if (xl && q8) {
+        if (kq) gemv_multi_kernel<1, 1, 1, false, true, true, true><<<grid, 256, lds, s>>>(ma);
+        else if (ppt == 1) gemv_multi_kernel<1, 1, 1, false, false, true, true><<<grid, 256, lds, s>>>(ma);
+        else gemv_multi_kernel<1, 2, 1, false, false, true, true><<<grid, 256, lds, s>>>(ma);
     } else if (xl) {
         if (kq) gemv_multi_kernel<1, 1, 1, false, true, true><<<grid, 256, lds, s>>>(ma);
         else if (ppt == 1) gemv_multi_kernel<1, 1, 1, false, false, true><<<grid, 256, lds, s>>>(ma);
@@ -2696,8 +2716,7 @@ GemmPlan plan_gemm_i8(uint32_t type, const int* Ns, int n, int K, int M) {
     if (type != T_Q6_K) {
         const void* k = gemm_kernel_for(type);
         int per_cu = 0;
-        if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 256, 0) != hipSuccess || per_cu <= 0)
-            per_cu = 1;
+        per_cu = k ? occupancy_per_cu(k, 0) : 1;
         pl.splits = choose_splits((int64_t)pl.n_tiles * pl.m_tiles, nsteps, per_cu * device_cus());
     }
     pl.steps_per_split = (nsteps + pl.splits - 1) / pl.splits;
