@@ -920,3 +920,41 @@ def test_produce_quant_rejects_bad_arguments(ctx):
         st = ctx.lib.ggq_produce_quantize_act_dev(ctx.h, producer, ptr(A), aux, 1024, 2, 1024, 1e-5, ptr(q), ptr(s),
                                                   stream_handle())
         assert st == gl.Status.INVALID_PARAM
+
+
+def test_q8_row_staged_batch_and_edges(ctx, orc):
+    """Single per-row-int8 rows below 16 MB run the LDS-staged fp32 kernels
+    with the row quantized in their staging: one ggq_mul_mat_batch_act_dev
+    call over mixed formats (one launch) and single calls on a zero row, a
+    row with one non-zero value and rows of extreme magnitude, against the
+    oracle's per-row int8 treatment."""
+    import torch
+    specs = [(12, 2048, 2048), (14, 512, 2048), (20, 300, 1024), (8, 96, 96), (23, 64, 4096)]
+    rng = np.random.default_rng(21)
+    keep, descs, ref = [], (gl.GemvDesc * len(specs))(), []
+    for i, (t, N, K) in enumerate(specs):
+        raw = weights(t, N, K, seed=90 + i)
+        A = rng.standard_normal((1, K)).astype(np.float32)
+        dW, dA = dev(raw), dev(A)
+        dC = torch.full((1, N), float("nan"), device="cuda")
+        keep += [dW, dA, dC]
+        descs[i].W, descs[i].type, descs[i].N, descs[i].K = dW.data_ptr(), t, N, K
+        descs[i].A, descs[i].C = dA.data_ptr(), dC.data_ptr()
+        ref.append((t, raw, N, K, A, dC))
+    ctx.check(ctx.lib.ggq_mul_mat_batch_act_dev(ctx.h, descs, len(specs), 1, 1, stream_handle()), "batch act")
+    for t, raw, N, K, A, dC in ref:
+        assert orc.rel_l2(host(dC), orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL, (t, N, K)
+    t, N, K = 12, 256, 2048
+    raw = weights(t, N, K, seed=3)
+    one = np.zeros(K, np.float32)
+    one[1234] = -2.5
+    rows = [np.zeros(K, np.float32), one, rng.standard_normal(K).astype(np.float32) * 1e30,
+            rng.standard_normal(K).astype(np.float32) * 1e-30]
+    for r in rows:
+        A = r[None, :]
+        got = run_mm(ctx, t, raw, N, K, A, 1)
+        want = orc.mul_mat_f64(t, raw, N, K, A, 1)
+        if not np.any(want):
+            assert not np.any(got)
+        else:
+            assert orc.rel_l2(got, want) < TOL
