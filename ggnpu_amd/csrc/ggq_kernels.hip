@@ -647,7 +647,7 @@ template <int T, int MB, int PPT, int U, bool F, bool XL = false, bool Q8 = fals
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int by, int bz, int gz,
                                           float (&red)[2][4][U * MB]) {
     static_assert(!XL || MB == 1, "LDS-staged activations: one activation row per pass");
-    static_assert(!Q8 || (XL && !F), "per-row int8 codes are formed in the LDS staging of the plain kernels");
+    static_assert(!Q8 || (!F && MB == 1), "per-row int8 codes: plain single-row kernels");
     if constexpr (XL) {
         // Every kernel argument the launch reads, in one round of scalar
         // loads: left to itself the compiler loads them next to their first
@@ -814,6 +814,29 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int bx, int gx, int
             }
         }
         if (F && a.rms) gemv_rms_norm<T, MB, PPT>(a, xr, lp, lpr, P, wave, lane, rsub, mc, mcount);
+        if constexpr (Q8 && !XL) {
+            // Per-row int8 codes of the row held in registers: every row
+            // group of the workgroup holds all of the row's pieces, so the
+            // workgroup's largest magnitude is the row's (amd_xdna.cpp:598-603,
+            // 633-639: s = max / 127, q = clamp(rint(x * (1 / s)))).
+            __shared__ float q8max[4];
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PPT; i++)
+#pragma unroll
+                for (int j = 0; j < 32; j++) mx = fmaxf(mx, fabsf(xr[i][0][j]));
+            mx = wave_max_lane0(mx);
+            if (mc != bz * MB) __syncthreads();  // the previous row's maxima are read
+            if (lane == 0) q8max[wave] = mx;
+            __syncthreads();
+            const float amax = fmaxf(fmaxf(q8max[0], q8max[1]), fmaxf(q8max[2], q8max[3]));
+            q8s = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+            const float inv = __fdiv_rn(1.0f, q8s);
+#pragma unroll
+            for (int i = 0; i < PPT; i++)
+#pragma unroll
+                for (int j = 0; j < 32; j++) xr[i][0][j] = fminf(fmaxf(__builtin_rintf(__fmul_rn(xr[i][0][j], inv)), -128.0f), 127.0f);
+        }
 #pragma unroll
         for (int i = 0; i < PPT; i++)
 #pragma unroll
@@ -1625,7 +1648,20 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
         gemv_kernel<T, 1, PPT_, 1, true, true><<<dim3(gx, 1, 1), 256, lds, s>>>(a);              \
     } while (0)
-    if (p.q8row && !(groups == 1 && u == 1 && !fused(p) && gemv_xlds(p, a))) return hipErrorInvalidValue;
+    if (p.q8row && !(groups == 1 && u == 1 && !fused(p) && mrows == 1 && ppt <= 4)) return hipErrorInvalidValue;
+    if (p.q8row && !gemv_xlds(p, a)) {  // the row quantized in registers (non-staged kernels)
+#define GQ(PPT_)                                                                                 \
+    do {                                                                                         \
+        int gx = resident_blocks(gemv_kernel<T, 1, PPT_, 1, false, false, true>, 0);             \
+        gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
+        gemv_kernel<T, 1, PPT_, 1, false, false, true><<<dim3(gx, 1, 1), 256, 0, s>>>(a);        \
+    } while (0)
+        if (ppt == 1) GQ(1);
+        else if (ppt == 2) GQ(2);
+        else GQ(4);
+#undef GQ
+        return hipGetLastError();
+    }
     if (groups == 1 && fused(p) && gemv_xlds(p, a)) {
         if (ppt == 1) GO_FX(1);
         else if (ppt == 2) GO_FX(2);
@@ -1768,7 +1804,14 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     xl = xl && mb == 1 && u == 1 && M == 1;
     const bool q8 = ps[0].q8row != 0;
     for (int i = 0; i < n; i++)
-        if ((ps[i].q8row != 0) != q8 || (q8 && (!xl || any_fused))) return hipErrorInvalidValue;  // quantized in the LDS staging only
+        if ((ps[i].q8row != 0) != q8 || (q8 && any_fused)) return hipErrorInvalidValue;
+    if (q8 && !xl) {  // the non-staged kernels quantize the row per launch
+        for (int i = 0; i < n; i++) {
+            const hipError_t e = launch_gemv(ps[i], s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     const size_t lds = xl ? (size_t)kmax * sizeof(float) : 0;
     int target;
     if (xl && any_fused) {
@@ -1840,11 +1883,11 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Single-row GGQ_ACT_Q8_ROW problems that the LDS-staged fp32 kernels take
-// with the row quantized in the staging (GemvArgs::q8row): K <= 4096 and a
-// multiple of 32, aligned rows, no fused options or grouping, and together
-// fewer weight bytes than the int8 matrix-core GEMV's threshold (its fixed
-// set-up only pays off above it).
+// Single-row GGQ_ACT_Q8_ROW problems that the fp32 kernels take with the row
+// quantized in their LDS staging or, for rows they do not stage (K > 4096,
+// unaligned rows), in registers (GemvArgs::q8row): K a multiple of 32, no
+// fused options or grouping, and together fewer weight bytes than the int8
+// matrix-core GEMV's threshold (its fixed set-up only pays off above it).
 bool gemv_q8row_eligible(const GemvProblem* ps, int n) {
     if (n < 1 || n > kMaxMulti || gemv_rows_per_iter() != 1) return false;
     int64_t bytes = 0;
@@ -1855,7 +1898,7 @@ bool gemv_q8row_eligible(const GemvProblem* ps, int n) {
         GemvProblem q = p;
         q.q8row = 1;
         const GemvPlan g = plan_gemv(q);
-        if (g.simple || !offsets_fit(p) || !gemv_xlds(p, g.a)) return false;
+        if (g.simple || g.ppt > 4 || !offsets_fit(p)) return false;
         bytes += (int64_t)p.N * row_bytes(p.type, p.K);
     }
     return bytes < (int64_t)env_int("GGQ_I8_MIN_BYTES", 16 << 20) && env_int("GGQ_GEMV_Q8XL", 1) != 0;

@@ -958,3 +958,17 @@ def test_q8_row_staged_batch_and_edges(ctx, orc):
             assert not np.any(got)
         else:
             assert orc.rel_l2(got, want) < TOL
+
+
+@pytest.mark.parametrize("t,N,K,pad", [(14, 200, 8192, 0), (12, 96, 16384, 0), (20, 128, 2048, 3), (8, 70, 4096, 1)])
+def test_q8_row_in_registers(ctx, orc, t, N, K, pad):
+    """Single per-row-int8 rows that the fp32 kernels do not stage in LDS
+    (K > 4096, or rows that are not 16-byte aligned) are quantized in
+    registers after the workgroup's row maximum: against the oracle's
+    per-row int8 treatment."""
+    raw = weights(t, N, K, seed=K + t)
+    rng = np.random.default_rng(K + pad)
+    for scale in (1.0, 1e20, 1e-20):
+        A = (rng.standard_normal((1, K)) * scale).astype(np.float32)
+        got = run_mm(ctx, t, raw, N, K, A, 1, lda=K + pad)
+        assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL, (scale,)
