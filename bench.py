@@ -517,7 +517,9 @@ QWEN3_LAYERS = 28
 def bench_config4(torch, ctx, stream, steps=40):
     """28 Qwen3-0.6B layers of IQ4_NL / IQ4_XS / Q5_K matmuls with
     batch 1, 4 and 8 fp32 activation rows; one launch per dependency level
-    (q/k/v, o, gate/up, down) through ggq_mul_mat_batch_rows_dev."""
+    (q/k/v, o, gate/up, down) through ggq_mul_mat_batch_rows_dev, called
+    from Python per step ("us") and replayed as one captured HIP graph
+    ("us_graph")."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(4)
     cycle = [IQ4NL, IQ4XS, Q5K]
@@ -542,14 +544,29 @@ def bench_config4(torch, ctx, stream, steps=40):
                 arr[i].A, arr[i].C = m.x.data_ptr(), m.y.data_ptr()
             descs.append((arr, len(lv)))
 
-        def run(M=M, descs=descs):
+        def run_on(st, M=M, descs=descs):
             for arr, n in descs:
-                ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, arr, n, M, stream), "batch rows")
+                ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, arr, n, M, st), "batch rows")
 
-        sec = time_steps(torch, run, steps, 2)
+        sec = time_steps(torch, lambda: run_on(stream), steps, 2)
+        # The same 112 launches captured once as a HIP graph and replayed
+        # (no host enqueue per launch: batch 1 is close to host-bound from
+        # Python otherwise).
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            run_on(ctypes.c_void_p(s.cuda_stream))
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                run_on(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        gsec = time_steps(torch, g.replay, steps, 2)
         b = sum(m.bytes() for m in mats)
         res[f"batch{M}"] = {"bytes": b, "us": round(sec * 1e6, 1), "GBps": round(b / sec / 1e9, 1),
-                            "frac_hbm_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4)}
+                            "frac_hbm_peak": round(b / sec / 1e9 / HBM_PEAK_GBS, 4),
+                            "us_graph": round(gsec * 1e6, 1), "GBps_graph": round(b / gsec / 1e9, 1)}
+        del g
     return res
 
 
