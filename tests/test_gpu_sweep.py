@@ -26,7 +26,7 @@ def _rand_k(rng, ty):
     return int(256 * rng.integers(1, 33))
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(48))
 def test_sweep_mul_mat(ctx, orc, seed):
     rng = np.random.default_rng(1000 + seed)
     ty = int(rng.choice(KQ + SMALL))
@@ -70,6 +70,39 @@ def test_sweep_batched_level(ctx, orc, seed):
     for (ty, N, raw), C in zip(raws, outs):
         err = orc.rel_l2(host(C), orc.mul_mat_f64(ty, raw, N, K, A, 0))
         assert err < TOL, (types, ty, N, K, err)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sweep_batch_act(ctx, orc, seed):
+    """ggq_mul_mat_batch_act_dev over 1-5 matrices sharing one input of 1-8
+    rows, fp32 or per-row int8 activations: the single-row int8 rows
+    quantized inside the fp32 kernels (staged or in registers), the int8
+    matrix-core GEMV, the matrix-core GEMV for several fp32 rows."""
+    import torch
+    rng = np.random.default_rng(4000 + seed)
+    n = int(rng.integers(1, 6))
+    K = int(256 * rng.integers(1, 33))
+    M = 1 if seed % 2 == 0 else int(rng.integers(1, 9))
+    mode = int(rng.integers(0, 2))
+    A = (rng.standard_normal((M, K)) * rng.uniform(0.01, 100)).astype(np.float32)
+    dA = dev(A)
+    descs = (gl.GemvDesc * n)()
+    keep, outs, raws = [], [], []
+    for i in range(n):
+        ty = int(rng.choice(KQ + SMALL))
+        N = int(rng.integers(1, 500))
+        raw = t.weights(ty, N, K, seed=seed * 10 + i)
+        dW = dev(raw)
+        C = torch.full((M, N), float("nan"), device="cuda")
+        keep.append(dW)
+        outs.append(C)
+        raws.append((ty, N, raw))
+        descs[i].W, descs[i].type, descs[i].N, descs[i].K = dW.data_ptr(), ty, N, K
+        descs[i].A, descs[i].C = dA.data_ptr(), C.data_ptr()
+    ctx.check(ctx.lib.ggq_mul_mat_batch_act_dev(ctx.h, descs, n, M, mode, stream_handle()), "batch act")
+    for (ty, N, raw), C in zip(raws, outs):
+        err = orc.rel_l2(host(C), orc.mul_mat_f64(ty, raw, N, K, A, mode))
+        assert err < TOL, (ty, N, K, M, mode, err)
 
 
 @pytest.mark.parametrize("seed", range(8))
