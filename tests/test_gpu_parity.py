@@ -715,7 +715,7 @@ def test_logits_argmax_nan_row_and_errors(ctx):
                                          stream_handle()) == gl.Status.OK
 
 
-# --------------------------------------------- fused GEMV neighbours (§8f)
+# --------------------------------------------- fused GEMV neighbours
 def _fused(ctx, entries, M):
     """entries: dicts with W (raw), type, N, K, A (np [M][K]), optional Aup
     (np [M][K]), rms_w (np [K] or None), rms (bool), eps, residual (np [M][N])."""

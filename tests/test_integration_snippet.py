@@ -1,5 +1,6 @@
-"""The ggnpu-side backend that INTEGRATION.md section 1 shows a maintainer
-adding (src/backends/hip/hip_backend.cpp) compiles against the reference's
+"""The ggnpu-side backend that the repository's integration guide shows a
+maintainer adding (src/backends/hip/hip_backend.cpp; the guide's first C++
+block, read from the file below) compiles against the reference's
 own include/ggnpu/backend.h and links libggq_hip.so; without a device the
 backend reports itself unavailable and mul_mat_q returns NPU_UNAVAILABLE.
 Skipped where the reference tree is absent (the GPU box)."""
