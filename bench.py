@@ -119,12 +119,15 @@ def time_steps(torch, fn, steps, warmup, gpu_time=False):
 
 def back_to_back_times(torch, fns, reps):
     """Mean GPU seconds per call of each callable, from HIP events around
-    `reps` back-to-back calls (the queue stays full, so host submission time
-    is not counted; repeated small weights are partly served from cache)."""
+    `reps` back-to-back calls queued behind a ~1 ms spin kernel, so that the
+    queue is full when the first call starts and host submission time is not
+    counted (repeated small weights are partly served from cache)."""
     out = []
     for fn in fns:
         fn()
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(2_000_000)
         e0.record()
         for _ in range(reps):
             fn()
