@@ -143,9 +143,12 @@ def bench_decode_step(torch, ctx, steps, warmup, use_graph, stream, fuse_levels=
     mats, host_layer0 = [], []
     t0 = time.time()
     for layer in range(LLAMA_LAYERS):
+        # q/k/v read one normed input and gate/up another, as in a forward pass.
+        shared = {n: torch.randn((1, 2048), device="cuda", dtype=torch.float32) for n in ("attn", "ffn")}
         for name, t, N, K in LLAMA_LAYER:
             dev, raw = make_weight(torch, gen, t, N, K)
-            m = Mat(torch, f"blk{layer}.{name}", t, N, K, dev)
+            x = shared["attn"] if name in ("q", "k", "v") else shared["ffn"] if name in ("gate", "up") else None
+            m = Mat(torch, f"blk{layer}.{name}", t, N, K, dev, x=x)
             mats.append(m)
             if layer == 0:
                 host_layer0.append((m, raw))
@@ -534,7 +537,13 @@ def bench_config4(torch, ctx, stream, steps=40):
     res = {"workload": "Qwen3-0.6B shapes x 28 layers, types [IQ4_NL, IQ4_XS, Q5_K][i % 3] over q,k,v,o,gate,up,down",
            "types": {n: gl.GgmlType(t).name for n, t, _, _, _ in layer}}
     for M in (1, 4, 8):
-        mats = [Mat(torch, f"b{M}.{li}.{n}", t, N, K, d, M=M) for li in range(QWEN3_LAYERS) for n, t, N, K, d in weights[li]]
+        mats = []
+        for li in range(QWEN3_LAYERS):
+            # q/k/v share one input (K=1024), gate/up another, as in a forward pass.
+            shared = {n: torch.randn((M, 1024), device="cuda", dtype=torch.float32) for n in ("attn", "ffn")}
+            for n, t, N, K, d in weights[li]:
+                x = shared["attn"] if n in ("q", "k", "v") else shared["ffn"] if n in ("gate", "up") else None
+                mats.append(Mat(torch, f"b{M}.{li}.{n}", t, N, K, d, M=M, x=x))
         levels = []
         for li in range(QWEN3_LAYERS):
             q, k, v, o, g, u, dn = mats[7 * li: 7 * li + 7]
