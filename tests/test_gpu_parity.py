@@ -615,6 +615,37 @@ def test_q8_batch_matches_single_and_oracle(ctx, orc, t):
                                             stream_handle()) == gl.Status.INVALID_PARAM
 
 
+@pytest.mark.parametrize("M,Ns,K", [(512, (1536, 256, 256), 1536), (512, (1536,), 8960), (77, (1000, 33), 4096),
+                                     (130, (64,), 1024)])
+def test_q8_0_split_levels_strided(ctx, orc, M, Ns, K):
+    """Q8_0 levels whose output tiles alone do not fill the chip (prefill
+    q/k/v, o and down at their benchmarked shapes, and ragged shapes) split K
+    over workgroups: every column against the Q8_ROW oracle, the padding
+    columns of a strided C untouched, and repeated calls bitwise identical
+    (the slices are added in slice order)."""
+    import torch
+    t = 8
+    raws = [weights(t, N, K, seed=N + K) for N in Ns]
+    A = np.random.default_rng(M + K).standard_normal((M, K)).astype(np.float32)
+    dA, dq, ds = _quantized(ctx, A)
+    dWs = [dev(r) for r in raws]
+    outs = [torch.full((M, N + 5), float("nan"), device="cuda") for N in Ns]
+    descs = (gl.GemmDesc * len(Ns))(*[gl.GemmDesc(ptr(w), N, ptr(o), N + 5) for w, N, o in zip(dWs, Ns, outs)])
+    first = None
+    for rep in range(2):
+        ctx.check(ctx.lib.ggq_mul_mat_q8_batch_dev(ctx.h, descs, len(Ns), t, K, ptr(dq), ptr(ds), M,
+                                                   stream_handle()), "q8 batch")
+        got = [host(o) for o in outs]
+        if first is None:
+            first = got
+        else:
+            assert all(np.array_equal(a, b, equal_nan=True) for a, b in zip(first, got))
+    for raw, N, g in zip(raws, Ns, first):
+        assert np.all(np.isnan(g[:, N:])), "wrote past N"
+        err = orc.rel_l2(g[:, :N], orc.mul_mat_f64(t, raw, N, K, A, 1))
+        assert err < TOL, (M, N, K, err)
+
+
 def test_gemm_split_k_deterministic(ctx, orc):
     """Long K over few tiles splits K across workgroups; the reduction adds
     slices in a fixed order, so repeated calls are bitwise identical, and a

@@ -435,3 +435,22 @@ def test_flash_attn_matches_reference_and_f64(orc, n_head, n_kv, hd, ctx, qpos):
     assert np.allclose(got64[0], np.einsum("hj,hjd->hd", w, V[:, : qpos + 1]), rtol=1e-10, atol=1e-12)
     if qpos == 0:  # one visible position: the output is V[0] of each head's kv head
         assert np.allclose(got64[0], V[:, 0], rtol=0, atol=1e-15)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_per_row_weight_requant_vs_reference_vectors(orc, golden, name):
+    """A11, the XDNA host's per-row weight requantization (decode_*_for_npu,
+    q8_0.cpp:30-77, q4_k.cpp:43-91, q5_k.cpp, q6_k.cpp:41-89, iq4_nl.cpp:36-82,
+    iq4_xs.cpp:41-87): dequantize the row, scale = max|x| / 127 (1 for an
+    all-zero row), code = clamp(nearbyint(x * (1 / scale))).  The oracle's
+    dequant followed by its per-row activation quantizer (the same rule,
+    amd_xdna.cpp:598-603) reproduces the int8 codes and scales that the
+    compiled reference wrote, bit for bit.  The weights are never requantized
+    on the GPU path; this pins the CPU baseline's host-preparation step."""
+    t = TYPES[name]
+    raw = golden[f"{name}_npu_raw"]
+    N, K = (int(v) for v in golden[f"{name}_npu_shape"])
+    rows = orc.dequant(t, raw).reshape(N, K)
+    q, s = orc.quant_act(rows, 1)
+    assert np.array_equal(s.view(np.uint32), golden[f"{name}_npu_s"].astype(np.float32).view(np.uint32))
+    assert np.array_equal(q.reshape(-1), golden[f"{name}_npu_q"].astype(np.int8))
