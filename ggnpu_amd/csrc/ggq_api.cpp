@@ -764,6 +764,21 @@ int ggq_block_dot_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64
     GGQ_END(c)
 }
 
+// A routed (grouped) expert launch of the fp32 MoE path: on the int8
+// matrix cores when the grouped form takes it (the expert's weights are
+// decoded to int8 codes, about a third of the VALU work per weight of the
+// fp16 matrix-core GEMV), else on the matrix-core / FMA GEMV.  The down
+// projection's groups run in passes of 1-2 rows there, each re-reading the
+// expert's weights, so it stays on the GEMV unless GGQ_MOE_I8_DOWN=1.
+static hipError_t moe_grouped_gemv(const ggq::GemvProblem& g, void* items, size_t items_bytes, hipStream_t s,
+                                   bool down = false) {
+    const char* v = getenv("GGQ_MOE_I8_DOWN");  // read per call: a process can switch it
+    const bool i8_down = v && *v && atoi(v) != 0;
+    if ((!down || i8_down) && ggq::i8_gemv_grouped_eligible(g) && ggq::i8_gemv_grouped_ws_bytes(g) <= items_bytes)
+        return ggq::launch_i8_gemv_grouped(g, items, s);
+    return ggq::launch_gemv(g, s);
+}
+
 // MoE layer with per-row int8 activations (GGQ_ACT_Q8_ROW): route, group,
 // quantize the token rows once, one grouped int8 GEMM for every expert's
 // gate and up (and the shared expert's, as group E), SwiGLU fused into the
@@ -892,6 +907,9 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
                  o_tok = take(4 * nk), o_pos = take(4 * nk), o_g = take(4 * (nk + ts) * F),
                  o_u = take(4 * (nk + ts) * F), o_h = take(4 * (nk + ts) * F), o_d = take(4 * nk * H);
     const size_t o_sd = shared ? take(4 * (size_t)T * H) : 0;
+    // chunk list of the grouped int8 launches (chunks of 2 or more rows)
+    const size_t it_bytes = 8 * ((nk + 1) / 2 + std::min<size_t>((size_t)E, nk)) + 16;
+    const size_t o_it = take(it_bytes);
     if ((st = grow(c, c->dev.ws, off, s, "workspace")) != GGQ_OK) return st;
     hipError_t e;
     char* base = (char*)c->dev.ws.ptr;
@@ -917,12 +935,12 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
         // gate and up of each expert in one launch: each workgroup loads a
         // token's activations once for both.
         g.W2 = p->up_exps; g.Y2 = U; g.n1 = F; g.N = 2 * F;
-        if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe gate+up");
+        if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s)) != hipSuccess) return hip_status(c, e, "moe gate+up");
         g.W2 = nullptr; g.Y2 = nullptr; g.n1 = 0;
     } else {
-        if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe gate");
+        if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s)) != hipSuccess) return hip_status(c, e, "moe gate");
         g.type = p->up_type; g.W = p->up_exps; g.w_group_stride = (int64_t)F * ggq::row_bytes(p->up_type, H); g.Y = U;
-        if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe up");
+        if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s)) != hipSuccess) return hip_status(c, e, "moe up");
     }
     float* Dsh = nullptr;
     ggq::GemvProblem q{};
@@ -948,7 +966,7 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     // down: rows H, K = F, activations are the sorted pair rows themselves.
     g.N = H; g.K = F; g.X = Hh; g.ldx = F; g.x_idx = nullptr; g.ldy = H; g.Y = D;
     g.type = p->down_type; g.W = p->down_exps; g.w_group_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
-    if ((e = ggq::launch_gemv(g, s)) != hipSuccess) return hip_status(c, e, "moe down");
+    if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s, true)) != hipSuccess) return hip_status(c, e, "moe down");
     if (shared) {
         q.N = H; q.K = F; q.X = Hh + nk * F; q.ldx = F; q.ldy = H; q.type = p->down_type; q.W = p->down_shexp; q.Y = Dsh;
         if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared down");

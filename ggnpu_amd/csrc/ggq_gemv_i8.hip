@@ -458,14 +458,17 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// M_ activation rows; row m of the activations is row xrow[m] of X (the
+// row itself when xrow is null) and its outputs go to row yrow0 + m of Y.
 template <int T, int D, int NE, int NP, bool FU>
-__device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx, uint8_t* lds) {
+__device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx, uint8_t* lds, int M_,
+                             const int32_t* xrow, int yrow0) {
     typedef Geo<T, D, NE, NP> GEO;
     constexpr int G = GEO::G, RG = GEO::RG, RP = GEO::RP, MT = GEO::MT;
     typedef typename IF<T>::Raw Raw;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, col = lane & 15;
-    const int M = args.M, K = a.K, N = a.N;
+    const int M = M_, K = a.K, N = a.N;
     const int NC = K >> 8;
     const int KW = 1 << a.kw_log2, TPI = kWaves >> a.kw_log2;
     const int kp = w & (KW - 1), slot_t = w >> a.kw_log2;
@@ -521,7 +524,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
     constexpr int KR = 1;
     float xk[KR][16];
     auto load_hex = [&](int m, int x, float (&v)[16]) __attribute__((always_inline)) {
-        const float* xr = a.X + (int64_t)m * a.ldx + 16 * x;
+        const float* xr = a.X + (int64_t)(xrow ? xrow[m] : m) * a.ldx + 16 * x;
         if (a.x_vec4) {
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -877,7 +880,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
             float v = outl[idx];
             if (FU && a.silu) v = v / (1.0f + expf(-v));  // cpu_ref.cpp:200-209
             if (FU && a.R) v = a.R[(int64_t)m * a.ldr + n] + v;
-            a.Y[(int64_t)m * a.ldy + n] = v;
+            a.Y[(int64_t)(yrow0 + m) * a.ldy + n] = v;
         }
     }
 }
@@ -895,21 +898,83 @@ __host__ __device__ constexpr int fs_bit(uint32_t t) {
 }
 
 template <int D, int NE, int NP, int FS>
+__device__ __forceinline__ void i8_dispatch(const I8Args& args, const I8Prob& a, int bx, int gx, uint8_t* lds, int M,
+                                            const int32_t* xrow, int yrow0) {
+    switch (a.type) {
+    case T_Q4_K: if constexpr ((FS & FS_Q4K) != 0) i8_gemv_body<T_Q4_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds, M, xrow, yrow0); break;
+    case T_Q5_K: if constexpr ((FS & FS_Q5K) != 0) i8_gemv_body<T_Q5_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds, M, xrow, yrow0); break;
+    case T_Q6_K: if constexpr ((FS & FS_Q6K) != 0) i8_gemv_body<T_Q6_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds, M, xrow, yrow0); break;
+    case T_Q8_0: if constexpr ((FS & FS_Q80) != 0) i8_gemv_body<T_Q8_0, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds, M, xrow, yrow0); break;
+    case T_IQ4_NL: if constexpr ((FS & FS_IQ4NL) != 0) i8_gemv_body<T_IQ4_NL, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds, M, xrow, yrow0); break;
+    case T_IQ4_XS: if constexpr ((FS & FS_IQ4XS) != 0) i8_gemv_body<T_IQ4_XS, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds, M, xrow, yrow0); break;
+    default: break;
+    }
+}
+
+template <int D, int NE, int NP, int FS>
 __global__ __launch_bounds__(kThreads) void i8_gemv_kernel(I8Args args) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int q = 0;
     while (q + 1 < args.n && (int)blockIdx.x >= args.begin[q + 1]) q++;
     const int bx = blockIdx.x - args.begin[q], gx = args.begin[q + 1] - args.begin[q];
-    const I8Prob& a = args.p[q];
-    switch (a.type) {
-    case T_Q4_K: if constexpr ((FS & FS_Q4K) != 0) i8_gemv_body<T_Q4_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
-    case T_Q5_K: if constexpr ((FS & FS_Q5K) != 0) i8_gemv_body<T_Q5_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
-    case T_Q6_K: if constexpr ((FS & FS_Q6K) != 0) i8_gemv_body<T_Q6_K, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
-    case T_Q8_0: if constexpr ((FS & FS_Q80) != 0) i8_gemv_body<T_Q8_0, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
-    case T_IQ4_NL: if constexpr ((FS & FS_IQ4NL) != 0) i8_gemv_body<T_IQ4_NL, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
-    case T_IQ4_XS: if constexpr ((FS & FS_IQ4XS) != 0) i8_gemv_body<T_IQ4_XS, D, NE, NP, (FS & FS_FUSED) != 0>(args, a, bx, gx, lds); break;
-    default: break;
+    i8_dispatch<D, NE, NP, FS>(args, args.p[q], bx, gx, lds, args.M, nullptr, 0);
+}
+
+// Grouped launches (MoE experts, fp32 mode): the rows of group e (pair rows
+// grp_off[e] .. grp_off[e+1]-1) are cut into chunks of at most args.M rows;
+// item i = (e, first row) of the device-built chunk list is grid row
+// blockIdx.y.  Its weights are the problem's matrix advanced by e *
+// w_stride bytes, its activation rows X rows x_idx[row] (the row itself
+// when x_idx is null), its outputs Y rows row ..  Grid rows past the list
+// end exit.  Each chunk is a full pass over its group's weights.
+struct I8Group {
+    const int32_t* grp_off;
+    const int32_t* x_idx;
+    int64_t w_stride;
+    const int2* items;
+    const int32_t* n_items;
+};
+
+template <int D, int NE, int NP, int FS>
+__global__ __launch_bounds__(kThreads) void i8_gemv_grouped_kernel(I8Args args, I8Group gp) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    if ((int)blockIdx.y >= *gp.n_items) return;
+    const int2 it = gp.items[blockIdx.y];
+    const int e = it.x, r = it.y;
+    const int end = gp.grp_off[e + 1];
+    const int mc = end - r < args.M ? end - r : args.M;
+    int q = 0;
+    while (q + 1 < args.n && (int)blockIdx.x >= args.begin[q + 1]) q++;
+    const int bx = blockIdx.x - args.begin[q], gx = args.begin[q + 1] - args.begin[q];
+    I8Prob a = args.p[q];
+    a.W += (int64_t)e * gp.w_stride;
+    if (!gp.x_idx) a.X += (int64_t)r * a.ldx;  // the chunk's own rows
+    i8_dispatch<D, NE, NP, FS>(args, a, bx, gx, lds, mc, gp.x_idx ? gp.x_idx + r : nullptr, r);
+}
+
+// The chunk list: one thread per group counts its chunks, a scan over the
+// workgroup places them (groups <= 1024).
+__global__ __launch_bounds__(1024) void i8_chunks_kernel(const int32_t* __restrict__ grp_off, int groups, int mt,
+                                                         int2* __restrict__ items, int32_t* __restrict__ n_items) {
+    __shared__ int cnt[1024];
+    const int tid = threadIdx.x;
+    int mine = 0, r0 = 0;
+    if (tid < groups) {
+        r0 = grp_off[tid];
+        const int rows = grp_off[tid + 1] - r0;
+        mine = rows > 0 ? (rows + mt - 1) / mt : 0;
     }
+    cnt[tid] = mine;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int v = tid >= off ? cnt[tid - off] : 0;
+        __syncthreads();
+        cnt[tid] += v;
+        __syncthreads();
+    }
+    const int first = cnt[tid] - mine;
+    for (int i = 0; i < mine; i++) items[first + i] = make_int2(tid, r0 + mt * i);
+    if (tid == 1023) *n_items = cnt[1023];
 }
 
 int env_i8(const char* name, int dflt) {
@@ -1137,6 +1202,119 @@ hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* 
     default: R(1, 4, 1);
     }
 #undef R
+}
+
+}  // namespace ggq
+
+namespace ggq {
+namespace {
+
+template <int D, int NE, int NP, int FS>
+hipError_t i8_run_grouped(I8Args& args, const I8Group& gp, int groups, int lds, hipStream_t s) {
+    auto kern = i8_gemv_grouped_kernel<D, NE, NP, FS>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        attr_set = true;
+    }
+    kern<<<dim3(args.begin[args.n], groups), kThreads, lds, s>>>(args, gp);  // groups: chunk-list bound
+    return hipGetLastError();
+}
+
+// Shape of a grouped launch: rows per pass, wavefronts per tile and
+// workgroups per problem and group, and the LDS it needs.
+struct I8GroupedPlan { I8Shape sh; int mt, kw_log2, gx, lds; };
+
+bool i8_grouped_plan(const GemvProblem& g, I8GroupedPlan& pl) {
+    const bool q6 = g4_format(g.type);
+    // fp32 mode: two rows per pass (one for four-slot formats), two passes
+    if (!i8_shape(q6 ? 2 : 4, 0, q6, pl.sh)) return false;
+    pl.mt = (q6 ? 1 : 2) * pl.sh.NP;
+    const int nc = g.K / 256;
+    // one workgroup per (problem, chunk), four wavefronts per tile: measured
+    // best at the qwen35moe shape (GGQ_MOE_I8_GX 1 / 2 / 4 / 8: 209 / 223 /
+    // 240 / 250 us per layer; the wavefront count per tile within noise)
+    int kw = env_i8("GGQ_MOE_I8_KW", 4);
+    int k2 = 1;
+    while (2 * k2 <= kw && 2 * k2 <= nc && k2 < kWaves) k2 *= 2;
+    pl.kw_log2 = __builtin_ctz(k2);
+    pl.gx = env_i8("GGQ_MOE_I8_GX", 1);
+    if (pl.gx < 1) pl.gx = 1;
+    const int n1 = g.n1 > 0 ? g.n1 : g.N;
+    const int tiles = (n1 + 15) / 16, tpi = kWaves / k2;
+    const int n_it = (tiles + tpi - 1) / tpi;
+    if (pl.gx > n_it) pl.gx = n_it;
+    const int iters_wg = (n_it + pl.gx - 1) / pl.gx;
+    pl.lds = i8_lds_bytes(g.K, pl.mt, q6, pl.sh) + iters_wg * tpi * 16 * pl.mt * 4;
+    return pl.lds <= kMaxLds;
+}
+
+}  // namespace
+
+// Upper bound of the chunk list: every chunk but the last of a group holds
+// mt rows, and at most min(groups, rows) groups are non-empty.
+static int i8_max_items(const GemvProblem& g, int mt) {
+    return (g.M + mt - 1) / mt + (g.groups < g.M ? g.groups : g.M);
+}
+
+size_t i8_gemv_grouped_ws_bytes(const GemvProblem& g) {
+    I8GroupedPlan pl;
+    if (!i8_grouped_plan(g, pl)) return 0;
+    return 8 * (size_t)i8_max_items(g, pl.mt) + 16;
+}
+
+bool i8_gemv_grouped_eligible(const GemvProblem& g) {
+    if (env_i8("GGQ_MOE_I8", 1) == 0 || env_i8("GGQ_GEMV_MFMA", 1) == 0) return false;
+    if (!g.grp_off || g.groups < 1 || g.groups > 1024 || g.M < 1 || !supported(g.type) || g.K % 256 != 0 || g.K <= 0 || g.N <= 0) return false;
+    if (g.X2 || g.rms || g.R || g.silu || g.q8row) return false;
+    const int n1 = g.n1 > 0 ? g.n1 : g.N;
+    if (g.n1 > 0 && (!g.W2 || !g.Y2 || g.N - g.n1 != g.n1)) return false;  // paired halves of equal size
+    if ((int64_t)n1 * row_bytes(g.type, g.K) >= (int64_t)kOOB) return false;
+    I8GroupedPlan pl;
+    return i8_grouped_plan(g, pl) && i8_max_items(g, pl.mt) <= 65535;
+}
+
+hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s) {
+    I8GroupedPlan pl;
+    if (!i8_grouped_plan(g, pl) || !ws || g.groups > 1024) return hipErrorInvalidValue;
+    const int max_items = i8_max_items(g, pl.mt);
+    int2* items = (int2*)ws;
+    int32_t* n_items = (int32_t*)((char*)ws + 8 * (size_t)max_items);
+    i8_chunks_kernel<<<1, 1024, 0, s>>>(g.grp_off, g.groups, pl.mt, items, n_items);
+    const int n1 = g.n1 > 0 ? g.n1 : g.N;
+    I8Args args{};
+    args.M = pl.mt;
+    args.mode = 0;
+    const int np = g.n1 > 0 ? 2 : 1;
+    for (int i = 0; i < np; i++) {
+        I8Prob& p = args.p[i];
+        p.W = (const uint8_t*)(i == 0 ? g.W : g.W2);
+        p.row_bytes = (uint32_t)row_bytes(g.type, g.K);
+        p.type = g.type;
+        p.N = n1;
+        p.K = g.K;
+        p.X = g.X;
+        p.ldx = g.ldx;
+        p.Y = i == 0 ? g.Y : g.Y2;
+        p.ldy = g.ldy;
+        p.kw_log2 = pl.kw_log2;
+        p.x_vec4 = ((uintptr_t)g.X % 16 == 0) && (g.ldx % 4 == 0);
+        args.begin[i + 1] = args.begin[i] + pl.gx;
+    }
+    args.n = np;
+    I8Group gp{g.grp_off, g.x_idx, g.w_group_stride, items, n_items};
+    const int fs = fs_bit(g.type);
+#define RG(NP_)                                                                                  \
+    switch (fs) {                                                                                \
+    case FS_Q4K: return i8_run_grouped<3, 1, NP_, FS_Q4K>(args, gp, max_items, pl.lds, s);      \
+    case FS_Q6K: return i8_run_grouped<3, 1, NP_, FS_Q6K>(args, gp, max_items, pl.lds, s);      \
+    case FS_Q80: return i8_run_grouped<3, 1, NP_, FS_Q80>(args, gp, max_items, pl.lds, s);      \
+    default: return i8_run_grouped<3, 1, NP_, FS_ALL>(args, gp, max_items, pl.lds, s);          \
+    }
+    if (pl.sh.D != 3) return hipErrorInvalidValue;
+    if (pl.sh.NP == 1) RG(1);
+    RG(2);
+#undef RG
 }
 
 }  // namespace ggq

@@ -76,6 +76,14 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s);
 bool i8_gemv_eligible(const GemvProblem* ps, int n, int mode);
 bool gemv_q8row_eligible(const GemvProblem* ps, int n);
 hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* qa, const float* sa, hipStream_t s);
+// Grouped (MoE) fp32-activation problems on the same kernel (groups <= 1024,
+// g.M = total rows): a group's rows run in chunks of up to 4 (2 for Q6_K /
+// IQ4) rows, one grid row per chunk from a chunk list built on the device;
+// paired gate / up halves are two problems.  `ws`: device workspace of
+// i8_gemv_grouped_ws_bytes(g) bytes.
+bool i8_gemv_grouped_eligible(const GemvProblem& g);
+size_t i8_gemv_grouped_ws_bytes(const GemvProblem& g);
+hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s);
 // Largest K the register-resident GEMV supports.
 constexpr int kGemvMaxK = 32768;
 

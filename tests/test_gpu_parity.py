@@ -393,6 +393,35 @@ def test_moe_other_formats_vs_oracle(ctx, orc, tg, tu, td):
         assert orc.rel_l2(out, ref) < TOL, (tg, tu, td, shared)
 
 
+@pytest.mark.parametrize("tg,tu,td", [(12, 12, 14), (13, 13, 14), (20, 23, 8)])
+@pytest.mark.parametrize("T,E,k", [(40, 16, 4), (7, 64, 8), (96, 4, 2)])
+def test_moe_int8_grouped_launches(ctx, orc, monkeypatch, tg, tu, td, T, E, k):
+    """fp32-activation MoE with the routed projections on the grouped int8
+    GEMV (experts' rows in chunks of 4, or 2 for IQ4 / Q6_K, from a chunk
+    list built on the device; experts with 0, 1 and dozens of rows), against
+    the oracle and against the same layer on the matrix-core GEMV
+    (GGQ_MOE_I8=0); GGQ_MOE_I8_DOWN=1 puts the down projection on it too, and
+    three workgroups per chunk with one wavefront per tile split the rows and
+    K differently."""
+    H, F = 512, 256
+    outs = {}
+    for i8, down, gx, kw in ((0, 0, 1, 4), (1, 0, 1, 4), (1, 1, 1, 4), (1, 1, 3, 1)):
+        monkeypatch.setenv("GGQ_MOE_I8", str(i8))
+        monkeypatch.setenv("GGQ_MOE_I8_DOWN", str(down))
+        monkeypatch.setenv("GGQ_MOE_I8_GX", str(gx))  # workgroups per (problem, chunk)
+        monkeypatch.setenv("GGQ_MOE_I8_KW", str(kw))  # wavefronts per tile
+        for shared in (False, True):
+            (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(
+                ctx, T, H, F, E, k, shared, seed=T + E + tg, tg=tg, tu=tu, td=td)
+            ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, tg, Wg, tu, Wu, td, Wd, Sg, Su, Sd, sw)
+            assert np.array_equal(sel, rsel)
+            assert orc.rel_l2(out, ref) < TOL, (i8, down, gx, kw, shared)
+            outs[(i8, down, gx, shared)] = out
+    for shared in (False, True):
+        for key in ((1, 0, 1), (1, 1, 1), (1, 1, 3)):
+            assert orc.rel_l2(outs[key + (shared,)], outs[(0, 0, 1, shared)]) < TOL, key
+
+
 @pytest.mark.parametrize("E,k", [(64, 8), (100, 6), (128, 8), (500, 8), (1000, 8)])
 def test_moe_routing_expert_counts(ctx, orc, E, k):
     """Routing for every per-lane logit count (1, 2, 4, 8, 16 experts per
