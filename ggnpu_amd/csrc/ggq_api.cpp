@@ -794,6 +794,9 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
                  o_tok = take(4 * rows), o_pos = take(4 * nk), o_qx = take((size_t)T * H), o_sx = take(4 * (size_t)T),
                  o_g = take(4 * rows * F), o_u = take(4 * rows * F), o_qh = take(rows * F), o_sh = take(4 * rows),
                  o_d = take(4 * rows * H), o_tl = take(8 * (size_t)max_tiles), o_nt = take(4);
+    // chunk list of the grouped int8 GEMV (chunks of 4 or more rows)
+    const size_t it_bytes = 8 * ((rows + 3) / 4 + std::min<size_t>((size_t)E + 1, rows)) + 16;
+    const size_t o_it = take(it_bytes);
     int st;
     if ((st = grow(c, c->dev.ws, off, s, "workspace")) != GGQ_OK) return st;
     hipError_t e;
@@ -819,6 +822,19 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         return hip_status(c, e, "quant x");
     ggq::MoeGemm g{};
     g.E = E; g.grp = grp; g.tiles = tiles; g.n_tiles = ntiles; g.max_tiles = max_tiles;
+    // Few rows per expert (decode-sized batches): the grouped int8 GEMV in
+    // its given-codes mode (chunks of 8 rows, 4 for Q6_K / IQ4), whose
+    // lanes carry the rows; more rows per expert: the expert-grouped GEMM's
+    // 32-row tiles (GGQ_MOE_I8_MAX_AVG: largest average rows per group that
+    // takes the GEMV, default 8).
+    const char* avg_env = getenv("GGQ_MOE_I8_MAX_AVG");
+    const size_t max_avg = avg_env && *avg_env ? (size_t)atoi(avg_env) : 8;
+    const bool small = rows <= max_avg * (size_t)(E + (shared ? 1 : 0));
+    auto grouped = [&](uint32_t type) -> hipError_t {
+        if (small && ggq::i8_moe_q8_eligible(type, g, (int)rows) && ggq::i8_moe_q8_ws_bytes(type, g, (int)rows) <= it_bytes)
+            return ggq::launch_i8_moe_q8(type, g, (int)rows, base + o_it, s);
+        return ggq::launch_moe_gemm(type, g, s);
+    };
     // gate and up: K = H, token rows gathered through tok; paired when the
     // types match, else two launches.
     g.K = H; g.QA = qx; g.sa = sx; g.x_idx = tok; g.ldc = F;
@@ -826,14 +842,14 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if (p->up_type == p->gate_type) {
         g.W = p->gate_exps; g.W2 = p->up_exps; g.Wsh = p->gate_shexp; g.W2sh = p->up_shexp;
         g.N = 2 * F; g.n1 = F; g.C = G; g.C2 = U;
-        if ((e = ggq::launch_moe_gemm(p->gate_type, g, s)) != hipSuccess) return hip_status(c, e, "moe gate+up");
+        if ((e = grouped(p->gate_type)) != hipSuccess) return hip_status(c, e, "moe gate+up");
     } else {
         g.W = p->gate_exps; g.W2 = nullptr; g.Wsh = p->gate_shexp; g.W2sh = nullptr;
         g.N = F; g.n1 = F; g.C = G; g.C2 = nullptr;
-        if ((e = ggq::launch_moe_gemm(p->gate_type, g, s)) != hipSuccess) return hip_status(c, e, "moe gate");
+        if ((e = grouped(p->gate_type)) != hipSuccess) return hip_status(c, e, "moe gate");
         g.W = p->up_exps; g.Wsh = p->up_shexp; g.C = U;
         g.w_stride = (int64_t)F * ggq::row_bytes(p->up_type, H);
-        if ((e = ggq::launch_moe_gemm(p->up_type, g, s)) != hipSuccess) return hip_status(c, e, "moe up");
+        if ((e = grouped(p->up_type)) != hipSuccess) return hip_status(c, e, "moe up");
     }
     // SwiGLU of every pair row (routed and shared) and its int8 row codes.
     if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s)) != hipSuccess)
@@ -843,7 +859,7 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     g.W = p->down_exps; g.W2 = nullptr; g.Wsh = p->down_shexp; g.W2sh = nullptr;
     g.w_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
     g.N = H; g.n1 = H; g.C = D; g.C2 = nullptr;
-    if ((e = ggq::launch_moe_gemm(p->down_type, g, s)) != hipSuccess) return hip_status(c, e, "moe down");
+    if ((e = grouped(p->down_type)) != hipSuccess) return hip_status(c, e, "moe down");
     if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, shared ? D + nk * H : nullptr, p->shared_w, p->out, s)) !=
         hipSuccess)
         return hip_status(c, e, "moe combine");

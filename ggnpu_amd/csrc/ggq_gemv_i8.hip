@@ -638,7 +638,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
     for (int m = 0; m < M; m++) {
         float rs_m = 1.0f, inv = 0.0f;
         if (mode == 2) {
-            rs_m = a.SA[m];
+            rs_m = a.SA[xrow ? xrow[m] : m];
         } else if (mode == 1) {
             float amax = 0.0f;
 #pragma unroll
@@ -654,7 +654,7 @@ __device__ void i8_gemv_body(const I8Args& args, const I8Prob& a, int bx, int gx
             uint4 pl[3];
             float gsum = 0.0f, gscale = 1.0f;
             if (mode == 2) {
-                const uint4 q = *(const uint4*)(a.QA + (int64_t)m * K + 16 * x);
+                const uint4 q = *(const uint4*)(a.QA + (int64_t)(xrow ? xrow[m] : m) * K + 16 * x);
                 pl[0] = q;
                 const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
                 int sum = 0;
@@ -920,19 +920,23 @@ __global__ __launch_bounds__(kThreads) void i8_gemv_kernel(I8Args args) {
     i8_dispatch<D, NE, NP, FS>(args, args.p[q], bx, gx, lds, args.M, nullptr, 0);
 }
 
-// Grouped launches (MoE experts, fp32 mode): the rows of group e (pair rows
-// grp_off[e] .. grp_off[e+1]-1) are cut into chunks of at most args.M rows;
-// item i = (e, first row) of the device-built chunk list is grid row
-// blockIdx.y.  Its weights are the problem's matrix advanced by e *
-// w_stride bytes, its activation rows X rows x_idx[row] (the row itself
-// when x_idx is null), its outputs Y rows row ..  Grid rows past the list
-// end exit.  Each chunk is a full pass over its group's weights.
+// Grouped launches (MoE experts; fp32 rows, mode 0, or given int8 codes and
+// row scales, mode 2): the rows of group e (pair rows grp_off[e] ..
+// grp_off[e+1]-1) are cut into chunks of at most args.M rows; item i = (e,
+// first row) of the device-built chunk list is grid row blockIdx.y.  Its
+// weights are the problem's matrix advanced by e * w_stride bytes (group
+// shared_group: the shared expert's matrix wsh[problem]), its activation
+// rows rows x_idx[row] of X (or of QA / SA) (the row itself when x_idx is
+// null), its outputs Y rows row ..  Grid rows past the list end exit.  Each
+// chunk is a full pass over its group's weights.
 struct I8Group {
     const int32_t* grp_off;
     const int32_t* x_idx;
     int64_t w_stride;
     const int2* items;
     const int32_t* n_items;
+    int shared_group;  // -1: none
+    const uint8_t* wsh[2];
 };
 
 template <int D, int NE, int NP, int FS>
@@ -947,8 +951,15 @@ __global__ __launch_bounds__(kThreads) void i8_gemv_grouped_kernel(I8Args args, 
     while (q + 1 < args.n && (int)blockIdx.x >= args.begin[q + 1]) q++;
     const int bx = blockIdx.x - args.begin[q], gx = args.begin[q + 1] - args.begin[q];
     I8Prob a = args.p[q];
-    a.W += (int64_t)e * gp.w_stride;
-    if (!gp.x_idx) a.X += (int64_t)r * a.ldx;  // the chunk's own rows
+    if (e == gp.shared_group) a.W = gp.wsh[q];
+    else a.W += (int64_t)e * gp.w_stride;
+    if (!gp.x_idx) {  // the chunk's own rows
+        if (a.X) a.X += (int64_t)r * a.ldx;
+        if (a.QA) {
+            a.QA += (int64_t)r * a.K;
+            a.SA += r;
+        }
+    }
     i8_dispatch<D, NE, NP, FS>(args, a, bx, gx, lds, mc, gp.x_idx ? gp.x_idx + r : nullptr, r);
 }
 
@@ -1302,7 +1313,7 @@ hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s)
         args.begin[i + 1] = args.begin[i] + pl.gx;
     }
     args.n = np;
-    I8Group gp{g.grp_off, g.x_idx, g.w_group_stride, items, n_items};
+    I8Group gp{g.grp_off, g.x_idx, g.w_group_stride, items, n_items, -1, {nullptr, nullptr}};
     const int fs = fs_bit(g.type);
 #define RG(NP_)                                                                                  \
     switch (fs) {                                                                                \
@@ -1315,6 +1326,93 @@ hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s)
     if (pl.sh.NP == 1) RG(1);
     RG(2);
 #undef RG
+}
+
+}  // namespace ggq
+
+namespace ggq {
+
+// Per-row int8 MoE (mode 2: the codes and row scales are given): chunks of
+// up to 8 rows (4 for the four-slot formats), the shared expert as group E.
+static bool i8_moe_q8_plan(uint32_t type, const MoeGemm& g, I8GroupedPlan& pl) {
+    const bool q6 = g4_format(type);
+    if (!i8_shape(q6 ? 4 : 8, 2, q6, pl.sh) || pl.sh.NP != 1 || pl.sh.NE != 4) return false;
+    pl.mt = (q6 ? 1 : 2) * 4;
+    const int nc = g.K / 256;
+    int kw = env_i8("GGQ_MOE_I8_KW", 4), k2 = 1;
+    while (2 * k2 <= kw && 2 * k2 <= nc && k2 < kWaves) k2 *= 2;
+    pl.kw_log2 = __builtin_ctz(k2);
+    pl.gx = env_i8("GGQ_MOE_I8_GX", 1);
+    if (pl.gx < 1) pl.gx = 1;
+    const int n1 = g.n1 > 0 ? g.n1 : g.N;
+    const int tiles = (n1 + 15) / 16, tpi = kWaves / k2;
+    const int n_it = (tiles + tpi - 1) / tpi;
+    if (pl.gx > n_it) pl.gx = n_it;
+    const int iters_wg = (n_it + pl.gx - 1) / pl.gx;
+    pl.lds = i8_lds_bytes(g.K, pl.mt, q6, pl.sh) + iters_wg * tpi * 16 * pl.mt * 4;
+    return pl.lds <= kMaxLds;
+}
+
+static int i8_moe_groups(const MoeGemm& g) { return g.E + (g.Wsh ? 1 : 0); }
+
+size_t i8_moe_q8_ws_bytes(uint32_t type, const MoeGemm& g, int rows) {
+    I8GroupedPlan pl;
+    if (!i8_moe_q8_plan(type, g, pl)) return 0;
+    const int groups = i8_moe_groups(g);
+    return 8 * (size_t)((rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows)) + 16;
+}
+
+bool i8_moe_q8_eligible(uint32_t type, const MoeGemm& g, int rows) {
+    if (env_i8("GGQ_MOE_I8", 1) == 0 || env_i8("GGQ_GEMV_MFMA", 1) == 0) return false;
+    if (!supported(type) || g.K % 256 != 0 || g.K <= 0 || g.N <= 0 || rows < 1) return false;
+    const int groups = i8_moe_groups(g);
+    if (groups > 1024) return false;
+    const int n1 = g.n1 > 0 ? g.n1 : g.N;
+    if (g.W2 && g.N - n1 != n1) return false;  // paired halves of equal size
+    if (g.Wsh && g.W2 && !g.W2sh) return false;
+    if ((int64_t)n1 * row_bytes(type, g.K) >= (int64_t)kOOB) return false;
+    I8GroupedPlan pl;
+    if (!i8_moe_q8_plan(type, g, pl)) return false;
+    return (rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows) <= 65535;
+}
+
+hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws, hipStream_t s) {
+    I8GroupedPlan pl;
+    if (!i8_moe_q8_plan(type, g, pl) || !ws) return hipErrorInvalidValue;
+    const int groups = i8_moe_groups(g);
+    if (groups > 1024) return hipErrorInvalidValue;
+    const int max_items = (rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows);
+    int2* items = (int2*)ws;
+    int32_t* n_items = (int32_t*)((char*)ws + 8 * (size_t)max_items);
+    i8_chunks_kernel<<<1, 1024, 0, s>>>(g.grp, groups, pl.mt, items, n_items);
+    const int n1 = g.n1 > 0 ? g.n1 : g.N;
+    I8Args args{};
+    args.M = pl.mt;
+    args.mode = 2;
+    const int np = g.W2 ? 2 : 1;
+    for (int i = 0; i < np; i++) {
+        I8Prob& p = args.p[i];
+        p.W = (const uint8_t*)(i == 0 ? g.W : g.W2);
+        p.row_bytes = (uint32_t)row_bytes(type, g.K);
+        p.type = type;
+        p.N = n1;
+        p.K = g.K;
+        p.QA = g.QA;
+        p.SA = g.sa;
+        p.Y = i == 0 ? g.C : g.C2;
+        p.ldy = g.ldc;
+        p.kw_log2 = pl.kw_log2;
+        args.begin[i + 1] = args.begin[i] + pl.gx;
+    }
+    args.n = np;
+    I8Group gp{g.grp, g.x_idx, g.w_stride, items, n_items, g.Wsh ? g.E : -1,
+               {(const uint8_t*)g.Wsh, (const uint8_t*)g.W2sh}};
+    switch (fs_bit(type)) {
+    case FS_Q4K: return i8_run_grouped<1, 4, 1, FS_Q4K>(args, gp, max_items, pl.lds, s);
+    case FS_Q6K: return i8_run_grouped<1, 4, 1, FS_Q6K>(args, gp, max_items, pl.lds, s);
+    case FS_Q80: return i8_run_grouped<1, 4, 1, FS_Q80>(args, gp, max_items, pl.lds, s);
+    default: return i8_run_grouped<1, 4, 1, FS_ALL>(args, gp, max_items, pl.lds, s);
+    }
 }
 
 }  // namespace ggq

@@ -160,6 +160,14 @@ struct MoeGemm {
 constexpr int kMoeTileRows = 32;  // pair rows per grouped-GEMM tile
 hipError_t launch_moe_tiles(int32_t* grp, int32_t* x_idx, int E, int T_sh, int2* tiles, int32_t* n_tiles, hipStream_t s);
 hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s);
+// The same layer's grouped launches on the int8 GEMV in its given-codes
+// mode (per-row int8 codes g.QA / g.sa): a group's rows in chunks of up to 8
+// (4 for Q6_K / IQ4) from a chunk list built on the device over the E groups
+// and the shared expert (group E, when g.Wsh is set); rows = total pair rows
+// (grp[E + 1]).  `ws`: i8_moe_q8_ws_bytes(...) bytes.
+bool i8_moe_q8_eligible(uint32_t type, const MoeGemm& g, int rows);
+size_t i8_moe_q8_ws_bytes(uint32_t type, const MoeGemm& g, int rows);
+hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws, hipStream_t s);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int64_t n, hipStream_t s);
 hipError_t launch_moe_combine(const float* D, const int32_t* pos_of, const float* wsel, int T,
                               int topk, int H, const float* Dsh, const float* shared_w, float* out,

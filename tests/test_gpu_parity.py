@@ -355,6 +355,29 @@ def test_moe_q8_row_vs_oracle(ctx, orc, types, shared):
     assert_q8_moe_close(orc, out, ref)
 
 
+@pytest.mark.parametrize("types", [(12, 12, 14), (12, 13, 14), (8, 8, 23), (20, 20, 12), (13, 13, 8)])
+@pytest.mark.parametrize("T,E,k", [(24, 8, 3), (64, 64, 8), (5, 40, 2)])
+def test_moe_q8_row_int8_gemv_path(ctx, orc, monkeypatch, types, T, E, k):
+    """GGQ_ACT_Q8_ROW MoE with the routed and shared projections on the
+    grouped int8 GEMV in its given-codes mode (chunks of 8 rows, 4 for Q6_K /
+    IQ4, the shared expert as one more group; experts with 0 to ~30 rows),
+    forced by GGQ_MOE_I8_MAX_AVG, and the same layer forced onto the
+    expert-grouped GEMM (GGQ_MOE_I8_MAX_AVG=0): both against the oracle's
+    per-token loop in the same mode, paired and unpaired gate / up, with and
+    without the shared expert."""
+    tg, tu, td = types
+    H, F = 512, 256
+    for avg in ("100000", "0"):
+        monkeypatch.setenv("GGQ_MOE_I8_MAX_AVG", avg)
+        for shared in (False, True):
+            (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(
+                ctx, T, H, F, E, k, shared, seed=sum(types) + T, tg=tg, tu=tu, td=td, act_mode=1)
+            ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, tg, Wg, tu, Wu, td, Wd, Sg, Su, Sd, sw,
+                                            act_mode=1)
+            assert np.array_equal(sel, rsel)
+            assert_q8_moe_close(orc, out, ref)
+
+
 @pytest.mark.parametrize("T,E,k", [(160, 16, 8), (3, 40, 2), (1, 8, 8)])
 def test_moe_q8_row_tiles_vs_oracle(ctx, orc, T, E, k):
     """Groups of several 32-row tiles (160 tokens x 8 of 16 experts), many
