@@ -825,10 +825,12 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     // Few rows per expert (decode-sized batches): the grouped int8 GEMV in
     // its given-codes mode (chunks of 8 rows, 4 for Q6_K / IQ4), whose
     // lanes carry the rows; more rows per expert: the expert-grouped GEMM's
-    // 32-row tiles (GGQ_MOE_I8_MAX_AVG: largest average rows per group that
-    // takes the GEMV, default 8).
+    // 32-row tiles.  GGQ_MOE_I8_MAX_AVG: largest average rows per group that
+    // takes the GEMV, default 5 (qwen35moe, GEMV vs GEMM: 64 tokens, 2.2 rows
+    // per group, 181 vs 235 us; 128 tokens, 4.5 rows, 271 vs 282 us; 256
+    // tokens, 9.0 rows, 379 vs 297 us).
     const char* avg_env = getenv("GGQ_MOE_I8_MAX_AVG");
-    const size_t max_avg = avg_env && *avg_env ? (size_t)atoi(avg_env) : 8;
+    const size_t max_avg = avg_env && *avg_env ? (size_t)atoi(avg_env) : 5;
     const bool small = rows <= max_avg * (size_t)(E + (shared ? 1 : 0));
     auto grouped = [&](uint32_t type) -> hipError_t {
         if (small && ggq::i8_moe_q8_eligible(type, g, (int)rows) && ggq::i8_moe_q8_ws_bytes(type, g, (int)rows) <= it_bytes)
