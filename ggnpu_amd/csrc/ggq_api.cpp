@@ -771,11 +771,17 @@ int ggq_block_dot_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64
 // projection's groups run in passes of 1-2 rows there, each re-reading the
 // expert's weights, so it stays on the GEMV unless GGQ_MOE_I8_DOWN=1.
 static hipError_t moe_grouped_gemv(const ggq::GemvProblem& g, void* items, size_t items_bytes, hipStream_t s,
-                                   bool down = false) {
+                                   bool down = false, const ggq::I8Shared* sh = nullptr, bool* took_shared = nullptr) {
     const char* v = getenv("GGQ_MOE_I8_DOWN");  // read per call: a process can switch it
     const bool i8_down = v && *v && atoi(v) != 0;
-    if ((!down || i8_down) && ggq::i8_gemv_grouped_eligible(g) && ggq::i8_gemv_grouped_ws_bytes(g) <= items_bytes)
-        return ggq::launch_i8_gemv_grouped(g, items, s);
+    if (took_shared) *took_shared = false;
+    if ((!down || i8_down) && ggq::i8_gemv_grouped_eligible(g)) {
+        if (sh && ggq::i8_gemv_grouped_ws_bytes(g, sh->T) <= items_bytes) {
+            if (took_shared) *took_shared = true;
+            return ggq::launch_i8_gemv_grouped(g, items, s, sh);
+        }
+        if (ggq::i8_gemv_grouped_ws_bytes(g) <= items_bytes) return ggq::launch_i8_gemv_grouped(g, items, s);
+    }
     return ggq::launch_gemv(g, s);
 }
 
@@ -921,12 +927,12 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     // The shared expert's gate / up / SwiGLU rows follow the routed ones in
     // the same buffers (one SwiGLU launch covers both).
     const size_t ts = shared ? (size_t)T : 0;
-    const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 1)),
-                 o_tok = take(4 * nk), o_pos = take(4 * nk), o_g = take(4 * (nk + ts) * F),
+    const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 2)),
+                 o_tok = take(4 * (nk + ts)), o_pos = take(4 * nk), o_g = take(4 * (nk + ts) * F),
                  o_u = take(4 * (nk + ts) * F), o_h = take(4 * (nk + ts) * F), o_d = take(4 * nk * H);
     const size_t o_sd = shared ? take(4 * (size_t)T * H) : 0;
     // chunk list of the grouped int8 launches (chunks of 2 or more rows)
-    const size_t it_bytes = 8 * ((nk + 1) / 2 + std::min<size_t>((size_t)E, nk)) + 16;
+    const size_t it_bytes = 8 * ((nk + ts + 1) / 2 + std::min<size_t>((size_t)E + 1, nk + ts)) + 16;
     const size_t o_it = take(it_bytes);
     if ((st = grow(c, c->dev.ws, off, s, "workspace")) != GGQ_OK) return st;
     hipError_t e;
@@ -941,6 +947,7 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
     if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s)) != hipSuccess) return hip_status(c, e, "moe_group");
 
+    bool shared_done = false;  // the shared expert's gate / up ran in the routed launch
     ggq::GemvProblem g{};
     g.groups = E;
     g.grp_off = grp;
@@ -953,7 +960,12 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
         // gate and up of each expert in one launch: each workgroup loads a
         // token's activations once for both.
         g.W2 = p->up_exps; g.Y2 = U; g.n1 = F; g.N = 2 * F;
-        if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s)) != hipSuccess) return hip_status(c, e, "moe gate+up");
+        // the shared expert joins the grouped int8 launch as one more group
+        // (its rows nk .. nk + T - 1 of G / U), when that launch takes it
+        const ggq::I8Shared shx{p->gate_shexp, p->up_shexp, T};
+        if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s, false, shared ? &shx : nullptr, &shared_done)) !=
+            hipSuccess)
+            return hip_status(c, e, "moe gate+up");
         g.W2 = nullptr; g.Y2 = nullptr; g.n1 = 0;
     } else {
         if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s)) != hipSuccess) return hip_status(c, e, "moe gate");
@@ -962,11 +974,11 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     }
     float* Dsh = nullptr;
     ggq::GemvProblem q{};
-    if (shared) {
+    q.groups = 1;
+    q.M = T;
+    if (shared) Dsh = (float*)(base + o_sd);
+    if (shared && !shared_done) {
         float *SG = G + nk * F, *SU = U + nk * F;
-        Dsh = (float*)(base + o_sd);
-        q.groups = 1;
-        q.M = T;
         q.N = F; q.K = H; q.X = p->x; q.ldx = H; q.ldy = F;
         q.type = p->gate_type; q.W = p->gate_shexp; q.Y = SG;
         if (p->up_type == p->gate_type && H % 32 == 0) {

@@ -964,11 +964,21 @@ __global__ __launch_bounds__(kThreads) void i8_gemv_grouped_kernel(I8Args args, 
 }
 
 // The chunk list: one thread per group counts its chunks, a scan over the
-// workgroup places them (groups <= 1024).
-__global__ __launch_bounds__(1024) void i8_chunks_kernel(const int32_t* __restrict__ grp_off, int groups, int mt,
+// workgroup places them (groups <= 1024).  t_sh > 0 appends a last group of
+// t_sh rows (the shared expert: every token) first: grp_off[groups] =
+// grp_off[groups - 1] + t_sh and x_idx of its rows = the token itself.
+__global__ __launch_bounds__(1024) void i8_chunks_kernel(int32_t* __restrict__ grp_off, int groups, int mt,
+                                                         int t_sh, int32_t* __restrict__ x_idx,
                                                          int2* __restrict__ items, int32_t* __restrict__ n_items) {
     __shared__ int cnt[1024];
     const int tid = threadIdx.x;
+    if (t_sh > 0) {
+        const int base = grp_off[groups - 1];
+        for (int t = tid; t < t_sh; t += 1024) x_idx[base + t] = t;
+        __syncthreads();  // every thread has read grp_off[groups - 1]
+        if (tid == 0) grp_off[groups] = base + t_sh;
+        __syncthreads();
+    }
     int mine = 0, r0 = 0;
     if (tid < groups) {
         r0 = grp_off[tid];
@@ -1264,19 +1274,20 @@ bool i8_grouped_plan(const GemvProblem& g, I8GroupedPlan& pl) {
 
 // Upper bound of the chunk list: every chunk but the last of a group holds
 // mt rows, and at most min(groups, rows) groups are non-empty.
-static int i8_max_items(const GemvProblem& g, int mt) {
-    return (g.M + mt - 1) / mt + (g.groups < g.M ? g.groups : g.M);
+static int i8_max_items(const GemvProblem& g, int mt, int t_sh = 0) {
+    const int rows = g.M + t_sh, groups = g.groups + (t_sh > 0 ? 1 : 0);
+    return (rows + mt - 1) / mt + (groups < rows ? groups : rows);
 }
 
-size_t i8_gemv_grouped_ws_bytes(const GemvProblem& g) {
+size_t i8_gemv_grouped_ws_bytes(const GemvProblem& g, int t_sh) {
     I8GroupedPlan pl;
     if (!i8_grouped_plan(g, pl)) return 0;
-    return 8 * (size_t)i8_max_items(g, pl.mt) + 16;
+    return 8 * (size_t)i8_max_items(g, pl.mt, t_sh) + 16;
 }
 
 bool i8_gemv_grouped_eligible(const GemvProblem& g) {
     if (env_i8("GGQ_MOE_I8", 1) == 0 || env_i8("GGQ_GEMV_MFMA", 1) == 0) return false;
-    if (!g.grp_off || g.groups < 1 || g.groups > 1024 || g.M < 1 || !supported(g.type) || g.K % 256 != 0 || g.K <= 0 || g.N <= 0) return false;
+    if (!g.grp_off || g.groups < 1 || g.groups > 1023 || g.M < 1 || !supported(g.type) || g.K % 256 != 0 || g.K <= 0 || g.N <= 0) return false;
     if (g.X2 || g.rms || g.R || g.silu || g.q8row) return false;
     const int n1 = g.n1 > 0 ? g.n1 : g.N;
     if (g.n1 > 0 && (!g.W2 || !g.Y2 || g.N - g.n1 != g.n1)) return false;  // paired halves of equal size
@@ -1285,13 +1296,16 @@ bool i8_gemv_grouped_eligible(const GemvProblem& g) {
     return i8_grouped_plan(g, pl) && i8_max_items(g, pl.mt) <= 65535;
 }
 
-hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s) {
+hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s, const I8Shared* sh) {
     I8GroupedPlan pl;
-    if (!i8_grouped_plan(g, pl) || !ws || g.groups > 1024) return hipErrorInvalidValue;
-    const int max_items = i8_max_items(g, pl.mt);
+    if (!i8_grouped_plan(g, pl) || !ws || g.groups + (sh ? 1 : 0) > 1024) return hipErrorInvalidValue;
+    if (sh && (!g.x_idx || sh->T < 1 || (g.n1 > 0 && !sh->W2))) return hipErrorInvalidValue;
+    const int max_items = i8_max_items(g, pl.mt, sh ? sh->T : 0);
     int2* items = (int2*)ws;
     int32_t* n_items = (int32_t*)((char*)ws + 8 * (size_t)max_items);
-    i8_chunks_kernel<<<1, 1024, 0, s>>>(g.grp_off, g.groups, pl.mt, items, n_items);
+    const int groups = g.groups + (sh ? 1 : 0);
+    i8_chunks_kernel<<<1, 1024, 0, s>>>((int32_t*)g.grp_off, groups, pl.mt, sh ? sh->T : 0, (int32_t*)g.x_idx, items,
+                                        n_items);
     const int n1 = g.n1 > 0 ? g.n1 : g.N;
     I8Args args{};
     args.M = pl.mt;
@@ -1313,7 +1327,8 @@ hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s)
         args.begin[i + 1] = args.begin[i] + pl.gx;
     }
     args.n = np;
-    I8Group gp{g.grp_off, g.x_idx, g.w_group_stride, items, n_items, -1, {nullptr, nullptr}};
+    I8Group gp{g.grp_off, g.x_idx, g.w_group_stride, items, n_items, sh ? g.groups : -1,
+               {sh ? (const uint8_t*)sh->W : nullptr, sh ? (const uint8_t*)sh->W2 : nullptr}};
     const int fs = fs_bit(g.type);
 #define RG(NP_)                                                                                  \
     switch (fs) {                                                                                \
@@ -1384,7 +1399,7 @@ hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws,
     const int max_items = (rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows);
     int2* items = (int2*)ws;
     int32_t* n_items = (int32_t*)((char*)ws + 8 * (size_t)max_items);
-    i8_chunks_kernel<<<1, 1024, 0, s>>>(g.grp, groups, pl.mt, items, n_items);
+    i8_chunks_kernel<<<1, 1024, 0, s>>>((int32_t*)g.grp, groups, pl.mt, 0, nullptr, items, n_items);
     const int n1 = g.n1 > 0 ? g.n1 : g.N;
     I8Args args{};
     args.M = pl.mt;

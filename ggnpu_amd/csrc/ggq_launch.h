@@ -81,9 +81,13 @@ hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* 
 // IQ4) rows, one grid row per chunk from a chunk list built on the device;
 // paired gate / up halves are two problems.  `ws`: device workspace of
 // i8_gemv_grouped_ws_bytes(g) bytes.
+// With `sh`, the shared expert (weights sh->W / sh->W2, every one of its
+// sh->T tokens) joins the launch as group g.groups: its rows follow the
+// routed ones (grp_off needs g.groups + 2 entries and x_idx g.M + T).
+struct I8Shared { const void* W; const void* W2; int T; };
 bool i8_gemv_grouped_eligible(const GemvProblem& g);
-size_t i8_gemv_grouped_ws_bytes(const GemvProblem& g);
-hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s);
+size_t i8_gemv_grouped_ws_bytes(const GemvProblem& g, int t_sh = 0);
+hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s, const I8Shared* sh = nullptr);
 // Largest K the register-resident GEMV supports.
 constexpr int kGemvMaxK = 32768;
 
