@@ -786,9 +786,10 @@ static hipError_t moe_grouped_gemv(const ggq::GemvProblem& g, void* items, size_
 }
 
 // MoE layer with per-row int8 activations (GGQ_ACT_Q8_ROW): route, group,
-// quantize the token rows once, one grouped int8 GEMM for every expert's
-// gate and up (and the shared expert's, as group E), SwiGLU fused into the
-// row quantization of the pair rows, one grouped GEMM for down, combine.
+// quantize the token rows once, one grouped int8 launch for every expert's
+// gate and up (and the shared expert's, as group E: the expert-grouped GEMM,
+// or the grouped int8 GEMV when the groups are small), SwiGLU fused into the
+// row quantization of the pair rows, one grouped launch for down, combine.
 static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     const int T = p->T, H = p->H, F = p->F, E = p->E, k = p->top_k;
     const bool shared = p->gate_shexp != nullptr;
