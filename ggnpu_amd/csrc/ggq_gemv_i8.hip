@@ -1246,6 +1246,21 @@ hipError_t i8_run_grouped(I8Args& args, const I8Group& gp, int groups, int lds, 
 // workgroups per problem and group, and the LDS it needs.
 struct I8GroupedPlan { I8Shape sh; int mt, kw_log2, gx, lds; };
 
+// Workgroups per (problem, chunk): GGQ_MOE_I8_GX when set, else enough to
+// fill one 1024-thread workgroup per CU over the chunk-list bound (one per
+// chunk once the chunks alone fill the chip: 64 qwen35moe tokens), at most
+// one per tile iteration.
+int i8_grouped_gx(int rows, int groups, int mt, int np, int n_it) {
+    int gx = env_i8("GGQ_MOE_I8_GX", 0);
+    if (gx <= 0) {
+        const int items = (rows + mt - 1) / mt + (groups < rows ? groups : rows);
+        const int per = np * (items > 0 ? items : 1);
+        gx = (cu_count() + per - 1) / per;
+    }
+    if (gx < 1) gx = 1;
+    return gx > n_it ? n_it : gx;
+}
+
 bool i8_grouped_plan(const GemvProblem& g, I8GroupedPlan& pl) {
     const bool q6 = g4_format(g.type);
     // fp32 mode: two rows per pass (one for four-slot formats), two passes
@@ -1259,12 +1274,10 @@ bool i8_grouped_plan(const GemvProblem& g, I8GroupedPlan& pl) {
     int k2 = 1;
     while (2 * k2 <= kw && 2 * k2 <= nc && k2 < kWaves) k2 *= 2;
     pl.kw_log2 = __builtin_ctz(k2);
-    pl.gx = env_i8("GGQ_MOE_I8_GX", 1);
-    if (pl.gx < 1) pl.gx = 1;
     const int n1 = g.n1 > 0 ? g.n1 : g.N;
     const int tiles = (n1 + 15) / 16, tpi = kWaves / k2;
     const int n_it = (tiles + tpi - 1) / tpi;
-    if (pl.gx > n_it) pl.gx = n_it;
+    pl.gx = i8_grouped_gx(g.M, g.groups, pl.mt, g.n1 > 0 ? 2 : 1, n_it);
     const int iters_wg = (n_it + pl.gx - 1) / pl.gx;
     pl.lds = i8_lds_bytes(g.K, pl.mt, q6, pl.sh) + iters_wg * tpi * 16 * pl.mt * 4;
     return pl.lds <= kMaxLds;
@@ -1349,7 +1362,7 @@ namespace ggq {
 
 // Per-row int8 MoE (mode 2: the codes and row scales are given): chunks of
 // up to 8 rows (4 for the four-slot formats), the shared expert as group E.
-static bool i8_moe_q8_plan(uint32_t type, const MoeGemm& g, I8GroupedPlan& pl) {
+static bool i8_moe_q8_plan(uint32_t type, const MoeGemm& g, int rows, I8GroupedPlan& pl) {
     const bool q6 = g4_format(type);
     if (!i8_shape(q6 ? 4 : 8, 2, q6, pl.sh) || pl.sh.NP != 1 || pl.sh.NE != 4) return false;
     pl.mt = (q6 ? 1 : 2) * 4;
@@ -1357,12 +1370,10 @@ static bool i8_moe_q8_plan(uint32_t type, const MoeGemm& g, I8GroupedPlan& pl) {
     int kw = env_i8("GGQ_MOE_I8_KW", 4), k2 = 1;
     while (2 * k2 <= kw && 2 * k2 <= nc && k2 < kWaves) k2 *= 2;
     pl.kw_log2 = __builtin_ctz(k2);
-    pl.gx = env_i8("GGQ_MOE_I8_GX", 1);
-    if (pl.gx < 1) pl.gx = 1;
     const int n1 = g.n1 > 0 ? g.n1 : g.N;
     const int tiles = (n1 + 15) / 16, tpi = kWaves / k2;
     const int n_it = (tiles + tpi - 1) / tpi;
-    if (pl.gx > n_it) pl.gx = n_it;
+    pl.gx = i8_grouped_gx(rows, g.E + (g.Wsh ? 1 : 0), pl.mt, g.W2 ? 2 : 1, n_it);
     const int iters_wg = (n_it + pl.gx - 1) / pl.gx;
     pl.lds = i8_lds_bytes(g.K, pl.mt, q6, pl.sh) + iters_wg * tpi * 16 * pl.mt * 4;
     return pl.lds <= kMaxLds;
@@ -1372,7 +1383,7 @@ static int i8_moe_groups(const MoeGemm& g) { return g.E + (g.Wsh ? 1 : 0); }
 
 size_t i8_moe_q8_ws_bytes(uint32_t type, const MoeGemm& g, int rows) {
     I8GroupedPlan pl;
-    if (!i8_moe_q8_plan(type, g, pl)) return 0;
+    if (!i8_moe_q8_plan(type, g, rows, pl)) return 0;
     const int groups = i8_moe_groups(g);
     return 8 * (size_t)((rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows)) + 16;
 }
@@ -1387,13 +1398,13 @@ bool i8_moe_q8_eligible(uint32_t type, const MoeGemm& g, int rows) {
     if (g.Wsh && g.W2 && !g.W2sh) return false;
     if ((int64_t)n1 * row_bytes(type, g.K) >= (int64_t)kOOB) return false;
     I8GroupedPlan pl;
-    if (!i8_moe_q8_plan(type, g, pl)) return false;
+    if (!i8_moe_q8_plan(type, g, rows, pl)) return false;
     return (rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows) <= 65535;
 }
 
 hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws, hipStream_t s) {
     I8GroupedPlan pl;
-    if (!i8_moe_q8_plan(type, g, pl) || !ws) return hipErrorInvalidValue;
+    if (!i8_moe_q8_plan(type, g, rows, pl) || !ws) return hipErrorInvalidValue;
     const int groups = i8_moe_groups(g);
     if (groups > 1024) return hipErrorInvalidValue;
     const int max_items = (rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows);
