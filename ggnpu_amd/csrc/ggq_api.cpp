@@ -771,16 +771,17 @@ int ggq_block_dot_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64
 // projection's groups run in passes of 1-2 rows there, each re-reading the
 // expert's weights, so it stays on the GEMV unless GGQ_MOE_I8_DOWN=1.
 static hipError_t moe_grouped_gemv(const ggq::GemvProblem& g, void* items, size_t items_bytes, hipStream_t s,
-                                   bool down = false, const ggq::I8Shared* sh = nullptr, bool* took_shared = nullptr) {
+                                   bool down = false, const ggq::I8Shared* sh = nullptr, bool* took_shared = nullptr,
+                                   bool list_ready = false) {
     const char* v = getenv("GGQ_MOE_I8_DOWN");  // read per call: a process can switch it
     const bool i8_down = v && *v && atoi(v) != 0;
     if (took_shared) *took_shared = false;
     if ((!down || i8_down) && ggq::i8_gemv_grouped_eligible(g)) {
         if (sh && ggq::i8_gemv_grouped_ws_bytes(g, sh->T) <= items_bytes) {
             if (took_shared) *took_shared = true;
-            return ggq::launch_i8_gemv_grouped(g, items, s, sh);
+            return ggq::launch_i8_gemv_grouped(g, items, s, sh, list_ready);
         }
-        if (ggq::i8_gemv_grouped_ws_bytes(g) <= items_bytes) return ggq::launch_i8_gemv_grouped(g, items, s);
+        if (ggq::i8_gemv_grouped_ws_bytes(g) <= items_bytes) return ggq::launch_i8_gemv_grouped(g, items, s, nullptr, list_ready);
     }
     return ggq::launch_gemv(g, s);
 }
@@ -803,7 +804,7 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
                  o_d = take(4 * rows * H), o_tl = take(8 * (size_t)max_tiles), o_nt = take(4);
     // chunk list of the grouped int8 GEMV (chunks of 4 or more rows)
     const size_t it_bytes = 8 * ((rows + 3) / 4 + std::min<size_t>((size_t)E + 1, rows)) + 16;
-    const size_t o_it = take(it_bytes);
+    const size_t o_it = take(it_bytes), o_it2 = take(it_bytes);  // gate / up, down
     int st;
     if ((st = grow(c, c->dev.ws, off, s, "workspace")) != GGQ_OK) return st;
     hipError_t e;
@@ -822,11 +823,6 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     int32_t* ntiles = (int32_t*)(base + o_nt);
 
     if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
-    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s)) != hipSuccess) return hip_status(c, e, "moe_group");
-    if ((e = ggq::launch_moe_tiles(grp, tok, E, (int)ts, (int2*)tiles, ntiles, s)) != hipSuccess)
-        return hip_status(c, e, "moe_tiles");
-    if ((e = ggq::launch_quant_act(p->x, H, T, H, GGQ_ACT_Q8_ROW, qx, sx, nullptr, s)) != hipSuccess)
-        return hip_status(c, e, "quant x");
     ggq::MoeGemm g{};
     g.E = E; g.grp = grp; g.tiles = tiles; g.n_tiles = ntiles; g.max_tiles = max_tiles;
     // Few rows per expert (decode-sized batches): the grouped int8 GEMV in
@@ -839,36 +835,63 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     const char* avg_env = getenv("GGQ_MOE_I8_MAX_AVG");
     const size_t max_avg = avg_env && *avg_env ? (size_t)atoi(avg_env) : 5;
     const bool small = rows <= max_avg * (size_t)(E + (shared ? 1 : 0));
-    auto grouped = [&](uint32_t type) -> hipError_t {
-        if (small && ggq::i8_moe_q8_eligible(type, g, (int)rows) && ggq::i8_moe_q8_ws_bytes(type, g, (int)rows) <= it_bytes)
-            return ggq::launch_i8_moe_q8(type, g, (int)rows, base + o_it, s);
-        return ggq::launch_moe_gemm(type, g, s);
+    auto i8_ok = [&](uint32_t type, const ggq::MoeGemm& d) {
+        return small && ggq::i8_moe_q8_eligible(type, d, (int)rows) &&
+               ggq::i8_moe_q8_ws_bytes(type, d, (int)rows) <= it_bytes;
     };
     // gate and up: K = H, token rows gathered through tok; paired when the
-    // types match, else two launches.
-    g.K = H; g.QA = qx; g.sa = sx; g.x_idx = tok; g.ldc = F;
-    g.w_stride = (int64_t)F * ggq::row_bytes(p->gate_type, H);
-    if (p->up_type == p->gate_type) {
-        g.W = p->gate_exps; g.W2 = p->up_exps; g.Wsh = p->gate_shexp; g.W2sh = p->up_shexp;
-        g.N = 2 * F; g.n1 = F; g.C = G; g.C2 = U;
-        if ((e = grouped(p->gate_type)) != hipSuccess) return hip_status(c, e, "moe gate+up");
+    // types match, else two launches.  down: K = F, the pair rows themselves.
+    ggq::MoeGemm gu = g, gd = g;
+    gu.K = H; gu.QA = qx; gu.sa = sx; gu.x_idx = tok; gu.ldc = F;
+    gu.w_stride = (int64_t)F * ggq::row_bytes(p->gate_type, H);
+    gd.K = F; gd.QA = qh; gd.sa = sh; gd.x_idx = nullptr; gd.ldc = H;
+    gd.W = p->down_exps; gd.W2 = nullptr; gd.Wsh = p->down_shexp; gd.W2sh = nullptr;
+    gd.w_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
+    gd.N = H; gd.n1 = H; gd.C = D; gd.C2 = nullptr;
+    const bool paired = p->up_type == p->gate_type;
+    if (paired) {
+        gu.W = p->gate_exps; gu.W2 = p->up_exps; gu.Wsh = p->gate_shexp; gu.W2sh = p->up_shexp;
+        gu.N = 2 * F; gu.n1 = F; gu.C = G; gu.C2 = U;
+    }
+    const bool gu_i8 = paired && i8_ok(p->gate_type, gu), dn_i8 = i8_ok(p->down_type, gd);
+    // The grouping launch builds the chunk lists of the grouped int8
+    // launches (and the shared expert's group end and token rows); the tile
+    // list is built only when a launch takes the expert-grouped GEMM.
+    ggq::ChunkList lists[2];
+    int nl = 0;
+    if (gu_i8) lists[nl++] = ggq::i8_moe_q8_list(p->gate_type, gu, (int)rows, base + o_it);
+    if (dn_i8) lists[nl++] = ggq::i8_moe_q8_list(p->down_type, gd, (int)rows, base + o_it2);
+    bool built = false;
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, nl > 0 ? (int)ts : 0, lists, nl, &built)) !=
+        hipSuccess)
+        return hip_status(c, e, "moe_group");
+    if (!(built && gu_i8 && dn_i8) &&
+        (e = ggq::launch_moe_tiles(grp, tok, E, (int)ts, (int2*)tiles, ntiles, s)) != hipSuccess)
+        return hip_status(c, e, "moe_tiles");
+    if ((e = ggq::launch_quant_act(p->x, H, T, H, GGQ_ACT_Q8_ROW, qx, sx, nullptr, s)) != hipSuccess)
+        return hip_status(c, e, "quant x");
+    auto grouped = [&](uint32_t type, const ggq::MoeGemm& d) -> hipError_t {
+        if (i8_ok(type, d)) return ggq::launch_i8_moe_q8(type, d, (int)rows, base + o_it, s);
+        return ggq::launch_moe_gemm(type, d, s);
+    };
+    if (paired) {
+        if (gu_i8) e = ggq::launch_i8_moe_q8(p->gate_type, gu, (int)rows, base + o_it, s, built);
+        else e = ggq::launch_moe_gemm(p->gate_type, gu, s);
+        if (e != hipSuccess) return hip_status(c, e, "moe gate+up");
     } else {
-        g.W = p->gate_exps; g.W2 = nullptr; g.Wsh = p->gate_shexp; g.W2sh = nullptr;
-        g.N = F; g.n1 = F; g.C = G; g.C2 = nullptr;
-        if ((e = grouped(p->gate_type)) != hipSuccess) return hip_status(c, e, "moe gate");
-        g.W = p->up_exps; g.Wsh = p->up_shexp; g.C = U;
-        g.w_stride = (int64_t)F * ggq::row_bytes(p->up_type, H);
-        if ((e = grouped(p->up_type)) != hipSuccess) return hip_status(c, e, "moe up");
+        gu.W = p->gate_exps; gu.W2 = nullptr; gu.Wsh = p->gate_shexp; gu.W2sh = nullptr;
+        gu.N = F; gu.n1 = F; gu.C = G; gu.C2 = nullptr;
+        if ((e = grouped(p->gate_type, gu)) != hipSuccess) return hip_status(c, e, "moe gate");
+        gu.W = p->up_exps; gu.Wsh = p->up_shexp; gu.C = U;
+        gu.w_stride = (int64_t)F * ggq::row_bytes(p->up_type, H);
+        if ((e = grouped(p->up_type, gu)) != hipSuccess) return hip_status(c, e, "moe up");
     }
     // SwiGLU of every pair row (routed and shared) and its int8 row codes.
     if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s)) != hipSuccess)
         return hip_status(c, e, "swiglu quant");
-    // down: K = F, the pair rows themselves.
-    g.K = F; g.QA = qh; g.sa = sh; g.x_idx = nullptr; g.ldc = H;
-    g.W = p->down_exps; g.W2 = nullptr; g.Wsh = p->down_shexp; g.W2sh = nullptr;
-    g.w_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
-    g.N = H; g.n1 = H; g.C = D; g.C2 = nullptr;
-    if ((e = grouped(p->down_type)) != hipSuccess) return hip_status(c, e, "moe down");
+    if (dn_i8) e = ggq::launch_i8_moe_q8(p->down_type, gd, (int)rows, base + o_it2, s, built);
+    else e = ggq::launch_moe_gemm(p->down_type, gd, s);
+    if (e != hipSuccess) return hip_status(c, e, "moe down");
     if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, shared ? D + nk * H : nullptr, p->shared_w, p->out, s)) !=
         hipSuccess)
         return hip_status(c, e, "moe combine");
@@ -946,7 +969,6 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     float *G = (float*)(base + o_g), *U = (float*)(base + o_u), *Hh = (float*)(base + o_h), *D = (float*)(base + o_d);
 
     if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
-    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s)) != hipSuccess) return hip_status(c, e, "moe_group");
 
     bool shared_done = false;  // the shared expert's gate / up ran in the routed launch
     ggq::GemvProblem g{};
@@ -957,14 +979,28 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     // gate / up: rows F, K = H, activations gathered by token.
     g.N = F; g.K = H; g.X = p->x; g.ldx = H; g.x_idx = tok; g.ldy = F;
     g.type = p->gate_type; g.W = p->gate_exps; g.w_group_stride = (int64_t)F * ggq::row_bytes(p->gate_type, H); g.Y = G;
-    if (p->up_type == p->gate_type && H % 32 == 0) {
+    const bool paired = p->up_type == p->gate_type && H % 32 == 0;
+    // The paired gate / up launch's chunk list (with the shared expert as one
+    // more group) is built by the grouping launch itself when the grouped
+    // int8 GEMV takes that launch (the same conditions as moe_grouped_gemv).
+    ggq::GemvProblem gp = g;
+    gp.W2 = p->up_exps; gp.Y2 = U; gp.n1 = F; gp.N = 2 * F;
+    const int t_list = shared ? T : 0;
+    const bool pre = paired && ggq::i8_gemv_grouped_eligible(gp) &&
+                     ggq::i8_gemv_grouped_ws_bytes(gp, t_list) <= it_bytes;
+    const ggq::ChunkList cl = pre ? ggq::i8_gemv_grouped_list(gp, base + o_it, t_list) : ggq::ChunkList{0, nullptr, nullptr};
+    bool built = false;
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, pre ? t_list : 0, pre ? &cl : nullptr, pre ? 1 : 0,
+                                   &built)) != hipSuccess)
+        return hip_status(c, e, "moe_group");
+    if (paired) {
         // gate and up of each expert in one launch: each workgroup loads a
         // token's activations once for both.
         g.W2 = p->up_exps; g.Y2 = U; g.n1 = F; g.N = 2 * F;
         // the shared expert joins the grouped int8 launch as one more group
         // (its rows nk .. nk + T - 1 of G / U), when that launch takes it
         const ggq::I8Shared shx{p->gate_shexp, p->up_shexp, T};
-        if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s, false, shared ? &shx : nullptr, &shared_done)) !=
+        if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s, false, shared ? &shx : nullptr, &shared_done, built)) !=
             hipSuccess)
             return hip_status(c, e, "moe gate+up");
         g.W2 = nullptr; g.Y2 = nullptr; g.n1 = 0;

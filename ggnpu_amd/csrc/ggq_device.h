@@ -21,6 +21,7 @@
 // src/quant/q8_0.cpp:19-25, src/quant/iq4_nl.cpp:16-31,
 // src/quant/iq4_xs.cpp:21-38.
 #pragma once
+#include "ggq_launch.h"
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "ggq_formats.h"
@@ -535,6 +536,61 @@ __device__ __forceinline__ void ubytes_to_f32(uint4 u, float* f) {
         f[4 * i + 2] = (float)((w[i] >> 16) & 0xFFu);
         f[4 * i + 3] = (float)(w[i] >> 24);
     }
+}
+
+// ------------------------------------------------- MoE chunk lists -----
+// (group, first row) chunk lists for grouped launches (struct ChunkList,
+// ggq_launch.h).
+
+// Built by one workgroup of 1024 threads (groups <= 1024); cnt: 16 ints of
+// LDS (build_chunk_lists reads the offsets from global memory;
+// chunk_lists_from_rows takes each group's rows from its thread).  With t_sh > 0 the last group is the shared expert, t_sh rows (every
+// token) after the others: its end grp_off[groups] = grp_off[groups - 1] +
+// t_sh and the x_idx of its rows (the token itself) are written first.
+// grp_off is read from global memory, so a caller that has just written it
+// from the same workgroup synchronizes first.
+// Thread tid < groups passes its group's first row r0 and row count; the
+// other threads pass 0 rows.
+__device__ inline void chunk_lists_from_rows(int r0, int rows, const ChunkList* lists, int n_lists, int* cnt) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int li = 0; li < n_lists; li++) {
+        const int mt = lists[li].mt;
+        const int mine = rows > 0 ? (rows + mt - 1) / mt : 0;
+        // chunks of the groups before this one: a scan within the
+        // wavefront, then the totals of the earlier wavefronts
+        int incl = mine;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) cnt[wave] = incl;
+        __syncthreads();
+        int before = 0;
+        for (int w = 0; w < wave; w++) before += cnt[w];
+        const int first = before + incl - mine;
+        for (int i = 0; i < mine; i++) lists[li].items[first + i] = make_int2(tid, r0 + mt * i);
+        if (tid == 1023) *lists[li].n_items = before + incl;  // the last lane of the last wavefront: the total
+        __syncthreads();  // cnt is reused by the next list
+    }
+}
+
+__device__ inline void build_chunk_lists(int32_t* grp_off, int groups, int t_sh, int32_t* x_idx,
+                                         const ChunkList* lists, int n_lists, int* cnt) {
+    const int tid = threadIdx.x;
+    if (t_sh > 0) {
+        const int base = grp_off[groups - 1];
+        for (int t = tid; t < t_sh; t += 1024) x_idx[base + t] = t;
+        __syncthreads();  // every thread has read grp_off[groups - 1]
+        if (tid == 0) grp_off[groups] = base + t_sh;
+        __syncthreads();
+    }
+    int rows = 0, r0 = 0;
+    if (tid < groups) {
+        r0 = grp_off[tid];
+        rows = grp_off[tid + 1] - r0;
+    }
+    chunk_lists_from_rows(r0, rows, lists, n_lists, cnt);
 }
 
 }  // namespace ggq

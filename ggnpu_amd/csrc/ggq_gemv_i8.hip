@@ -971,31 +971,8 @@ __global__ __launch_bounds__(1024) void i8_chunks_kernel(int32_t* __restrict__ g
                                                          int t_sh, int32_t* __restrict__ x_idx,
                                                          int2* __restrict__ items, int32_t* __restrict__ n_items) {
     __shared__ int cnt[1024];
-    const int tid = threadIdx.x;
-    if (t_sh > 0) {
-        const int base = grp_off[groups - 1];
-        for (int t = tid; t < t_sh; t += 1024) x_idx[base + t] = t;
-        __syncthreads();  // every thread has read grp_off[groups - 1]
-        if (tid == 0) grp_off[groups] = base + t_sh;
-        __syncthreads();
-    }
-    int mine = 0, r0 = 0;
-    if (tid < groups) {
-        r0 = grp_off[tid];
-        const int rows = grp_off[tid + 1] - r0;
-        mine = rows > 0 ? (rows + mt - 1) / mt : 0;
-    }
-    cnt[tid] = mine;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int v = tid >= off ? cnt[tid - off] : 0;
-        __syncthreads();
-        cnt[tid] += v;
-        __syncthreads();
-    }
-    const int first = cnt[tid] - mine;
-    for (int i = 0; i < mine; i++) items[first + i] = make_int2(tid, r0 + mt * i);
-    if (tid == 1023) *n_items = cnt[1023];
+    const ChunkList l{mt, items, n_items};
+    build_chunk_lists(grp_off, groups, t_sh, x_idx, &l, 1, cnt);
 }
 
 int env_i8(const char* name, int dflt) {
@@ -1309,16 +1286,25 @@ bool i8_gemv_grouped_eligible(const GemvProblem& g) {
     return i8_grouped_plan(g, pl) && i8_max_items(g, pl.mt) <= 65535;
 }
 
-hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s, const I8Shared* sh) {
+ChunkList i8_gemv_grouped_list(const GemvProblem& g, void* ws, int t_sh) {
+    I8GroupedPlan pl;
+    if (!i8_grouped_plan(g, pl)) return ChunkList{0, nullptr, nullptr};
+    const int max_items = i8_max_items(g, pl.mt, t_sh);
+    return ChunkList{pl.mt, (int2*)ws, (int32_t*)((char*)ws + 8 * (size_t)max_items)};
+}
+
+hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s, const I8Shared* sh, bool list_ready) {
     I8GroupedPlan pl;
     if (!i8_grouped_plan(g, pl) || !ws || g.groups + (sh ? 1 : 0) > 1024) return hipErrorInvalidValue;
     if (sh && (!g.x_idx || sh->T < 1 || (g.n1 > 0 && !sh->W2))) return hipErrorInvalidValue;
     const int max_items = i8_max_items(g, pl.mt, sh ? sh->T : 0);
-    int2* items = (int2*)ws;
-    int32_t* n_items = (int32_t*)((char*)ws + 8 * (size_t)max_items);
+    const ChunkList cl = i8_gemv_grouped_list(g, ws, sh ? sh->T : 0);
+    int2* items = cl.items;
+    int32_t* n_items = cl.n_items;
     const int groups = g.groups + (sh ? 1 : 0);
-    i8_chunks_kernel<<<1, 1024, 0, s>>>((int32_t*)g.grp_off, groups, pl.mt, sh ? sh->T : 0, (int32_t*)g.x_idx, items,
-                                        n_items);
+    if (!list_ready)
+        i8_chunks_kernel<<<1, 1024, 0, s>>>((int32_t*)g.grp_off, groups, pl.mt, sh ? sh->T : 0, (int32_t*)g.x_idx,
+                                            items, n_items);
     const int n1 = g.n1 > 0 ? g.n1 : g.N;
     I8Args args{};
     args.M = pl.mt;
@@ -1402,15 +1388,24 @@ bool i8_moe_q8_eligible(uint32_t type, const MoeGemm& g, int rows) {
     return (rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows) <= 65535;
 }
 
-hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws, hipStream_t s) {
+ChunkList i8_moe_q8_list(uint32_t type, const MoeGemm& g, int rows, void* ws) {
+    I8GroupedPlan pl;
+    if (!i8_moe_q8_plan(type, g, rows, pl)) return ChunkList{0, nullptr, nullptr};
+    const int groups = i8_moe_groups(g);
+    const int max_items = (rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows);
+    return ChunkList{pl.mt, (int2*)ws, (int32_t*)((char*)ws + 8 * (size_t)max_items)};
+}
+
+hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws, hipStream_t s, bool list_ready) {
     I8GroupedPlan pl;
     if (!i8_moe_q8_plan(type, g, rows, pl) || !ws) return hipErrorInvalidValue;
     const int groups = i8_moe_groups(g);
     if (groups > 1024) return hipErrorInvalidValue;
     const int max_items = (rows + pl.mt - 1) / pl.mt + (groups < rows ? groups : rows);
-    int2* items = (int2*)ws;
-    int32_t* n_items = (int32_t*)((char*)ws + 8 * (size_t)max_items);
-    i8_chunks_kernel<<<1, 1024, 0, s>>>((int32_t*)g.grp, groups, pl.mt, 0, nullptr, items, n_items);
+    const ChunkList cl = i8_moe_q8_list(type, g, rows, ws);
+    int2* items = cl.items;
+    int32_t* n_items = cl.n_items;
+    if (!list_ready) i8_chunks_kernel<<<1, 1024, 0, s>>>((int32_t*)g.grp, groups, pl.mt, 0, nullptr, items, n_items);
     const int n1 = g.n1 > 0 ? g.n1 : g.N;
     I8Args args{};
     args.M = pl.mt;

@@ -3447,7 +3447,8 @@ constexpr int kGroupFastE = 256;
 __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __restrict__ sel, int n, int E,
                                                                int topk, int32_t* __restrict__ grp_off,
                                                                int32_t* __restrict__ tok_idx,
-                                                               int32_t* __restrict__ pos_of) {
+                                                               int32_t* __restrict__ pos_of, int t_sh,
+                                                               ChunkList l0, ChunkList l1, int n_lists) {
     __shared__ __attribute__((aligned(16))) int32_t s_sel[1024];
     __shared__ int32_t hist[16][kGroupFastE];  // per wavefront; then exclusive prefix over wavefronts
     __shared__ int32_t start[kGroupFastE];     // first position of each expert, advanced by each round
@@ -3514,13 +3515,39 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
         if (tid < kGroupFastE) start[tid] += total;
         __syncthreads();
     }
+    // The grouped int8 launches' chunk lists (and the shared expert's group
+    // end and token rows) from the offsets just written, saving their own
+    // launch.
+    if (n_lists > 0) {
+        __shared__ ChunkList lists[2];
+        if (tid == 0) { lists[0] = l0; lists[1] = l1; }
+        // start[e] has advanced to the end of expert e's rows
+        int r0 = 0, rows = 0;
+        if (tid < E) {
+            r0 = tid > 0 ? start[tid - 1] : 0;
+            rows = start[tid] - r0;
+        } else if (tid == E && t_sh > 0) {  // the shared expert: every token after the routed rows
+            r0 = n;
+            rows = t_sh;
+            grp_off[E + 1] = n + t_sh;
+        }
+        for (int t = tid; t < t_sh; t += 1024) tok_idx[n + t] = t;
+        __syncthreads();
+        chunk_lists_from_rows(r0, rows, lists, n_lists, &hist[0][0]);
+    }
 }
 
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
-                            int32_t* tok_idx, int32_t* pos_of, hipStream_t s) {
-    if (E > 1024) return hipErrorInvalidValue;
+                            int32_t* tok_idx, int32_t* pos_of, hipStream_t s, int t_sh, const ChunkList* lists,
+                            int n_lists, bool* lists_built) {
+    if (lists_built) *lists_built = false;
+    if (E > 1024 || n_lists < 0 || n_lists > 2) return hipErrorInvalidValue;
     if (E <= kGroupFastE) {
-        moe_group_small_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);
+        const ChunkList none{0, nullptr, nullptr};
+        moe_group_small_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of, t_sh,
+                                                  n_lists > 0 ? lists[0] : none, n_lists > 1 ? lists[1] : none,
+                                                  n_lists);
+        if (lists_built) *lists_built = n_lists > 0;
         return hipGetLastError();
     }
     moe_group_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);

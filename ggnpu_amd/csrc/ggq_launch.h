@@ -76,6 +76,14 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s);
 bool i8_gemv_eligible(const GemvProblem* ps, int n, int mode);
 bool gemv_q8row_eligible(const GemvProblem* ps, int n);
 hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* qa, const float* sa, hipStream_t s);
+// A list of (group, first row) chunks of at most mt rows over groups whose
+// rows are grp_off[g] .. grp_off[g+1]-1, for grouped launches that give a
+// grid row to each chunk (n_items: its length).
+struct ChunkList {
+    int mt;
+    int2* items;
+    int32_t* n_items;
+};
 // Grouped (MoE) fp32-activation problems on the same kernel (groups <= 1024,
 // g.M = total rows): a group's rows run in chunks of up to 4 (2 for Q6_K /
 // IQ4) rows, one grid row per chunk from a chunk list built on the device;
@@ -87,7 +95,11 @@ hipError_t launch_i8_gemv(const GemvProblem* ps, int n, int mode, const int8_t* 
 struct I8Shared { const void* W; const void* W2; int T; };
 bool i8_gemv_grouped_eligible(const GemvProblem& g);
 size_t i8_gemv_grouped_ws_bytes(const GemvProblem& g, int t_sh = 0);
-hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s, const I8Shared* sh = nullptr);
+hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s, const I8Shared* sh = nullptr,
+                                  bool list_ready = false);
+// The chunk list that launch would use in `ws` (mt 0 when the plan fails), for
+// launch_moe_group to build ahead of it (then list_ready = true).
+ChunkList i8_gemv_grouped_list(const GemvProblem& g, void* ws, int t_sh);
 // Largest K the register-resident GEMV supports.
 constexpr int kGemvMaxK = 32768;
 
@@ -139,7 +151,8 @@ hipError_t scratch_device_ptr(int device, void** out);
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel,
                             float* wsel, hipStream_t s);
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
-                            int32_t* tok_idx, int32_t* pos_of, hipStream_t s);
+                            int32_t* tok_idx, int32_t* pos_of, hipStream_t s, int t_sh = 0,
+                            const ChunkList* lists = nullptr, int n_lists = 0, bool* lists_built = nullptr);
 // Expert-grouped int8 GEMM over a device-built tile list (see
 // moe_gemm_kernel): C[p] = sa[row(p)] * codes(p) . W_e^T for every pair row
 // p of group e; rows [n1, N) of the output come from W2 into C2.
@@ -171,7 +184,8 @@ hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s);
 // (grp[E + 1]).  `ws`: i8_moe_q8_ws_bytes(...) bytes.
 bool i8_moe_q8_eligible(uint32_t type, const MoeGemm& g, int rows);
 size_t i8_moe_q8_ws_bytes(uint32_t type, const MoeGemm& g, int rows);
-hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws, hipStream_t s);
+hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws, hipStream_t s, bool list_ready = false);
+ChunkList i8_moe_q8_list(uint32_t type, const MoeGemm& g, int rows, void* ws);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int64_t n, hipStream_t s);
 hipError_t launch_moe_combine(const float* D, const int32_t* pos_of, const float* wsel, int T,
                               int topk, int H, const float* Dsh, const float* shared_w, float* out,
