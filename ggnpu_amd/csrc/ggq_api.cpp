@@ -64,7 +64,8 @@ struct ggq_ctx {
     Buffer attn;  // attention chunk partials
     Buffer pin;   // pinned host staging of A and C for the synchronous host-pointer entry points
     std::vector<void*> retired;  // outgrown device buffers, freed by ggq_destroy
-    void* scratch = nullptr;     // this device's fixed scratch region (ggq_mul_mat_noalloc_dev)
+    ggq_moe_trace trace{};       // intermediates of the last MoE call
+    bool trace_rows = false;     // Q8_ROW MoE calls keep their fp32 SwiGLU rows
 };
 
 namespace {
@@ -334,6 +335,20 @@ int mul_mat_host(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Last use of a device's fixed scratch region by ggq_mul_mat_noalloc_dev
+// (eager calls; work queued under graph capture is not tracked): the stream
+// it was queued on and an event recorded after it.  Process-wide, like the
+// region itself.
+struct ScratchGate {
+    std::mutex mu;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev = nullptr;
+};
+ScratchGate& scratch_gate(int device) {
+    static ScratchGate gates[64];
+    return gates[device & 63];
+}
+
 }  // namespace
 
 #define GGQ_GUARD(ctx)                                   \
@@ -364,13 +379,6 @@ int ggq_create(int device, ggq_ctx** out) {
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return GGQ_DEVICE_UNAVAILABLE;
-    }
-    // This device's copy of the fixed scratch region (looked up once per
-    // device, with the device current).
-    if (ggq::scratch_device_ptr(device, &c->scratch) != hipSuccess) {
-        hipStreamDestroy(c->stream);
-        delete c;
-        return GGQ_ERROR;
     }
     *out = c;
     return GGQ_OK;
@@ -489,10 +497,33 @@ int ggq_mul_mat_noalloc_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N,
     if (!aligned16(W)) return set_status(c, GGQ_INVALID_PARAM, "W must be 16-byte aligned");
     int st = check_matmul_shape(c, type, N, K, M, lda, ldc, act_mode);
     if (st != GGQ_OK) return st;
-    if (!c->scratch) return set_status(c, GGQ_ERROR, "no scratch region on device %d", c->device);
+    // This device's copy of the fixed region, looked up on the first call
+    // made on the device (with it current); a failed lookup fails this
+    // entry point only.
+    void* scratch = nullptr;
+    hipError_t e = ggq::scratch_device_ptr(c->device, &scratch);
+    if (e != hipSuccess) return hip_status(c, e, "scratch region lookup");
     const hipStream_t s = pick_stream(c, stream);
-    Arena ar{c, nullptr, (char*)c->scratch, ggq::kScratchBytes, s};
-    return mul_mat_queue(c, ar, W, type, N, K, A, lda, C, ldc, M, act_mode, s);
+    // One region per GPU: refuse a call that would overlap unfinished work
+    // queued by an earlier call on another stream (any context or thread).
+    ScratchGate& gate = scratch_gate(c->device);
+    std::lock_guard<std::mutex> lock(gate.mu);
+    if (gate.ev && gate.stream != s && hipEventQuery(gate.ev) == hipErrorNotReady)
+        return set_status(c, GGQ_ERROR,
+                          "the scratch region of device %d is still in use by a call queued on another stream; "
+                          "order the calls (same stream, or wait for the earlier one)",
+                          c->device);
+    Arena ar{c, nullptr, (char*)scratch, ggq::kScratchBytes, s};
+    st = mul_mat_queue(c, ar, W, type, N, K, A, lda, C, ldc, M, act_mode, s);
+    if (st != GGQ_OK) return st;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+        if (!gate.ev && (e = hipEventCreateWithFlags(&gate.ev, hipEventDisableTiming)) != hipSuccess)
+            return hip_status(c, e, "scratch event");
+        if ((e = hipEventRecord(gate.ev, s)) != hipSuccess) return hip_status(c, e, "scratch event");
+        gate.stream = s;
+    }
+    return st;
     GGQ_END(c)
 }
 
@@ -786,6 +817,99 @@ static hipError_t moe_grouped_gemv(const ggq::GemvProblem& g, void* items, size_
     return ggq::launch_gemv(g, s);
 }
 
+// Largest average of pair rows per group (experts, plus the shared expert)
+// that the grouped GEMVs take; above it the expert-grouped GEMMs run (their
+// 32-row tiles would be mostly empty below).  GGQ_MOE_GEMV_MAX_AVG
+// overrides the default of 5 (qwen35moe, per-row int8, GEMV vs GEMM: 64
+// tokens, 2.2 rows per group, 181 vs 235 us; 128 tokens, 4.5 rows, 271 vs
+// 282 us; 256 tokens, 9.0 rows, 379 vs 297 us).
+static bool moe_small_groups(size_t rows, int groups) {
+    const char* v = getenv("GGQ_MOE_GEMV_MAX_AVG");  // read per call: a process can switch it
+    const size_t max_avg = v && *v ? (size_t)atoi(v) : 5;
+    return rows <= max_avg * (size_t)groups;
+}
+
+// MoE layer with fp32 activations at prefill-sized batches: route, group
+// (tile list over the experts and the shared expert as group E), the token
+// rows split once into fp16 hi + lo planes, one expert-grouped fp16 GEMM
+// for every expert's gate and up (paired when their types match), SwiGLU
+// fused into the split of the pair rows, one grouped GEMM for down,
+// combine.  Requires H and F multiples of 64 (at most 16384), E <= 1023,
+// x 16-byte aligned (checked by the caller).
+static int moe_ffn_f16(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
+    const int T = p->T, H = p->H, F = p->F, E = p->E, k = p->top_k;
+    const bool shared = p->gate_shexp != nullptr;
+    const size_t nk = (size_t)T * k, ts = shared ? (size_t)T : 0, rows = nk + ts;
+    const int max_tiles = (int)((rows + ggq::kMoeTileRows - 1) / ggq::kMoeTileRows) + E + 1;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off = align256(off + bytes); return o; };
+    const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 2)),
+                 o_tok = take(4 * rows), o_pos = take(4 * nk), o_xh = take(2 * (size_t)T * H),
+                 o_xl = take(2 * (size_t)T * H), o_xs = take(4 * (size_t)T * (H / 32)), o_xe = take(4 * (size_t)T),
+                 o_g = take(4 * rows * F), o_u = take(4 * rows * F), o_hh = take(2 * rows * F),
+                 o_hl = take(2 * rows * F), o_hs = take(4 * rows * (F / 32)), o_he = take(4 * rows),
+                 o_d = take(4 * rows * H), o_tl = take(8 * (size_t)max_tiles), o_nt = take(4);
+    const size_t o_hf = c->trace_rows ? take(4 * rows * F) : 0;
+    int st;
+    if ((st = grow(c, c->dev.ws, off, s, "workspace")) != GGQ_OK) return st;
+    hipError_t e;
+    char* base = (char*)c->dev.ws.ptr;
+    int32_t* sel = (int32_t*)(base + o_sel);
+    float* wsel = (float*)(base + o_w);
+    int32_t* grp = (int32_t*)(base + o_go);
+    int32_t* tok = (int32_t*)(base + o_tok);
+    int32_t* pos = (int32_t*)(base + o_pos);
+    float *G = (float*)(base + o_g), *U = (float*)(base + o_u), *D = (float*)(base + o_d);
+    float* hf = c->trace_rows ? (float*)(base + o_hf) : nullptr;
+    void* tiles = base + o_tl;
+    int32_t* ntiles = (int32_t*)(base + o_nt);
+
+    if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s)) != hipSuccess) return hip_status(c, e, "moe_group");
+    if ((e = ggq::launch_moe_tiles(grp, tok, E, (int)ts, (int2*)tiles, ntiles, s)) != hipSuccess)
+        return hip_status(c, e, "moe_tiles");
+    if ((e = ggq::launch_split_rows(0, p->x, nullptr, H, T, H, base + o_xh, base + o_xl, (float*)(base + o_xs),
+                                    (float*)(base + o_xe), nullptr, s)) != hipSuccess)
+        return hip_status(c, e, "split x");
+    ggq::MoeGemm g{};
+    g.E = E; g.grp = grp; g.tiles = tiles; g.n_tiles = ntiles; g.max_tiles = max_tiles;
+    ggq::MoeGemm gu = g, gd = g;
+    gu.K = H; gu.x_idx = tok; gu.ldc = F;
+    gu.XH = base + o_xh; gu.XL = base + o_xl; gu.XS = (const float*)(base + o_xs); gu.xs = (const float*)(base + o_xe);
+    gu.w_stride = (int64_t)F * ggq::row_bytes(p->gate_type, H);
+    if (p->up_type == p->gate_type) {
+        gu.W = p->gate_exps; gu.W2 = p->up_exps; gu.Wsh = p->gate_shexp; gu.W2sh = p->up_shexp;
+        gu.N = 2 * F; gu.n1 = F; gu.C = G; gu.C2 = U;
+        if ((e = ggq::launch_moe_gemm(p->gate_type, gu, s)) != hipSuccess) return hip_status(c, e, "moe gate+up");
+    } else {
+        gu.W = p->gate_exps; gu.Wsh = p->gate_shexp; gu.N = F; gu.n1 = F; gu.C = G;
+        if ((e = ggq::launch_moe_gemm(p->gate_type, gu, s)) != hipSuccess) return hip_status(c, e, "moe gate");
+        gu.W = p->up_exps; gu.Wsh = p->up_shexp; gu.C = U;
+        gu.w_stride = (int64_t)F * ggq::row_bytes(p->up_type, H);
+        if ((e = ggq::launch_moe_gemm(p->up_type, gu, s)) != hipSuccess) return hip_status(c, e, "moe up");
+    }
+    // SwiGLU of every pair row (routed and shared), split for down.
+    if ((e = ggq::launch_split_rows(2, G, U, F, (int)rows, F, base + o_hh, base + o_hl, (float*)(base + o_hs),
+                                    (float*)(base + o_he), hf, s)) != hipSuccess)
+        return hip_status(c, e, "swiglu split");
+    gd.K = F; gd.x_idx = nullptr; gd.ldc = H;
+    gd.XH = base + o_hh; gd.XL = base + o_hl; gd.XS = (const float*)(base + o_hs); gd.xs = (const float*)(base + o_he);
+    gd.W = p->down_exps; gd.Wsh = p->down_shexp;
+    gd.w_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
+    gd.N = H; gd.n1 = H; gd.C = D;
+    if ((e = ggq::launch_moe_gemm(p->down_type, gd, s)) != hipSuccess) return hip_status(c, e, "moe down");
+    if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, shared ? D + nk * H : nullptr, p->shared_w, p->out, s)) !=
+        hipSuccess)
+        return hip_status(c, e, "moe combine");
+    c->trace = ggq_moe_trace{GGQ_ACT_F32, T, H, F, E, k, (int)rows, shared ? 1 : 0, grp, tok, pos, G, U, hf, nullptr,
+                             nullptr, D, shared ? D + nk * H : nullptr};
+    if (p->sel_experts && (e = hipMemcpyAsync(p->sel_experts, sel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_status(c, e, "copy selection");
+    if (p->sel_weights && (e = hipMemcpyAsync(p->sel_weights, wsel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+        return hip_status(c, e, "copy weights");
+    return set_status(c, GGQ_OK);
+}
+
 // MoE layer with per-row int8 activations (GGQ_ACT_Q8_ROW): route, group,
 // quantize the token rows once, one grouped int8 launch for every expert's
 // gate and up (and the shared expert's, as group E: the expert-grouped GEMM,
@@ -802,6 +926,7 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
                  o_tok = take(4 * rows), o_pos = take(4 * nk), o_qx = take((size_t)T * H), o_sx = take(4 * (size_t)T),
                  o_g = take(4 * rows * F), o_u = take(4 * rows * F), o_qh = take(rows * F), o_sh = take(4 * rows),
                  o_d = take(4 * rows * H), o_tl = take(8 * (size_t)max_tiles), o_nt = take(4);
+    const size_t o_hf = c->trace_rows ? take(4 * rows * F) : 0;
     // chunk list of the grouped int8 GEMV (chunks of 4 or more rows)
     const size_t it_bytes = 8 * ((rows + 3) / 4 + std::min<size_t>((size_t)E + 1, rows)) + 16;
     const size_t o_it = take(it_bytes), o_it2 = take(it_bytes);  // gate / up, down
@@ -828,13 +953,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     // Few rows per expert (decode-sized batches): the grouped int8 GEMV in
     // its given-codes mode (chunks of 8 rows, 4 for Q6_K / IQ4), whose
     // lanes carry the rows; more rows per expert: the expert-grouped GEMM's
-    // 32-row tiles.  GGQ_MOE_I8_MAX_AVG: largest average rows per group that
-    // takes the GEMV, default 5 (qwen35moe, GEMV vs GEMM: 64 tokens, 2.2 rows
-    // per group, 181 vs 235 us; 128 tokens, 4.5 rows, 271 vs 282 us; 256
-    // tokens, 9.0 rows, 379 vs 297 us).
-    const char* avg_env = getenv("GGQ_MOE_I8_MAX_AVG");
-    const size_t max_avg = avg_env && *avg_env ? (size_t)atoi(avg_env) : 5;
-    const bool small = rows <= max_avg * (size_t)(E + (shared ? 1 : 0));
+    // 32-row tiles (moe_small_groups).
+    const bool small = moe_small_groups(rows, E + (shared ? 1 : 0));
     auto i8_ok = [&](uint32_t type, const ggq::MoeGemm& d) {
         return small && ggq::i8_moe_q8_eligible(type, d, (int)rows) &&
                ggq::i8_moe_q8_ws_bytes(type, d, (int)rows) <= it_bytes;
@@ -887,7 +1007,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         if ((e = grouped(p->up_type, gu)) != hipSuccess) return hip_status(c, e, "moe up");
     }
     // SwiGLU of every pair row (routed and shared) and its int8 row codes.
-    if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s)) != hipSuccess)
+    float* hf = c->trace_rows ? (float*)(base + o_hf) : nullptr;
+    if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s, hf)) != hipSuccess)
         return hip_status(c, e, "swiglu quant");
     if (dn_i8) e = ggq::launch_i8_moe_q8(p->down_type, gd, (int)rows, base + o_it2, s, built);
     else e = ggq::launch_moe_gemm(p->down_type, gd, s);
@@ -895,6 +1016,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, shared ? D + nk * H : nullptr, p->shared_w, p->out, s)) !=
         hipSuccess)
         return hip_status(c, e, "moe combine");
+    c->trace = ggq_moe_trace{GGQ_ACT_Q8_ROW, T, H, F, E, k, (int)rows, shared ? 1 : 0, grp, tok, pos, G, U, hf, qh,
+                             sh, D, shared ? D + nk * H : nullptr};
     if (p->sel_experts && (e = hipMemcpyAsync(p->sel_experts, sel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
         return hip_status(c, e, "copy selection");
     if (p->sel_weights && (e = hipMemcpyAsync(p->sel_weights, wsel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
@@ -944,6 +1067,11 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
         if (w && !aligned16(w)) return set_status(c, GGQ_INVALID_PARAM, "weights must be 16-byte aligned");
     if (T == 0) return set_status(c, GGQ_OK);
     hipStream_t s = pick_stream(c, stream);
+    // Prefill-sized batches: the expert-grouped fp16 GEMM, where its shape
+    // limits allow.
+    if (!moe_small_groups((size_t)T * k + (shared ? T : 0), E + (shared ? 1 : 0)) && E <= 1023 && H % 64 == 0 &&
+        F % 64 == 0 && H <= 16384 && F <= 16384 && ((uintptr_t)p->x & 15u) == 0)
+        return moe_ffn_f16(c, p, s);
 
     const size_t nk = (size_t)T * k;
     size_t off = 0;
@@ -1040,12 +1168,27 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     }
     if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, Dsh, p->shared_w, p->out, s)) != hipSuccess)
         return hip_status(c, e, "moe combine");
+    c->trace = ggq_moe_trace{GGQ_ACT_F32, T, H, F, E, k, (int)(nk + ts), shared ? 1 : 0, grp, tok, pos, G, U, Hh,
+                             nullptr, nullptr, D, Dsh};
     if (p->sel_experts && (e = hipMemcpyAsync(p->sel_experts, sel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
         return hip_status(c, e, "copy selection");
     if (p->sel_weights && (e = hipMemcpyAsync(p->sel_weights, wsel, 4 * nk, hipMemcpyDeviceToDevice, s)) != hipSuccess)
         return hip_status(c, e, "copy weights");
     return set_status(c, GGQ_OK);
     GGQ_END(c)
+}
+
+int ggq_moe_trace_get(const ggq_ctx* c, ggq_moe_trace* out) {
+    if (!c || !out) return GGQ_INVALID_PARAM;
+    *out = c->trace;
+    return c->trace.grp ? GGQ_OK : GGQ_NOT_FOUND;
+}
+
+int ggq_moe_trace_rows(ggq_ctx* c, int on) {
+    if (!c) return GGQ_INVALID_PARAM;
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
+    c->trace_rows = on != 0;
+    return GGQ_OK;
 }
 
 }  // extern "C"

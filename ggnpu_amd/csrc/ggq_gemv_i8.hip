@@ -1074,11 +1074,11 @@ I8Grid i8_grid(const GemvProblem* ps, int n, const int* lds_need, int M) {
 template <int D, int NE, int NP, int FS>
 hipError_t i8_run(I8Args& args, const I8Grid& gr, int n, hipStream_t s) {
     auto kern = i8_gemv_kernel<D, NE, NP, FS>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
-        attr_set = true;
-    }
+    // set once per process (thread-safe static initialisation); a failure
+    // is reported by every launch that needs the attribute
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    if (attr != hipSuccess) return attr;
     const int lds = gr.lds;
     args.begin[0] = 0;
     for (int i = 0; i < n; i++) {
@@ -1210,11 +1210,11 @@ namespace {
 template <int D, int NE, int NP, int FS>
 hipError_t i8_run_grouped(I8Args& args, const I8Group& gp, int groups, int lds, hipStream_t s) {
     auto kern = i8_gemv_grouped_kernel<D, NE, NP, FS>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
-        attr_set = true;
-    }
+    // set once per process (thread-safe static initialisation); a failure
+    // is reported by every launch that needs the attribute
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    if (attr != hipSuccess) return attr;
     kern<<<dim3(args.begin[args.n], groups), kThreads, lds, s>>>(args, gp);  // groups: chunk-list bound
     return hipGetLastError();
 }

@@ -148,7 +148,7 @@ enum { PROD_NONE = 0, PROD_RMS = 1, PROD_SWIGLU = 2 };
 template <int P>
 __device__ __forceinline__ void quant_row_regs(const float* a, const float* aux, float eps, int m, int K,
                                                int8_t* __restrict__ q, float* __restrict__ scales,
-                                               float* __restrict__ x_eff) {
+                                               float* __restrict__ x_eff, float* __restrict__ prod_out = nullptr) {
     __shared__ float wmax[4];
     constexpr int R = 16;
     float4 v[R];
@@ -192,6 +192,16 @@ __device__ __forceinline__ void quant_row_regs(const float* a, const float* aux,
             v[i].w = __fmul_rn(__fmul_rn(v[i].w, is), w.w);
         }
     }
+    // The produced row itself, when asked for (stage-by-stage checks of the
+    // layers that quantize a produced row).
+    if (prod_out) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 4 * threadIdx.x + 1024 * i;
+            if (k >= K) break;
+            *(float4*)(prod_out + (int64_t)m * K + k) = v[i];
+        }
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < R; i++)
@@ -225,10 +235,11 @@ template <int P>
 __global__ __launch_bounds__(256) void produce_quant_row_kernel(const float* __restrict__ A,
                                                                 const float* __restrict__ aux, int lda, int K,
                                                                 float eps, int8_t* __restrict__ q,
-                                                                float* __restrict__ scales) {
+                                                                float* __restrict__ scales,
+                                                                float* __restrict__ prod_out) {
     const int m = blockIdx.x;
     const float* au = P == PROD_SWIGLU ? aux + (int64_t)m * lda : aux;
-    quant_row_regs<P>(A + (int64_t)m * lda, au, eps, m, K, q, scales, nullptr);
+    quant_row_regs<P>(A + (int64_t)m * lda, au, eps, m, K, q, scales, nullptr, prod_out);
 }
 
 // One workgroup per row: absolute maximum, then codes.  With 16-byte
@@ -318,15 +329,15 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
 }
 
 hipError_t launch_produce_quant(int producer, const float* A, const float* aux, int lda, int M, int K, float eps,
-                                int8_t* q, float* scales, hipStream_t s) {
+                                int8_t* q, float* scales, hipStream_t s, float* prod_out) {
     if (M == 0) return hipSuccess;
     if (K <= 0 || K > 1024 * 16 || K % 4 || lda % 4 || (uintptr_t)A % 16 || (uintptr_t)aux % 16 ||
-        (uintptr_t)q % 4)
+        (uintptr_t)q % 4 || (uintptr_t)prod_out % 16)
         return hipErrorInvalidValue;
     if (producer == PROD_RMS)
-        produce_quant_row_kernel<PROD_RMS><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales);
+        produce_quant_row_kernel<PROD_RMS><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out);
     else if (producer == PROD_SWIGLU && aux)
-        produce_quant_row_kernel<PROD_SWIGLU><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales);
+        produce_quant_row_kernel<PROD_SWIGLU><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -2401,6 +2412,12 @@ struct MoeGemmArgs {
     float* C;
     float* C2;
     int ldc;
+    // fp32-row mode (moe_gemm_f16_kernel): hi / lo planes [rows][K], group
+    // sums [rows][K/32] and row scales 2^-e [rows] of the activation rows
+    const _Float16* XH;
+    const _Float16* XL;
+    const float* XS;
+    const float* xs;
 };
 constexpr int kMoeBM = kMoeTileRows, kMoeBN = 128;
 
@@ -2599,6 +2616,280 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     }
 }
 
+// ------------------------------- expert-grouped fp16 GEMM (MoE, fp32 rows)
+// The prefill-sized MoE layer with fp32 activations.  Each activation row
+// is written once (split_rows_kernel) as two fp16 planes under a power of
+// two per row, x * 2^e = hi + lo with the row's largest magnitude in
+// [2^14, 2^15): |x 2^e - hi - lo| <= 2^-8, i.e. 2^-23 of the row maximum.
+// The weights' integer codes are exact in fp16 (|code| <= 128), so each
+// product code * (hi + lo) is exact in the fp32 accumulator of
+// v_mfma_f32_32x32x16_f16; per 32-value scale group four MFMAs (hi and lo
+// of the two 16-value halves) chain into one fp32 sum P, and the epilogue
+// is the exact-code one of the int8 GEMM: acc += dl * P (- ml * S, S the
+// group sum of hi + lo from the split).  Q6_K's 16-value groups take one
+// hi / lo pair each.  The result is scaled by 2^-e of its row at the
+// store.  Tiles, staging of the weights and the gate / up pairing are those
+// of moe_gemm_kernel; K-steps of 64 values keep the LDS at 45 KB.
+constexpr int kF16BK = 64;                 // values per K-step
+constexpr int kF16ALd = kF16BK + 8;        // fp16 per A row in LDS (144 B: conflict-free)
+constexpr int kF16BLd = kF16BK + 16;       // code bytes per B row in LDS (80 B)
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Eight int8 codes (two dwords) as eight fp16 values: biased to unsigned,
+// placed as the low mantissa byte of 1024.0, then 1024 + 128 subtracted.
+__device__ __forceinline__ uint32_t s8x2_f16(uint32_t w, uint32_t sel) {
+    const h2v v = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, w, sel));
+    const h2v off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(uint32_t, v - off);
+}
+__device__ __forceinline__ v8h s8x8_f16(uint2 c) {
+    const uint32_t a = c.x ^ 0x80808080u, b = c.y ^ 0x80808080u;
+    return __builtin_bit_cast(v8h, make_uint4(s8x2_f16(a, 0x04010400u), s8x2_f16(a, 0x04030402u),
+                                              s8x2_f16(b, 0x04010400u), s8x2_f16(b, 0x04030402u)));
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void moe_gemm_f16_kernel(MoeGemmArgs a) {
+    constexpr bool kMin = T == T_Q4_K || T == T_Q5_K;
+    constexpr bool kQ6 = T == T_Q6_K;
+    constexpr int G = kF16BK / 32;       // 32-value groups per K-step
+    constexpr int GS = kQ6 ? 2 * G : G;  // scales per row and step
+    __shared__ __attribute__((aligned(16))) _Float16 Ah[2][kMoeBM][kF16ALd];
+    __shared__ __attribute__((aligned(16))) _Float16 Al[2][kMoeBM][kF16ALd];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[2][kMoeBN][kF16BLd];
+    __shared__ __attribute__((aligned(16))) float Bd[2][kMoeBN][GS];
+    __shared__ __attribute__((aligned(16))) float Bm[2][kMoeBN][G];
+    __shared__ __attribute__((aligned(16))) float As[2][G][kMoeBM];
+
+    const int tile = blockIdx.y;
+    if (tile >= *a.n_tiles) return;
+    const int2 te = a.tiles[tile];
+    const int e = te.x, p0 = te.y, p_end = a.grp[e + 1];
+    const uint8_t* const W1 = e == a.E ? a.Wsh : a.W + (int64_t)e * a.w_stride;
+    const uint8_t* const W2 = e == a.E ? a.W2sh : (a.W2 ? a.W2 + (int64_t)e * a.w_stride : nullptr);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lk = lane >> 5;
+    const int n_tile = blockIdx.x * kMoeBN;
+    const int nsteps = a.K / kF16BK;  // K is a multiple of 256 or of 64 (checked by the caller)
+    const int KG = a.K / 32;
+
+    // Activations: thread t stages 8 values of row t / 8 from both planes.
+    const int ar = tid >> 3, akc = (tid & 7) * 8;
+    const int pa = p0 + ar;
+    const bool arow_ok = pa < p_end;
+    const int arow = a.x_idx ? a.x_idx[arow_ok ? pa : p0] : (arow_ok ? pa : p0);
+    const _Float16* const hptr = a.XH + (int64_t)arow * a.K + akc;
+    const _Float16* const lptr = a.XL + (int64_t)arow * a.K + akc;
+    // Group sums (K-quant mins): threads 0..63 stage (group, row) entries.
+    const int sr = tid & 31, sg = (tid >> 5) & 1;
+    const int ps = p0 + sr;
+    const int srow = a.x_idx ? a.x_idx[ps < p_end ? ps : p0] : (ps < p_end ? ps : p0);
+    const float* const sptr = a.XS + (int64_t)srow * KG + sg;
+    // Weights: 128 rows x 2 groups per step, one (row, group) slot per thread.
+    const int br = tid / G, bg = tid % G;
+    const int bn = n_tile + br;
+    const bool brow_ok = bn < a.N;
+    const int bnn = brow_ok ? bn : 0;
+    const uint8_t* const bptr = bnn < a.n1 ? W1 + (int64_t)bnn * a.row_bytes : W2 + (int64_t)(bnn - a.n1) * a.row_bytes;
+
+    uint4 ahr, alr;
+    float asr = 0.0f;
+    MStage<T> breg;
+    auto fetch = [&](int st) {
+        const int k0 = st * kF16BK;
+        ahr = arow_ok ? *(const uint4*)(hptr + k0) : make_uint4(0, 0, 0, 0);
+        alr = arow_ok ? *(const uint4*)(lptr + k0) : make_uint4(0, 0, 0, 0);
+        if constexpr (kMin)
+            if (tid < 64) asr = ps < p_end ? sptr[k0 / 32] : 0.0f;
+        breg.fetch(bptr, brow_ok ? k0 + 32 * bg : 0, brow_ok);
+    };
+    auto store = [&](int buf) {
+        *(uint4*)&Ah[buf][ar][akc] = ahr;
+        *(uint4*)&Al[buf][ar][akc] = alr;
+        if constexpr (kMin)
+            if (tid < 64) As[buf][sg][sr] = asr;
+        if constexpr (kQ6) breg.store2(&Bs[buf][br][32 * bg], &Bd[buf][br][2 * bg], nullptr);
+        else breg.store2(&Bs[buf][br][32 * bg], &Bd[buf][br][bg], &Bm[buf][br][bg]);
+    };
+
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    const v16f zero = {};
+    const int wn = 32 * wave;
+
+    fetch(0);
+    store(0);
+    if (nsteps > 1) fetch(1);
+    __syncthreads();
+    for (int st = 0; st < nsteps; st++) {
+        const int buf = st & 1;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            v8h H[2], L[2], B[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int k = 32 * g + 16 * hh + 8 * lk;
+                H[hh] = *(const v8h*)&Ah[buf][li][k];
+                L[hh] = *(const v8h*)&Al[buf][li][k];
+                B[hh] = s8x8_f16(*(const uint2*)&Bs[buf][wn + li][k]);
+            }
+            if constexpr (kQ6) {
+                v16f P0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[0], B[0], zero, 0, 0, 0);
+                P0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[0], B[0], P0, 0, 0, 0);
+                v16f P1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[1], B[1], zero, 0, 0, 0);
+                P1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[1], B[1], P1, 0, 0, 0);
+                const float d0 = Bd[buf][wn + li][2 * g], d1 = Bd[buf][wn + li][2 * g + 1];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    acc[r] = fmaf(d0, P0[r], acc[r]);
+                    acc[r] = fmaf(d1, P1[r], acc[r]);
+                }
+            } else {
+                v16f P = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[0], B[0], zero, 0, 0, 0);
+                P = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[0], B[0], P, 0, 0, 0);
+                P = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[1], B[1], P, 0, 0, 0);
+                P = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[1], B[1], P, 0, 0, 0);
+                const float dl = Bd[buf][wn + li][g];
+                if constexpr (kMin) {
+                    const float ml = Bm[buf][wn + li][g];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float4 sv = *(const float4*)&As[buf][g][8 * j + 4 * lk];
+                        const float sj[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int r = 4 * j + i;
+                            acc[r] = fmaf(dl, P[r], acc[r]);
+                            acc[r] = fmaf(-ml, sj[i], acc[r]);
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[r] = fmaf(dl, P[r], acc[r]);
+                }
+            }
+        }
+        if (st + 1 < nsteps) {
+            store(buf ^ 1);
+            if (st + 2 < nsteps) fetch(st + 2);
+            __syncthreads();
+        }
+    }
+
+    // Lane (li, lk) holds weight row n = n_tile + wn + li and pair rows
+    // p0 + 8 (r >> 2) + 4 lk + (r & 3).
+    const int n = n_tile + wn + li;
+    if (n >= a.N) return;
+    float* const Cb = n < a.n1 ? a.C + n : a.C2 + (n - a.n1);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int p = p0 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (p < p_end) Cb[(int64_t)p * a.ldc] = acc[r] * a.xs[a.x_idx ? a.x_idx[p] : p];
+    }
+}
+
+// Rows of fp32 activations as the fp16 hi + lo planes of the grouped fp16
+// GEMM: per row the power of two 2^e that puts its largest magnitude in
+// [2^14, 2^15) (e clamped to 126: all-subnormal rows keep fewer bits), hi =
+// fp16(x 2^e), lo = fp16(x 2^e - hi), the group sums of hi + lo per 32
+// values, and 2^-e.  P = PROD_SWIGLU forms each row as silu(g) * u first
+// (the SwiGLU of quant_row_regs, same expression); prod_out receives the
+// produced rows when set.  One workgroup per row, K <= 16384, K a multiple
+// of 32, rows 16-byte aligned.
+template <int P>
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ A, const float* __restrict__ aux,
+                                                         int lda, int K, _Float16* __restrict__ XH,
+                                                         _Float16* __restrict__ XL, float* __restrict__ XS,
+                                                         float* __restrict__ xs, float* __restrict__ prod_out) {
+    __shared__ float wmax[4];
+    constexpr int R = 16;
+    const int m = blockIdx.x;
+    const float* a = A + (int64_t)m * lda;
+    float4 v[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int k = 4 * threadIdx.x + 1024 * i;
+        v[i] = k < K ? *(const float4*)(a + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if constexpr (P == PROD_SWIGLU) {
+        const float* u = aux + (int64_t)m * lda;
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 4 * threadIdx.x + 1024 * i;
+            if (k >= K) break;
+            const float4 w = *(const float4*)(u + k);
+            v[i].x = (v[i].x / (1.0f + expf(-v[i].x))) * w.x;
+            v[i].y = (v[i].y / (1.0f + expf(-v[i].y))) * w.y;
+            v[i].z = (v[i].z / (1.0f + expf(-v[i].z))) * w.z;
+            v[i].w = (v[i].w / (1.0f + expf(-v[i].w))) * w.w;
+        }
+    }
+    if (prod_out) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 4 * threadIdx.x + 1024 * i;
+            if (k >= K) break;
+            *(float4*)(prod_out + (int64_t)m * K + k) = v[i];
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+        amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i].x), fabsf(v[i].y))), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int ex = 0;
+    if (amax > 0.0f) {
+        int x2;
+        (void)frexpf(amax, &x2);  // amax in [2^(x2-1), 2^x2)
+        ex = 15 - x2;
+        if (ex > 126) ex = 126;
+    }
+    if (threadIdx.x == 0) xs[m] = ldexpf(1.0f, -ex);
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int k = 4 * threadIdx.x + 1024 * i;
+        if (k >= K) break;
+        const float y[4] = {ldexpf(v[i].x, ex), ldexpf(v[i].y, ex), ldexpf(v[i].z, ex), ldexpf(v[i].w, ex)};
+        _Float16 h[4], l[4];
+        float gs = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            h[j] = (_Float16)y[j];
+            l[j] = (_Float16)(y[j] - (float)h[j]);
+            gs += (float)h[j] + (float)l[j];
+        }
+        *(uint2*)(XH + (int64_t)m * K + k) = __builtin_bit_cast(uint2, h4v{h[0], h[1], h[2], h[3]});
+        *(uint2*)(XL + (int64_t)m * K + k) = __builtin_bit_cast(uint2, h4v{l[0], l[1], l[2], l[3]});
+        // eight consecutive threads hold one 32-value group
+        gs += __shfl_xor(gs, 1, 64);
+        gs += __shfl_xor(gs, 2, 64);
+        gs += __shfl_xor(gs, 4, 64);
+        if ((threadIdx.x & 7) == 0) XS[(int64_t)m * (K / 32) + k / 32] = gs;
+    }
+}
+
+hipError_t launch_split_rows(int producer, const float* A, const float* aux, int lda, int M, int K, void* XH,
+                             void* XL, float* XS, float* xs, float* prod_out, hipStream_t s) {
+    if (M == 0) return hipSuccess;
+    if (K <= 0 || K > 1024 * 16 || K % 32 || lda % 4 || (uintptr_t)A % 16 || (uintptr_t)aux % 16 ||
+        (uintptr_t)XH % 8 || (uintptr_t)XL % 8 || (uintptr_t)prod_out % 16)
+        return hipErrorInvalidValue;
+    if (producer == PROD_SWIGLU)
+        split_rows_kernel<PROD_SWIGLU><<<M, 256, 0, s>>>(A, aux, lda, K, (_Float16*)XH, (_Float16*)XL, XS, xs,
+                                                          prod_out);
+    else
+        split_rows_kernel<PROD_NONE><<<M, 256, 0, s>>>(A, aux, lda, K, (_Float16*)XH, (_Float16*)XL, XS, xs,
+                                                        prod_out);
+    return hipGetLastError();
+}
+
 // The tile list of the grouped GEMM: group e (experts 0..E-1, then the
 // shared expert as group E with T_sh rows after the routed ones) covers
 // ceil(rows / 32) tiles.  One workgroup: a prefix sum over the groups.
@@ -2651,8 +2942,22 @@ hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s) {
     a.QA = g.QA; a.sa = g.sa; a.x_idx = g.x_idx; a.grp = g.grp;
     a.tiles = (const int2*)g.tiles; a.n_tiles = g.n_tiles;
     a.C = g.C; a.C2 = g.C2; a.ldc = g.ldc;
+    a.XH = (const _Float16*)g.XH; a.XL = (const _Float16*)g.XL; a.XS = g.XS; a.xs = g.xs;
     const dim3 grid((g.N + kMoeBN - 1) / kMoeBN, g.max_tiles);
     if (g.max_tiles <= 0) return hipSuccess;
+    if (g.XH) {  // fp32 rows as fp16 hi + lo
+        if (g.K % kF16BK || !g.XL || !g.XS || !g.xs) return hipErrorInvalidValue;
+        switch (type) {
+        case T_Q4_K: moe_gemm_f16_kernel<T_Q4_K><<<grid, 256, 0, s>>>(a); break;
+        case T_Q5_K: moe_gemm_f16_kernel<T_Q5_K><<<grid, 256, 0, s>>>(a); break;
+        case T_Q6_K: moe_gemm_f16_kernel<T_Q6_K><<<grid, 256, 0, s>>>(a); break;
+        case T_Q8_0: moe_gemm_f16_kernel<T_Q8_0><<<grid, 256, 0, s>>>(a); break;
+        case T_IQ4_NL: moe_gemm_f16_kernel<T_IQ4_NL><<<grid, 256, 0, s>>>(a); break;
+        case T_IQ4_XS: moe_gemm_f16_kernel<T_IQ4_XS><<<grid, 256, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (type) {
     case T_Q4_K: moe_gemm_kernel<T_Q4_K><<<grid, 256, 0, s>>>(a); break;
     case T_Q5_K: moe_gemm_kernel<T_Q5_K><<<grid, 256, 0, s>>>(a); break;

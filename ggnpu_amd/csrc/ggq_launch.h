@@ -23,8 +23,10 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
 // 2; A = gate rows, aux = up rows, both with row stride lda) of each row,
 // then the per-row quantization of launch_quant_act mode 1.  K <= 16384,
 // K and lda multiples of 4, A and aux 16-byte aligned, q dense [M][K].
+// prod_out (optional, dense [M][K], 16-byte aligned) receives the produced
+// fp32 rows that were quantized.
 hipError_t launch_produce_quant(int producer, const float* A, const float* aux, int lda, int M, int K, float eps,
-                                int8_t* q, float* scales, hipStream_t s);
+                                int8_t* q, float* scales, hipStream_t s, float* prod_out = nullptr);
 
 // Decode GEMV with fp32 activations: Y[y_row][n] = sum_k X[x_row][k] W[n][k].
 // Plain mode: grp_off == null, rows 0..M-1.  Grouped mode (MoE): group g uses
@@ -173,6 +175,12 @@ struct MoeGemm {
     float* C;
     float* C2;
     int ldc;
+    // fp32 activation rows (the fp16 hi + lo kernel) when XH is set: planes
+    // from launch_split_rows (K a multiple of 64); QA / sa unused then.
+    const void* XH = nullptr;
+    const void* XL = nullptr;
+    const float* XS = nullptr;
+    const float* xs = nullptr;
 };
 constexpr int kMoeTileRows = 32;  // pair rows per grouped-GEMM tile
 hipError_t launch_moe_tiles(int32_t* grp, int32_t* x_idx, int E, int T_sh, int2* tiles, int32_t* n_tiles, hipStream_t s);
@@ -186,6 +194,13 @@ bool i8_moe_q8_eligible(uint32_t type, const MoeGemm& g, int rows);
 size_t i8_moe_q8_ws_bytes(uint32_t type, const MoeGemm& g, int rows);
 hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws, hipStream_t s, bool list_ready = false);
 ChunkList i8_moe_q8_list(uint32_t type, const MoeGemm& g, int rows, void* ws);
+// fp32 rows (producer 0) or their SwiGLU silu(A) * aux (producer 2, both
+// with row stride lda) as the fp16 hi + lo planes XH / XL [M][K] (fp16),
+// group sums XS [M][K/32] and row scales xs [M] of the grouped fp16 GEMM;
+// prod_out (optional, [M][K]) receives the produced rows.  K <= 16384, a
+// multiple of 32; A, aux 16-byte aligned.
+hipError_t launch_split_rows(int producer, const float* A, const float* aux, int lda, int M, int K, void* XH,
+                             void* XL, float* XS, float* xs, float* prod_out, hipStream_t s);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, int64_t n, hipStream_t s);
 hipError_t launch_moe_combine(const float* D, const int32_t* pos_of, const float* wsel, int T,
                               int topk, int H, const float* Dsh, const float* shared_w, float* out,

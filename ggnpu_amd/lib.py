@@ -78,6 +78,18 @@ class MoeParams(ctypes.Structure):
     ]
 
 
+class MoeTrace(ctypes.Structure):
+    """ggq_moe_trace (include/ggq.h)."""
+    _fields_ = [
+        ("act_mode", ctypes.c_int), ("T", ctypes.c_int), ("H", ctypes.c_int), ("F", ctypes.c_int),
+        ("E", ctypes.c_int), ("top_k", ctypes.c_int), ("rows", ctypes.c_int), ("shared", ctypes.c_int),
+        ("grp", ctypes.c_void_p), ("tok", ctypes.c_void_p), ("pos", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("h", ctypes.c_void_p),
+        ("h_codes", ctypes.c_void_p), ("h_scales", ctypes.c_void_p),
+        ("down", ctypes.c_void_p), ("down_shared", ctypes.c_void_p),
+    ]
+
+
 class GemvDesc(ctypes.Structure):
     _fields_ = [("W", ctypes.c_void_p), ("type", ctypes.c_uint32), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
                 ("A", ctypes.c_void_p), ("C", ctypes.c_void_p)]
@@ -139,6 +151,8 @@ SIGNATURES = {
     "ggq_block_dot_dev": (_I, [_P, _P, _U32, _I64, _I64, _P, _I, _P, _P]),
     "ggq_moe_ffn_dev": (_I, [_P, ctypes.POINTER(MoeParams), _P]),
     "ggq_moe_ffn_act_dev": (_I, [_P, ctypes.POINTER(MoeParams), _I, _P]),
+    "ggq_moe_trace_get": (_I, [_P, ctypes.POINTER(MoeTrace)]),
+    "ggq_moe_trace_rows": (_I, [_P, _I]),
     "ggq_encode": (_I, [_U32, _P, _I64, _I64, _P]),
     "ggq_row_bytes": (_I64, [_U32, _I64]),
 }

@@ -151,8 +151,13 @@ int ggq_mul_mat_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64
  * region of GGQ_NOALLOC_SCRATCH_BYTES per GPU, held from library load until
  * the process ends and shared by every context on that GPU; a call that
  * would need more fails with GGQ_INVALID_PARAM before queuing anything.
- * Calls that overlap on one GPU (several streams, threads or contexts) race
- * on that region: order them.  Results equal ggq_mul_mat_dev's. */
+ * Calls that overlap on one GPU (several streams, threads or contexts) would
+ * race on that region: order them.  An eager call is refused with GGQ_ERROR,
+ * before queuing anything, while work an earlier eager call queued on
+ * another stream is unfinished (calls queued under graph capture are not
+ * tracked).  The region's address is looked up on the first call on a
+ * device; if that fails only this entry point fails.  Results equal
+ * ggq_mul_mat_dev's. */
 #define GGQ_NOALLOC_SCRATCH_BYTES (32u << 20)
 int ggq_mul_mat_noalloc_dev(ggq_ctx* ctx, const void* W, uint32_t type, int64_t N, int64_t K,
                             const float* A, int lda, float* C, int ldc, int M, int act_mode, void* stream);
@@ -355,6 +360,38 @@ int ggq_moe_ffn_dev(ggq_ctx* ctx, const ggq_moe_params* p, void* stream);
  * token rows) -- the prefill-sized path.  Extra requirements in that mode:
  * H and F multiples of 32 and at most 16384, E <= 1023, x 16-byte aligned. */
 int ggq_moe_ffn_act_dev(ggq_ctx* ctx, const ggq_moe_params* p, int act_mode, void* stream);
+
+/* Intermediates of the most recent MoE call on the context
+ * (ggq_moe_ffn_dev or ggq_moe_ffn_act_dev), for checking the layer stage by
+ * stage against the per-token loop of src/cli/main.cpp:3110-3193.  Device
+ * pointers into the context's workspace, valid until the next call that uses
+ * the workspace.  No reference counterpart (the reference keeps no
+ * intermediates).  "Pair rows" are the (token, expert) rows sorted by expert:
+ * routed rows grp[e] .. grp[e+1]-1 belong to expert e (grp[E] = T*top_k);
+ * with a shared expert, rows T*top_k + t (t < T) are token t's shared-expert
+ * rows. */
+typedef struct {
+    int act_mode;           /* GGQ_ACT_F32 or GGQ_ACT_Q8_ROW */
+    int T, H, F, E, top_k;
+    int rows;               /* T*top_k, plus T with a shared expert */
+    int shared;
+    const int32_t* grp;     /* [E + 1] */
+    const int32_t* tok;     /* [T*top_k] token of each routed pair row */
+    const int32_t* pos;     /* [T][top_k] pair row of each (token, slot) */
+    const float* gate;      /* [rows][F] gate projection outputs */
+    const float* up;        /* [rows][F] up projection outputs */
+    const float* h;         /* [rows][F] SwiGLU rows silu(gate) * up: always
+                               with GGQ_ACT_F32; with GGQ_ACT_Q8_ROW only after
+                               ggq_moe_trace_rows(ctx, 1) (else NULL) */
+    const int8_t* h_codes;  /* [rows][F] GGQ_ACT_Q8_ROW: int8 codes of h */
+    const float* h_scales;  /* [rows] their row scales */
+    const float* down;      /* [T*top_k][H] down projection of each routed pair row */
+    const float* down_shared; /* [T][H] the shared expert's, or NULL */
+} ggq_moe_trace;
+int ggq_moe_trace_get(const ggq_ctx* ctx, ggq_moe_trace* out);
+/* on != 0: later GGQ_ACT_Q8_ROW MoE calls also write the fp32 SwiGLU rows
+ * they quantize (trace.h), from the same registers the codes come from. */
+int ggq_moe_trace_rows(ggq_ctx* ctx, int on);
 
 /* ------------------------------------------------------- synthetic data */
 

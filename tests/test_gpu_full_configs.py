@@ -215,3 +215,73 @@ def test_moe_layer_as_benchmarked(ctx, orc, T, act_mode, n_check):
     assert err < TOL, err
     for i, t in enumerate(rows):
         assert orc.rel_l2(got[t], ref[i]) < TOL, t
+
+
+IQ4NL, IQ4XS, Q5K = 20, 23, 13
+QWEN3_LAYER = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048),
+               ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072)]
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_config4_layer_as_benchmarked(ctx, orc, M):
+    """one Qwen3-0.6B layer (types [IQ4_NL, IQ4_XS, Q5_K][i % 3]
+    over q, k, v, o, gate, up, down) with M = 1, 4 and 8 fp32 activation rows,
+    one ggq_mul_mat_batch_rows_dev launch per dependency level (q+k+v, o,
+    gate+up, down) exactly as bench.py's bench_config4 launches them (q/k/v
+    sharing one input, gate/up another), eagerly and then as a captured HIP
+    graph replayed on fresh inputs; 512 sampled weight rows of every matrix
+    (all rows up to 512) against the fp64 oracle, every activation row."""
+    import torch
+    cycle = [IQ4NL, IQ4XS, Q5K]
+    rng = np.random.default_rng(40 + M)
+    mats = []
+    for i, (name, N, K) in enumerate(QWEN3_LAYER):
+        t = cycle[i % 3]
+        raw = make(t, N, K, 4000 + 10 * M + i)
+        mats.append(dict(name=name, t=t, N=N, K=K, raw=raw, dW=dev(raw),
+                         dC=torch.full((M, N), float("nan"), device="cuda")))
+    ins = {lv: torch.empty((M, K), device="cuda") for lv, K in (("attn", 1024), ("o", 2048), ("ffn", 1024),
+                                                                 ("down", 3072))}
+    which = {"q": "attn", "k": "attn", "v": "attn", "o": "o", "gate": "ffn", "up": "ffn", "down": "down"}
+    levels = [mats[0:3], mats[3:4], mats[4:6], mats[6:7]]
+    descs = []
+    for lv in levels:
+        arr = (gl.GemvDesc * len(lv))()
+        for i, m in enumerate(lv):
+            arr[i].W, arr[i].type, arr[i].N, arr[i].K = m["dW"].data_ptr(), m["t"], m["N"], m["K"]
+            arr[i].A, arr[i].C = ins[which[m["name"]]].data_ptr(), m["dC"].data_ptr()
+        descs.append((arr, len(lv)))
+
+    def run_on(s):
+        for arr, n in descs:
+            ctx.check(ctx.lib.ggq_mul_mat_batch_rows_dev(ctx.h, arr, n, M, s), "batch rows")
+
+    def check(tag):
+        torch.cuda.synchronize()
+        for j, m in enumerate(mats):
+            C = host(m["dC"])
+            assert not np.isnan(C).any(), (tag, m["name"])
+            A = host(ins[which[m["name"]]])
+            check_rows(orc, m["t"], m["raw"], m["N"], m["K"], A, C, 0, 512, j, f"{tag} M={M} {m['name']}")
+            m["dC"].fill_(float("nan"))
+
+    for x in ins.values():
+        x.copy_(torch.from_numpy(rng.standard_normal(tuple(x.shape)).astype(np.float32)))
+    run_on(stream_handle())
+    check("eager")
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run_on(ctypes.c_void_p(s.cuda_stream))
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            run_on(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for x in ins.values():
+            x.copy_(torch.from_numpy(rng.standard_normal(tuple(x.shape)).astype(np.float32)))
+        torch.cuda.synchronize()
+        g.replay()
+        check(f"graph replay {rep}")
+    del g

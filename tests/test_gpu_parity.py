@@ -361,14 +361,14 @@ def test_moe_q8_row_int8_gemv_path(ctx, orc, monkeypatch, types, T, E, k):
     """GGQ_ACT_Q8_ROW MoE with the routed and shared projections on the
     grouped int8 GEMV in its given-codes mode (chunks of 8 rows, 4 for Q6_K /
     IQ4, the shared expert as one more group; experts with 0 to ~30 rows),
-    forced by GGQ_MOE_I8_MAX_AVG, and the same layer forced onto the
-    expert-grouped GEMM (GGQ_MOE_I8_MAX_AVG=0): both against the oracle's
+    forced by GGQ_MOE_GEMV_MAX_AVG, and the same layer forced onto the
+    expert-grouped GEMM (GGQ_MOE_GEMV_MAX_AVG=0): both against the oracle's
     per-token loop in the same mode, paired and unpaired gate / up, with and
     without the shared expert."""
     tg, tu, td = types
     H, F = 512, 256
     for avg in ("100000", "0"):
-        monkeypatch.setenv("GGQ_MOE_I8_MAX_AVG", avg)
+        monkeypatch.setenv("GGQ_MOE_GEMV_MAX_AVG", avg)
         for shared in (False, True):
             (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(
                 ctx, T, H, F, E, k, shared, seed=sum(types) + T, tg=tg, tu=tu, td=td, act_mode=1)
@@ -402,11 +402,15 @@ def test_moe_large_grouping_vs_oracle(ctx, orc, T, E, k):
     assert orc.rel_l2(out, ref) < TOL
 
 
-@pytest.mark.parametrize("tg,tu,td", [(8, 8, 8), (20, 23, 20), (23, 20, 23), (8, 13, 14)])
-def test_moe_other_formats_vs_oracle(ctx, orc, tg, tu, td):
-    """Expert weights in Q8_0 / IQ4_NL / IQ4_XS (and mixed with K-quants):
-    the grouped matrix-core path for every format, paired and unpaired
-    gate/up, with and without the shared expert."""
+@pytest.mark.parametrize("tg,tu,td", [(8, 8, 8), (20, 23, 20), (23, 20, 23), (8, 13, 14), (12, 12, 14),
+                                      (13, 13, 13)])
+@pytest.mark.parametrize("avg", ["100000", "0"])
+def test_moe_other_formats_vs_oracle(ctx, orc, monkeypatch, tg, tu, td, avg):
+    """fp32-activation MoE with every format (and mixes) as gate / up /
+    down, paired and unpaired gate/up, with and without the shared expert,
+    on the grouped GEMVs (GGQ_MOE_GEMV_MAX_AVG large) and on the
+    expert-grouped fp16 GEMM (GGQ_MOE_GEMV_MAX_AVG=0)."""
+    monkeypatch.setenv("GGQ_MOE_GEMV_MAX_AVG", avg)
     T, H, F, E, k = 24, 512, 256, 32, 4
     for shared in (False, True):
         (out, sel, wsel), (x, logits, Wg, Wu, Wd, Sg, Su, Sd, sw) = run_moe(ctx, T, H, F, E, k, shared, seed=tg + tu + td,
@@ -428,6 +432,7 @@ def test_moe_int8_grouped_launches(ctx, orc, monkeypatch, tg, tu, td, T, E, k):
     chip) with one wavefront per tile split the rows and K differently."""
     H, F = 512, 256
     outs = {}
+    monkeypatch.setenv("GGQ_MOE_GEMV_MAX_AVG", "100000")  # the grouped GEMVs at every batch size
     for i8, down, gx, kw in ((0, 0, 0, 4), (1, 0, 0, 4), (1, 1, 1, 4), (1, 1, 3, 1)):
         monkeypatch.setenv("GGQ_MOE_I8", str(i8))
         monkeypatch.setenv("GGQ_MOE_I8_DOWN", str(down))
