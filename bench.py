@@ -442,13 +442,15 @@ def bench_host_api(torch, ctx, stream, steps=5, warmup=2):
             "us_per_call": round(sec * 1e6 / len(params), 2)}
 
 
-def bench_prefill(torch, ctx, stream, steps=3):
+def bench_prefill(torch, ctx, stream, steps=3, fused=False):
     """28 layers of Q8_0 matmuls on 512 tokens, per-row int8
     activations (reference XDNA semantics).  Each layer quantizes its four
     distinct inputs once (q/k/v share one, gate/up share one; o and down
     have their own), as a forward pass would, and the quantization kernels
     are inside the timed region.  int8-MFMA GEMM; weights sharing an input
-    run as one launch (ggq_mul_mat_q8_batch_dev)."""
+    run as one launch (ggq_mul_mat_q8_batch_dev).  fused=True instead calls
+    ggq_mul_mat_batch_act_dev per level on the fp32 inputs (quantization
+    inside the GEMM launch where K <= 2048)."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2)
     layer = []
@@ -492,7 +494,7 @@ def bench_prefill(torch, ctx, stream, steps=3):
                       ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), T, stream)
         ctx.check(st, "mul_mat_q8(h)_batch_dev")
 
-    def run():
+    def run_given_codes():
         for li in range(QWEN_LAYERS):
             lm = mats[7 * li: 7 * li + 7]
             quant("qkv")
@@ -504,6 +506,23 @@ def bench_prefill(torch, ctx, stream, steps=3):
             quant("down")
             mm(lm[6])
 
+    # Each dependency level as one ggq_mul_mat_batch_act_dev call on the fp32
+    # input (the reference's mul_mat_q quantizes inside the call).
+    level_descs = []
+    for li in range(QWEN_LAYERS):
+        lm = mats[7 * li: 7 * li + 7]
+        for ms in (lm[:3], lm[3:4], lm[4:6], lm[6:7]):
+            arr = (gl.GemvDesc * len(ms))()
+            for i, m in enumerate(ms):
+                arr[i].W, arr[i].type, arr[i].N, arr[i].K = m.w.data_ptr(), m.t, m.N, m.K
+                arr[i].A, arr[i].C = m.x.data_ptr(), m.y.data_ptr()
+            level_descs.append((arr, len(ms)))
+
+    def run_levels():
+        for arr, n in level_descs:
+            ctx.check(ctx.lib.ggq_mul_mat_batch_act_dev(ctx.h, arr, n, T, qmode, stream), "batch_act")
+
+    run = run_levels if fused else run_given_codes
     sec = time_steps(torch, run, steps, 1)
     ops = sum(2 * m.M * m.N * m.K for m in mats)
     return {"workload": "Qwen2.5-1.5B Q8_0 prefill, 512 tokens x 28 layers, per-row int8 activations "

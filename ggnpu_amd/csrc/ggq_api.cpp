@@ -206,6 +206,11 @@ int mul_mat_queue(ggq_ctx* c, Arena& ar, const void* W, uint32_t type, int64_t N
         if (ggq::i8_gemv_eligible(&g, 1, 1))
             return hip_status(c, ggq::launch_i8_gemv(&g, 1, 1, nullptr, nullptr, s), "gemv_i8");
     }
+    if (act_mode == GGQ_ACT_Q8_ROW && M > 8 && ggq::gemm_panel_eligible(type, (int)K, M, A, lda)) {
+        // quantized per row inside the GEMM (no workspace)
+        const ggq::GemmDesc gd{W, C, (int)N, ldc};
+        return hip_status(c, ggq::launch_gemm_panel(type, &gd, 1, (int)K, A, lda, nullptr, nullptr, M, s), "gemm_panel");
+    }
     const size_t q_off = 0;
     const size_t s_off = align256(q_off + (size_t)M * K);
     const size_t x_off = align256(s_off + sizeof(float) * (size_t)M * (K / 32));
@@ -239,6 +244,10 @@ int mul_mat_q8_queue(ggq_ctx* c, Arena& ar, const void* W, uint32_t type, int64_
     int st;
     void* ws;
     float* part;
+    if (M > 8 && ggq::gemm_panel_eligible(type, (int)K, M, nullptr, 0)) {
+        const ggq::GemmDesc gd{W, C, (int)N, ldc};
+        return hip_status(c, ggq::launch_gemm_panel(type, &gd, 1, (int)K, nullptr, 0, qa, sa, M, s), "gemm_panel");
+    }
     if (M > 8) {
         const int n32 = (int)N;
         const size_t part_bytes = gemm_part_bytes(ggq::plan_gemm_i8(type, &n32, 1, (int)K, M));
@@ -626,6 +635,8 @@ int ggq_mul_mat_q8_batch_dev(ggq_ctx* c, const ggq_gemm_desc* d, int n, uint32_t
         gd[i] = ggq::GemmDesc{d[i].W, d[i].C, (int)d[i].N, d[i].ldc};
         Ns[i] = (int)d[i].N;
     }
+    if (ggq::gemm_panel_eligible(type, (int)K, M, nullptr, 0))
+        return hip_status(c, ggq::launch_gemm_panel(type, gd, n, (int)K, nullptr, 0, qa, sa, M, s), "gemm_panel batch");
     void* ws;
     float* part;
     const int st = ar.get(0, gemm_part_bytes(ggq::plan_gemm_i8(type, Ns, n, (int)K, M)), &ws, &part, "workspace");
@@ -710,7 +721,8 @@ int ggq_mul_mat_batch_act_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, int M, 
     if (act_mode == GGQ_ACT_F32) return ggq_mul_mat_batch_rows_dev(c, d, n, M, stream);
     GGQ_GUARD(c)
     if (!d || n < 1 || n > GGQ_MAX_BATCH) return set_status(c, GGQ_INVALID_PARAM, "need 1..%d descriptors", GGQ_MAX_BATCH);
-    if (M < 0 || M > GGQ_MAX_BATCH_ROWS) return set_status(c, GGQ_INVALID_PARAM, "M=%d outside 0..%d", M, GGQ_MAX_BATCH_ROWS);
+    if (M < 0 || (M > GGQ_MAX_BATCH_ROWS && act_mode != GGQ_ACT_Q8_ROW))
+        return set_status(c, GGQ_INVALID_PARAM, "M=%d outside 0..%d", M, GGQ_MAX_BATCH_ROWS);
     ggq::GemvProblem ps[GGQ_MAX_BATCH];
     for (int i = 0; i < n; i++) {
         if (!d[i].W || !d[i].A || !d[i].C) return set_status(c, GGQ_INVALID_PARAM, "null pointer in entry %d", i);
@@ -739,8 +751,27 @@ int ggq_mul_mat_batch_act_dev(ggq_ctx* c, const ggq_gemv_desc* d, int n, int M, 
     }
     if (act_mode == GGQ_ACT_Q8_ROW && M <= 8 && ggq::i8_gemv_eligible(ps, n, 1))
         return hip_status(c, ggq::launch_i8_gemv(ps, n, 1, nullptr, nullptr, s), "gemv_i8 batch");
+    bool done[GGQ_MAX_BATCH] = {};
+    if (act_mode == GGQ_ACT_Q8_ROW && M > 8) {
+        // Prefill-sized: entries that share the activations, type and K (q/k/v,
+        // gate/up) as one activation-panel GEMM that quantizes the rows itself.
+        for (int i = 0; i < n; i++) {
+            if (done[i] || !ggq::gemm_panel_eligible(d[i].type, (int)d[i].K, M, d[i].A, (int)d[i].K)) continue;
+            ggq::GemmDesc gd[GGQ_MAX_GEMM_BATCH];
+            int ng = 0;
+            for (int j = i; j < n && ng < GGQ_MAX_GEMM_BATCH; j++)
+                if (!done[j] && d[j].A == d[i].A && d[j].type == d[i].type && d[j].K == d[i].K) {
+                    gd[ng++] = ggq::GemmDesc{d[j].W, d[j].C, (int)d[j].N, (int)d[j].N};
+                    done[j] = true;
+                }
+            const hipError_t e =
+                ggq::launch_gemm_panel(d[i].type, gd, ng, (int)d[i].K, d[i].A, (int)d[i].K, nullptr, nullptr, M, s);
+            if (e != hipSuccess) return hip_status(c, e, "gemm_panel batch");
+        }
+    }
     Arena ar = dev_arena(c, s);
     for (int i = 0; i < n; i++) {
+        if (done[i]) continue;
         int st = mul_mat_queue(c, ar, d[i].W, d[i].type, d[i].N, d[i].K, d[i].A, (int)d[i].K, d[i].C, (int)d[i].N, M,
                                act_mode, s);
         if (st != GGQ_OK) return st;

@@ -16,7 +16,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <mutex>
+#include <set>
 #include <vector>
 
 #include "ggq_device.h"
@@ -2378,6 +2380,407 @@ __global__ __launch_bounds__(256) void gemm_i8_lds_kernel(GemmMultiArgs a) {
         }
 }
 
+// ------------------------------------- activation-panel GEMM (prefill, i8)
+// One 768-thread workgroup per (64-row activation panel, N-range): the
+// panel's int8 rows for the whole K stay in LDS (64 x (K + 16) bytes, K <=
+// 2048), quantized per row inside the kernel from the fp32 rows
+// (amd_xdna.cpp:598-603, 633-639: scale = amax / 127, q = rint(a * (1 /
+// scale)) -- the quantizer of quant_row_regs, bit for bit) or copied from
+// given codes.  Each wavefront then takes (32 weight rows x 32 activation
+// rows) items of its N-range and runs the whole K for one: the weight
+// codes go from memory straight into the B operand of
+// v_mfma_i32_32x32x32_i8 (a lane's 16 codes and its group scale, fetched
+// kPanelPD groups ahead), the activation codes come from the panel, and the
+// exact per-group epilogue acc += dl * P (- ml * S) runs in registers.  No
+// LDS staging of the weights, no barrier after the panel is loaded, no
+// split of K and hence no reduction launch, and no separate quantization
+// launch.  Workgroup id = panel * ranges + range with ranges a multiple of
+// 8, so the panels sharing an N-range run on one XCD (its L2 serves the
+// weights to all of them).
+constexpr int kPanelRows = 64;
+constexpr int kPanelMaxK = 2048;
+constexpr int kPanelThreads = 768;   // 12 wavefronts: 3 per SIMD, up to 168 VGPRs
+constexpr int kPanelWaves = kPanelThreads / 64;
+constexpr int kPanelPD = 4;        // weight groups in flight per lane
+constexpr int kPanelRegK = 1536;   // rows up to this K are quantized from registers
+
+struct PanelArgs {
+    GemmProb p[kGemmMaxProb];  // tile_begin: first 32-row N-block of each weight
+    int np;
+    int64_t row_bytes;
+    int K, M;
+    const float* A;   // fp32 rows [M][lda] (quantized in the kernel), or null
+    int lda;
+    const int8_t* QA; // given codes [M][K] and scales sa when A is null
+    const float* sa;
+    int nblocks;      // 32-row N-blocks over all weights
+    int ranges;       // N-ranges per panel
+};
+
+// Weight operand of one lane for one 32-value group: the 16 codes of half
+// lk of the group of row `row` and the group's scales.  Generic formats
+// load at decode time; Q8_0 fetches its dword window early.
+template <int T> struct PStage {
+    const uint8_t* row;
+    int k;
+    __device__ __forceinline__ void fetch(const uint8_t* r, int g, int h) { row = r; k = 32 * g + 16 * h; }
+    __device__ __forceinline__ uint4 codes(GroupScale& gs) const {
+        gs = group_scale<T>(row, k & ~31);
+        return codes16<T>(row, k);
+    }
+};
+template <> struct PStage<T_Q8_0> {
+    uint4 c;
+    uint32_t d;
+    // the 16 codes of half h start 2 + 16 h bytes into the 34-byte block:
+    // one 16-byte load at a 2-byte-aligned address (exact on gfx950) and
+    // the fp16 scale
+    __device__ __forceinline__ void fetch(const uint8_t* r, int g, int h) {
+        const uint8_t* b = r + 34 * g;
+        c = *(const uint4*)(b + 2 + 16 * h);
+        d = ld_u16(b);
+    }
+    __device__ __forceinline__ uint4 codes(GroupScale& gs) const {
+        gs = {h2f(d), 0.0f};
+        return c;
+    }
+};
+
+template <int T>
+__global__ __launch_bounds__(kPanelThreads) void gemm_panel_kernel(PanelArgs a) {
+    constexpr bool kMin = T == T_Q4_K || T == T_Q5_K;
+    extern __shared__ __attribute__((aligned(16))) int8_t panel[];
+    __shared__ float sa_s[kPanelRows];
+    const int K = a.K, ld = K + 16;
+    // the wavefront index as a scalar: items, and the weight each item reads
+    // (a kernel-argument array indexed per item), stay uniform
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 31, lk = lane >> 5;
+    const int mp = (int)blockIdx.x / a.ranges, rg = (int)blockIdx.x % a.ranges;
+    const int m0 = mp * kPanelRows;
+
+    // ---- the panel: 32 threads per row, rows tid / 32 + 24 j
+    constexpr int RPP = kPanelThreads / 32;                 // rows per pass
+    constexpr int NP = (kPanelRows + RPP - 1) / RPP;        // passes
+    const int c = tid & 31;
+    if (a.A && K <= kPanelRegK) {
+        // every load of the thread's rows issued before the first is used,
+        // unconditional (positions past K and rows past M read valid
+        // memory and are zeroed after): a branch around a load makes the
+        // compiler wait for the loads in flight
+        constexpr int NV = kPanelRegK / 128;
+        float4 v[NP][NV];
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const int r = tid / 32 + RPP * j, m = m0 + (r < kPanelRows ? r : 0);
+            const float* arow = a.A + (int64_t)(m < a.M ? m : 0) * a.lda;
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const int k = 4 * c + 128 * i;
+                v[j][i] = *(const float4*)(arow + (k < K ? k : 0));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const int r = tid / 32 + RPP * j;
+            if (r >= kPanelRows) break;
+            const bool ok = m0 + r < a.M;
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                if (!ok || 4 * c + 128 * i >= K) v[j][i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[j][i].x), fabsf(v[j][i].y))),
+                             fmaxf(fabsf(v[j][i].z), fabsf(v[j][i].w)));
+            }
+#pragma unroll
+            for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+            const float inv = __fdiv_rn(1.0f, sc);
+            if (c == 0) sa_s[r] = sc;
+            int8_t* prow = panel + r * ld;
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const int k = 4 * c + 128 * i;
+                if (k < K)
+                    *(uint32_t*)(prow + k) = (uint32_t)(uint8_t)to_i8(__fmul_rn(v[j][i].x, inv)) |
+                                             (uint32_t)(uint8_t)to_i8(__fmul_rn(v[j][i].y, inv)) << 8 |
+                                             (uint32_t)(uint8_t)to_i8(__fmul_rn(v[j][i].z, inv)) << 16 |
+                                             (uint32_t)(uint8_t)to_i8(__fmul_rn(v[j][i].w, inv)) << 24;
+            }
+        }
+    }
+    for (int r = tid >> 5; r < kPanelRows && !(a.A && K <= kPanelRegK); r += RPP) {
+        const int m = m0 + r;
+        const bool ok = m < a.M;
+        int8_t* prow = panel + r * ld;
+        if (a.A) {  // longer rows: the maximum, then the codes, both streamed
+            const float* arow = a.A + (int64_t)(ok ? m : 0) * a.lda;
+            float amax = 0.0f;
+            for (int k = 4 * c; k < K; k += 128) {
+                const float4 v = ok ? *(const float4*)(arow + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+            }
+#pragma unroll
+            for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+            const float inv = __fdiv_rn(1.0f, sc);
+            if (c == 0) sa_s[r] = sc;
+            for (int k = 4 * c; k < K; k += 128) {
+                const float4 v = ok ? *(const float4*)(arow + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                *(uint32_t*)(prow + k) = (uint32_t)(uint8_t)to_i8(__fmul_rn(v.x, inv)) |
+                                         (uint32_t)(uint8_t)to_i8(__fmul_rn(v.y, inv)) << 8 |
+                                         (uint32_t)(uint8_t)to_i8(__fmul_rn(v.z, inv)) << 16 |
+                                         (uint32_t)(uint8_t)to_i8(__fmul_rn(v.w, inv)) << 24;
+            }
+        } else {
+            const int8_t* qrow = a.QA + (int64_t)(ok ? m : 0) * K;
+            constexpr int NQ = kPanelMaxK / 512;
+            uint4 v[NQ];
+#pragma unroll
+            for (int i = 0; i < NQ; i++) {
+                const int k = 16 * c + 512 * i;
+                v[i] = *(const uint4*)(qrow + (k < K ? k : 0));
+            }
+#pragma unroll
+            for (int i = 0; i < NQ; i++) {
+                const int k = 16 * c + 512 * i;
+                if (k < K) *(uint4*)(prow + k) = ok ? v[i] : make_uint4(0, 0, 0, 0);
+            }
+            if (c == 0) sa_s[r] = ok ? a.sa[m] : 1.0f;
+        }
+    }
+    __syncthreads();
+
+    // ---- items: 32-row N-blocks, strided over the waves; each item covers
+    // the panel's 64 rows (two MFMAs per group share the weight operand)
+    const int nb_here = a.nblocks > rg ? (a.nblocks - rg + a.ranges - 1) / a.ranges : 0;
+    const bool two = a.M - m0 > 32;  // uniform: the panel's second half holds rows
+    const int G = K / 32;
+    const v16i zero = {};
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    // Fewer items than wavefronts (the small levels): each item's K is split
+    // over ks wavefronts in whole 4-group chunks, and the slices' sums are
+    // added in slice order through LDS (the panel's space, once every
+    // wavefront is done with it) by the slice-0 wavefront.
+    const int nch_all = (G + 3) / 4;
+    int ks = nb_here > 0 ? kPanelWaves / nb_here : 1;
+    if (ks > nch_all) ks = nch_all;
+    if (ks < 1) ks = 1;
+    const int n_work = nb_here * ks;
+    float acc0[16], acc1[16];
+    int n = 0, N = 0, q = 0;
+    for (int w = wave; w < n_work; w += kPanelWaves) {
+        const int it = w / ks, sl = w % ks;
+        const int c_lo = nch_all * sl / ks, c_hi = nch_all * (sl + 1) / ks;
+        const int nbk = rg + a.ranges * it;
+        q = 0;
+        while (q + 1 < a.np && nbk >= a.p[q + 1].tile_begin) q++;
+        N = a.p[q].N;
+        n = (nbk - a.p[q].tile_begin) * 32 + li;
+        const uint8_t* wrow = a.p[q].W + (int64_t)(n < N ? n : 0) * a.row_bytes;
+        const int8_t* arow0 = panel + li * ld + 16 * lk;
+        const int8_t* arow1 = arow0 + 32 * ld;
+
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc0[r] = acc1[r] = 0.0f;
+        // one group's MFMAs (both panel halves) and exact epilogue
+        auto group = [&](int g, const uint4& bv, const GroupScale& gs) {
+            const v4i Bv = v4i{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w};
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                if (h == 1 && !two) break;
+                const uint4 av = *(const uint4*)((h ? arow1 : arow0) + 32 * g);
+                const v4i Av = v4i{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+                float* acc = h ? acc1 : acc0;
+                const v16i P = __builtin_amdgcn_mfma_i32_32x32x32_i8(Av, Bv, zero, 0, 0, 0);
+                if constexpr (kMin) {
+                    const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(Av, ones, zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        acc[r] = fmaf(gs.dl, (float)P[r], acc[r]);
+                        acc[r] = fmaf(-gs.ml, (float)S[r], acc[r]);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[r] = fmaf(gs.dl, (float)P[r], acc[r]);
+                }
+            }
+        };
+        if constexpr (T == T_Q8_0) {
+            // Chunks of four blocks (136 bytes of the row): lane (li, lk)
+            // loads bytes 68 lk .. 68 lk + 67 of row li's chunk (blocks 2 lk
+            // and 2 lk + 1, whole), so each cache line of the row is read
+            // once; one v_permlane32_swap per dword then gives every lane
+            // half lk of all four blocks (the lower lanes' half-0 codes and
+            // the upper lanes' half-1 codes of the same blocks trade places).
+            constexpr int CH = 2;  // chunks in flight
+            const uint8_t* seg = wrow + 68 * lk;
+            uint32_t R[CH][17];
+            auto load = [&](int ch, uint32_t (&wv)[17]) {
+                const uint32_t* p = (const uint32_t*)(seg + 136 * ch);
+#pragma unroll
+                for (int i = 0; i < 4; i++) *(uint4*)&wv[4 * i] = *(const uint4*)(p + 4 * i);
+                wv[16] = p[16];
+            };
+#pragma unroll
+            for (int j = 0; j < CH; j++) load(c_lo + j < c_hi ? c_lo + j : c_lo, R[j]);
+            for (int c0 = c_lo; c0 < c_hi; c0 += CH) {
+#pragma unroll
+                for (int j = 0; j < CH; j++) {
+                    const int ch = c0 + j;
+                    if (ch >= c_hi) break;
+                    uint32_t a0[4], a1[4], b0[4], b1[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        // block A (bytes 0..33, codes from byte 2), block B (34..67, codes from 36)
+                        const auto sa = __builtin_amdgcn_permlane32_swap(__builtin_amdgcn_alignbyte(R[j][i + 1], R[j][i], 2),
+                                                                         __builtin_amdgcn_alignbyte(R[j][i + 5], R[j][i + 4], 2),
+                                                                         false, false);
+                        const auto sb = __builtin_amdgcn_permlane32_swap(R[j][9 + i], R[j][13 + i], false, false);
+                        a0[i] = sa[0], a1[i] = sa[1], b0[i] = sb[0], b1[i] = sb[1];
+                    }
+                    // the two fp16 scales of the lane's blocks in one dword
+                    const uint32_t sc = (R[j][0] & 0xFFFFu) | (R[j][8] & 0xFFFF0000u);
+                    const auto ss = __builtin_amdgcn_permlane32_swap(sc, sc, false, false);
+                    if (ch + CH < c_hi) load(ch + CH, R[j]);
+                    const int g = 4 * ch;
+                    group(g, make_uint4(a0[0], a0[1], a0[2], a0[3]), GroupScale{h2f(ss[0] & 0xFFFFu), 0.0f});
+                    if (g + 1 < G) group(g + 1, make_uint4(b0[0], b0[1], b0[2], b0[3]), GroupScale{h2f(ss[0] >> 16), 0.0f});
+                    if (g + 2 < G) group(g + 2, make_uint4(a1[0], a1[1], a1[2], a1[3]), GroupScale{h2f(ss[1] & 0xFFFFu), 0.0f});
+                    if (g + 3 < G) group(g + 3, make_uint4(b1[0], b1[1], b1[2], b1[3]), GroupScale{h2f(ss[1] >> 16), 0.0f});
+                }
+            }
+        } else {
+            const int g_lo = 4 * c_lo, g_hi = 4 * c_hi < G ? 4 * c_hi : G;
+            PStage<T> st[kPanelPD];
+#pragma unroll
+            for (int j = 0; j < kPanelPD; j++) st[j].fetch(wrow, g_lo + j < g_hi ? g_lo + j : g_lo, lk);
+            for (int g0 = g_lo; g0 < g_hi; g0 += kPanelPD) {
+#pragma unroll
+                for (int j = 0; j < kPanelPD; j++) {
+                    const int g = g0 + j;
+                    if (g >= g_hi) break;
+                    GroupScale gs;
+                    const uint4 bv = st[j].codes(gs);
+                    if (g + kPanelPD < g_hi) st[j].fetch(wrow, g + kPanelPD, lk);
+                    group(g, bv, gs);
+                }
+            }
+        }
+        if (ks == 1 && n < N) {
+            float* const C = a.p[q].C;
+            const int ldc = a.p[q].ldc;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int mr = 32 * h + 8 * (r >> 2) + 4 * lk + (r & 3);
+                    const int m = m0 + mr;
+                    if (m < a.M) C[(int64_t)m * ldc + n] = (h ? acc1[r] : acc0[r]) * sa_s[mr];
+                }
+            }
+        }
+    }
+    if (ks > 1) {  // uniform over the workgroup (n_work <= kPanelWaves)
+        float* red = (float*)panel;  // [wave][32 values][64 lanes]
+        __syncthreads();
+        if (wave < n_work) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                red[(wave * 32 + r) * 64 + lane] = acc0[r];
+                red[(wave * 32 + 16 + r) * 64 + lane] = acc1[r];
+            }
+        }
+        __syncthreads();
+        if (wave < n_work && wave % ks == 0) {
+            for (int sl = 1; sl < ks; sl++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    acc0[r] += red[((wave + sl) * 32 + r) * 64 + lane];
+                    acc1[r] += red[((wave + sl) * 32 + 16 + r) * 64 + lane];
+                }
+            }
+            if (n < N) {
+                float* const C = a.p[q].C;
+                const int ldc = a.p[q].ldc;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int mr = 32 * h + 8 * (r >> 2) + 4 * lk + (r & 3);
+                        const int m = m0 + mr;
+                        if (m < a.M) C[(int64_t)m * ldc + n] = (h ? acc1[r] : acc0[r]) * sa_s[mr];
+                    }
+                }
+            }
+        }
+    }
+}
+
+bool gemm_panel_eligible(uint32_t type, int K, int M, const float* A, int lda) {
+    if (type == T_Q6_K || K <= 0 || K > kPanelMaxK || K % 32 || M <= 0) return false;
+    if (A && (((uintptr_t)A & 15u) || lda % 4)) return false;
+    return true;
+}
+
+hipError_t launch_gemm_panel(uint32_t type, const GemmDesc* d, int n, int K, const float* A, int lda,
+                             const int8_t* qa, const float* sa, int M, hipStream_t s) {
+    if (M == 0 || n == 0) return hipSuccess;
+    if (n > kGemmMaxProb || !gemm_panel_eligible(type, K, M, A, lda) || (!A && (!qa || !sa)))
+        return hipErrorInvalidValue;
+    PanelArgs a;
+    int nb = 0;
+    for (int i = 0; i < n; i++) {
+        a.p[i].W = (const uint8_t*)d[i].W;
+        a.p[i].C = d[i].C;
+        a.p[i].N = d[i].N;
+        a.p[i].ldc = d[i].ldc;
+        a.p[i].tile_begin = nb;
+        nb += (d[i].N + 31) / 32;
+    }
+    a.np = n;
+    a.row_bytes = row_bytes(type, K);
+    a.K = K;
+    a.M = M;
+    a.A = A;
+    a.lda = lda;
+    a.QA = qa;
+    a.sa = sa;
+    a.nblocks = nb;
+    const int panels = (M + kPanelRows - 1) / kPanelRows;
+    // ranges: a multiple of 8, at most one per N-block (rounded up), and
+    // panels x ranges about one workgroup per CU
+    int ranges = (device_cus() / panels) & ~7;
+    if (ranges < 8) ranges = 8;
+    const int nb8 = (nb + 7) & ~7;
+    if (ranges > nb8) ranges = nb8;
+    a.ranges = ranges;
+    // the panel, and room for the K-split partial sums (8 KB per wavefront)
+    const size_t lds = std::max((size_t)kPanelRows * (K + 16), (size_t)kPanelWaves * 8192);
+    const void* k = nullptr;
+    switch (type) {
+    case T_Q8_0: k = (const void*)gemm_panel_kernel<T_Q8_0>; break;
+    case T_Q4_K: k = (const void*)gemm_panel_kernel<T_Q4_K>; break;
+    case T_Q5_K: k = (const void*)gemm_panel_kernel<T_Q5_K>; break;
+    case T_IQ4_NL: k = (const void*)gemm_panel_kernel<T_IQ4_NL>; break;
+    case T_IQ4_XS: k = (const void*)gemm_panel_kernel<T_IQ4_XS>; break;
+    default: return hipErrorInvalidValue;
+    }
+    static std::mutex mu;
+    static std::set<const void*> attr_done;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!attr_done.count(k)) {
+            const hipError_t e =
+                hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kPanelRows * (kPanelMaxK + 16));
+            if (e != hipSuccess) return e;
+            attr_done.insert(k);
+        }
+    }
+    void* args[] = {&a};
+    return hipLaunchKernel(k, dim3(panels * ranges), dim3(kPanelThreads), args, lds, s);
+}
+
 // ------------------------------------------ expert-grouped int8 GEMM (MoE)
 // Prefill-sized MoE batches (tens of tokens per expert) with per-row int8
 // activations: one launch multiplies every expert's weight matrix by the
@@ -2650,7 +3053,7 @@ __device__ __forceinline__ v8h s8x8_f16(uint2 c) {
                                               s8x2_f16(b, 0x04010400u), s8x2_f16(b, 0x04030402u)));
 }
 
-template <int T>
+template <int T, int PF>
 __global__ __launch_bounds__(256) void moe_gemm_f16_kernel(MoeGemmArgs a) {
     constexpr bool kMin = T == T_Q4_K || T == T_Q5_K;
     constexpr bool kQ6 = T == T_Q6_K;
@@ -2694,24 +3097,25 @@ __global__ __launch_bounds__(256) void moe_gemm_f16_kernel(MoeGemmArgs a) {
     const int bnn = brow_ok ? bn : 0;
     const uint8_t* const bptr = bnn < a.n1 ? W1 + (int64_t)bnn * a.row_bytes : W2 + (int64_t)(bnn - a.n1) * a.row_bytes;
 
-    uint4 ahr, alr;
-    float asr = 0.0f;
-    MStage<T> breg;
-    auto fetch = [&](int st) {
+    // PF register stages: the global loads of K-step st + PF are in flight
+    // while step st computes.
+    uint4 ahr[PF], alr[PF];
+    float asr[PF];
+    MStage<T> breg[PF];
+    auto fetch = [&](int st, int j) {
         const int k0 = st * kF16BK;
-        ahr = arow_ok ? *(const uint4*)(hptr + k0) : make_uint4(0, 0, 0, 0);
-        alr = arow_ok ? *(const uint4*)(lptr + k0) : make_uint4(0, 0, 0, 0);
-        if constexpr (kMin)
-            if (tid < 64) asr = ps < p_end ? sptr[k0 / 32] : 0.0f;
-        breg.fetch(bptr, brow_ok ? k0 + 32 * bg : 0, brow_ok);
+        ahr[j] = arow_ok ? *(const uint4*)(hptr + k0) : make_uint4(0, 0, 0, 0);
+        alr[j] = arow_ok ? *(const uint4*)(lptr + k0) : make_uint4(0, 0, 0, 0);
+        if constexpr (kMin) asr[j] = tid < 64 && ps < p_end ? sptr[k0 / 32] : 0.0f;
+        breg[j].fetch(bptr, brow_ok ? k0 + 32 * bg : 0, brow_ok);
     };
-    auto store = [&](int buf) {
-        *(uint4*)&Ah[buf][ar][akc] = ahr;
-        *(uint4*)&Al[buf][ar][akc] = alr;
+    auto store = [&](int buf, int j) {
+        *(uint4*)&Ah[buf][ar][akc] = ahr[j];
+        *(uint4*)&Al[buf][ar][akc] = alr[j];
         if constexpr (kMin)
-            if (tid < 64) As[buf][sg][sr] = asr;
-        if constexpr (kQ6) breg.store2(&Bs[buf][br][32 * bg], &Bd[buf][br][2 * bg], nullptr);
-        else breg.store2(&Bs[buf][br][32 * bg], &Bd[buf][br][bg], &Bm[buf][br][bg]);
+            if (tid < 64) As[buf][sg][sr] = asr[j];
+        if constexpr (kQ6) breg[j].store2(&Bs[buf][br][32 * bg], &Bd[buf][br][2 * bg], nullptr);
+        else breg[j].store2(&Bs[buf][br][32 * bg], &Bd[buf][br][bg], &Bm[buf][br][bg]);
     };
 
     float acc[16];
@@ -2720,62 +3124,72 @@ __global__ __launch_bounds__(256) void moe_gemm_f16_kernel(MoeGemmArgs a) {
     const v16f zero = {};
     const int wn = 32 * wave;
 
-    fetch(0);
-    store(0);
-    if (nsteps > 1) fetch(1);
+    // Step st lives in register stage st % PF until it is stored to LDS
+    // buffer st & 1 at the end of step st - 1.
+    fetch(0, 0);
+    store(0, 0);
+#pragma unroll
+    for (int j = 1; j <= PF; j++)
+        if (j < nsteps) fetch(j, j % PF);
     __syncthreads();
-    for (int st = 0; st < nsteps; st++) {
-        const int buf = st & 1;
+    for (int sb = 0; sb < nsteps; sb += PF) {
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            v8h H[2], L[2], B[2];
+        for (int d = 0; d < PF; d++) {
+            const int st = sb + d;
+            if (st >= nsteps) break;
+            const int buf = st & 1;
 #pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                const int k = 32 * g + 16 * hh + 8 * lk;
-                H[hh] = *(const v8h*)&Ah[buf][li][k];
-                L[hh] = *(const v8h*)&Al[buf][li][k];
-                B[hh] = s8x8_f16(*(const uint2*)&Bs[buf][wn + li][k]);
-            }
-            if constexpr (kQ6) {
-                v16f P0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[0], B[0], zero, 0, 0, 0);
-                P0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[0], B[0], P0, 0, 0, 0);
-                v16f P1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[1], B[1], zero, 0, 0, 0);
-                P1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[1], B[1], P1, 0, 0, 0);
-                const float d0 = Bd[buf][wn + li][2 * g], d1 = Bd[buf][wn + li][2 * g + 1];
+            for (int g = 0; g < G; g++) {
+                v8h H[2], L[2], B[2];
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    acc[r] = fmaf(d0, P0[r], acc[r]);
-                    acc[r] = fmaf(d1, P1[r], acc[r]);
+                for (int hh = 0; hh < 2; hh++) {
+                    const int k = 32 * g + 16 * hh + 8 * lk;
+                    H[hh] = *(const v8h*)&Ah[buf][li][k];
+                    L[hh] = *(const v8h*)&Al[buf][li][k];
+                    B[hh] = s8x8_f16(*(const uint2*)&Bs[buf][wn + li][k]);
                 }
-            } else {
-                v16f P = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[0], B[0], zero, 0, 0, 0);
-                P = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[0], B[0], P, 0, 0, 0);
-                P = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[1], B[1], P, 0, 0, 0);
-                P = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[1], B[1], P, 0, 0, 0);
-                const float dl = Bd[buf][wn + li][g];
-                if constexpr (kMin) {
-                    const float ml = Bm[buf][wn + li][g];
+                if constexpr (kQ6) {
+                    v16f P0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[0], B[0], zero, 0, 0, 0);
+                    P0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[0], B[0], P0, 0, 0, 0);
+                    v16f P1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[1], B[1], zero, 0, 0, 0);
+                    P1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[1], B[1], P1, 0, 0, 0);
+                    const float d0 = Bd[buf][wn + li][2 * g], d1 = Bd[buf][wn + li][2 * g + 1];
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const float4 sv = *(const float4*)&As[buf][g][8 * j + 4 * lk];
-                        const float sj[4] = {sv.x, sv.y, sv.z, sv.w};
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const int r = 4 * j + i;
-                            acc[r] = fmaf(dl, P[r], acc[r]);
-                            acc[r] = fmaf(-ml, sj[i], acc[r]);
-                        }
+                    for (int r = 0; r < 16; r++) {
+                        acc[r] = fmaf(d0, P0[r], acc[r]);
+                        acc[r] = fmaf(d1, P1[r], acc[r]);
                     }
                 } else {
+                    v16f P = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[0], B[0], zero, 0, 0, 0);
+                    P = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[0], B[0], P, 0, 0, 0);
+                    P = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[1], B[1], P, 0, 0, 0);
+                    P = __builtin_amdgcn_mfma_f32_32x32x16_f16(L[1], B[1], P, 0, 0, 0);
+                    const float dl = Bd[buf][wn + li][g];
+                    if constexpr (kMin) {
+                        const float ml = Bm[buf][wn + li][g];
 #pragma unroll
-                    for (int r = 0; r < 16; r++) acc[r] = fmaf(dl, P[r], acc[r]);
+                        for (int j = 0; j < 4; j++) {
+                            const float4 sv = *(const float4*)&As[buf][g][8 * j + 4 * lk];
+                            const float sj[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                            for (int i = 0; i < 4; i++) {
+                                const int r = 4 * j + i;
+                                acc[r] = fmaf(dl, P[r], acc[r]);
+                                acc[r] = fmaf(-ml, sj[i], acc[r]);
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[r] = fmaf(dl, P[r], acc[r]);
+                    }
                 }
             }
-        }
-        if (st + 1 < nsteps) {
-            store(buf ^ 1);
-            if (st + 2 < nsteps) fetch(st + 2);
-            __syncthreads();
+            if (st + 1 < nsteps) {
+                const int nx = (d + 1) % PF;  // a constant once the d loop is unrolled
+                store(buf ^ 1, nx);
+                if (st + 1 + PF < nsteps) fetch(st + 1 + PF, nx);
+                __syncthreads();
+            }
         }
     }
 
@@ -2948,12 +3362,12 @@ hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s) {
     if (g.XH) {  // fp32 rows as fp16 hi + lo
         if (g.K % kF16BK || !g.XL || !g.XS || !g.xs) return hipErrorInvalidValue;
         switch (type) {
-        case T_Q4_K: moe_gemm_f16_kernel<T_Q4_K><<<grid, 256, 0, s>>>(a); break;
-        case T_Q5_K: moe_gemm_f16_kernel<T_Q5_K><<<grid, 256, 0, s>>>(a); break;
-        case T_Q6_K: moe_gemm_f16_kernel<T_Q6_K><<<grid, 256, 0, s>>>(a); break;
-        case T_Q8_0: moe_gemm_f16_kernel<T_Q8_0><<<grid, 256, 0, s>>>(a); break;
-        case T_IQ4_NL: moe_gemm_f16_kernel<T_IQ4_NL><<<grid, 256, 0, s>>>(a); break;
-        case T_IQ4_XS: moe_gemm_f16_kernel<T_IQ4_XS><<<grid, 256, 0, s>>>(a); break;
+        case T_Q4_K: moe_gemm_f16_kernel<T_Q4_K, 1><<<grid, 256, 0, s>>>(a); break;
+        case T_Q5_K: moe_gemm_f16_kernel<T_Q5_K, 1><<<grid, 256, 0, s>>>(a); break;
+        case T_Q6_K: moe_gemm_f16_kernel<T_Q6_K, 1><<<grid, 256, 0, s>>>(a); break;
+        case T_Q8_0: moe_gemm_f16_kernel<T_Q8_0, 1><<<grid, 256, 0, s>>>(a); break;
+        case T_IQ4_NL: moe_gemm_f16_kernel<T_IQ4_NL, 1><<<grid, 256, 0, s>>>(a); break;
+        case T_IQ4_XS: moe_gemm_f16_kernel<T_IQ4_XS, 1><<<grid, 256, 0, s>>>(a); break;
         default: return hipErrorInvalidValue;
         }
         return hipGetLastError();

@@ -124,6 +124,16 @@ hipError_t launch_gemm_i8_multi(uint32_t type, const GemmDesc* d, int n, int K, 
                                 int M, float* part, hipStream_t s);
 hipError_t launch_gemm_i8(uint32_t type, const void* W, int N, int K, const int8_t* qa, const float* sa, int M,
                           float* C, int ldc, float* part, hipStream_t s);
+// Activation-panel GEMM (gemm_panel_kernel): the per-row int8 activations of
+// a 64-row panel resident in LDS for the whole K, quantized in the kernel
+// from fp32 rows A [M][lda] (GGQ_ACT_Q8_ROW, bit-exact with
+// launch_quant_act) or taken from given codes qa / sa when A is null.  Up to
+// 4 weights of one type sharing the activations; no workspace.  Types other
+// than Q6_K, K a multiple of 32 and at most 2048, A 16-byte aligned with lda
+// a multiple of 4.
+bool gemm_panel_eligible(uint32_t type, int K, int M, const float* A, int lda);
+hipError_t launch_gemm_panel(uint32_t type, const GemmDesc* d, int n, int K, const float* A, int lda,
+                             const int8_t* qa, const float* sa, int M, hipStream_t s);
 // idx[m] = first index of the largest value of row m of L ([M][ld], N
 // values); val[m] = that value (val may be null).  `ws`: device workspace
 // of argmax_workspace_bytes(M) bytes.

@@ -280,7 +280,10 @@ int ggq_mul_mat_batch_rows_dev(ggq_ctx* ctx, const ggq_gemv_desc* descs, int n, 
  * ggq_mul_mat_dev): same result as one ggq_mul_mat_dev call per entry with
  * that act_mode.  GGQ_ACT_Q8_ROW with M <= 8 quantizes each entry's rows as
  * amd_xdna.cpp:598-603 and runs all entries in one int8 launch where the
- * shapes allow.  No reference counterpart as a batched call (the reference
+ * shapes allow; with M > 8 (any M: the GGQ_MAX_BATCH_ROWS limit applies to
+ * the other modes) entries that share A, type and K run as one int8 GEMM
+ * launch that quantizes the rows itself, the prefill form of the
+ * reference's quantize-inside-mul_mat_q (amd_xdna.cpp:633-639).  No reference counterpart as a batched call (the reference
  * issues one mul_mat_q per weight, main.cpp:3256-3267). */
 int ggq_mul_mat_batch_act_dev(ggq_ctx* ctx, const ggq_gemv_desc* descs, int n, int M, int act_mode, void* stream);
 

@@ -1060,3 +1060,29 @@ def test_q8_row_in_registers(ctx, orc, t, N, K, pad):
         A = (rng.standard_normal((1, K)) * scale).astype(np.float32)
         got = run_mm(ctx, t, raw, N, K, A, 1, lda=K + pad)
         assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL, (scale,)
+
+
+@pytest.mark.parametrize("t,K", [(8, 1568), (8, 2048), (12, 2048), (13, 1792), (20, 1600), (23, 1792)])
+@pytest.mark.parametrize("M", [100, 33])
+def test_prefill_gemm_panel_shapes(ctx, orc, t, K, M):
+    """The activation-panel GEMM beyond the benchmark's K = 1536: rows longer
+    than the register path (quantized by the streamed two-pass path), K not a
+    multiple of 128 (a partial last chunk of Q8_0 blocks), panels whose second
+    half is partly or wholly empty (M = 100, 33), through ggq_mul_mat_dev
+    (the rows quantized in the kernel) and ggq_mul_mat_q8_dev (given codes,
+    from ggq_quantize_act_dev): both against the oracle in the same mode,
+    and equal to each other bit for bit."""
+    import torch
+    N = 200
+    rng = np.random.default_rng(K + M + t)
+    raw = weights(t, N, K, seed=K + t)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    got = run_mm(ctx, t, raw, N, K, A, 1)
+    assert orc.rel_l2(got, orc.mul_mat_f64(t, raw, N, K, A, 1)) < TOL
+    dW, dA = dev(raw), dev(A)
+    q = empty((M, K), torch.int8)
+    sc = empty((M,), torch.float32)
+    ctx.check(ctx.lib.ggq_quantize_act_dev(ctx.h, ptr(dA), K, M, K, 1, ptr(q), ptr(sc), stream_handle()), "quant")
+    C = torch.full((M, N), float("nan"), device="cuda")
+    ctx.check(ctx.lib.ggq_mul_mat_q8_dev(ctx.h, ptr(dW), t, N, K, ptr(q), ptr(sc), M, ptr(C), N, stream_handle()), "q8")
+    assert np.array_equal(host(C).view(np.uint32), got.view(np.uint32))

@@ -24,7 +24,7 @@ def test_capture_refuses_growth_then_reserve(orc):
     import torch
     c = gl.Context(0)
     try:
-        N, K, M = 512, 1536, 64
+        N, K, M = 512, 4096, 64  # K > 2048: quantized into the workspace, split-K partials
         raw = t.weights(8, N, K, seed=3)
         dW = dev(raw)
         A = np.random.default_rng(3).standard_normal((M, K)).astype(np.float32)
@@ -64,7 +64,7 @@ def test_graph_survives_workspace_growth(orc):
     import torch
     c = gl.Context(0)
     try:
-        N, K = 384, 1536
+        N, K = 384, 4096  # the workspace path (K > 2048)
         raw = t.weights(8, N, K, seed=4)
         dW = dev(raw)
         rng = np.random.default_rng(4)
@@ -91,5 +91,37 @@ def test_graph_survives_workspace_growth(orc):
             g.replay()
             torch.cuda.synchronize()
             assert orc.rel_l2(y1.cpu().numpy(), ref1) < t.TOL
+    finally:
+        c.close()
+
+
+def test_capture_needs_no_workspace_on_the_panel_gemm(orc):
+    """K <= 2048: the prefill GEMM quantizes the rows inside its own launch
+    and uses no workspace, so a fresh context captures it without
+    ggq_reserve; replays on fresh inputs match the oracle."""
+    import torch
+    c = gl.Context(0)
+    try:
+        N, K, M = 640, 1536, 96
+        raw = t.weights(8, N, K, seed=5)
+        dW = dev(raw)
+        rng = np.random.default_rng(5)
+        x = torch.zeros((M, K), device="cuda")
+        y = torch.zeros((M, N), device="cuda")
+        s = torch.cuda.Stream()
+        sh = ctypes.c_void_p(s.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                c.check(q8_call(c, dW, N, K, x, y, M, sh), "captured panel GEMM")
+        for _ in range(3):
+            A = rng.standard_normal((M, K)).astype(np.float32)
+            x.copy_(torch.from_numpy(A))
+            y.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert orc.rel_l2(y.cpu().numpy(), orc.mul_mat_f64(8, raw, N, K, A, 1)) < t.TOL
     finally:
         c.close()
