@@ -830,15 +830,14 @@ int ggq_block_dot_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64
 // matrix cores when the grouped form takes it (the expert's weights are
 // decoded to int8 codes, about a third of the VALU work per weight of the
 // fp16 matrix-core GEMV), else on the matrix-core / FMA GEMV.  The down
-// projection's groups run in passes of 1-2 rows there, each re-reading the
-// expert's weights, so it stays on the GEMV unless GGQ_MOE_I8_DOWN=1.
+// projection's groups would run in passes of 1-2 rows there, each
+// re-reading the expert's weights (measured slower), so down stays on the
+// GEMV.
 static hipError_t moe_grouped_gemv(const ggq::GemvProblem& g, void* items, size_t items_bytes, hipStream_t s,
                                    bool down = false, const ggq::I8Shared* sh = nullptr, bool* took_shared = nullptr,
                                    bool list_ready = false) {
-    const char* v = getenv("GGQ_MOE_I8_DOWN");  // read per call: a process can switch it
-    const bool i8_down = v && *v && atoi(v) != 0;
     if (took_shared) *took_shared = false;
-    if ((!down || i8_down) && ggq::i8_gemv_grouped_eligible(g)) {
+    if (!down && ggq::i8_gemv_grouped_eligible(g)) {
         if (sh && ggq::i8_gemv_grouped_ws_bytes(g, sh->T) <= items_bytes) {
             if (took_shared) *took_shared = true;
             return ggq::launch_i8_gemv_grouped(g, items, s, sh, list_ready);

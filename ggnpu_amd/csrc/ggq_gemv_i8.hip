@@ -1094,7 +1094,7 @@ hipError_t i8_run(I8Args& args, const I8Grid& gr, int n, hipStream_t s) {
 
 bool i8_gemv_eligible(const GemvProblem* ps, int n, int mode) {
     // GGQ_GEMV_MFMA=0 keeps every GEMV on the fp32 FMA kernels
-    if (env_i8("GGQ_GEMV_I8", 1) == 0 || env_i8("GGQ_GEMV_MFMA", 1) == 0 || n < 1 || n > kMaxProbs) return false;
+    if (env_i8("GGQ_GEMV_MFMA", 1) == 0 || n < 1 || n > kMaxProbs) return false;
     bool q6 = false;
     for (int i = 0; i < n; i++) q6 = q6 || g4_format(ps[i].type);
     I8Shape sh;

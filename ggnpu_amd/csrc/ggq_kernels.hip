@@ -1380,17 +1380,6 @@ static int ilog2_ceil(int v) {
     return l;
 }
 
-// Workgroups of a non-grouped launch: by default exactly as many as can be
-// resident at once (occupancy x CUs), each looping over its share of rows, so
-// no launch runs a partial second round.  GGQ_GEMV_BLOCKS overrides.
-static int gemv_blocks_override() {
-    static int v = [] {
-        const char* e = getenv("GGQ_GEMV_BLOCKS");
-        return e && *e ? atoi(e) : 0;
-    }();
-    return v;
-}
-
 static int device_cus() {
     static int v = [] {
         int dev = 0, n = 0;
@@ -1415,70 +1404,35 @@ static int occupancy_per_cu(const void* kernel, size_t lds) {
     return per_cu;
 }
 
+// Workgroups of a non-grouped launch: exactly as many as can be resident at
+// once (occupancy x CUs), each looping over its share of rows, so no launch
+// runs a partial second round.
 template <typename K>
 static int resident_blocks(K kernel, size_t lds) {
-    if (gemv_blocks_override() > 0) return gemv_blocks_override();
     return occupancy_per_cu((const void*)kernel, lds) * device_cus();
-}
-
-// Row-iterations processed together per wavefront (their loads are issued
-// together and their reductions interleave).
-static int gemv_rows_per_iter() {
-    static int v = [] {
-        const char* e = getenv("GGQ_GEMV_U");
-        return e && *e ? atoi(e) : 1;
-    }();
-    return v;
-}
-
-
-static int gemv_prefetch() {
-    static int v = [] {
-        const char* e = getenv("GGQ_GEMV_PREFETCH");
-        return e && *e ? atoi(e) : 1;
-    }();
-    return v;
 }
 
 static bool fused(const GemvProblem& p) { return p.rms || p.X2 || p.R || p.silu; }
 
 // Single-row launches stage the activation row in LDS once per workgroup
 // (K <= 4096, at most 4 slots per thread; 16-byte aligned rows) instead of
-// every wavefront reading it from memory; GGQ_GEMV_XLDS=0 selects the
-// per-wavefront loads.
+// every wavefront reading it from memory.
 static bool gemv_xlds(const GemvProblem& p, const GemvArgs& a) {
-    static int v = [] {
-        const char* e = getenv("GGQ_GEMV_XLDS");
-        return e && *e ? atoi(e) : 1;
-    }();
-    return v != 0 && p.M <= 1 && !p.grp_off && !p.x_idx && a.x_vec4 && a.lpr_log2 < 8 && p.K >= 64 && p.K <= 4096 && p.K % 32 == 0;
-}
-
-static int gemv_max_lpr() {
-    static int v = [] {
-        const char* e = getenv("GGQ_GEMV_MAXLPR");
-        const int x = e && *e ? atoi(e) : 256;
-        return x == 64 || x == 128 ? x : 256;
-    }();
-    return v;
+    return p.M <= 1 && !p.grp_off && !p.x_idx && a.x_vec4 && a.lpr_log2 < 8 && p.K >= 64 && p.K <= 4096 && p.K % 32 == 0;
 }
 
 static int env_int(const char* name, int dflt) {
     const char* e = getenv(name);
     return e && *e ? atoi(e) : dflt;
 }
-// Grouped (MoE) launches: largest rows per pass, workgroups per group
-// (0 = from the resident capacity) and resident rounds to fill.
-// Largest rows per pass of plain multi-row launches (1, 2 or 4).  One row
-// per pass measured fastest on gfx950 for 4 and 8 rows: MB = 2 / 4 keep
-// 2x / 4x the activations in VGPRs (178 / 250 registers), which halves the
-// resident wavefronts, and the extra weight passes of MB = 1 are served
-// from cache.  These knobs are read at every multi-row / grouped launch
-// (never on the single-row decode path), so a process can switch them.
-static int gemv_mb_cap() { const int v = env_int("GGQ_GEMV_MBCAP", 1); return v < 1 ? 1 : v; }
-static int moe_mb() { return env_int("GGQ_MOE_MB", 2); }
-static int moe_gx() { return env_int("GGQ_MOE_GX", 0); }
-static int moe_rounds() { const int v = env_int("GGQ_MOE_ROUNDS", 4); return v < 1 ? 1 : v; }
+// Grouped (MoE) launches on the FMA kernels take two token rows per pass
+// and size their grid to four resident rounds shared among the groups.
+// Plain multi-row launches on the FMA kernels take one row per pass (two or
+// four rows per pass hold 2x / 4x the activations in VGPRs and measured
+// slower: the extra weight passes of one row per pass are served from
+// cache).
+constexpr int kMoeRowsPerPass = 2;
+constexpr int kMoeRounds = 4;
 
 
 // Matrix-core GEMV (gemv_mfma_kernel) for M >= 2 plain fp32-activation
@@ -1496,8 +1450,7 @@ struct MfmaPlan {
 static size_t mfma_xl_bytes(int K, int ms) { return (size_t)8 * (4 * ms * (K / 32) + 1) * 16; }
 static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
     if (env_int("GGQ_GEMV_MFMA", 1) == 0 || p.q8row) return false;
-    if (M < (env_int("GGQ_GEMV_MFMA1", 0) ? 1 : 2) || fused(p) || (p.K % 32) != 0 || p.K <= 0) return false;
-    if (p.grp_off && env_int("GGQ_MOE_MFMA", 1) == 0) return false;
+    if (M < 2 || fused(p) || (p.K % 32) != 0 || p.K <= 0) return false;
     const int P = p.K / 32;
     m.sl2 = P <= 16 ? 4 : (P <= 32 ? 5 : 6);
     const int S = 1 << m.sl2;
@@ -1506,20 +1459,16 @@ static bool mfma_plan(const GemvProblem& p, int M, MfmaPlan& m) {
     // 8 rows per pass (MS 2) halves the passes over each weight row but
     // holds twice the activations: it pays off for expert groups averaging
     // 8 rows or more (prefill-sized MoE batches), not for plain batches.
-    // GGQ_GEMV_MFMA_MS=1 / 2 forces either.
-    const int ms_env = env_int("GGQ_GEMV_MFMA_MS", 0);
-    const bool eight = ms_env ? ms_env >= 2 : (p.grp_off && p.groups > 1 && (int64_t)p.M >= 8LL * p.groups);
+    const bool eight = p.grp_off && p.groups > 1 && (int64_t)p.M >= 8LL * p.groups;
     m.ms = (M > 4 && m.ppt == 1 && eight) ? 2 : 1;
     // Plain batches of up to 8 rows: fp32 activations straight into 4x4x1
     // fp32 products.  Grouped (expert) launches and larger batches: the fp16
     // hi + lo split into 4x4x4 fp16 products (half the MFMA issues per row
-    // set), faster there.  GGQ_GEMV_MFMA32=0 / 1 forces either.
-    m.x32 = env_int("GGQ_GEMV_MFMA32", p.grp_off || M > 8 ? 0 : 1) != 0;
+    // set), faster there.
+    m.x32 = !p.grp_off && M <= 8;
     // Rows staged in LDS once per workgroup when two or more row groups of
-    // the workgroup would read the same activations (K <= 1024);
-    // GGQ_GEMV_MFMA_XL=0 never.
-    m.xl = env_int("GGQ_GEMV_MFMA_XL", 1) != 0 && P >= 2 && P <= 32 && !p.grp_off && !p.x_idx && (uintptr_t)p.X % 16 == 0 &&
-           p.ldx % 4 == 0;
+    // the workgroup would read the same activations (K <= 1024).
+    m.xl = P >= 2 && P <= 32 && !p.grp_off && !p.x_idx && (uintptr_t)p.X % 16 == 0 && p.ldx % 4 == 0;
     const int rows_per_iter = 4 * (64 / S);
     m.n_iters = (p.N + rows_per_iter - 1) / rows_per_iter;
     return true;
@@ -1543,7 +1492,7 @@ static GemvPlan plan_gemv(const GemvProblem& p) {
     GemvArgs& a = g.a;
     g.simple = (p.K % 32) != 0;
     const int P = p.K / 32 > 0 ? p.K / 32 : 1;
-    const int lpr_log2 = ilog2_ceil(P < gemv_max_lpr() ? P : gemv_max_lpr());
+    const int lpr_log2 = ilog2_ceil(P < 256 ? P : 256);
     const int lpr = 1 << lpr_log2;
     const int rpi = 256 / lpr;
     a.W = (const uint8_t*)p.W;
@@ -1558,7 +1507,7 @@ static GemvPlan plan_gemv(const GemvProblem& p) {
     a.lpr_log2 = lpr_log2;
     a.x_vec4 = ((uintptr_t)p.X % 16 == 0) && (p.ldx % 4 == 0) && ((uintptr_t)p.X2 % 16 == 0);
     a.p_div = (uint32_t)((0x100000000ull + P - 1) / P);
-    a.prefetch = gemv_prefetch();
+    a.prefetch = 1;
     a.X2 = p.X2;
     a.silu = p.silu;
     a.rms = p.rms;
@@ -1581,8 +1530,7 @@ static void launch_mfma_one(const GemvArgs& a, const MfmaPlan& mp, int K, int gr
     void (*k)(GemvArgs) = mp.x32 ? (mp.xl ? gemv_mfma_kernel<T, PPT, MS, ONE, true, true> : gemv_mfma_kernel<T, PPT, MS, ONE, true, false>)
                                  : (mp.xl ? gemv_mfma_kernel<T, PPT, MS, ONE, false, true> : gemv_mfma_kernel<T, PPT, MS, ONE, false, false>);
     const size_t lds = mp.xl ? mfma_xl_bytes(K, MS) : 0;
-    int gx = resident_blocks(k, lds) * (groups > 1 ? moe_rounds() : 1) / (gz * groups);
-    if (groups > 1 && moe_gx() > 0) gx = moe_gx();
+    int gx = resident_blocks(k, lds) * (groups > 1 ? kMoeRounds : 1) / (gz * groups);
     gx = gx < 1 ? 1 : (gx > mp.n_iters ? mp.n_iters : gx);
     hipLaunchKernelGGL(k, dim3(gx, groups, gz), dim3(256), lds, s, a);
 }
@@ -1633,8 +1581,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
 #define GO(MB_, PPT_, U_)                                                                        \
     do {                                                                                         \
         const int gz = groups > 1 ? 1 : (mrows + MB_ - 1) / MB_;                                 \
-        int gx = resident_blocks(gemv_kernel<T, MB_, PPT_, U_>, 0) * (groups > 1 ? moe_rounds() : 1) / (gz * groups); \
-        if (groups > 1 && moe_gx() > 0) gx = moe_gx();                                           \
+        int gx = resident_blocks(gemv_kernel<T, MB_, PPT_, U_>, 0) * (groups > 1 ? kMoeRounds : 1) / (gz * groups); \
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
         gemv_kernel<T, MB_, PPT_, U_><<<dim3(gx, groups, gz), 256, 0, s>>>(a);                   \
     } while (0)
@@ -1649,7 +1596,6 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
         gemv_kernel<T, 1, PPT_, 1, true><<<dim3(gx, 1, gz), 256, 0, s>>>(a);                     \
     } while (0)
-    const int u = gemv_rows_per_iter();
 #define GO_X(PPT_)                                                                               \
     do {                                                                                         \
         const size_t lds = (size_t)p.K * sizeof(float);                                          \
@@ -1665,7 +1611,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         gx = gx < 1 ? 1 : (gx > g.n_iters ? g.n_iters : gx);                                     \
         gemv_kernel<T, 1, PPT_, 1, true, true><<<dim3(gx, 1, 1), 256, lds, s>>>(a);              \
     } while (0)
-    if (p.q8row && !(groups == 1 && u == 1 && !fused(p) && mrows == 1 && ppt <= 4)) return hipErrorInvalidValue;
+    if (p.q8row && !(groups == 1 && !fused(p) && mrows == 1 && ppt <= 4)) return hipErrorInvalidValue;
     if (p.q8row && !gemv_xlds(p, a)) {  // the row quantized in registers (non-staged kernels)
 #define GQ(PPT_)                                                                                 \
     do {                                                                                         \
@@ -1687,7 +1633,7 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
 #undef GO_FX
         return hipGetLastError();
     }
-    if (groups == 1 && u == 1 && !fused(p) && gemv_xlds(p, a)) {
+    if (groups == 1 && !fused(p) && gemv_xlds(p, a)) {
         if (ppt == 1) GO_X(1);
         else if (ppt == 2) GO_X(2);
         else if (ppt <= 4) GO_X(4);
@@ -1702,17 +1648,11 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
         else if (ppt <= 4) GO_F(4);
         else return hipErrorInvalidValue;
     } else if (groups > 1 && ppt == 1 && mrows > 1) {
-        const int mb = moe_mb();
-        if (mb <= 1) GO(1, 1, 1);
-        else if (mb == 2) GO(2, 1, 1);
-        else GO(4, 1, 1);
+        GO(kMoeRowsPerPass, 1, 1);
     } else if (ppt == 1) {
-        if (mrows <= 1 || gemv_mb_cap() <= 1) { if (u >= 4) GO(1, 1, 4); else if (u >= 2) GO(1, 1, 2); else GO(1, 1, 1); }
-        else if (mrows == 2 || gemv_mb_cap() == 2) GO(2, 1, 1);
-        else GO(4, 1, 1);
+        GO(1, 1, 1);
     } else if (ppt == 2) {
-        if (mrows <= 1 || gemv_mb_cap() <= 1) GO(1, 2, 1);
-        else GO(2, 2, 1);
+        GO(1, 2, 1);
     } else if (ppt <= 4) {
         GO(1, 4, 1);
     } else {
@@ -1721,14 +1661,6 @@ static hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t s) {
 #undef GO
 #undef GO_F
     return hipGetLastError();
-}
-
-// Rows per pass of a multi-problem launch for M activation rows.
-static int multi_mb(int ppt, int M) {
-    if (M <= 1) return 1;
-    const int mb = ppt == 1 ? (M == 2 ? 2 : 4) : 2;
-    const int cap = gemv_mb_cap();
-    return mb > cap ? cap : mb;
 }
 
 template <int MB, int PPT, int U, bool F = false, bool KQ = false>
@@ -1814,11 +1746,9 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
         xl = xl && gemv_xlds(ps[i], plans[i].a);
         kmax = ps[i].K > kmax ? ps[i].K : kmax;
     }
-    const int u = any_fused ? 1 : gemv_rows_per_iter();
-    const int mb = any_fused ? 1 : multi_mb(ppt, M);
-    const int gz = (M + mb - 1) / mb;
-    kq = kq && ppt == 1 && mb == 1 && u == 1;  // the variants compiled with KQ
-    xl = xl && mb == 1 && u == 1 && M == 1;
+    const int gz = M;  // one activation row per pass
+    kq = kq && ppt == 1;  // the variants compiled with KQ
+    xl = xl && M == 1;
     const bool q8 = ps[0].q8row != 0;
     for (int i = 0; i < n; i++)
         if ((ps[i].q8row != 0) != q8 || (q8 && any_fused)) return hipErrorInvalidValue;
@@ -1845,11 +1775,9 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     } else if (kq) {
         target = multi_resident<1, 1, 1, false, true>();
     } else if (ppt == 1) {
-        if (mb == 1) target = u >= 4 ? multi_resident<1, 1, 4>() : u >= 2 ? multi_resident<1, 1, 2>() : multi_resident<1, 1, 1>();
-        else if (mb == 2) target = multi_resident<2, 1, 1>();
-        else target = multi_resident<4, 1, 1>();
+        target = multi_resident<1, 1, 1>();
     } else {
-        target = mb == 1 ? multi_resident<1, 2, 1>() : multi_resident<2, 2, 1>();
+        target = multi_resident<1, 2, 1>();
     }
     target = target / gz > 0 ? target / gz : 1;
     int b = 0;
@@ -1884,18 +1812,9 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
     } else if (kq) {
         gemv_multi_kernel<1, 1, 1, false, true><<<grid, 256, 0, s>>>(ma);
     } else if (ppt == 1) {
-        if (mb == 1) {
-            if (u >= 4) gemv_multi_kernel<1, 1, 4><<<grid, 256, 0, s>>>(ma);
-            else if (u >= 2) gemv_multi_kernel<1, 1, 2><<<grid, 256, 0, s>>>(ma);
-            else gemv_multi_kernel<1, 1, 1><<<grid, 256, 0, s>>>(ma);
-        } else if (mb == 2) {
-            gemv_multi_kernel<2, 1, 1><<<grid, 256, 0, s>>>(ma);
-        } else {
-            gemv_multi_kernel<4, 1, 1><<<grid, 256, 0, s>>>(ma);
-        }
+        gemv_multi_kernel<1, 1, 1><<<grid, 256, 0, s>>>(ma);
     } else {
-        if (mb == 1) gemv_multi_kernel<1, 2, 1><<<grid, 256, 0, s>>>(ma);
-        else gemv_multi_kernel<2, 2, 1><<<grid, 256, 0, s>>>(ma);
+        gemv_multi_kernel<1, 2, 1><<<grid, 256, 0, s>>>(ma);
     }
     return hipGetLastError();
 }
@@ -1906,7 +1825,7 @@ hipError_t launch_gemv_multi(const GemvProblem* ps, int n, hipStream_t s) {
 // fused options or grouping, and together fewer weight bytes than the int8
 // matrix-core GEMV's threshold (its fixed set-up only pays off above it).
 bool gemv_q8row_eligible(const GemvProblem* ps, int n) {
-    if (n < 1 || n > kMaxMulti || gemv_rows_per_iter() != 1) return false;
+    if (n < 1 || n > kMaxMulti) return false;
     int64_t bytes = 0;
     for (int i = 0; i < n; i++) {
         const GemvProblem& p = ps[i];
@@ -1918,7 +1837,7 @@ bool gemv_q8row_eligible(const GemvProblem* ps, int n) {
         if (g.simple || g.ppt > 4 || !offsets_fit(p)) return false;
         bytes += (int64_t)p.N * row_bytes(p.type, p.K);
     }
-    return bytes < (int64_t)env_int("GGQ_I8_MIN_BYTES", 16 << 20) && env_int("GGQ_GEMV_Q8XL", 1) != 0;
+    return bytes < (int64_t)env_int("GGQ_I8_MIN_BYTES", 16 << 20);
 }
 
 hipError_t launch_gemv(const GemvProblem& p, hipStream_t s) {
@@ -3414,46 +3333,15 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmMultiArgs a) {
     }
 }
 
-// Workgroup tile: 64x64 (32x32 per wavefront).  GGQ_GEMM_TILE=128 selects
-// 128x64 tiles (64x32 per wavefront).
-static bool gemm_big_tile() {
-    static int v = [] {
-        const char* e = getenv("GGQ_GEMM_TILE");
-        return e && *e ? atoi(e) : 64;
-    }();
-    return v == 128;
-}
-
-// Register prefetch depth of the LDS GEMM in K-steps (GGQ_GEMM_PF, 1..4).
-static int gemm_prefetch() {
-    static int v = [] {
-        const char* e = getenv("GGQ_GEMM_PF");
-        const int x = e && *e ? atoi(e) : 2;
-        return x < 1 ? 1 : (x > 4 ? 4 : x);
-    }();
-    return v;
-}
-
-template <int T>
-static const void* gemm_kernel_ptr(bool big, int pf) {
-    if (big) return (const void*)gemm_i8_lds_kernel<T, 128, 64, 1>;
-    switch (pf) {
-    case 1: return (const void*)gemm_i8_lds_kernel<T, 64, 64, 1>;
-    case 3: return (const void*)gemm_i8_lds_kernel<T, 64, 64, 3>;
-    case 4: return (const void*)gemm_i8_lds_kernel<T, 64, 64, 4>;
-    default: return (const void*)gemm_i8_lds_kernel<T, 64, 64, 2>;
-    }
-}
-
+// Workgroup tile 64x64 (32x32 per wavefront), register prefetch two
+// K-steps ahead (128x64 tiles and depths 1, 3, 4 measured slower).
 static const void* gemm_kernel_for(uint32_t type) {
-    const bool big = gemm_big_tile();
-    const int pf = gemm_prefetch();
     switch (type) {
-    case T_Q4_K: return gemm_kernel_ptr<T_Q4_K>(big, pf);
-    case T_Q5_K: return gemm_kernel_ptr<T_Q5_K>(big, pf);
-    case T_Q8_0: return gemm_kernel_ptr<T_Q8_0>(big, pf);
-    case T_IQ4_NL: return gemm_kernel_ptr<T_IQ4_NL>(big, pf);
-    case T_IQ4_XS: return gemm_kernel_ptr<T_IQ4_XS>(big, pf);
+    case T_Q4_K: return (const void*)gemm_i8_lds_kernel<T_Q4_K, 64, 64, 2>;
+    case T_Q5_K: return (const void*)gemm_i8_lds_kernel<T_Q5_K, 64, 64, 2>;
+    case T_Q8_0: return (const void*)gemm_i8_lds_kernel<T_Q8_0, 64, 64, 2>;
+    case T_IQ4_NL: return (const void*)gemm_i8_lds_kernel<T_IQ4_NL, 64, 64, 2>;
+    case T_IQ4_XS: return (const void*)gemm_i8_lds_kernel<T_IQ4_XS, 64, 64, 2>;
     default: return nullptr;
     }
 }
@@ -3471,8 +3359,7 @@ static int choose_splits(int64_t tiles, int nsteps, int resident) {
 
 GemmPlan plan_gemm_i8(uint32_t type, const int* Ns, int n, int K, int M) {
     GemmPlan pl{};
-    const bool big = gemm_big_tile();
-    pl.bm = big ? 128 : 64;
+    pl.bm = 64;
     pl.bn = 64;
     pl.n_tiles = 0;
     for (int i = 0; i < n; i++) pl.n_tiles += (Ns[i] + pl.bn - 1) / pl.bn;
@@ -3540,8 +3427,7 @@ hipError_t launch_gemm_i8_multi(uint32_t type, const GemmDesc* d, int n, int K, 
     hipError_t e = hipLaunchKernel(k, grid, dim3(256), args, 0, s);
     if (e != hipSuccess || pl.splits == 1) return e;
     // (BM*BN/256) register elements per thread, four per workgroup.
-    if (pl.bm == 128) gemm_reduce_kernel<128, 64><<<dim3(pl.n_tiles, pl.m_tiles, 128 * 64 / 1024), 256, 0, s>>>(a);
-    else gemm_reduce_kernel<64, 64><<<dim3(pl.n_tiles, pl.m_tiles, 64 * 64 / 1024), 256, 0, s>>>(a);
+    gemm_reduce_kernel<64, 64><<<dim3(pl.n_tiles, pl.m_tiles, 64 * 64 / 1024), 256, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -1,17 +1,20 @@
-"""Parity of the GEMV variants that the default launch configuration does
-not select: the fp32 FMA kernels for several rows (GGQ_GEMV_MFMA=0) with
-GGQ_GEMV_MBCAP 2 / 4; GGQ_MOE_MB 1 / 4 (the grouped default being 2); the
-matrix-core kernel with 8 rows per pass (GGQ_GEMV_MFMA_MS=2) and for a
-single row (GGQ_GEMV_MFMA1=1); its fp16 hi + lo products for plain batches
-and fp32 products for expert groups (GGQ_GEMV_MFMA32=0 / 1), and its
-activation rows read per wavefront instead of staged in LDS
-(GGQ_GEMV_MFMA_XL=0); per-row int8 decode without the int8
-matrix-core GEMV (GGQ_GEMV_I8=0: quantize, dequantize, fp32 kernel) and
-fp32 launches of every size on it (GGQ_I8_MIN_BYTES=0); single per-row
-int8 rows on it rather than quantized in the fp32 kernel's staging
-(GGQ_GEMV_Q8XL=0).  The
-library reads these knobs at each multi-row / grouped launch, so the checks
-set them in this process and restore them afterwards."""
+"""Parity of the kernel routes that the default launch configuration does not
+select at the tests' shapes, reached through the library's remaining
+path-selection variables (read at every launch, so the checks set them in
+this process and restore them afterwards):
+
+  GGQ_GEMV_MFMA=0      several activation rows on the fp32 FMA kernels (one
+                       row per pass; the route of fused launches and of
+                       K > 4096) instead of the matrix-core GEMV, plain and
+                       expert-grouped;
+  GGQ_I8_MIN_BYTES=0   fp32 and per-row int8 decode launches of every size on
+                       the int8 matrix-core GEMV (by default only launches of
+                       16 MB or more of weights).
+
+GGQ_MOE_I8, GGQ_MOE_I8_GX, GGQ_MOE_I8_KW and GGQ_I8_KW (grouped int8 GEMV
+decompositions) are exercised in test_gpu_parity.py, GGQ_MOE_GEMV_MAX_AVG in
+test_gpu_parity.py and test_gpu_moe_stages.py, GGQ_ATTN_SPANS in
+test_gpu_attention.py."""
 import os
 
 import pytest
@@ -23,83 +26,34 @@ pytestmark = pytest.mark.gpu
 ctx = t.ctx  # module-scoped context fixture
 
 
-def _set_env(values):
-    old = {k: os.environ.get(k) for k in values}
-    os.environ.update(values)
-    return old
-
-
-def _restore(old):
-    for k, v in old.items():
-        if v is None:
-            os.environ.pop(k, None)
-        else:
-            os.environ[k] = v
-
-
 @pytest.fixture
-def wide_rows(request):
-    old = _set_env({"GGQ_GEMV_MBCAP": request.param, "GGQ_MOE_MB": request.param, "GGQ_GEMV_MFMA": "0"})
-    yield request.param
-    _restore(old)
-
-
-@pytest.fixture
-def mfma_knob(request):
+def knob(request):
     name, value = request.param
-    old = _set_env({name: value})
+    old = os.environ.get(name)
+    os.environ[name] = value
     yield request.param
-    _restore(old)
+    if old is None:
+        os.environ.pop(name, None)
+    else:
+        os.environ[name] = old
 
 
-@pytest.mark.parametrize("wide_rows", ["2", "4"], indirect=True)
+@pytest.mark.parametrize("knob", [("GGQ_GEMV_MFMA", "0")], indirect=True)
 @pytest.mark.parametrize("M", [2, 3, 4, 8])
-def test_batched_rows_wide(ctx, orc, wide_rows, M):
+def test_batched_rows_fma(ctx, orc, knob, M):
     t.test_batched_rows_gemv(ctx, orc, M)
 
 
-@pytest.mark.parametrize("wide_rows", ["1", "2", "4"], indirect=True)
-def test_moe_wide(ctx, orc, wide_rows):
+@pytest.mark.parametrize("knob", [("GGQ_GEMV_MFMA", "0")], indirect=True)
+def test_moe_fma(ctx, orc, knob, monkeypatch):
+    monkeypatch.setenv("GGQ_MOE_GEMV_MAX_AVG", "100000")
     t.test_moe_small_vs_oracle(ctx, orc, True)
     t.test_moe_qwen35moe_shape_vs_oracle(ctx, orc)
 
 
-@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA_MS", "2")], indirect=True)
-@pytest.mark.parametrize("M", [5, 8, 9, 16])
-def test_mfma_eight_rows_per_pass(ctx, orc, mfma_knob, M):
-    t.test_batched_rows_gemv(ctx, orc, M)
-
-
-@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA32", "0"), ("GGQ_GEMV_MFMA_XL", "0")],
-                         indirect=True)
-@pytest.mark.parametrize("M", [2, 5, 8, 16])
-def test_mfma_product_and_staging(ctx, orc, mfma_knob, M):
-    t.test_batched_rows_gemv(ctx, orc, M)
-
-
-@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA32", "1")], indirect=True)
-def test_moe_fp32_products(ctx, orc, mfma_knob):
-    t.test_moe_small_vs_oracle(ctx, orc, True)
-    t.test_moe_qwen35moe_shape_vs_oracle(ctx, orc)
-
-
-@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA1", "1")], indirect=True)
-@pytest.mark.parametrize("ty", [8, 12, 13, 14, 20, 23])
-def test_mfma_single_row(ctx, orc, mfma_knob, ty):
-    """One activation row through the matrix-core kernel (one and two pieces
-    per lane) against the fp64 oracle."""
-    import numpy as np
-    for K in (1024, 4096):
-        N = 333
-        raw = t.weights(ty, N, K, seed=ty + K)
-        A = np.random.default_rng(K).standard_normal((1, K)).astype(np.float32)
-        got = t.run_mm(ctx, ty, raw, N, K, A, 0)
-        assert orc.rel_l2(got, orc.mul_mat_f64(ty, raw, N, K, A, 0)) < t.TOL, (ty, K)
-
-
-@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_MFMA", "0")], indirect=True)
+@pytest.mark.parametrize("knob", [("GGQ_GEMV_MFMA", "0")], indirect=True)
 @pytest.mark.parametrize("ty", [12, 14, 20])
-def test_fma_path_batch_invariant(ctx, orc, mfma_knob, ty):
+def test_fma_path_batch_invariant(ctx, orc, knob, ty):
     """On the FMA kernels every row of a batch equals the same row computed
     alone, bit for bit."""
     import numpy as np
@@ -113,10 +67,9 @@ def test_fma_path_batch_invariant(ctx, orc, mfma_knob, ty):
             assert np.array_equal(batch[m].view(np.uint32), alone[0].view(np.uint32)), (M, m)
 
 
-@pytest.mark.parametrize("mfma_knob", [("GGQ_GEMV_I8", "0"), ("GGQ_I8_MIN_BYTES", "0"), ("GGQ_GEMV_Q8XL", "0")],
-                         indirect=True)
+@pytest.mark.parametrize("knob", [("GGQ_I8_MIN_BYTES", "0")], indirect=True)
 @pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q8_0", "IQ4_XS"])
-def test_i8_gemv_switches(ctx, orc, mfma_knob, name):
+def test_i8_gemv_all_sizes(ctx, orc, knob, name):
     for M in (1, 3):
         t.test_gemv_f32_vs_oracle(ctx, orc, name, M)
     t.test_gemv_q8_act_vs_oracle(ctx, orc, name, 1)

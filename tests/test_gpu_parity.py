@@ -427,15 +427,14 @@ def test_moe_int8_grouped_launches(ctx, orc, monkeypatch, tg, tu, td, T, E, k):
     GEMV (experts' rows in chunks of 4, or 2 for IQ4 / Q6_K, from a chunk
     list built on the device; experts with 0, 1 and dozens of rows), against
     the oracle and against the same layer on the matrix-core GEMV
-    (GGQ_MOE_I8=0); GGQ_MOE_I8_DOWN=1 puts the down projection on it too, and
-    one or three workgroups per chunk (instead of the count sized to the
-    chip) with one wavefront per tile split the rows and K differently."""
+    (GGQ_MOE_I8=0); one or three workgroups per chunk (instead of the count
+    sized to the chip) with one wavefront per tile split the rows and K
+    differently."""
     H, F = 512, 256
     outs = {}
     monkeypatch.setenv("GGQ_MOE_GEMV_MAX_AVG", "100000")  # the grouped GEMVs at every batch size
-    for i8, down, gx, kw in ((0, 0, 0, 4), (1, 0, 0, 4), (1, 1, 1, 4), (1, 1, 3, 1)):
+    for i8, gx, kw in ((0, 0, 4), (1, 0, 4), (1, 1, 4), (1, 3, 1)):
         monkeypatch.setenv("GGQ_MOE_I8", str(i8))
-        monkeypatch.setenv("GGQ_MOE_I8_DOWN", str(down))
         monkeypatch.setenv("GGQ_MOE_I8_GX", str(gx))  # workgroups per (problem, chunk); 0: sized to the chip
         monkeypatch.setenv("GGQ_MOE_I8_KW", str(kw))  # wavefronts per tile
         for shared in (False, True):
@@ -443,11 +442,11 @@ def test_moe_int8_grouped_launches(ctx, orc, monkeypatch, tg, tu, td, T, E, k):
                 ctx, T, H, F, E, k, shared, seed=T + E + tg, tg=tg, tu=tu, td=td)
             ref, rsel, rw = orc.moe_ffn_f64(x, logits, H, F, E, k, tg, Wg, tu, Wu, td, Wd, Sg, Su, Sd, sw)
             assert np.array_equal(sel, rsel)
-            assert orc.rel_l2(out, ref) < TOL, (i8, down, gx, kw, shared)
-            outs[(i8, down, gx, shared)] = out
+            assert orc.rel_l2(out, ref) < TOL, (i8, gx, kw, shared)
+            outs[(i8, gx, shared)] = out
     for shared in (False, True):
-        for key in ((1, 0, 0), (1, 1, 1), (1, 1, 3)):
-            assert orc.rel_l2(outs[key + (shared,)], outs[(0, 0, 0, shared)]) < TOL, key
+        for key in ((1, 0), (1, 1), (1, 3)):
+            assert orc.rel_l2(outs[key + (shared,)], outs[(0, 0, shared)]) < TOL, key
 
 
 @pytest.mark.parametrize("E,k", [(64, 8), (100, 6), (128, 8), (500, 8), (1000, 8)])
