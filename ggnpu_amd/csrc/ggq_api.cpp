@@ -955,7 +955,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     const size_t o_sel = take(4 * nk), o_w = take(4 * nk), o_go = take(4 * (size_t)(E + 2)),
                  o_tok = take(4 * rows), o_pos = take(4 * nk), o_qx = take((size_t)T * H), o_sx = take(4 * (size_t)T),
                  o_g = take(4 * rows * F), o_u = take(4 * rows * F), o_qh = take(rows * F), o_sh = take(4 * rows),
-                 o_d = take(4 * rows * H), o_tl = take(8 * (size_t)max_tiles), o_nt = take(4);
+                 o_d = take(4 * rows * H), o_tl = take(8 * (size_t)max_tiles), o_nt = take(4),
+                 o_qsx = take(4 * (size_t)T * (H / 32)), o_qsh = take(4 * rows * (F / 32));
     const size_t o_hf = c->trace_rows ? take(4 * rows * F) : 0;
     // chunk list of the grouped int8 GEMV (chunks of 4 or more rows)
     const size_t it_bytes = 8 * ((rows + 3) / 4 + std::min<size_t>((size_t)E + 1, rows)) + 16;
@@ -1018,7 +1019,13 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if (!(built && gu_i8 && dn_i8) &&
         (e = ggq::launch_moe_tiles(grp, tok, E, (int)ts, (int2*)tiles, ntiles, s)) != hipSuccess)
         return hip_status(c, e, "moe_tiles");
-    if ((e = ggq::launch_quant_act(p->x, H, T, H, GGQ_ACT_Q8_ROW, qx, sx, nullptr, s)) != hipSuccess)
+    // the token rows' codes, and their sums per 32 values for the K-quant
+    // min term of the grouped GEMM
+    float* qsx = (float*)(base + o_qsx);
+    float* qsh = (float*)(base + o_qsh);
+    gu.QS = qsx;
+    gd.QS = qsh;
+    if ((e = ggq::launch_produce_quant(0, p->x, nullptr, H, T, H, 0.0f, qx, sx, s, nullptr, qsx)) != hipSuccess)
         return hip_status(c, e, "quant x");
     auto grouped = [&](uint32_t type, const ggq::MoeGemm& d) -> hipError_t {
         if (i8_ok(type, d)) return ggq::launch_i8_moe_q8(type, d, (int)rows, base + o_it, s);
@@ -1038,7 +1045,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     }
     // SwiGLU of every pair row (routed and shared) and its int8 row codes.
     float* hf = c->trace_rows ? (float*)(base + o_hf) : nullptr;
-    if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s, hf)) != hipSuccess)
+    if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s, hf, qsh)) !=
+        hipSuccess)
         return hip_status(c, e, "swiglu quant");
     if (dn_i8) e = ggq::launch_i8_moe_q8(p->down_type, gd, (int)rows, base + o_it2, s, built);
     else e = ggq::launch_moe_gemm(p->down_type, gd, s);

@@ -150,7 +150,8 @@ enum { PROD_NONE = 0, PROD_RMS = 1, PROD_SWIGLU = 2 };
 template <int P>
 __device__ __forceinline__ void quant_row_regs(const float* a, const float* aux, float eps, int m, int K,
                                                int8_t* __restrict__ q, float* __restrict__ scales,
-                                               float* __restrict__ x_eff, float* __restrict__ prod_out = nullptr) {
+                                               float* __restrict__ x_eff, float* __restrict__ prod_out = nullptr,
+                                               float* __restrict__ gsum = nullptr) {
     __shared__ float wmax[4];
     constexpr int R = 16;
     float4 v[R];
@@ -229,6 +230,13 @@ __device__ __forceinline__ void quant_row_regs(const float* a, const float* aux,
             *(float4*)(x_eff + (int64_t)m * K + k) =
                 make_float4(__fmul_rn((float)c0, sc), __fmul_rn((float)c1, sc), __fmul_rn((float)c2, sc),
                             __fmul_rn((float)c3, sc));
+        if (gsum) {  // code sums per 32 values (eight consecutive threads), exact in fp32
+            int cs = (int)c0 + (int)c1 + (int)c2 + (int)c3;
+            cs += __shfl_xor(cs, 1, 64);
+            cs += __shfl_xor(cs, 2, 64);
+            cs += __shfl_xor(cs, 4, 64);
+            if ((threadIdx.x & 7) == 0) gsum[(int64_t)m * (K / 32) + k / 32] = (float)cs;
+        }
     }
 }
 
@@ -238,10 +246,11 @@ __global__ __launch_bounds__(256) void produce_quant_row_kernel(const float* __r
                                                                 const float* __restrict__ aux, int lda, int K,
                                                                 float eps, int8_t* __restrict__ q,
                                                                 float* __restrict__ scales,
-                                                                float* __restrict__ prod_out) {
+                                                                float* __restrict__ prod_out,
+                                                                float* __restrict__ gsum) {
     const int m = blockIdx.x;
     const float* au = P == PROD_SWIGLU ? aux + (int64_t)m * lda : aux;
-    quant_row_regs<P>(A + (int64_t)m * lda, au, eps, m, K, q, scales, nullptr, prod_out);
+    quant_row_regs<P>(A + (int64_t)m * lda, au, eps, m, K, q, scales, nullptr, prod_out, gsum);
 }
 
 // One workgroup per row: absolute maximum, then codes.  With 16-byte
@@ -331,15 +340,17 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
 }
 
 hipError_t launch_produce_quant(int producer, const float* A, const float* aux, int lda, int M, int K, float eps,
-                                int8_t* q, float* scales, hipStream_t s, float* prod_out) {
+                                int8_t* q, float* scales, hipStream_t s, float* prod_out, float* gsum) {
     if (M == 0) return hipSuccess;
     if (K <= 0 || K > 1024 * 16 || K % 4 || lda % 4 || (uintptr_t)A % 16 || (uintptr_t)aux % 16 ||
-        (uintptr_t)q % 4 || (uintptr_t)prod_out % 16)
+        (uintptr_t)q % 4 || (uintptr_t)prod_out % 16 || (gsum && K % 32))
         return hipErrorInvalidValue;
     if (producer == PROD_RMS)
-        produce_quant_row_kernel<PROD_RMS><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out);
+        produce_quant_row_kernel<PROD_RMS><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out, gsum);
     else if (producer == PROD_SWIGLU && aux)
-        produce_quant_row_kernel<PROD_SWIGLU><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out);
+        produce_quant_row_kernel<PROD_SWIGLU><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out, gsum);
+    else if (producer == PROD_NONE)
+        produce_quant_row_kernel<PROD_NONE><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out, gsum);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -2734,6 +2745,7 @@ struct MoeGemmArgs {
     float* C;
     float* C2;
     int ldc;
+    const float* QS;  // int8 mode, K-quant mins: code sums per 32 values [rows][K/32]
     // fp32-row mode (moe_gemm_f16_kernel): hi / lo planes [rows][K], group
     // sums [rows][K/32] and row scales 2^-e [rows] of the activation rows
     const _Float16* XH;
@@ -2820,6 +2832,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t Bs[2][kMoeBN][kGemmLd];
     __shared__ __attribute__((aligned(16))) float Bd[2][kMoeBN][GS];
     __shared__ __attribute__((aligned(16))) float Bm[2][kMoeBN][G];
+    __shared__ __attribute__((aligned(16))) float Ss[2][G][kMoeBM];  // activation code sums (K-quant mins)
 
     const int tile = blockIdx.y;
     if (tile >= *a.n_tiles) return;
@@ -2831,6 +2844,12 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     const int li = lane & 31, lk = lane >> 5;
     const int n_tile = blockIdx.x * kMoeBN;
     const int nsteps = (a.K + kGemmBK - 1) / kGemmBK;
+    const int KG = a.K / 32;
+    // Group sums: threads 0..127 stage (group, row) entries, 4 groups x 32 rows.
+    const int sr = tid & 31, sg = (tid >> 5) & 3;
+    const int ps = p0 + sr;
+    const int srow = a.x_idx ? a.x_idx[ps < p_end ? ps : p0] : (ps < p_end ? ps : p0);
+    const float* const qsp = kMin ? a.QS + (int64_t)srow * KG + sg : nullptr;
 
     // Activations: 32 rows x 128 bytes per step, one 16-byte chunk per thread.
     const int ar = tid >> 3, akc = (tid & 7) * 16;
@@ -2850,10 +2869,12 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     }
 
     uint4 areg;
+    float sreg = 0.0f;
     MStage<T> breg[2];
     auto fetch = [&](int st) {
         const int k0 = st * kGemmBK;
         areg = arow_ok && k0 + akc < a.K ? *(const uint4*)(aptr + k0) : make_uint4(0, 0, 0, 0);
+        if constexpr (kMin) sreg = tid < 128 && ps < p_end && k0 / 32 + sg < KG ? qsp[k0 / 32] : 0.0f;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int k = k0 + 32 * ((tid + 256 * i) % G);
@@ -2863,6 +2884,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     };
     auto store = [&](int buf) {
         *(uint4*)&As[buf][ar][akc] = areg;
+        if constexpr (kMin)
+            if (tid < 128) Ss[buf][sg][sr] = sreg;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int sl = tid + 256 * i, r = sl / G, g = sl % G;
@@ -2875,7 +2898,6 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
     const v16i zero = {};
-    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     const int wn = 32 * wave;
 
     fetch(0);
@@ -2906,12 +2928,19 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
                 const v16i P = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, zero, 0, 0, 0);
                 const float dl = Bd[buf][wn + li][g];
                 if constexpr (kMin) {
-                    const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, ones, zero, 0, 0, 0);
+                    // the activation rows' code sums of this group, staged
+                    // from the quantizer's output (no MFMA against ones)
                     const float ml = Bm[buf][wn + li][g];
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        acc[r] = fmaf(dl, (float)P[r], acc[r]);
-                        acc[r] = fmaf(-ml, (float)S[r], acc[r]);
+                    for (int j = 0; j < 4; j++) {
+                        const float4 sv = *(const float4*)&Ss[buf][g][8 * j + 4 * lk];
+                        const float sj[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int r = 4 * j + i;
+                            acc[r] = fmaf(dl, (float)P[r], acc[r]);
+                            acc[r] = fmaf(-ml, sj[i], acc[r]);
+                        }
                     }
                 } else {
 #pragma unroll
@@ -3276,6 +3305,8 @@ hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s) {
     a.tiles = (const int2*)g.tiles; a.n_tiles = g.n_tiles;
     a.C = g.C; a.C2 = g.C2; a.ldc = g.ldc;
     a.XH = (const _Float16*)g.XH; a.XL = (const _Float16*)g.XL; a.XS = g.XS; a.xs = g.xs;
+    a.QS = g.QS;
+    if (!g.XH && (type == T_Q4_K || type == T_Q5_K) && !g.QS) return hipErrorInvalidValue;
     const dim3 grid((g.N + kMoeBN - 1) / kMoeBN, g.max_tiles);
     if (g.max_tiles <= 0) return hipSuccess;
     if (g.XH) {  // fp32 rows as fp16 hi + lo

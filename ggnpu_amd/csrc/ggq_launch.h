@@ -25,8 +25,12 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
 // K and lda multiples of 4, A and aux 16-byte aligned, q dense [M][K].
 // prod_out (optional, dense [M][K], 16-byte aligned) receives the produced
 // fp32 rows that were quantized.
+// gsum (optional, [M][K/32], K a multiple of 32) receives the sums of each
+// row's codes per 32 values (the K-quant min term of the grouped GEMM);
+// producer 0 quantizes the rows as they are.
 hipError_t launch_produce_quant(int producer, const float* A, const float* aux, int lda, int M, int K, float eps,
-                                int8_t* q, float* scales, hipStream_t s, float* prod_out = nullptr);
+                                int8_t* q, float* scales, hipStream_t s, float* prod_out = nullptr,
+                                float* gsum = nullptr);
 
 // Decode GEMV with fp32 activations: Y[y_row][n] = sum_k X[x_row][k] W[n][k].
 // Plain mode: grp_off == null, rows 0..M-1.  Grouped mode (MoE): group g uses
@@ -185,6 +189,9 @@ struct MoeGemm {
     float* C;
     float* C2;
     int ldc;
+    // int8 codes: their sums per 32 values [rows][K/32] (needed for Q4_K /
+    // Q5_K, whose min term they feed)
+    const float* QS = nullptr;
     // fp32 activation rows (the fp16 hi + lo kernel) when XH is set: planes
     // from launch_split_rows (K a multiple of 64); QA / sa unused then.
     const void* XH = nullptr;

@@ -208,3 +208,38 @@ def test_i8_fused_unaligned_and_default_norm(ctx, orc):
         ref = _fused_ref(orc, dict(A=A, type=12, W=raw, N=N, K=K, rms=True, eps=1e-5,
                                    rms_w=None if norm is None else nw), M)
         assert orc.rel_l2(host(C), ref) < TOL
+
+
+def test_i8_gemv_f32_fixed_point_bound(ctx, orc, monkeypatch):
+    """The worst case of the fixed point that carries fp32 activations on
+    the int8 matrix cores: X = rint(x 2^e) with the row's largest magnitude
+    in [2^21, 2^22), so |x - X 2^-e| <= 2^-22 max|x| for every value and
+    |y_n - y_n(exact)| <= 2^-22 max|x| sum_k |w_nk| per output (plus fp32
+    rounding).  The case: one 1e4 outlier whose weight column is zero and
+    1e-3 values elsewhere, so the outputs rest entirely on values below the
+    fixed-point step; the int8 path stays within that bound (and, as the
+    bound allows, far from these small outputs).  The fp32 FMA kernel that
+    launches of this size take by default folds each block's code bias into
+    a run sum (a sum(x u) + b sum(x), Q8_0: b = -128 d), so its rounding is
+    relative to sum |x| (|w| + 128 d) over the row: the same case costs it
+    precision too, within that bound (2^-21 covers the two sums' roundings)."""
+    t, N, K, j = TYPES["Q8_0"], 64, 4096, 777
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w[:, j] = 0.0
+    raw = gl.encode(t, w)
+    x = (rng.standard_normal((1, K)) * 1e-3).astype(np.float32)
+    x[0, j] = 1e4
+    ref = orc.mul_mat_f64(t, raw, N, K, x, 0)
+    wd = orc.dequant(t, raw).reshape(N, K).astype(np.float64)
+    assert np.all(wd[:, j] == 0.0)
+    slack = 1e-6 * np.abs(ref[0])
+    bound_i8 = 2.0 ** -22 * 1e4 * np.abs(wd).sum(axis=1) + slack
+    got = run_mm(ctx, t, raw, N, K, x, 0)  # GGQ_I8_MIN_BYTES=0: the int8 matrix cores
+    assert np.all(np.abs(got[0] - ref[0]) <= bound_i8), np.max(np.abs(got[0] - ref[0]) / bound_i8)
+    scales = np.frombuffer(raw.reshape(N, K // 32, 34)[:, :, :2].tobytes(), dtype=np.float16).astype(np.float64)
+    bias = 128.0 * np.abs(np.repeat(scales.reshape(N, K // 32), 32, axis=1))
+    bound_fma = 2.0 ** -21 * (np.abs(x[0]).astype(np.float64) * (np.abs(wd) + bias)).sum(axis=1) + slack
+    monkeypatch.setenv("GGQ_I8_MIN_BYTES", str(16 << 20))  # the default: the fp32 FMA kernel
+    got = run_mm(ctx, t, raw, N, K, x, 0)
+    assert np.all(np.abs(got[0] - ref[0]) <= bound_fma), np.max(np.abs(got[0] - ref[0]) / bound_fma)
