@@ -605,7 +605,9 @@ def bench_config5(torch, ctx, stream, steps=20, T=64, act_mode=0):
     """one qwen35moe-A3B MoE FFN layer, 64 tokens (T), top-8 of
     256 experts (FFN 512, Q4_K gate/up, Q6_K down) + 1 shared expert, as one
     expert-grouped ggq_moe_ffn_act_dev call (act_mode 0: fp32 activations,
-    1: per-row int8 activations, the grouped int8 GEMM)."""
+    1: per-row int8 activations).  Up to 5 pair rows per expert on average
+    (64 tokens) the grouped GEMVs run, above it (512 tokens) the
+    expert-grouped GEMMs (fp16 hi + lo for fp32, int8 for per-row int8)."""
     H, F, E, k = 2048, 512, 256, 8
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
@@ -1133,6 +1135,7 @@ def main():
                 ("config4_iq4_q5k", bench_config4, cpu_baseline_config3),
                 ("config5_moe", bench_config5, cpu_baseline_config4),
                 ("config5_moe_q8_row", lambda t, c, st: bench_config5(t, c, st, act_mode=1), None),
+                ("config5_moe_512", lambda t, c, st: bench_config5(t, c, st, steps=10, T=512, act_mode=0), None),
                 ("config5_moe_512_q8_row", lambda t, c, st: bench_config5(t, c, st, steps=10, T=512, act_mode=1), None),
                 ("logits_argmax", bench_logits, None), ("attention_decode", bench_attention, None),
                 ("host_api_decode", bench_host_api, None), ("decode_fused", bench_decode_fused, None),
