@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -63,6 +64,8 @@ struct ggq_ctx {
     Buffer logits;  // vocab projection output when the caller does not keep it
     Buffer attn;  // attention chunk partials
     Buffer pin;   // pinned host staging of A and C for the synchronous host-pointer entry points
+    uint32_t* done = nullptr;  // pinned completion word of the synchronous entry points
+    uint32_t done_seq = 0;
     std::vector<void*> retired;  // outgrown device buffers, freed by ggq_destroy
     ggq_moe_trace trace{};       // intermediates of the last MoE call
     bool trace_rows = false;     // Q8_ROW MoE calls keep their fp32 SwiGLU rows
@@ -305,10 +308,36 @@ hipError_t ensure_pinned(Buffer& b, size_t need) {
     b.ptr = nullptr;
     b.size = 0;
     const size_t sz = need + need / 4 + 4096;
-    hipError_t e = hipHostMalloc(&b.ptr, sz, hipHostMallocDefault);
+    // coherent: the device's stores of C reach host memory without being
+    // held in its caches
+    hipError_t e = hipHostMalloc(&b.ptr, sz, hipHostMallocCoherent);
     if (e != hipSuccess) return e;
     b.size = sz;
     return hipSuccess;
+}
+
+// Waits for everything queued on the context's stream.  A one-lane kernel
+// queued last stores a sequence number into pinned memory, which the host
+// polls: at decode sizes a stream synchronization costs ~3 us more per
+// call (its wake-up).  After 200 us of polling the wait falls back to the
+// stream synchronization, which also reports a failed launch or fault.
+hipError_t wait_stream(ggq_ctx* c) {
+    hipError_t e;
+    if (!c->done) {
+        if ((e = hipHostMalloc((void**)&c->done, 256, hipHostMallocCoherent)) != hipSuccess) {
+            c->done = nullptr;
+            return e;
+        }
+        __atomic_store_n(c->done, 0u, __ATOMIC_RELAXED);
+    }
+    const uint32_t v = ++c->done_seq;
+    if ((e = ggq::launch_host_flag(c->done, v, c->stream)) != hipSuccess) return e;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0;; i++) {
+        if (__atomic_load_n(c->done, __ATOMIC_ACQUIRE) == v) return hipSuccess;
+        if ((i & 255) == 255 && std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(200)) break;
+    }
+    return hipStreamSynchronize(c->stream);
 }
 
 // Synchronous matmul with host A and C: the caller's rows are packed into a
@@ -337,7 +366,7 @@ int mul_mat_host(ggq_ctx* c, const ggq_weight* w, const float* A, int lda, float
     Arena ar{c, &c->host, nullptr, 0, c->stream};
     st = mul_mat_queue(c, ar, w->dev, w->type, w->N, w->K, dA, (int)w->K, hC, (int)w->N, M, act_mode, c->stream);
     if (st != GGQ_OK) return st;
-    if ((e = hipStreamSynchronize(c->stream)) != hipSuccess) return hip_status(c, e, "sync");
+    if ((e = wait_stream(c)) != hipSuccess) return hip_status(c, e, "sync");
     for (int m = 0; m < M; m++) memcpy(C + (size_t)m * ldc, hC + (size_t)m * w->N, sizeof(float) * w->N);
     return set_status(c, GGQ_OK);
 }
@@ -408,6 +437,7 @@ void ggq_destroy(ggq_ctx* c) {
     if (c->logits.ptr) hipFree(c->logits.ptr);
     if (c->attn.ptr) hipFree(c->attn.ptr);
     if (c->pin.ptr) hipHostFree(c->pin.ptr);
+    if (c->done) hipHostFree(c->done);
     hipStreamDestroy(c->stream);
     delete c;
 }

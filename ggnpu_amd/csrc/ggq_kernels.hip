@@ -3492,6 +3492,18 @@ hipError_t launch_copy_bytes(void* dst, const void* src, size_t n, hipStream_t s
     return hipGetLastError();
 }
 
+// Completion word for a host that waits by polling pinned memory instead of
+// a stream synchronization: one lane stores v with a system-scope release
+// after everything queued before it on the stream has finished.
+__global__ __launch_bounds__(64) void host_flag_kernel(uint32_t* flag, uint32_t v) {
+    if (threadIdx.x == 0) __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+hipError_t launch_host_flag(uint32_t* flag, uint32_t v, hipStream_t s) {
+    host_flag_kernel<<<1, 64, 0, s>>>(flag, v);
+    return hipGetLastError();
+}
+
 // x_eff[m][k] = q[m][k] * scale[m] (fp32) from pre-quantized activations.
 __global__ __launch_bounds__(256) void dequant_act_kernel(const int8_t* __restrict__ q, const float* __restrict__ sa,
                                                           int M, int K, float* __restrict__ x) {

@@ -152,6 +152,7 @@ hipError_t launch_attn_decode(const float* Q, const float* K, const float* V, in
                               int head_dim, int64_t ctx_len, int64_t pos0, float* out, float* ws, hipStream_t s);
 // n-byte copy by a kernel (either end may be pinned host memory).
 hipError_t launch_copy_bytes(void* dst, const void* src, size_t n, hipStream_t s);
+hipError_t launch_host_flag(uint32_t* flag, uint32_t v, hipStream_t s);
 // x[m][k] = q[m][k] * sa[m] (dense fp32 [M][K]).
 hipError_t launch_dequant_act(const int8_t* q, const float* sa, int M, int K, float* x, hipStream_t s);
 
