@@ -861,8 +861,8 @@ int ggq_block_dot_dev(ggq_ctx* c, const void* W, uint32_t type, int64_t N, int64
 // decoded to int8 codes, about a third of the VALU work per weight of the
 // fp16 matrix-core GEMV), else on the matrix-core / FMA GEMV.  The down
 // projection's groups would run in passes of 1-2 rows there, each
-// re-reading the expert's weights (measured slower), so down stays on the
-// GEMV.
+// re-reading the expert's weights (measured slower): down takes the
+// expert-grouped row tiles (Q6_K) or the GEMV.
 static hipError_t moe_grouped_gemv(const ggq::GemvProblem& g, void* items, size_t items_bytes, hipStream_t s,
                                    bool down = false, const ggq::I8Shared* sh = nullptr, bool* took_shared = nullptr,
                                    bool list_ready = false) {
@@ -1229,8 +1229,18 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     // down: rows H, K = F, activations are the sorted pair rows themselves.
     g.N = H; g.K = F; g.X = Hh; g.ldx = F; g.x_idx = nullptr; g.ldy = H; g.Y = D;
     g.type = p->down_type; g.W = p->down_exps; g.w_group_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
-    if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s, true)) != hipSuccess) return hip_status(c, e, "moe down");
-    if (shared) {
+    // Q6_K down: expert-grouped row tiles on the int8 matrix cores (each
+    // expert's weights decoded once per 4 of its rows), the shared expert as
+    // one more group of the same launch.
+    const bool tiles = ggq::i8_tile_grouped_eligible(p->down_type, H, F, E, g.w_group_stride, shared) && F % 4 == 0;
+    if (tiles) {
+        if ((e = ggq::launch_i8_tile_grouped(p->down_type, p->down_exps, g.w_group_stride, shared ? p->down_shexp : nullptr,
+                                             Hh, F, grp, E, shared ? T : 0, D, Dsh, H, H, F, s)) != hipSuccess)
+            return hip_status(c, e, "moe down");
+    } else if ((e = moe_grouped_gemv(g, base + o_it, it_bytes, s, true)) != hipSuccess) {
+        return hip_status(c, e, "moe down");
+    }
+    if (shared && !tiles) {
         q.N = H; q.K = F; q.X = Hh + nk * F; q.ldx = F; q.ldy = H; q.type = p->down_type; q.W = p->down_shexp; q.Y = Dsh;
         if ((e = ggq::launch_gemv(q, s)) != hipSuccess) return hip_status(c, e, "shared down");
     }

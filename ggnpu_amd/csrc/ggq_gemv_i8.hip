@@ -1436,4 +1436,402 @@ hipError_t launch_i8_moe_q8(uint32_t type, const MoeGemm& g, int rows, void* ws,
     }
 }
 
+namespace {
+
+// ============================================ expert-grouped row tiles
+// The down projection of a MoE layer at decode-sized batches (a few pair
+// rows per expert), fp32 activations: a unit of work is 128 weight rows
+// (a row tile) of one group (expert, or the shared expert) times up to 4 of
+// the group's activation rows (a pass) on v_mfma_i32_32x32x32_i8, so the
+// weight codes are decoded once per 4 rows.  The units are spread evenly
+// over a grid of resident workgroups.
+//
+// MFMA layout (32 x 32 x 32, int8): lane l supplies row / column l % 32 of
+// A / B for K-slice 16 (l / 32) .. + 16, and holds output rows 8 (r / 4) +
+// 4 (l / 32) + r % 4 (register r) of column l % 32.  B column c is weight
+// row n0 + c; K-step j covers values 32 j .. 32 j + 31, lane half h values
+// 32 j + 16 h + [0, 16): one Q6_K 16-value scale group.  Activation rows
+// are fixed point X = rint(x 2^e) with the row's largest magnitude in
+// [2^29, 2^30), written as four signed int8 digits (X = sum_d digit_d
+// 256^d), so |x - 2^-e X| <= 2^-30 of the row maximum.  A row 8 m + 4 s + d
+// holds digit d of activation row m in lane half s and zeros in the other
+// half; so output lane (c, h) finds in registers 4 m + d the digit-d dot
+// products of row m with its own 16 codes (scale group sc[.., h]), and
+// accumulates sc * C in int32 per Q6_K block (exact: |C| <= 2^16,
+// |sc * C| <= 2^23, 8 K-steps), then d_block * sum_d I_d 256^d in fp32.
+// Codes are taken signed (q - 32), so no offset term remains.  The two lane
+// halves' sums are added at the end and scaled by 2^-e.
+constexpr int kTileRows = 128;   // weight rows per workgroup (4 wavefronts x 32)
+constexpr int kTileMR = 4;       // activation rows per pass
+constexpr int kTileMaxK = 1024;  // K limit: a pass's digit planes take 16 K bytes of LDS (two buffers)
+constexpr int kTilePre = 4160;   // LDS bytes of the unit prefix (up to 1024 groups + 1)
+
+struct I8TileArgs {
+    const uint8_t* W;  // group g's matrix at W + g * w_stride
+    int64_t w_stride;
+    const uint8_t* Wsh;  // group E (optional): the shared expert
+    const float* X;      // activation rows, grouped: group g's rows grp_off[g] .. grp_off[g+1]-1
+    int ldx;
+    const int32_t* grp_off;
+    int E, t_sh;  // routed groups; rows of the shared group (grp_off[E] ..)
+    float* Y;     // output rows, as X's
+    float* Ysh;   // the shared group's output rows (from 0)
+    int ldy;
+    int N, K;
+    uint32_t row_bytes;
+    int groups;  // E, plus the shared group
+};
+
+// Q6_K block (kquant.h:182-202) of one lane: for half nh, ql[64 nh + 16 h]
+// (values 128 nh + 16 h + i, low nibbles; + 64, high nibbles), ql[64 nh +
+// 32 + 16 h] (+ 32 / + 96) and qh[32 nh + 16 h] (2-bit fields 0, 2, 4, 6 for
+// + 0, + 32, + 64, + 96); scales sc[8 nh + 2 t + h] for K-step t of the
+// half; d at 208.
+struct TileQ6 {
+    v4u ql0[2], ql1[2], qh[2], sc;
+    uint32_t d;
+};
+// (d and the scales are loaded first: loads complete in issue order, so
+// waiting for the first codes covers them)
+__device__ __forceinline__ TileQ6 tile_q6_fetch(Rsrc rs, uint32_t off, int h) {
+    TileQ6 r;
+    r.d = bl2(rs, off + 208);
+    r.sc = bl16(rs, off + 192);
+#pragma unroll
+    for (int nh = 0; nh < 2; nh++) {
+        r.ql0[nh] = bl16(rs, off + 64 * nh + 16 * h);
+        r.ql1[nh] = bl16(rs, off + 64 * nh + 32 + 16 * h);
+        r.qh[nh] = bl16(rs, off + 128 + 32 * nh + 16 * h);
+    }
+    return r;
+}
+// Signed codes q - 32 of K-step t of half nh: low 4 bits from ql, the top
+// two (hh) as the 4-bit two's complement of hh - 2 in bits 4..7.
+__device__ __forceinline__ uint32_t q6_signed(uint32_t ql, uint32_t qh, int t) {
+    const uint32_t lo = (t >> 1) ? (ql >> 4) & 0x0F0F0F0Fu : ql & 0x0F0F0F0Fu;
+    const uint32_t hh = (qh >> (2 * t)) & 0x03030303u;
+    return lo | (((hh + 0x0E0E0E0Eu) & 0x0F0F0F0Fu) << 4);
+}
+__device__ __forceinline__ v4i tile_q6_codes(const TileQ6& r, int nh, int t) {
+    const v4u ql = (t & 1) ? r.ql1[nh] : r.ql0[nh];
+    const v4u qh = r.qh[nh];
+    v4i c;
+    c.x = (int)q6_signed(ql.x, qh.x, t); c.y = (int)q6_signed(ql.y, qh.y, t);
+    c.z = (int)q6_signed(ql.z, qh.z, t); c.w = (int)q6_signed(ql.w, qh.w, t);
+    return c;
+}
+__device__ __forceinline__ int tile_q6_scale(const TileQ6& r, int nh, int t, int h) {
+    const int i = 2 * nh + (t >> 1);
+    const uint32_t w = i == 0 ? r.sc.x : i == 1 ? r.sc.y : i == 2 ? r.sc.z : r.sc.w;
+    return __builtin_amdgcn_sbfe((int)w, 16 * (t & 1) + 8 * h, 8);
+}
+
+// Work units (group g, pass of up to 4 of its rows, row tile), ordered
+// group-major, are split evenly over a resident grid; each workgroup
+// streams its units' weight blocks with loads two blocks ahead across unit
+// boundaries, and rebuilds the activation planes (double-buffered, one
+// barrier) when the unit's (group, pass) changes.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i8_tile_grouped_kernel(I8TileArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31, h = lane >> 5;
+    const int NB = a.K >> 8, NJ = a.K >> 5, G = a.groups;
+    const int ntiles = (a.N + kTileRows - 1) / kTileRows;
+    // LDS: unit prefix [G + 1], two plane buffers [m][d][j][half] (16 B
+    // entries), a zero plane [j][half], the rows' exponents [2][4], the
+    // scan's wavefront totals
+    int* pre = (int*)lds;
+    const int PB = kTileMR * 4 * NJ * 32;
+    uint8_t* planes = lds + kTilePre;
+    uint8_t* zero = planes + 2 * PB;
+    int* lexp = (int*)(zero + NJ * 32);
+    int* wsum = lexp + 2 * kTileMR;
+    for (int i = tid; i < NJ * 2; i += 256) ((uint4*)zero)[i] = make_uint4(0u, 0u, 0u, 0u);
+    auto group_rows = [&](int g, int& r0) __attribute__((always_inline)) {
+        if (g == a.E) {
+            r0 = a.grp_off[a.E];
+            return a.t_sh;
+        }
+        r0 = a.grp_off[g];
+        return a.grp_off[g + 1] - r0;
+    };
+    // units per group, exclusive prefix over the workgroup (4 groups per
+    // thread, G <= 1024)
+    {
+        int cnt[4], tsum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int g = 4 * tid + i;
+            int r0 = 0;
+            const int rows = g < G ? group_rows(g, r0) : 0;
+            cnt[i] = (rows + kTileMR - 1) / kTileMR * ntiles;
+            tsum += cnt[i];
+        }
+        int x = tsum;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        if (lane == 63) wsum[w] = x;
+        __syncthreads();
+        int ex = x - tsum;
+        for (int k = 0; k < w; k++) ex += wsum[k];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int g = 4 * tid + i;
+            if (g <= G) pre[g] = ex;
+            ex += cnt[i];
+        }
+        __syncthreads();
+    }
+    // (values read from LDS are uniform: kept in scalar registers, so the
+    // buffer resource chosen from them needs no per-lane loop)
+    auto upre = [&](int g) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(pre[g]); };
+    const int U = upre(G);
+    const int u0 = (int)((int64_t)U * blockIdx.x / gridDim.x), u1 = (int)((int64_t)U * (blockIdx.x + 1) / gridDim.x);
+    if (u0 >= u1) return;
+    // the group of unit u: the last g with pre[g] <= u (groups without units
+    // have pre[g] == pre[g + 1])
+    auto group_of = [&](int u) __attribute__((always_inline)) {
+        int lo = 0, hi = G - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (upre(mid) <= u) lo = mid;
+            else hi = mid - 1;
+        }
+        return lo;
+    };
+    const Rsrc rs_r = make_rsrc(a.W, (uint32_t)(a.E >= 0 ? a.E : G) * (uint32_t)a.w_stride);
+    const Rsrc rs_s = make_rsrc(a.Wsh ? a.Wsh : a.W, (uint32_t)a.N * a.row_bytes);
+    // Unit cursors (group, unit index within it, the group's unit count),
+    // advanced one unit at a time: the fetch cursor runs one unit ahead of
+    // the compute cursor.
+    struct UCur { int g, local, end; };
+    auto ucur_next = [&](UCur& c) __attribute__((always_inline)) {
+        if (++c.local >= c.end) {
+            do {
+                ++c.g;
+            } while (c.g < G && upre(c.g + 1) == upre(c.g));
+            c.local = 0;
+            c.end = c.g < G ? upre(c.g + 1) - upre(c.g) : 0;
+        }
+    };
+    UCur fc;
+    fc.g = group_of(u0);
+    fc.local = u0 - upre(fc.g);
+    fc.end = upre(fc.g + 1) - upre(fc.g);
+    UCur cc = fc;
+    const int n_pos = (u1 - u0) * NB;
+    int fq = 0, fb = 0;
+    // the next position's weights (this lane's row of the unit's tile,
+    // block fb); out of range past the last position
+    auto fetch = [&]() __attribute__((always_inline)) {
+        uint32_t off = kOOB;
+        bool sh = false;
+        if (fq < n_pos) {
+            const int n = (fc.local % ntiles) * kTileRows + w * 32 + col;
+            sh = fc.g == a.E;
+            off = (sh ? 0u : (uint32_t)fc.g * (uint32_t)a.w_stride) + (uint32_t)(n < a.N ? n : a.N - 1) * a.row_bytes +
+                  (uint32_t)fb * 210u;
+            if (++fb == NB) {
+                fb = 0;
+                ucur_next(fc);
+            }
+            fq++;
+        }
+        // (the matrix choice is uniform: one resource, no per-lane loop)
+        return tile_q6_fetch(__builtin_amdgcn_readfirstlane((int)sh) ? rs_s : rs_r, off, h);
+    };
+    const int rho = lane & 31, m_l = rho >> 3, s_l = (rho >> 2) & 1, d_l = rho & 3;
+
+    TileQ6 ra = fetch();
+    TileQ6 rb = fetch();
+    int buf = 1, mc = 0, r0 = 0, gr0 = 0;
+    uint32_t abase = 0;
+    int es[kTileMR];
+    float acc[kTileMR];
+    int tile = 0;
+    bool shg = false;
+    // unit start: its group, pass and tile; new planes when (group, pass)
+    // changes
+    // a segment: the units of one (group, pass) in this workgroup's range;
+    // its activation planes are built once (set-up loads drain the load
+    // queue, so they stay out of the streaming loop)
+    auto start_segment = [&]() __attribute__((always_inline)) {
+        const int g = __builtin_amdgcn_readfirstlane(cc.g), local = __builtin_amdgcn_readfirstlane(cc.local);
+        const int pass = local / ntiles;
+        tile = local % ntiles;
+        shg = g == a.E;
+        const int rows = group_rows(g, gr0);
+        r0 = gr0 + kTileMR * pass;
+        mc = rows - kTileMR * pass < kTileMR ? rows - kTileMR * pass : kTileMR;
+        buf ^= 1;
+        uint8_t* pl = planes + buf * PB;
+        // wavefront w writes activation row r0 + w
+        constexpr int KV = kTileMaxK / 512;
+        float4 v[KV][2];
+        const float* xr = a.X + (int64_t)(r0 + (w < mc ? w : 0)) * a.ldx;
+#pragma unroll
+        for (int i = 0; i < KV; i++) {
+            const int k0 = 8 * lane + 512 * i;
+            const int kc = k0 < a.K ? k0 : 0;
+            v[i][0] = *(const float4*)(xr + kc);
+            v[i][1] = *(const float4*)(xr + kc + 4);
+        }
+        if (w < mc) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < KV; i++) {
+                if (8 * lane + 512 * i >= a.K) v[i][0] = v[i][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i][0].x), fabsf(v[i][0].y)), fmaxf(fabsf(v[i][0].z), fabsf(v[i][0].w))));
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i][1].x), fabsf(v[i][1].y)), fmaxf(fabsf(v[i][1].z), fabsf(v[i][1].w))));
+            }
+            mx = wave_max(mx);
+            int Ex = 0;
+            frexpf(mx, &Ex);
+            const int e = mx > 0.0f ? 30 - Ex : 0;
+            auto fx = [&](float x) __attribute__((always_inline)) {
+                return (uint32_t)(int)__builtin_rintf(ldexpf(x, e)) + 0x80808080u;
+            };
+#pragma unroll
+            for (int i = 0; i < KV; i++) {
+                const int k0 = 8 * lane + 512 * i;
+                if (k0 >= a.K) continue;
+                uint32_t p[2][4];
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++) {
+                    const uint32_t x0 = fx(v[i][qq].x), x1 = fx(v[i][qq].y), x2 = fx(v[i][qq].z), x3 = fx(v[i][qq].w);
+                    const uint32_t lo01 = __builtin_amdgcn_perm(x1, x0, 0x05010400u), hi01 = __builtin_amdgcn_perm(x1, x0, 0x07030602u);
+                    const uint32_t lo23 = __builtin_amdgcn_perm(x3, x2, 0x05010400u), hi23 = __builtin_amdgcn_perm(x3, x2, 0x07030602u);
+                    p[qq][0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+                    p[qq][1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+                    p[qq][2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+                    p[qq][3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u) ^ 0x80808080u;
+                }
+                const int j = k0 >> 5, hh = (k0 >> 4) & 1;
+#pragma unroll
+                for (int d = 0; d < 4; d++)
+                    *(uint2*)(pl + (((w * 4 + d) * NJ + j) * 2 + hh) * 16 + (k0 & 8)) = make_uint2(p[0][d], p[1][d]);
+            }
+            if (lane == 0) lexp[buf * kTileMR + w] = e;
+        }
+        // (the other buffer was last read before the previous set-up's
+        // barrier: one barrier per set-up)
+        __syncthreads();
+        const bool act = s_l == h && m_l < mc;
+        abase = act ? (uint32_t)(buf * PB + (((m_l * 4 + d_l) * NJ) * 2 + h) * 16)
+                    : (uint32_t)(2 * PB + h * 16);
+#pragma unroll
+        for (int m = 0; m < kTileMR; m++) es[m] = lexp[buf * kTileMR + m];
+    };
+    auto block = [&](const TileQ6& r, int b) __attribute__((always_inline)) {
+        const float dd = h2f(r.d & 0xFFFFu);
+        int I[kTileMR][4];
+#pragma unroll
+        for (int m = 0; m < kTileMR; m++)
+#pragma unroll
+            for (int d = 0; d < 4; d++) I[m][d] = 0;
+#pragma unroll
+        for (int nh = 0; nh < 2; nh++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int j = 8 * b + 4 * nh + t;
+                const v4i A = *(const v4i*)(planes + abase + (uint32_t)j * 32u);
+                const v4i B = tile_q6_codes(r, nh, t);
+                typedef int v16i __attribute__((ext_vector_type(16)));
+                const v16i Z = {};
+                const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, Z, 0, 0, 0);
+                const int sc = tile_q6_scale(r, nh, t, h);
+#pragma unroll
+                for (int m = 0; m < kTileMR; m++)
+                    if (m < mc) {  // (uniform)
+#pragma unroll
+                        for (int d = 0; d < 4; d++) I[m][d] += __mul24(sc, C[4 * m + d]);
+                    }
+                // one K-step's results live at a time (other wavefronts
+                // cover the MFMA latency): the sums are formed here
+#pragma unroll
+                for (int m = 0; m < kTileMR; m++)
+                    asm volatile("" : "+v"(I[m][0]), "+v"(I[m][1]), "+v"(I[m][2]), "+v"(I[m][3]));
+            }
+#pragma unroll
+        for (int m = 0; m < kTileMR; m++) {
+            const float P = fmaf(fmaf(fmaf((float)I[m][3], 256.0f, (float)I[m][2]), 256.0f, (float)I[m][1]), 256.0f,
+                                 (float)I[m][0]);
+            acc[m] = fmaf(dd, P, acc[m]);
+        }
+    };
+    auto finish = [&]() __attribute__((always_inline)) {
+        // the two halves' scale groups, then the row's 2^-e
+        const int n = tile * kTileRows + w * 32 + col;
+#pragma unroll
+        for (int m = 0; m < kTileMR; m++) {
+            const float v = acc[m] + __shfl_xor(acc[m], 32, 64);
+            if (m < mc && h == 0 && n < a.N) {
+                const int r = r0 + m;
+                float* y = shg ? a.Ysh + (int64_t)(r - gr0) * a.ldy : a.Y + (int64_t)r * a.ldy;
+                y[n] = ldexpf(v, -es[m]);
+            }
+        }
+    };
+    int q = 0;
+#define GGQ_TILE_STEP(R)                                                           \
+    {                                                                              \
+        const int b = q % NB;                                                      \
+        if (b == 0) {                                                              \
+            _Pragma("unroll") for (int m = 0; m < kTileMR; m++) acc[m] = 0.0f;     \
+        }                                                                          \
+        block(R, b);                                                               \
+        R = fetch();                                                               \
+        if (b == NB - 1) {                                                         \
+            finish();                                                              \
+            tile++;                                                                \
+            ucur_next(cc);                                                         \
+        }                                                                          \
+        if (++q >= seg_end) break;                                                 \
+    }
+    while (q < n_pos) {
+        start_segment();
+        // units left in this pass of the group, within the range
+        const int seg_units = min(ntiles - tile, u1 - u0 - q / NB);
+        const int seg_end = q + seg_units * NB;
+        // position q is in ra when q is even, in rb when odd
+        if (q & 1) {
+            do GGQ_TILE_STEP(rb) while (false);
+            if (q >= seg_end) continue;
+        }
+        while (true) {
+            GGQ_TILE_STEP(ra)
+            GGQ_TILE_STEP(rb)
+        }
+    }
+#undef GGQ_TILE_STEP
+}
+
+}  // namespace
+
+bool i8_tile_grouped_eligible(uint32_t type, int N, int K, int E, int64_t w_stride, bool shared) {
+    if (type != T_Q6_K || K % 256 != 0 || K <= 0 || K > kTileMaxK || N <= 0 || E < 1 || E + (shared ? 1 : 0) > 1023)
+        return false;
+    // one buffer resource over the routed matrices: offsets below kOOB
+    return w_stride >= (int64_t)N * row_bytes(type, K) && (int64_t)E * w_stride < (int64_t)kOOB;
+}
+
+hipError_t launch_i8_tile_grouped(uint32_t type, const void* W, int64_t w_stride, const void* Wsh, const float* X,
+                                  int ldx, const int32_t* grp_off, int E, int t_sh, float* Y, float* Ysh, int ldy,
+                                  int N, int K, hipStream_t s) {
+    const int groups = E + (Wsh && t_sh > 0 ? 1 : 0);
+    if (!i8_tile_grouped_eligible(type, N, K, E, w_stride, Wsh && t_sh > 0) || ldx % 4 != 0 || ((uintptr_t)X & 15u) != 0)
+        return hipErrorInvalidValue;
+    I8TileArgs a{(const uint8_t*)W, w_stride, (const uint8_t*)Wsh, X, ldx, grp_off, Wsh && t_sh > 0 ? E : -1, t_sh,
+                 Y, Ysh, ldy, N, K, (uint32_t)row_bytes(type, K), groups};
+    const int lds = kTilePre + 2 * kTileMR * 4 * K + K + 4 * (2 * kTileMR + 4);
+    // resident grid: 3 workgroups per CU (the kernel's register budget)
+    const dim3 grid((unsigned)(3 * cu_count()));
+    i8_tile_grouped_kernel<<<grid, 256, lds, s>>>(a);
+    return hipGetLastError();
+}
+
 }  // namespace ggq

@@ -106,6 +106,14 @@ hipError_t launch_i8_gemv_grouped(const GemvProblem& g, void* ws, hipStream_t s,
 // The chunk list that launch would use in `ws` (mt 0 when the plan fails), for
 // launch_moe_group to build ahead of it (then list_ready = true).
 ChunkList i8_gemv_grouped_list(const GemvProblem& g, void* ws, int t_sh);
+// Expert-grouped row tiles on the int8 matrix cores (fp32 activation rows,
+// 4 per pass; Q6_K, K <= 2048): Y rows grp_off[g] .. grp_off[g+1]-1 = X rows
+// times group g's matrix (W + g * w_stride); with Wsh, group E is the shared
+// expert (X rows grp_off[E] .. + t_sh, outputs Ysh from row 0).
+bool i8_tile_grouped_eligible(uint32_t type, int N, int K, int E, int64_t w_stride, bool shared);
+hipError_t launch_i8_tile_grouped(uint32_t type, const void* W, int64_t w_stride, const void* Wsh, const float* X,
+                                  int ldx, const int32_t* grp_off, int E, int t_sh, float* Y, float* Ysh, int ldy,
+                                  int N, int K, hipStream_t s);
 // Largest K the register-resident GEMV supports.
 constexpr int kGemvMaxK = 32768;
 

@@ -86,7 +86,7 @@ def per_row_err(got, ref):
     return num / np.where(den > 0, den, 1.0)
 
 
-def run_layer(ctx, T, H, F, E, k, types, act_mode, seed, shared=True):
+def run_layer(ctx, T, H, F, E, k, types, act_mode, seed, shared=True, hot=0):
     import torch
     tg, tu, td = types
     rng = np.random.default_rng(seed)
@@ -102,6 +102,8 @@ def run_layer(ctx, T, H, F, E, k, types, act_mode, seed, shared=True):
         sw = (1.0 / (1.0 + np.exp(-rng.standard_normal(T)))).astype(np.float32)
     x = rng.standard_normal((T, H)).astype(np.float32)
     logits = rng.standard_normal((T, E)).astype(np.float32)
+    if hot:  # the first `hot` experts take most tokens
+        logits[:, :hot] += 3.0
     keep = [dev(a) for a in (x, logits, Wg, Wu, Wd)] + [dev(a) if a is not None else None for a in (*S, sw)]
     out = empty((T, H), torch.float32)
     sel = empty((T, k), torch.int32)
@@ -266,3 +268,20 @@ def test_moe_stages_many_experts_shared(ctx, orc, monkeypatch, E, act_mode):
     assert np.array_equal(L["sel"], rsel)
     if act_mode == 0:
         assert orc.rel_l2(L["out"], ref) < TOL
+
+
+@pytest.mark.parametrize("H,F,types", [(2048, 512, (Q4K, Q4K, Q6K)), (1024, 256, (Q4K, Q4K, Q6K)),
+                                       (1024, 768, (Q4K, Q4K, Q6K)), (1024, 1024, (Q4K, Q4K, Q6K)),
+                                       (1056, 512, (8, 8, Q6K))])
+def test_moe_stages_f32_down_row_tiles(ctx, orc, H, F, types):
+    """fp32 MoE at decode-sized batches with a Q6_K down projection, which
+    runs on the expert-grouped row tiles (4 pair rows per pass): K = F of
+    1, 2, 3 and 4 Q6_K blocks, N = H a multiple of the 128-row tile or not
+    (1056), and routing skewed so that a few experts take many rows (several
+    passes over their weights) next to experts with none, plus the shared
+    expert's rows (8 passes); every stage of every expert."""
+    T, E, k = 32, 32, 4
+    L = run_layer(ctx, T, H, F, E, k, types, 0, seed=H + F, hot=3)
+    grp = d2h(L["tr"].grp, (E + 1,), np.int32)
+    assert np.diff(grp).max() > 8 and (np.diff(grp) == 0).any()
+    check_stages(orc, L, T, H, F, E, k, types, 0)
