@@ -1526,6 +1526,42 @@ __device__ __forceinline__ int tile_q6_scale(const TileQ6& r, int nh, int t, int
     return __builtin_amdgcn_sbfe((int)w, 16 * (t & 1) + 8 * h, 8);
 }
 
+// A wavefront's 32 rows of one Q6_K block, loaded coalesced: bytes 0..207
+// of each row as 13 16-byte pieces, chunk c = lane + 64 i (c < 416) being
+// piece c % 13 of row c / 13, staged in LDS at 240 bytes a row (stride 60
+// dwords: the 16-byte reads of 8 consecutive lanes fall in distinct banks)
+// and read back per lane; d (bytes 208..209) is loaded by each lane for its
+// own row (a 16-byte piece there would reach past the end of the matrix).
+constexpr int kTileStageRow = 240;
+constexpr int kTileStage = 32 * kTileStageRow;  // LDS bytes per wavefront
+struct TileRaw {
+    v4u c[7];
+    uint32_t d;
+};
+__device__ __forceinline__ TileRaw tile_raw_fetch(Rsrc rs, const uint32_t (&off)[7], uint32_t doff) {
+    TileRaw r;
+    r.d = bl2(rs, doff);
+#pragma unroll
+    for (int i = 0; i < 7; i++) r.c[i] = bl16(rs, off[i]);
+    return r;
+}
+__device__ __forceinline__ TileQ6 tile_q6_stage(const TileRaw& r, uint8_t* st, const uint32_t (&soff)[7], int col, int h) {
+#pragma unroll
+    for (int i = 0; i < 7; i++)
+        if (i < 6 || soff[i] != ~0u) *(v4u*)(st + soff[i]) = r.c[i];
+    const uint8_t* row = st + col * kTileStageRow;
+    TileQ6 q;
+#pragma unroll
+    for (int nh = 0; nh < 2; nh++) {
+        q.ql0[nh] = *(const v4u*)(row + 64 * nh + 16 * h);
+        q.ql1[nh] = *(const v4u*)(row + 64 * nh + 32 + 16 * h);
+        q.qh[nh] = *(const v4u*)(row + 128 + 32 * nh + 16 * h);
+    }
+    q.sc = *(const v4u*)(row + 192);
+    q.d = r.d;
+    return q;
+}
+
 // Work units (group g, pass of up to 4 of its rows, row tile), ordered
 // group-major, are split evenly over a resident grid; each workgroup
 // streams its units' weight blocks with loads two blocks ahead across unit
@@ -1547,6 +1583,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
     uint8_t* zero = planes + 2 * PB;
     int* lexp = (int*)(zero + NJ * 32);
     int* wsum = lexp + 2 * kTileMR;
+    uint8_t* stage = lds + kTilePre + 2 * PB + NJ * 32 + 64 + w * kTileStage;
     for (int i = tid; i < NJ * 2; i += 256) ((uint4*)zero)[i] = make_uint4(0u, 0u, 0u, 0u);
     auto group_rows = [&](int g, int& r0) __attribute__((always_inline)) {
         if (g == a.E) {
@@ -1625,29 +1662,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
     UCur cc = fc;
     const int n_pos = (u1 - u0) * NB;
     int fq = 0, fb = 0;
-    // the next position's weights (this lane's row of the unit's tile,
+    // this lane's pieces: chunk c = lane + 64 i is piece c % 14 of row c / 14
+    // of the wavefront's 32; its LDS staging offset
+    uint32_t soff[7], poff[7];
+    int prow[7];
+#pragma unroll
+    for (int i = 0; i < 7; i++) {
+        const int c = lane + 64 * i;
+        prow[i] = c < 416 ? c / 13 : 0;
+        poff[i] = 16u * (uint32_t)(c % 13);
+        soff[i] = c < 416 ? (uint32_t)(prow[i] * kTileStageRow) + poff[i] : ~0u;
+    }
+    // the next position's block (the wavefront's rows of the unit's tile,
     // block fb); out of range past the last position
     auto fetch = [&]() __attribute__((always_inline)) {
-        uint32_t off = kOOB;
+        uint32_t roff[7], doff = kOOB;
         bool sh = false;
         if (fq < n_pos) {
-            const int n = (fc.local % ntiles) * kTileRows + w * 32 + col;
+            const int n0 = (fc.local % ntiles) * kTileRows + w * 32;
             sh = fc.g == a.E;
-            off = (sh ? 0u : (uint32_t)fc.g * (uint32_t)a.w_stride) + (uint32_t)(n < a.N ? n : a.N - 1) * a.row_bytes +
-                  (uint32_t)fb * 210u;
+            const uint32_t base = (sh ? 0u : (uint32_t)fc.g * (uint32_t)a.w_stride) + (uint32_t)fb * 210u;
+#pragma unroll
+            for (int i = 0; i < 7; i++) {
+                const int n = n0 + prow[i];
+                roff[i] = i == 6 && soff[i] == ~0u ? kOOB : base + (uint32_t)(n < a.N ? n : a.N - 1) * a.row_bytes + poff[i];
+            }
+            const int nd = n0 + col;
+            doff = base + (uint32_t)(nd < a.N ? nd : a.N - 1) * a.row_bytes + 208u;
             if (++fb == NB) {
                 fb = 0;
                 ucur_next(fc);
             }
             fq++;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 7; i++) roff[i] = kOOB;
         }
         // (the matrix choice is uniform: one resource, no per-lane loop)
-        return tile_q6_fetch(__builtin_amdgcn_readfirstlane((int)sh) ? rs_s : rs_r, off, h);
+        return tile_raw_fetch(__builtin_amdgcn_readfirstlane((int)sh) ? rs_s : rs_r, roff, doff);
     };
     const int rho = lane & 31, m_l = rho >> 3, s_l = (rho >> 2) & 1, d_l = rho & 3;
 
-    TileQ6 ra = fetch();
-    TileQ6 rb = fetch();
+    TileRaw ra = fetch();
+    TileRaw rb = fetch();
     int buf = 1, mc = 0, r0 = 0, gr0 = 0;
     uint32_t abase = 0;
     int es[kTileMR];
@@ -1783,7 +1840,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
         if (b == 0) {                                                              \
             _Pragma("unroll") for (int m = 0; m < kTileMR; m++) acc[m] = 0.0f;     \
         }                                                                          \
-        block(R, b);                                                               \
+        block(tile_q6_stage(R, stage, soff, col, h), b);                           \
         R = fetch();                                                               \
         if (b == NB - 1) {                                                         \
             finish();                                                              \
@@ -1827,9 +1884,15 @@ hipError_t launch_i8_tile_grouped(uint32_t type, const void* W, int64_t w_stride
         return hipErrorInvalidValue;
     I8TileArgs a{(const uint8_t*)W, w_stride, (const uint8_t*)Wsh, X, ldx, grp_off, Wsh && t_sh > 0 ? E : -1, t_sh,
                  Y, Ysh, ldy, N, K, (uint32_t)row_bytes(type, K), groups};
-    const int lds = kTilePre + 2 * kTileMR * 4 * K + K + 4 * (2 * kTileMR + 4);
-    // resident grid: 3 workgroups per CU (the kernel's register budget)
-    const dim3 grid((unsigned)(3 * cu_count()));
+    const int lds = kTilePre + 2 * kTileMR * 4 * K + K + 64 + 4 * kTileStage;
+    // resident grid: 3 workgroups per CU (the kernel's register budget),
+    // fewer when their LDS does not fit (160 KB per CU)
+    int per_cu = (160 * 1024) / lds;
+    per_cu = per_cu > 3 ? 3 : per_cu < 1 ? 1 : per_cu;
+    const dim3 grid((unsigned)(per_cu * cu_count()));
+    static const hipError_t attr = hipFuncSetAttribute((const void*)i8_tile_grouped_kernel,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    if (attr != hipSuccess) return attr;
     i8_tile_grouped_kernel<<<grid, 256, lds, s>>>(a);
     return hipGetLastError();
 }
