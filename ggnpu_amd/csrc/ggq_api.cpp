@@ -878,14 +878,14 @@ static hipError_t moe_grouped_gemv(const ggq::GemvProblem& g, void* items, size_
 }
 
 // Largest average of pair rows per group (experts, plus the shared expert)
-// that the grouped GEMVs take; above it the expert-grouped GEMMs run (their
-// 32-row tiles would be mostly empty below).  GGQ_MOE_GEMV_MAX_AVG
-// overrides the default of 5 (qwen35moe, per-row int8, GEMV vs GEMM: 64
-// tokens, 2.2 rows per group, 181 vs 235 us; 128 tokens, 4.5 rows, 271 vs
-// 282 us; 256 tokens, 9.0 rows, 379 vs 297 us).
-static bool moe_small_groups(size_t rows, int groups) {
+// that the grouped GEMVs take; above it the expert-grouped GEMMs / row
+// tiles run.  GGQ_MOE_GEMV_MAX_AVG overrides the default: 5 for fp32
+// activations (their 32-row fp16 GEMM tiles would be mostly empty below),
+// 3 for per-row int8 (qwen35moe, GEMV vs the int8 row tiles: 64 tokens,
+// 2.2 rows per group, 175 vs 205 us; 128 tokens, 4.5 rows, 264 vs 222 us).
+static bool moe_small_groups(size_t rows, int groups, int dflt = 5) {
     const char* v = getenv("GGQ_MOE_GEMV_MAX_AVG");  // read per call: a process can switch it
-    const size_t max_avg = v && *v ? (size_t)atoi(v) : 5;
+    const size_t max_avg = v && *v ? (size_t)atoi(v) : (size_t)dflt;
     return rows <= max_avg * (size_t)groups;
 }
 
@@ -1013,9 +1013,9 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     g.E = E; g.grp = grp; g.tiles = tiles; g.n_tiles = ntiles; g.max_tiles = max_tiles;
     // Few rows per expert (decode-sized batches): the grouped int8 GEMV in
     // its given-codes mode (chunks of 8 rows, 4 for Q6_K / IQ4), whose
-    // lanes carry the rows; more rows per expert: the expert-grouped GEMM's
-    // 32-row tiles (moe_small_groups).
-    const bool small = moe_small_groups(rows, E + (shared ? 1 : 0));
+    // lanes carry the rows; more rows per expert: the int8 row tiles or the
+    // expert-grouped GEMM's 32-row tiles (moe_small_groups, below).
+    const bool small = moe_small_groups(rows, E + (shared ? 1 : 0), 3);
     auto i8_ok = [&](uint32_t type, const ggq::MoeGemm& d) {
         return small && ggq::i8_moe_q8_eligible(type, d, (int)rows) &&
                ggq::i8_moe_q8_ws_bytes(type, d, (int)rows) <= it_bytes;
@@ -1034,7 +1034,17 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         gu.W = p->gate_exps; gu.W2 = p->up_exps; gu.Wsh = p->gate_shexp; gu.W2sh = p->up_shexp;
         gu.N = 2 * F; gu.n1 = F; gu.C = G; gu.C2 = U;
     }
-    const bool gu_i8 = paired && i8_ok(p->gate_type, gu), dn_i8 = i8_ok(p->down_type, gd);
+    // Between 3 and 12 rows per group on average the int8 row tiles (16 rows
+    // of a group per pass) take Q4_K / Q6_K launches; above, gate / up go to
+    // the 32-row GEMM tiles and a Q6_K down projection stays on the row
+    // tiles (qwen35moe: 128 / 256 / 512 tokens 264 → 222, 289 → 237,
+    // 328 → 308 µs).
+    const bool mid = !small && rows <= 12 * (size_t)(E + (shared ? 1 : 0));
+    auto tc_ok = [&](uint32_t type, const ggq::MoeGemm& d, bool down) {
+        return !small && (mid || (down && type == ggq::T_Q6_K)) && ggq::i8_tile_codes_eligible(type, d);
+    };
+    const bool gu_tc = paired && tc_ok(p->gate_type, gu, false), dn_tc = tc_ok(p->down_type, gd, true);
+    const bool gu_i8 = paired && !gu_tc && i8_ok(p->gate_type, gu), dn_i8 = !dn_tc && i8_ok(p->down_type, gd);
     // The grouping launch builds the chunk lists of the grouped int8
     // launches (and the shared expert's group end and token rows); the tile
     // list is built only when a launch takes the expert-grouped GEMM.
@@ -1062,7 +1072,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         return ggq::launch_moe_gemm(type, d, s);
     };
     if (paired) {
-        if (gu_i8) e = ggq::launch_i8_moe_q8(p->gate_type, gu, (int)rows, base + o_it, s, built);
+        if (gu_tc) e = ggq::launch_i8_tile_codes(p->gate_type, gu, s);
+        else if (gu_i8) e = ggq::launch_i8_moe_q8(p->gate_type, gu, (int)rows, base + o_it, s, built);
         else e = ggq::launch_moe_gemm(p->gate_type, gu, s);
         if (e != hipSuccess) return hip_status(c, e, "moe gate+up");
     } else {
@@ -1078,7 +1089,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s, hf, qsh)) !=
         hipSuccess)
         return hip_status(c, e, "swiglu quant");
-    if (dn_i8) e = ggq::launch_i8_moe_q8(p->down_type, gd, (int)rows, base + o_it2, s, built);
+    if (dn_tc) e = ggq::launch_i8_tile_codes(p->down_type, gd, s);
+    else if (dn_i8) e = ggq::launch_i8_moe_q8(p->down_type, gd, (int)rows, base + o_it2, s, built);
     else e = ggq::launch_moe_gemm(p->down_type, gd, s);
     if (e != hipSuccess) return hip_status(c, e, "moe down");
     if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, shared ? D + nk * H : nullptr, p->shared_w, p->out, s)) !=

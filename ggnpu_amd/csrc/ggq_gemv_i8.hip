@@ -1867,6 +1867,319 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
 #undef GGQ_TILE_STEP
 }
 
+// ------------------------------------------- row tiles, given int8 codes
+// The same units (group, pass, 128-row tile) for per-row int8 activation
+// codes (the XDNA semantics: codes and a scale per row, as the quantizer
+// wrote them): one digit per row, so a pass carries 16 rows, A row 8 q +
+// 4 s + d holding the codes of row 4 q + d in lane half s, and output
+// register 4 q + d of lane (c, h) the dot product of that row with the
+// lane's own 16 codes.  Q6_K: signed codes (q - 32), I += sc * C per
+// K-step, acc += d * I per block.  Q4_K: unsigned nibbles, a 32-value
+// sub-block per K-step (both halves share its scale and min); the min term
+// takes the half's code sums from a second MFMA against ones: I += sc * C,
+// Mn += m * S, acc += d * I - dmin * Mn per block (exact integer sums: |C|
+// <= 16 * 128 * 15, sc, m <= 63, 8 K-steps).  Paired matrices (gate / up):
+// rows [0, n1) of a group from W, [n1, N) from W2.
+constexpr int kCodeMR = 16;
+constexpr int kCodeMaxK = 2048;  // a pass's codes: 16 K bytes of LDS
+
+template <int T> struct CodeFmt;
+template <> struct CodeFmt<T_Q6_K> {
+    static constexpr int BB = 210, PIECES = 13, LOADS = 7, STAGE_ROW = 240;
+};
+template <> struct CodeFmt<T_Q4_K> {
+    static constexpr int BB = 144, PIECES = 9, LOADS = 5, STAGE_ROW = 144;
+};
+
+template <int T, int MR>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i8_tile_codes_kernel(MoeGemm a) {
+    typedef CodeFmt<T> CF;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31, h = lane >> 5;
+    const int NB = a.K >> 8, NJ = a.K >> 5;
+    const int G = a.E + (a.Wsh ? 1 : 0);
+    const int ntiles = (a.N + kTileRows - 1) / kTileRows;
+    const uint32_t row_bytes = (uint32_t)(NB * CF::BB);
+    // LDS: unit prefix [G + 1] (16-byte padded), code planes [m][j][half]
+    // (16 B entries), row scales [16], wavefront totals of the scan,
+    // staging (32 rows of one block per wavefront)
+    const int pre_bytes = ((G + 1) * 4 + 15) & ~15;
+    int* pre = (int*)lds;
+    uint8_t* planes = lds + pre_bytes;
+    float* lsc = (float*)(planes + MR * a.K);
+    int* wsum = (int*)(lsc + MR);
+    uint8_t* stage = (uint8_t*)(wsum + 4) + w * 32 * CF::STAGE_ROW;
+    // units per group, exclusive prefix over the workgroup (4 groups per
+    // thread, G <= 1023)
+    {
+        int cnt[4], tsum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int g = 4 * tid + i;
+            const int rows = g < G ? a.grp[g + 1] - a.grp[g] : 0;
+            cnt[i] = (rows + MR - 1) / MR * ntiles;
+            tsum += cnt[i];
+        }
+        int x = tsum;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        if (lane == 63) wsum[w] = x;
+        __syncthreads();
+        int ex = x - tsum;
+        for (int k = 0; k < w; k++) ex += wsum[k];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int g = 4 * tid + i;
+            if (g <= G) pre[g] = ex;
+            ex += cnt[i];
+        }
+        __syncthreads();
+    }
+    auto upre = [&](int g) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(pre[g]); };
+    const int U = upre(G);
+    const int u0 = (int)((int64_t)U * blockIdx.x / gridDim.x), u1 = (int)((int64_t)U * (blockIdx.x + 1) / gridDim.x);
+    if (u0 >= u1) return;
+    int glo = 0, ghi = G - 1;
+    while (glo < ghi) {
+        const int mid = (glo + ghi + 1) >> 1;
+        if (upre(mid) <= u0) glo = mid;
+        else ghi = mid - 1;
+    }
+    struct UCur { int g, local, end; };
+    auto ucur_next = [&](UCur& c) __attribute__((always_inline)) {
+        if (++c.local >= c.end) {
+            do {
+                ++c.g;
+            } while (c.g < G && upre(c.g + 1) == upre(c.g));
+            c.local = 0;
+            c.end = c.g < G ? upre(c.g + 1) - upre(c.g) : 0;
+        }
+    };
+    UCur fc{glo, u0 - upre(glo), upre(glo + 1) - upre(glo)};
+    UCur cc = fc;
+    const int n_pos = (u1 - u0) * NB;
+    int fq = 0, fb = 0;
+    // the four matrices (routed / shared x first / second of the pair)
+    const int Er = a.E;
+    const Rsrc rs0 = make_rsrc((const uint8_t*)a.W, (uint32_t)Er * (uint32_t)a.w_stride);
+    const Rsrc rs1 = make_rsrc((const uint8_t*)(a.W2 ? a.W2 : a.W), (uint32_t)Er * (uint32_t)a.w_stride);
+    const Rsrc rs2 = make_rsrc((const uint8_t*)(a.Wsh ? a.Wsh : a.W), (uint32_t)a.n1 * row_bytes);
+    const Rsrc rs3 = make_rsrc((const uint8_t*)(a.W2sh ? a.W2sh : a.W), (uint32_t)(a.N - a.n1) * row_bytes);
+    // this lane's pieces of a block: chunk c = lane + 64 i is piece c % P of
+    // row c / P of the wavefront's 32
+    uint32_t soff[CF::LOADS], poff[CF::LOADS];
+    int prow[CF::LOADS];
+#pragma unroll
+    for (int i = 0; i < CF::LOADS; i++) {
+        const int c = lane + 64 * i;
+        const bool ok = c < 32 * CF::PIECES;
+        prow[i] = ok ? c / CF::PIECES : 0;
+        poff[i] = 16u * (uint32_t)(c % CF::PIECES);
+        soff[i] = ok ? (uint32_t)(prow[i] * CF::STAGE_ROW) + poff[i] : ~0u;
+    }
+    struct Raw { v4u c[CF::LOADS]; uint32_t d; };
+    auto fetch = [&]() __attribute__((always_inline)) {
+        uint32_t roff[CF::LOADS], doff = kOOB;
+        int which = 0;
+        if (fq < n_pos) {
+            const int n0 = (fc.local % ntiles) * kTileRows + w * 32;
+            const bool second = n0 >= a.n1;
+            which = (fc.g == Er ? 2 : 0) + (second ? 1 : 0);
+            const int nr = second ? n0 - a.n1 : n0;
+            const int nmax = (second ? a.N - a.n1 : a.n1) - 1;
+            const uint32_t base = (fc.g == Er ? 0u : (uint32_t)fc.g * (uint32_t)a.w_stride) + (uint32_t)fb * CF::BB;
+#pragma unroll
+            for (int i = 0; i < CF::LOADS; i++) {
+                const int n = nr + prow[i];
+                roff[i] = soff[i] == ~0u ? kOOB : base + (uint32_t)(n < nmax ? n : nmax) * row_bytes + poff[i];
+            }
+            if (T == T_Q6_K) {
+                const int n = nr + col;
+                doff = base + (uint32_t)(n < nmax ? n : nmax) * row_bytes + 208u;
+            }
+            if (++fb == NB) {
+                fb = 0;
+                ucur_next(fc);
+            }
+            fq++;
+        } else {
+#pragma unroll
+            for (int i = 0; i < CF::LOADS; i++) roff[i] = kOOB;
+        }
+        which = __builtin_amdgcn_readfirstlane(which);
+        const Rsrc rs = which == 0 ? rs0 : which == 1 ? rs1 : which == 2 ? rs2 : rs3;
+        Raw r;
+        r.d = T == T_Q6_K ? bl2(rs, doff) : 0u;
+#pragma unroll
+        for (int i = 0; i < CF::LOADS; i++) r.c[i] = bl16(rs, roff[i]);
+        return r;
+    };
+    const int rho = lane & 31, s_l = (rho >> 2) & 1;
+    const int m_l = 4 * (rho >> 3) + (rho & 3);  // activation row of this lane's A entries
+    Raw ra = fetch();
+    Raw rb = fetch();
+    int mc = 0, r0 = 0, tile = 0;
+    bool act = false;
+    uint32_t abase = 0;
+    float acc[MR];
+    auto start_segment = [&]() __attribute__((always_inline)) {
+        const int g = __builtin_amdgcn_readfirstlane(cc.g), local = __builtin_amdgcn_readfirstlane(cc.local);
+        const int pass = local / ntiles;
+        tile = local % ntiles;
+        const int gr0 = a.grp[g];
+        const int rows = a.grp[g + 1] - gr0;
+        r0 = gr0 + MR * pass;
+        mc = rows - MR * pass < MR ? rows - MR * pass : MR;
+        __syncthreads();  // the previous segment's planes are read
+        // codes of the pass's rows: 16-byte chunks, entry (m, j, half)
+        const int per_row = a.K >> 4;
+        for (int i = tid; i < mc * per_row; i += 256) {
+            const int m = i / per_row, k0 = 16 * (i - m * per_row);
+            const int r = r0 + m;
+            const int ar = a.x_idx ? a.x_idx[r] : r;
+            const uint4 v = *(const uint4*)(a.QA + (int64_t)ar * a.K + k0);
+            *(uint4*)(planes + ((m * NJ + (k0 >> 5)) * 2 + ((k0 >> 4) & 1)) * 16) = v;
+        }
+        if (tid < MR) {
+            const int r = r0 + (tid < mc ? tid : 0);
+            lsc[tid] = a.sa[a.x_idx ? a.x_idx[r] : r];
+        }
+        __syncthreads();
+        act = s_l == h && m_l < mc;
+        abase = (uint32_t)(((m_l * NJ) * 2 + h) * 16);
+    };
+    // One block: K-steps on the staged rows.
+    auto block = [&](const Raw& raw, int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < CF::LOADS; i++)
+            if (i < CF::LOADS - 1 || soff[i] != ~0u) *(v4u*)(stage + soff[i]) = raw.c[i];
+        const uint8_t* row = stage + col * CF::STAGE_ROW;
+        typedef int v16i __attribute__((ext_vector_type(16)));
+        const v16i Z = {};
+        int I[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) I[m] = 0;
+        if constexpr (T == T_Q6_K) {
+            TileQ6 q;
+#pragma unroll
+            for (int nh = 0; nh < 2; nh++) {
+                q.ql0[nh] = *(const v4u*)(row + 64 * nh + 16 * h);
+                q.ql1[nh] = *(const v4u*)(row + 64 * nh + 32 + 16 * h);
+                q.qh[nh] = *(const v4u*)(row + 128 + 32 * nh + 16 * h);
+            }
+            q.sc = *(const v4u*)(row + 192);
+            const float dd = h2f(raw.d & 0xFFFFu);
+#pragma unroll
+            for (int nh = 0; nh < 2; nh++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int j = 8 * b + 4 * nh + t;
+                    v4i A = *(const v4i*)(planes + abase + (uint32_t)j * 32u);
+                    if (!act) A = v4i{0, 0, 0, 0};
+                    const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, tile_q6_codes(q, nh, t), Z, 0, 0, 0);
+                    const int sc = tile_q6_scale(q, nh, t, h);
+                    // (rows past mc meet zero A entries: no branches)
+#pragma unroll
+                    for (int m = 0; m < MR; m++) I[m] += __mul24(sc, C[m]);
+#pragma unroll
+                    for (int m = 0; m < MR; m += 4)
+                        asm volatile("" : "+v"(I[m]), "+v"(I[m + 1]), "+v"(I[m + 2]), "+v"(I[m + 3]));
+                }
+#pragma unroll
+            for (int m = 0; m < MR; m++) acc[m] = fmaf(dd, (float)I[m], acc[m]);
+        } else {
+            const v4u hd = *(const v4u*)row;
+            v4u qs[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) qs[c] = *(const v4u*)(row + 16 + 32 * c + 16 * h);
+            const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+            int Mn[MR];
+#pragma unroll
+            for (int m = 0; m < MR; m++) Mn[m] = 0;
+            const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int j = 8 * b + t;
+                v4i A = *(const v4i*)(planes + abase + (uint32_t)j * 32u);
+                if (!act) A = v4i{0, 0, 0, 0};
+                const v4u w4 = qs[t >> 1];
+                v4i B;
+                if (t & 1) {
+                    B.x = (int)((w4.x >> 4) & 0x0F0F0F0Fu); B.y = (int)((w4.y >> 4) & 0x0F0F0F0Fu);
+                    B.z = (int)((w4.z >> 4) & 0x0F0F0F0Fu); B.w = (int)((w4.w >> 4) & 0x0F0F0F0Fu);
+                } else {
+                    B.x = (int)(w4.x & 0x0F0F0F0Fu); B.y = (int)(w4.y & 0x0F0F0F0Fu);
+                    B.z = (int)(w4.z & 0x0F0F0F0Fu); B.w = (int)(w4.w & 0x0F0F0F0Fu);
+                }
+                const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, Z, 0, 0, 0);
+                const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, ones, Z, 0, 0, 0);
+                // scale / min of sub-block t (kquant.h:56-64): bytes of pair t / 2
+                const uint32_t sm = kq_pair(hd.y, hd.z, hd.w, t >> 1);
+                const int sc = (int)((sm >> (8 * (t & 1))) & 0xFFu), mn = (int)((sm >> (16 + 8 * (t & 1))) & 0xFFu);
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    I[m] += __mul24(sc, C[m]);
+                    Mn[m] += __mul24(mn, S[m]);
+                }
+#pragma unroll
+                for (int m = 0; m < MR; m += 4) {
+                    asm volatile("" : "+v"(I[m]), "+v"(I[m + 1]), "+v"(I[m + 2]), "+v"(I[m + 3]));
+                    asm volatile("" : "+v"(Mn[m]), "+v"(Mn[m + 1]), "+v"(Mn[m + 2]), "+v"(Mn[m + 3]));
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MR; m++) acc[m] = fmaf(d, (float)I[m], fmaf(-dmin, (float)Mn[m], acc[m]));
+        }
+    };
+    auto finish = [&]() __attribute__((always_inline)) {
+        // the two halves, then the row's scale
+        const int n = tile * kTileRows + w * 32 + col;
+        const bool second = n - col >= a.n1;  // (uniform: the wavefront's rows are in one matrix)
+        float* Y = second ? a.C2 : a.C;
+        const int nn = second ? n - a.n1 : n;
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            const float v = acc[m] + __shfl_xor(acc[m], 32, 64);
+            if (m < mc && h == 0 && n < a.N) Y[(int64_t)(r0 + m) * a.ldc + nn] = v * lsc[m];
+        }
+    };
+    int q = 0;
+#define GGQ_CODE_STEP(R)                                                           \
+    {                                                                              \
+        const int b = q % NB;                                                      \
+        if (b == 0) {                                                              \
+            _Pragma("unroll") for (int m = 0; m < MR; m++) acc[m] = 0.0f;     \
+        }                                                                          \
+        block(R, b);                                                               \
+        R = fetch();                                                               \
+        if (b == NB - 1) {                                                         \
+            finish();                                                              \
+            tile++;                                                                \
+            ucur_next(cc);                                                         \
+        }                                                                          \
+        if (++q >= seg_end) break;                                                 \
+    }
+    while (q < n_pos) {
+        start_segment();
+        const int seg_units = min(ntiles - tile, u1 - u0 - q / NB);
+        const int seg_end = q + seg_units * NB;
+        if (q & 1) {
+            do GGQ_CODE_STEP(rb) while (false);
+            if (q >= seg_end) continue;
+        }
+        while (true) {
+            GGQ_CODE_STEP(ra)
+            GGQ_CODE_STEP(rb)
+        }
+    }
+#undef GGQ_CODE_STEP
+}
+
 }  // namespace
 
 bool i8_tile_grouped_eligible(uint32_t type, int N, int K, int E, int64_t w_stride, bool shared) {
@@ -1894,6 +2207,38 @@ hipError_t launch_i8_tile_grouped(uint32_t type, const void* W, int64_t w_stride
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
     if (attr != hipSuccess) return attr;
     i8_tile_grouped_kernel<<<grid, 256, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+bool i8_tile_codes_eligible(uint32_t type, const MoeGemm& g) {
+    if (type != T_Q6_K && type != T_Q4_K) return false;
+    const int G = g.E + (g.Wsh ? 1 : 0);
+    if (g.K % 256 != 0 || g.K <= 0 || g.K > kCodeMaxK || g.N <= 0 || g.E < 1 || G > 1023) return false;
+    if (g.W2 ? (g.n1 % 32 != 0 || g.n1 <= 0 || g.n1 >= g.N || !g.C2) : g.n1 != g.N) return false;
+    if (g.Wsh && g.W2 && !g.W2sh) return false;
+    const int64_t rb = row_bytes(type, g.K);
+    return g.w_stride >= (int64_t)g.n1 * rb && (int64_t)g.E * g.w_stride < (int64_t)kOOB;
+}
+
+hipError_t launch_i8_tile_codes(uint32_t type, const MoeGemm& g, hipStream_t s) {
+    if (!i8_tile_codes_eligible(type, g)) return hipErrorInvalidValue;
+    const int G = g.E + (g.Wsh ? 1 : 0);
+    const int stage_row = type == T_Q6_K ? CodeFmt<T_Q6_K>::STAGE_ROW : CodeFmt<T_Q4_K>::STAGE_ROW;
+    const int lds = (((G + 1) * 4 + 15) & ~15) + kCodeMR * g.K + 4 * kCodeMR + 16 + 4 * 32 * stage_row;
+    int per_cu = (160 * 1024) / lds;
+    per_cu = per_cu > 3 ? 3 : per_cu < 1 ? 1 : per_cu;
+    const dim3 grid((unsigned)(per_cu * cu_count()));
+    if (type == T_Q6_K) {
+        static const hipError_t attr = hipFuncSetAttribute((const void*)i8_tile_codes_kernel<T_Q6_K, kCodeMR>,
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (attr != hipSuccess) return attr;
+        i8_tile_codes_kernel<T_Q6_K, kCodeMR><<<grid, 256, lds, s>>>(g);
+    } else {
+        static const hipError_t attr = hipFuncSetAttribute((const void*)i8_tile_codes_kernel<T_Q4_K, kCodeMR>,
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (attr != hipSuccess) return attr;
+        i8_tile_codes_kernel<T_Q4_K, kCodeMR><<<grid, 256, lds, s>>>(g);
+    }
     return hipGetLastError();
 }
 
