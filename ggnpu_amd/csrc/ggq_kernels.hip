@@ -4097,19 +4097,40 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
                                                                int32_t* __restrict__ tok_idx,
                                                                int32_t* __restrict__ pos_of, int t_sh,
                                                                ChunkList l0, ChunkList l1, int n_lists) {
-    __shared__ __attribute__((aligned(16))) int32_t s_sel[1024];
-    __shared__ int32_t hist[16][kGroupFastE];  // per wavefront; then exclusive prefix over wavefronts
-    __shared__ int32_t start[kGroupFastE];     // first position of each expert, advanced by each round
+    __shared__ int32_t hist[16][kGroupFastE];  // per wavefront: pairs of each expert in its slice
+    __shared__ int32_t start[kGroupFastE];     // first position of each expert (then its end)
     __shared__ int32_t wsum[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Totals of all pairs, then their exclusive scan (four wavefronts cover
-    // 256 experts).
-    if (tid < kGroupFastE) start[tid] = 0;
+    for (int i = tid; i < 16 * kGroupFastE; i += 1024) (&hist[0][0])[i] = 0;
     __syncthreads();
-    for (int f = tid; f < n; f += 1024) atomicAdd(&start[expert_id(sel[f], E)], 1);
+    // Wavefront w ranks the pairs of its slice [w * S, (w + 1) * S), 64 at
+    // a time: lanes holding the same expert are found with one ballot per
+    // bit of the expert id; a pair's rank is its count of such lanes below
+    // it plus the slice's earlier pairs of that expert.  The rank goes to
+    // pos_of (read back by the same lane below).
+    const int S = ((n + 16 * 64 - 1) / (16 * 64)) * 64;
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int f0 = wave * S; f0 < (wave + 1) * S && f0 < n; f0 += 64) {
+        const int f = f0 + lane;
+        const bool ok = f < n;
+        const int e = ok ? expert_id(sel[f], E) : 0;
+        uint64_t same = __ballot(ok);
+#pragma unroll
+        for (int bit = 0; bit < 8; bit++) {
+            const uint64_t b1 = __ballot((e >> bit) & 1);
+            same &= ((e >> bit) & 1) ? b1 : ~b1;
+        }
+        const int before = hist[wave][e];
+        if (ok && (same & below) == 0) hist[wave][e] = before + __popcll(same);  // the first such lane
+        if (ok) pos_of[f] = before + __popcll(same & below);
+    }
     __syncthreads();
+    // Expert totals, their exclusive scan (four wavefronts cover 256
+    // experts), then each wavefront's base per expert.
     if (tid < kGroupFastE) {
-        const int c = start[tid];
+        int c = 0;
+#pragma unroll
+        for (int w = 0; w < 16; w++) c += hist[w][tid];
         int incl = c;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -4117,51 +4138,32 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
             if (lane >= off) incl += o;
         }
         if (lane == 63) wsum[wave] = incl;
-        hist[0][tid] = incl - c;  // staged: wsum is not complete yet
+        start[tid] = incl - c;  // within its wavefront of experts, for now
     }
     __syncthreads();
     if (tid < kGroupFastE) {
         int before = 0;
         for (int w = 0; w < wave; w++) before += wsum[w];
-        start[tid] = hist[0][tid] + before;
-        if (tid < E) grp_off[tid] = start[tid];
+        int b0 = start[tid] + before;
+        if (tid < E) grp_off[tid] = b0;
         if (tid == 0) grp_off[E] = n;
+#pragma unroll
+        for (int w = 0; w < 16; w++) {
+            const int c = hist[w][tid];
+            hist[w][tid] = b0;
+            b0 += c;
+        }
+        start[tid] = b0;  // the end of expert tid's rows
     }
     __syncthreads();
-    for (int r0 = 0; r0 < n; r0 += 1024) {
-        const int f = r0 + tid;
-        const int e = f < n ? expert_id(sel[f], E) : -1;
-        s_sel[tid] = e;
-        for (int i = tid; i < 16 * kGroupFastE; i += 1024) (&hist[0][0])[i] = 0;
-        __syncthreads();
-        if (e >= 0) atomicAdd(&hist[wave][e], 1);
-        // Pairs of e in earlier lanes of this wavefront.
-        int rank = 0;
-        const int32_t* ws = s_sel + 64 * wave;
-        for (int g = 0; g < lane; g += 4) {
-            const int4 v = *(const int4*)&ws[g];
-            rank += (v.x == e) + (g + 1 < lane && v.y == e) + (g + 2 < lane && v.z == e) + (g + 3 < lane && v.w == e);
-        }
-        __syncthreads();
-        // Thread x < 256: prefix of expert x over the round's wavefronts.
-        int total = 0;
-        if (tid < kGroupFastE) {
-#pragma unroll
-            for (int w = 0; w < 16; w++) {
-                const int c = hist[w][tid];
-                hist[w][tid] = total;
-                total += c;
-            }
-        }
-        __syncthreads();
-        if (e >= 0) {
-            const int pos = start[e] + hist[wave][e] + rank;
+    for (int f0 = wave * S; f0 < (wave + 1) * S && f0 < n; f0 += 64) {
+        const int f = f0 + lane;
+        if (f < n) {
+            const int e = expert_id(sel[f], E);
+            const int pos = hist[wave][e] + pos_of[f];
             tok_idx[pos] = f / topk;
             pos_of[f] = pos;
         }
-        __syncthreads();
-        if (tid < kGroupFastE) start[tid] += total;
-        __syncthreads();
     }
     // The grouped int8 launches' chunk lists (and the shared expert's group
     // end and token rows) from the offsets just written, saving their own
