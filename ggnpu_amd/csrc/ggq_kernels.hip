@@ -339,13 +339,105 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
     return hipGetLastError();
 }
 
+// Producer (none or SwiGLU) + row quantization for rows of up to 2048
+// values: one wavefront per row, four rows per workgroup, lane l holding the
+// 8-value chunks l, l + 64, ...; the row maximum by a wavefront reduction
+// (no barrier).  Same arithmetic per value as quant_row_regs, so the codes
+// and scales are identical; code sums per 32 values from 4 lanes.
+template <int P>
+__global__ __launch_bounds__(256) void produce_quant_wave_kernel(const float* __restrict__ A,
+                                                                 const float* __restrict__ aux, int lda, int M,
+                                                                 int K, int8_t* __restrict__ q,
+                                                                 float* __restrict__ scales,
+                                                                 float* __restrict__ prod_out,
+                                                                 float* __restrict__ gsum) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    constexpr int R = 4;  // chunks per lane (K <= 2048)
+    const float* a = A + (int64_t)m * lda;
+    const float* u = P == PROD_SWIGLU ? aux + (int64_t)m * lda : nullptr;
+    float4 v[R][2];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int k = 8 * (lane + 64 * i);
+        if (k < K) {
+            v[i][0] = *(const float4*)(a + k);
+            v[i][1] = *(const float4*)(a + k + 4);
+        } else {
+            v[i][0] = v[i][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+    if constexpr (P == PROD_SWIGLU) {
+        auto sw = [](float g, float uu) { return (g / (1.0f + expf(-g))) * uu; };
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 8 * (lane + 64 * i);
+            if (k >= K) continue;
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const float4 uv = *(const float4*)(u + k + 4 * hh);
+                float4& x = v[i][hh];
+                x = make_float4(sw(x.x, uv.x), sw(x.y, uv.y), sw(x.z, uv.z), sw(x.w, uv.w));
+            }
+        }
+    }
+    if (prod_out) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 8 * (lane + 64 * i);
+            if (k >= K) continue;
+            *(float4*)(prod_out + (int64_t)m * K + k) = v[i][0];
+            *(float4*)(prod_out + (int64_t)m * K + k + 4) = v[i][1];
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i][hh].x), fabsf(v[i][hh].y))), fmaxf(fabsf(v[i][hh].z), fabsf(v[i][hh].w)));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float sc = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+    const float inv = __fdiv_rn(1.0f, sc);
+    if (lane == 0 && scales) scales[m] = sc;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int k = 8 * (lane + 64 * i);
+        int cs = 0;
+        uint32_t w[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const float4 x = v[i][hh];
+            const int8_t c0 = to_i8(__fmul_rn(x.x, inv)), c1 = to_i8(__fmul_rn(x.y, inv));
+            const int8_t c2 = to_i8(__fmul_rn(x.z, inv)), c3 = to_i8(__fmul_rn(x.w, inv));
+            cs += (int)c0 + (int)c1 + (int)c2 + (int)c3;
+            w[hh] = (uint32_t)(uint8_t)c0 | (uint32_t)(uint8_t)c1 << 8 | (uint32_t)(uint8_t)c2 << 16 |
+                    (uint32_t)(uint8_t)c3 << 24;
+        }
+        if (k < K && q) *(uint2*)(q + (int64_t)m * K + k) = make_uint2(w[0], w[1]);
+        if (gsum) {  // 32 values = 4 consecutive lanes (exact in fp32)
+            cs += __shfl_xor(cs, 1, 64);
+            cs += __shfl_xor(cs, 2, 64);
+            if (k < K && (lane & 3) == 0) gsum[(int64_t)m * (K / 32) + k / 32] = (float)cs;
+        }
+    }
+}
+
 hipError_t launch_produce_quant(int producer, const float* A, const float* aux, int lda, int M, int K, float eps,
                                 int8_t* q, float* scales, hipStream_t s, float* prod_out, float* gsum) {
     if (M == 0) return hipSuccess;
     if (K <= 0 || K > 1024 * 16 || K % 4 || lda % 4 || (uintptr_t)A % 16 || (uintptr_t)aux % 16 ||
         (uintptr_t)q % 4 || (uintptr_t)prod_out % 16 || (gsum && K % 32))
         return hipErrorInvalidValue;
-    if (producer == PROD_RMS)
+    // rows of up to 2048 values: a wavefront per row
+    const bool wave = K <= 2048 && K % 8 == 0 && (uintptr_t)q % 8 == 0;
+    if (wave && producer == PROD_SWIGLU && aux)
+        produce_quant_wave_kernel<PROD_SWIGLU><<<(M + 3) / 4, 256, 0, s>>>(A, aux, lda, M, K, q, scales, prod_out, gsum);
+    else if (wave && producer == PROD_NONE)
+        produce_quant_wave_kernel<PROD_NONE><<<(M + 3) / 4, 256, 0, s>>>(A, aux, lda, M, K, q, scales, prod_out, gsum);
+    else if (producer == PROD_RMS)
         produce_quant_row_kernel<PROD_RMS><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out, gsum);
     else if (producer == PROD_SWIGLU && aux)
         produce_quant_row_kernel<PROD_SWIGLU><<<M, 256, 0, s>>>(A, aux, lda, K, eps, q, scales, prod_out, gsum);
