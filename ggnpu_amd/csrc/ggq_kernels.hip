@@ -3329,13 +3329,118 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
     }
 }
 
+// The same for rows of up to 2048 values: one wavefront per row, four rows
+// per workgroup, lane l holding the 8-value chunks l, l + 64, ...; the
+// per-value arithmetic and the order of the group sums are those of
+// split_rows_kernel (each 4-value sum, then pairs of them, then across 4
+// lanes), so the planes and sums are identical.
+template <int P>
+__global__ __launch_bounds__(256) void split_rows_wave_kernel(const float* __restrict__ A,
+                                                              const float* __restrict__ aux, int lda, int M, int K,
+                                                              _Float16* __restrict__ XH, _Float16* __restrict__ XL,
+                                                              float* __restrict__ XS, float* __restrict__ xs,
+                                                              float* __restrict__ prod_out) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    constexpr int R = 4;
+    const float* a = A + (int64_t)m * lda;
+    float4 v[R][2];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int k = 8 * (lane + 64 * i);
+        if (k < K) {
+            v[i][0] = *(const float4*)(a + k);
+            v[i][1] = *(const float4*)(a + k + 4);
+        } else {
+            v[i][0] = v[i][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+    if constexpr (P == PROD_SWIGLU) {
+        const float* u = aux + (int64_t)m * lda;
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 8 * (lane + 64 * i);
+            if (k >= K) continue;
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const float4 w = *(const float4*)(u + k + 4 * hh);
+                float4& x = v[i][hh];
+                x.x = (x.x / (1.0f + expf(-x.x))) * w.x;
+                x.y = (x.y / (1.0f + expf(-x.y))) * w.y;
+                x.z = (x.z / (1.0f + expf(-x.z))) * w.z;
+                x.w = (x.w / (1.0f + expf(-x.w))) * w.w;
+            }
+        }
+    }
+    if (prod_out) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int k = 8 * (lane + 64 * i);
+            if (k >= K) continue;
+            *(float4*)(prod_out + (int64_t)m * K + k) = v[i][0];
+            *(float4*)(prod_out + (int64_t)m * K + k + 4) = v[i][1];
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i][hh].x), fabsf(v[i][hh].y))), fmaxf(fabsf(v[i][hh].z), fabsf(v[i][hh].w)));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    int ex = 0;
+    if (amax > 0.0f) {
+        int x2;
+        (void)frexpf(amax, &x2);  // amax in [2^(x2-1), 2^x2)
+        ex = 15 - x2;
+        if (ex > 126) ex = 126;
+    }
+    if (lane == 0) xs[m] = ldexpf(1.0f, -ex);
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const int k = 8 * (lane + 64 * i);
+        float gq[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const float4 x = v[i][hh];
+            const float y[4] = {ldexpf(x.x, ex), ldexpf(x.y, ex), ldexpf(x.z, ex), ldexpf(x.w, ex)};
+            _Float16 hv[4], lv[4];
+            float gs = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                hv[j] = (_Float16)y[j];
+                lv[j] = (_Float16)(y[j] - (float)hv[j]);
+                gs += (float)hv[j] + (float)lv[j];
+            }
+            gq[hh] = gs;
+            if (k < K) {
+                *(uint2*)(XH + (int64_t)m * K + k + 4 * hh) = __builtin_bit_cast(uint2, h4v{hv[0], hv[1], hv[2], hv[3]});
+                *(uint2*)(XL + (int64_t)m * K + k + 4 * hh) = __builtin_bit_cast(uint2, h4v{lv[0], lv[1], lv[2], lv[3]});
+            }
+        }
+        float gs = gq[0] + gq[1];
+        gs += __shfl_xor(gs, 1, 64);
+        gs += __shfl_xor(gs, 2, 64);
+        if (k < K && (lane & 3) == 0) XS[(int64_t)m * (K / 32) + k / 32] = gs;
+    }
+}
+
 hipError_t launch_split_rows(int producer, const float* A, const float* aux, int lda, int M, int K, void* XH,
                              void* XL, float* XS, float* xs, float* prod_out, hipStream_t s) {
     if (M == 0) return hipSuccess;
     if (K <= 0 || K > 1024 * 16 || K % 32 || lda % 4 || (uintptr_t)A % 16 || (uintptr_t)aux % 16 ||
         (uintptr_t)XH % 8 || (uintptr_t)XL % 8 || (uintptr_t)prod_out % 16)
         return hipErrorInvalidValue;
-    if (producer == PROD_SWIGLU)
+    if (K <= 2048) {  // a wavefront per row
+        if (producer == PROD_SWIGLU)
+            split_rows_wave_kernel<PROD_SWIGLU><<<(M + 3) / 4, 256, 0, s>>>(A, aux, lda, M, K, (_Float16*)XH,
+                                                                          (_Float16*)XL, XS, xs, prod_out);
+        else
+            split_rows_wave_kernel<PROD_NONE><<<(M + 3) / 4, 256, 0, s>>>(A, aux, lda, M, K, (_Float16*)XH,
+                                                                        (_Float16*)XL, XS, xs, prod_out);
+    } else if (producer == PROD_SWIGLU)
         split_rows_kernel<PROD_SWIGLU><<<M, 256, 0, s>>>(A, aux, lda, K, (_Float16*)XH, (_Float16*)XL, XS, xs,
                                                           prod_out);
     else
