@@ -325,10 +325,20 @@ __global__ __launch_bounds__(256) void quant_act_b32_kernel(const float* __restr
     }
 }
 
+template <int P>
+__global__ void produce_quant_wave_kernel(const float* __restrict__ A, const float* __restrict__ aux, int lda, int M,
+                                          int K, int8_t* __restrict__ q, float* __restrict__ scales,
+                                          float* __restrict__ prod_out, float* __restrict__ gsum);
+
 hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int8_t* q,
                             float* scales, float* x_eff, hipStream_t s) {
     if (M == 0 || K == 0) return hipSuccess;
-    if (mode == 1) {
+    if (mode == 1 && !x_eff && K <= 2048 && K % 8 == 0 && (uintptr_t)A % 16 == 0 && lda % 4 == 0 &&
+        (uintptr_t)q % 8 == 0) {
+        // rows of up to 2048 values: a wavefront per row (the same codes)
+        produce_quant_wave_kernel<PROD_NONE><<<(M + 3) / 4, 256, 0, s>>>(A, nullptr, lda, M, K, q, scales, nullptr,
+                                                                         nullptr);
+    } else if (mode == 1) {
         const int vec4 = ((uintptr_t)A % 16 == 0) && lda % 4 == 0 && K % 4 == 0 && ((uintptr_t)q % 4 == 0) &&
                          ((uintptr_t)x_eff % 16 == 0);
         quant_act_row_kernel<<<M, 256, 0, s>>>(A, lda, K, q, scales, x_eff, vec4);
