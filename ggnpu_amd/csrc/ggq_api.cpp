@@ -1040,8 +1040,10 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     // tiles (qwen35moe: 128 / 256 / 512 tokens 264 → 222, 289 → 237,
     // 328 → 308 µs).
     const bool mid = !small && rows <= 12 * (size_t)(E + (shared ? 1 : 0));
+    // A Q6_K down projection takes the row tiles at every size (64 tokens:
+    // 68 -> 61 us against the grouped GEMV's 4-row chunks).
     auto tc_ok = [&](uint32_t type, const ggq::MoeGemm& d, bool down) {
-        return !small && (mid || (down && type == ggq::T_Q6_K)) && ggq::i8_tile_codes_eligible(type, d);
+        return ((!small && mid) || (down && type == ggq::T_Q6_K)) && ggq::i8_tile_codes_eligible(type, d);
     };
     const bool gu_tc = paired && tc_ok(p->gate_type, gu, false), dn_tc = tc_ok(p->down_type, gd, true);
     const bool gu_i8 = paired && !gu_tc && i8_ok(p->gate_type, gu), dn_i8 = !dn_tc && i8_ok(p->down_type, gd);
@@ -1056,7 +1058,10 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, nl > 0 ? (int)ts : 0, lists, nl, &built)) !=
         hipSuccess)
         return hip_status(c, e, "moe_group");
-    if (!(built && gu_i8 && dn_i8) &&
+    // The GEMM's tile list (and, when the grouping built no chunk lists, the
+    // shared expert's group end and token rows that the row tiles read too).
+    const bool any_gemm = (paired ? !gu_i8 && !gu_tc : true) || (!dn_i8 && !dn_tc);
+    if ((any_gemm || !built) &&
         (e = ggq::launch_moe_tiles(grp, tok, E, (int)ts, (int2*)tiles, ntiles, s)) != hipSuccess)
         return hip_status(c, e, "moe_tiles");
     // the token rows' codes, and their sums per 32 values for the K-quant
