@@ -1034,12 +1034,12 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         gu.W = p->gate_exps; gu.W2 = p->up_exps; gu.Wsh = p->gate_shexp; gu.W2sh = p->up_shexp;
         gu.N = 2 * F; gu.n1 = F; gu.C = G; gu.C2 = U;
     }
-    // Between 3 and 12 rows per group on average the int8 row tiles (16 rows
+    // Between 3 and 24 rows per group on average the int8 row tiles (16 rows
     // of a group per pass) take Q4_K / Q6_K launches; above, gate / up go to
-    // the 32-row GEMM tiles and a Q6_K down projection stays on the row
-    // tiles (qwen35moe: 128 / 256 / 512 tokens 264 → 222, 289 → 237,
-    // 328 → 308 µs).
-    const bool mid = !small && rows <= 12 * (size_t)(E + (shared ? 1 : 0));
+    // the 32-row GEMM tiles (qwen35moe: 128 / 256 / 384 / 512 tokens 264 →
+    // 194, 289 → 214, 271 → 248, 328 → 292 µs; 1024 tokens 445 on the GEMM
+    // vs 456 µs on the tiles).
+    const bool mid = !small && rows <= 24 * (size_t)(E + (shared ? 1 : 0));
     // A Q6_K down projection takes the row tiles at every size (64 tokens:
     // 68 -> 61 us against the grouped GEMV's 4-row chunks).
     auto tc_ok = [&](uint32_t type, const ggq::MoeGemm& d, bool down) {

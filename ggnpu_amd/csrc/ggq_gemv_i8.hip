@@ -1894,6 +1894,12 @@ template <> struct CodeFmt<T_Q4_K> {
 template <int T, int MR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i8_tile_codes_kernel(MoeGemm a) {
     typedef CodeFmt<T> CF;
+    // Q4_K: a K-step is one scale group for both lane halves, so A rows carry
+    // the whole 32 values of row 0..15 and each lane's output registers 0..7
+    // hold complete sums of 8 rows (8 (i / 4) + 4 h + i % 4); Q6_K: rows in
+    // one lane half per group, all 16 per lane, halves added at the end.
+    constexpr bool kFull = T == T_Q4_K;
+    constexpr int NA = kFull ? 8 : MR;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2020,13 +2026,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
         return r;
     };
     const int rho = lane & 31, s_l = (rho >> 2) & 1;
-    const int m_l = 4 * (rho >> 3) + (rho & 3);  // activation row of this lane's A entries
+    const int m_l = kFull ? rho : 4 * (rho >> 3) + (rho & 3);  // activation row of this lane's A entries
+    auto arow = [&](int i) __attribute__((always_inline)) { return kFull ? 8 * (i >> 2) + 4 * h + (i & 3) : i; };
     Raw ra = fetch();
     Raw rb = fetch();
     int mc = 0, r0 = 0, tile = 0;
     bool act = false;
     uint32_t abase = 0;
-    float acc[MR];
+    float acc[NA];
     auto start_segment = [&]() __attribute__((always_inline)) {
         const int g = __builtin_amdgcn_readfirstlane(cc.g), local = __builtin_amdgcn_readfirstlane(cc.local);
         const int pass = local / ntiles;
@@ -2050,7 +2057,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
             lsc[tid] = a.sa[a.x_idx ? a.x_idx[r] : r];
         }
         __syncthreads();
-        act = s_l == h && m_l < mc;
+        act = (kFull || s_l == h) && m_l < mc;
         abase = (uint32_t)(((m_l * NJ) * 2 + h) * 16);
     };
     // One block: K-steps on the staged rows.
@@ -2061,9 +2068,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
         const uint8_t* row = stage + col * CF::STAGE_ROW;
         typedef int v16i __attribute__((ext_vector_type(16)));
         const v16i Z = {};
-        int I[MR];
+        int I[NA];
 #pragma unroll
-        for (int m = 0; m < MR; m++) I[m] = 0;
+        for (int m = 0; m < NA; m++) I[m] = 0;
         if constexpr (T == T_Q6_K) {
             TileQ6 q;
 #pragma unroll
@@ -2098,9 +2105,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
 #pragma unroll
             for (int c = 0; c < 4; c++) qs[c] = *(const v4u*)(row + 16 + 32 * c + 16 * h);
             const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
-            int Mn[MR];
+            int Mn[NA];
 #pragma unroll
-            for (int m = 0; m < MR; m++) Mn[m] = 0;
+            for (int m = 0; m < NA; m++) Mn[m] = 0;
             const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
 #pragma unroll
             for (int t = 0; t < 8; t++) {
@@ -2122,30 +2129,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
                 const uint32_t sm = kq_pair(hd.y, hd.z, hd.w, t >> 1);
                 const int sc = (int)((sm >> (8 * (t & 1))) & 0xFFu), mn = (int)((sm >> (16 + 8 * (t & 1))) & 0xFFu);
 #pragma unroll
-                for (int m = 0; m < MR; m++) {
+                for (int m = 0; m < NA; m++) {
                     I[m] += __mul24(sc, C[m]);
                     Mn[m] += __mul24(mn, S[m]);
                 }
 #pragma unroll
-                for (int m = 0; m < MR; m += 4) {
+                for (int m = 0; m < NA; m += 4) {
                     asm volatile("" : "+v"(I[m]), "+v"(I[m + 1]), "+v"(I[m + 2]), "+v"(I[m + 3]));
                     asm volatile("" : "+v"(Mn[m]), "+v"(Mn[m + 1]), "+v"(Mn[m + 2]), "+v"(Mn[m + 3]));
                 }
             }
 #pragma unroll
-            for (int m = 0; m < MR; m++) acc[m] = fmaf(d, (float)I[m], fmaf(-dmin, (float)Mn[m], acc[m]));
+            for (int m = 0; m < NA; m++) acc[m] = fmaf(d, (float)I[m], fmaf(-dmin, (float)Mn[m], acc[m]));
         }
     };
     auto finish = [&]() __attribute__((always_inline)) {
-        // the two halves, then the row's scale
+        // (Q6_K: the two halves' groups added), then the row's scale
         const int n = tile * kTileRows + w * 32 + col;
         const bool second = n - col >= a.n1;  // (uniform: the wavefront's rows are in one matrix)
         float* Y = second ? a.C2 : a.C;
         const int nn = second ? n - a.n1 : n;
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            const float v = acc[m] + __shfl_xor(acc[m], 32, 64);
-            if (m < mc && h == 0 && n < a.N) Y[(int64_t)(r0 + m) * a.ldc + nn] = v * lsc[m];
+        for (int i = 0; i < NA; i++) {
+            const int m = arow(i);
+            const float v = kFull ? acc[i] : acc[i] + __shfl_xor(acc[i], 32, 64);
+            if (m < mc && (kFull || h == 0) && n < a.N) Y[(int64_t)(r0 + m) * a.ldc + nn] = v * lsc[m];
         }
     };
     int q = 0;
@@ -2153,7 +2161,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
     {                                                                              \
         const int b = q % NB;                                                      \
         if (b == 0) {                                                              \
-            _Pragma("unroll") for (int m = 0; m < MR; m++) acc[m] = 0.0f;     \
+            _Pragma("unroll") for (int m = 0; m < NA; m++) acc[m] = 0.0f;     \
         }                                                                          \
         block(R, b);                                                               \
         R = fetch();                                                               \
