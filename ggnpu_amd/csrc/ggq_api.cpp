@@ -1029,6 +1029,11 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     gd.W = p->down_exps; gd.W2 = nullptr; gd.Wsh = p->down_shexp; gd.W2sh = nullptr;
     gd.w_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
     gd.N = H; gd.n1 = H; gd.C = D; gd.C2 = nullptr;
+    // the token rows' and pair rows' code sums per 32 values (the K-quant min term)
+    float* qsx = (float*)(base + o_qsx);
+    float* qsh = (float*)(base + o_qsh);
+    gu.QS = qsx;
+    gd.QS = qsh;
     const bool paired = p->up_type == p->gate_type;
     if (paired) {
         gu.W = p->gate_exps; gu.W2 = p->up_exps; gu.Wsh = p->gate_shexp; gu.W2sh = p->up_shexp;
@@ -1040,6 +1045,7 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     // 194, 289 → 214, 271 → 248, 328 → 292 µs; 1024 tokens 445 on the GEMM
     // vs 456 µs on the tiles).
     const bool mid = !small && rows <= 24 * (size_t)(E + (shared ? 1 : 0));
+    const int rpg = (int)(rows / (size_t)(E + (shared ? 1 : 0)));
     // A Q6_K down projection takes the row tiles at every size (64 tokens:
     // 68 -> 61 us against the grouped GEMV's 4-row chunks).
     auto tc_ok = [&](uint32_t type, const ggq::MoeGemm& d, bool down) {
@@ -1066,10 +1072,6 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         return hip_status(c, e, "moe_tiles");
     // the token rows' codes, and their sums per 32 values for the K-quant
     // min term of the grouped GEMM
-    float* qsx = (float*)(base + o_qsx);
-    float* qsh = (float*)(base + o_qsh);
-    gu.QS = qsx;
-    gd.QS = qsh;
     if ((e = ggq::launch_produce_quant(0, p->x, nullptr, H, T, H, 0.0f, qx, sx, s, nullptr, qsx)) != hipSuccess)
         return hip_status(c, e, "quant x");
     auto grouped = [&](uint32_t type, const ggq::MoeGemm& d) -> hipError_t {
@@ -1077,7 +1079,7 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         return ggq::launch_moe_gemm(type, d, s);
     };
     if (paired) {
-        if (gu_tc) e = ggq::launch_i8_tile_codes(p->gate_type, gu, s);
+        if (gu_tc) e = ggq::launch_i8_tile_codes(p->gate_type, gu, rpg, s);
         else if (gu_i8) e = ggq::launch_i8_moe_q8(p->gate_type, gu, (int)rows, base + o_it, s, built);
         else e = ggq::launch_moe_gemm(p->gate_type, gu, s);
         if (e != hipSuccess) return hip_status(c, e, "moe gate+up");
@@ -1094,7 +1096,7 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if ((e = ggq::launch_produce_quant(GGQ_PRODUCE_SWIGLU, G, U, F, (int)rows, F, 0.0f, qh, sh, s, hf, qsh)) !=
         hipSuccess)
         return hip_status(c, e, "swiglu quant");
-    if (dn_tc) e = ggq::launch_i8_tile_codes(p->down_type, gd, s);
+    if (dn_tc) e = ggq::launch_i8_tile_codes(p->down_type, gd, rpg, s);
     else if (dn_i8) e = ggq::launch_i8_moe_q8(p->down_type, gd, (int)rows, base + o_it2, s, built);
     else e = ggq::launch_moe_gemm(p->down_type, gd, s);
     if (e != hipSuccess) return hip_status(c, e, "moe down");

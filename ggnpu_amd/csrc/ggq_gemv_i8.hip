@@ -1870,18 +1870,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
 // ------------------------------------------- row tiles, given int8 codes
 // The same units (group, pass, 128-row tile) for per-row int8 activation
 // codes (the XDNA semantics: codes and a scale per row, as the quantizer
-// wrote them): one digit per row, so a pass carries 16 rows, A row 8 q +
-// 4 s + d holding the codes of row 4 q + d in lane half s, and output
-// register 4 q + d of lane (c, h) the dot product of that row with the
-// lane's own 16 codes.  Q6_K: signed codes (q - 32), I += sc * C per
-// K-step, acc += d * I per block.  Q4_K: unsigned nibbles, a 32-value
-// sub-block per K-step (both halves share its scale and min); the min term
-// takes the half's code sums from a second MFMA against ones: I += sc * C,
-// Mn += m * S, acc += d * I - dmin * Mn per block (exact integer sums: |C|
-// <= 16 * 128 * 15, sc, m <= 63, 8 K-steps).  Paired matrices (gate / up):
+// wrote them): one digit per row, A row m holding the codes of row m of the
+// pass (MR of 16, 24 or 32 rows), so that a K-step is one scale group for
+// both lane halves and output register i of lane (c, h) is the complete
+// dot product of row 8 (i / 4) + 4 h + i % 4 with weight row c.  Q6_K:
+// signed codes (q - 32), K-steps of 16 (v_mfma_i32_32x32x16_i8: a scale
+// group), I += sc * C, acc += d * I per block.  Q4_K: unsigned nibbles,
+// K-steps of 32 (v_mfma_i32_32x32x32_i8: a sub-block); the min term takes
+// I += sc * C per K-step (exact integer I: |C| <= 32 * 128 * 15, sc <= 63,
+// 8 K-steps), acc += d * I per block, less the min term: for more than 16
+// rows a pass a product over sub-blocks on v_mfma_f32_32x32x2_f32 (A: the
+// row's code sums per sub-block, from the quantizer, staged in LDS; B:
+// dmin * m of the weight row; accumulated over the unit); for 16 rows
+// (whose LDS must leave room for 3 workgroups per CU) the code sums from a
+// second MFMA against ones, Mn += m * S, acc -= dmin * Mn per block.  Paired matrices (gate / up):
 // rows [0, n1) of a group from W, [n1, N) from W2.
-constexpr int kCodeMR = 16;
-constexpr int kCodeMaxK = 2048;  // a pass's codes: 16 K bytes of LDS
+constexpr int kCodeMaxK = 2048;
+// LDS bytes of one workgroup: unit prefix, code planes (rows padded by 16
+// bytes, so that the rows of a K-step fall in distinct banks), row scales,
+// scan totals, staging
+__host__ __device__ constexpr int code_lds_bytes(int G, int MR, int K, int stage_row, bool sums) {
+    return (((G + 1) * 4 + 15) & ~15) + MR * (K + 16) + (sums ? MR * (K / 32) * 4 : 0) + 4 * MR + 16 +
+           4 * 32 * stage_row;
+}
 
 template <int T> struct CodeFmt;
 template <> struct CodeFmt<T_Q6_K> {
@@ -1892,14 +1903,12 @@ template <> struct CodeFmt<T_Q4_K> {
 };
 
 template <int T, int MR>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i8_tile_codes_kernel(MoeGemm a) {
+// (3 wavefronts per SIMD for 16 rows a pass, 2 above: the accumulators)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR > 16 ? 2 : 3))) void i8_tile_codes_kernel(
+    MoeGemm a) {
     typedef CodeFmt<T> CF;
-    // Q4_K: a K-step is one scale group for both lane halves, so A rows carry
-    // the whole 32 values of row 0..15 and each lane's output registers 0..7
-    // hold complete sums of 8 rows (8 (i / 4) + 4 h + i % 4); Q6_K: rows in
-    // one lane half per group, all 16 per lane, halves added at the end.
-    constexpr bool kFull = T == T_Q4_K;
-    constexpr int NA = kFull ? 8 : MR;
+    static_assert(MR % 8 == 0 && MR <= 32, "rows per pass");
+    constexpr int NA = MR / 2;  // output registers per lane
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1912,9 +1921,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
     // (16 B entries), row scales [16], wavefront totals of the scan,
     // staging (32 rows of one block per wavefront)
     const int pre_bytes = ((G + 1) * 4 + 15) & ~15;
+    const int PS = a.K + 16;  // plane row stride
     int* pre = (int*)lds;
     uint8_t* planes = lds + pre_bytes;
-    float* lsc = (float*)(planes + MR * a.K);
+    // Q4_K: code sums [m][block][h][s] of sub-block 2 s + h (one 16-byte read
+    // per lane and block)
+    float* sums = (float*)(planes + MR * PS);
+    constexpr bool kSumsLds = T == T_Q4_K && MR > 16;
+    float* lsc = sums + (kSumsLds ? MR * NJ : 0);
     int* wsum = (int*)(lsc + MR);
     uint8_t* stage = (uint8_t*)(wsum + 4) + w * 32 * CF::STAGE_ROW;
     // units per group, exclusive prefix over the workgroup (4 groups per
@@ -2025,15 +2039,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
         for (int i = 0; i < CF::LOADS; i++) r.c[i] = bl16(rs, roff[i]);
         return r;
     };
-    const int rho = lane & 31, s_l = (rho >> 2) & 1;
-    const int m_l = kFull ? rho : 4 * (rho >> 3) + (rho & 3);  // activation row of this lane's A entries
-    auto arow = [&](int i) __attribute__((always_inline)) { return kFull ? 8 * (i >> 2) + 4 * h + (i & 3) : i; };
+    const int m_l = lane & 31;  // activation row of this lane's A entries
+    auto arow = [&](int i) __attribute__((always_inline)) { return 8 * (i >> 2) + 4 * h + (i & 3); };
     Raw ra = fetch();
     Raw rb = fetch();
     int mc = 0, r0 = 0, tile = 0;
     bool act = false;
     uint32_t abase = 0;
     float acc[NA];
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    v16f Mf = {};  // Q4_K min term for more than 16 rows a pass
+    uint32_t abase_s = 0;
     auto start_segment = [&]() __attribute__((always_inline)) {
         const int g = __builtin_amdgcn_readfirstlane(cc.g), local = __builtin_amdgcn_readfirstlane(cc.local);
         const int pass = local / ntiles;
@@ -2050,15 +2067,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
             const int r = r0 + m;
             const int ar = a.x_idx ? a.x_idx[r] : r;
             const uint4 v = *(const uint4*)(a.QA + (int64_t)ar * a.K + k0);
-            *(uint4*)(planes + ((m * NJ + (k0 >> 5)) * 2 + ((k0 >> 4) & 1)) * 16) = v;
+            *(uint4*)(planes + m * PS + k0) = v;
         }
         if (tid < MR) {
             const int r = r0 + (tid < mc ? tid : 0);
             lsc[tid] = a.sa[a.x_idx ? a.x_idx[r] : r];
         }
+        if constexpr (kSumsLds) {
+            for (int i = tid; i < mc * NJ; i += 256) {
+                const int m = i / NJ, j = i - m * NJ, t = j & 7;
+                const int r = r0 + m;
+                const int ar = a.x_idx ? a.x_idx[r] : r;
+                sums[m * NJ + (j & ~7) + 4 * (t & 1) + (t >> 1)] = a.QS[(int64_t)ar * NJ + j];
+            }
+        }
         __syncthreads();
-        act = (kFull || s_l == h) && m_l < mc;
-        abase = (uint32_t)(((m_l * NJ) * 2 + h) * 16);
+        act = m_l < mc;
+        // lane half h: bytes 8 h.. of a 16-value K-step (Q6_K), 16 h.. of a 32-value one (Q4_K)
+        abase = (uint32_t)(m_l * PS + (T == T_Q6_K ? 8 : 16) * h);
+        abase_s = (uint32_t)(m_l * NJ + 4 * h);
     };
     // One block: K-steps on the staged rows.
     auto block = [&](const Raw& raw, int b) __attribute__((always_inline)) {
@@ -2072,33 +2099,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
 #pragma unroll
         for (int m = 0; m < NA; m++) I[m] = 0;
         if constexpr (T == T_Q6_K) {
+            // lane half h: codes 8 h .. 8 h + 7 of each 16-value group, the
+            // two groups of a 32-value step in (x, y) and (z, w)
             TileQ6 q;
+            auto ld2 = [&](const uint8_t* p) __attribute__((always_inline)) {
+                const uint2 u0 = *(const uint2*)p, u1 = *(const uint2*)(p + 16);
+                return v4u{u0.x, u0.y, u1.x, u1.y};
+            };
 #pragma unroll
             for (int nh = 0; nh < 2; nh++) {
-                q.ql0[nh] = *(const v4u*)(row + 64 * nh + 16 * h);
-                q.ql1[nh] = *(const v4u*)(row + 64 * nh + 32 + 16 * h);
-                q.qh[nh] = *(const v4u*)(row + 128 + 32 * nh + 16 * h);
+                q.ql0[nh] = ld2(row + 64 * nh + 8 * h);
+                q.ql1[nh] = ld2(row + 64 * nh + 32 + 8 * h);
+                q.qh[nh] = ld2(row + 128 + 32 * nh + 8 * h);
             }
             q.sc = *(const v4u*)(row + 192);
             const float dd = h2f(raw.d & 0xFFFFu);
 #pragma unroll
             for (int nh = 0; nh < 2; nh++)
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const int j = 8 * b + 4 * nh + t;
-                    v4i A = *(const v4i*)(planes + abase + (uint32_t)j * 32u);
-                    if (!act) A = v4i{0, 0, 0, 0};
-                    const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, tile_q6_codes(q, nh, t), Z, 0, 0, 0);
-                    const int sc = tile_q6_scale(q, nh, t, h);
-                    // (rows past mc meet zero A entries: no branches)
+                for (int t = 0; t < 4; t++)
 #pragma unroll
-                    for (int m = 0; m < MR; m++) I[m] += __mul24(sc, C[m]);
+                    for (int g = 0; g < 2; g++) {
+                        const int j = 8 * b + 4 * nh + t;
+                        long A = *(const long*)(planes + abase + (uint32_t)(32 * j + 16 * g));
+                        if (!act) A = 0;
+                        const v4u ql = (t & 1) ? q.ql1[nh] : q.ql0[nh];
+                        const v4u qh = q.qh[nh];
+                        const uint32_t c0 = q6_signed(g ? ql.z : ql.x, g ? qh.z : qh.x, t);
+                        const uint32_t c1 = q6_signed(g ? ql.w : ql.y, g ? qh.w : qh.y, t);
+                        const long B = (long)(((uint64_t)c1 << 32) | c0);
+                        const v16i C = __builtin_amdgcn_mfma_i32_32x32x16_i8(A, B, Z, 0, 0, 0);
+                        const int sc = tile_q6_scale(q, nh, t, g);
+                        // (rows past mc meet zero A entries: no branches)
 #pragma unroll
-                    for (int m = 0; m < MR; m += 4)
-                        asm volatile("" : "+v"(I[m]), "+v"(I[m + 1]), "+v"(I[m + 2]), "+v"(I[m + 3]));
-                }
+                        for (int m = 0; m < NA; m++) I[m] += __mul24(sc, C[m]);
 #pragma unroll
-            for (int m = 0; m < MR; m++) acc[m] = fmaf(dd, (float)I[m], acc[m]);
+                        for (int m = 0; m < NA; m += 4)
+                            asm volatile("" : "+v"(I[m]), "+v"(I[m + 1]), "+v"(I[m + 2]), "+v"(I[m + 3]));
+                    }
+#pragma unroll
+            for (int m = 0; m < NA; m++) acc[m] = fmaf(dd, (float)I[m], acc[m]);
         } else {
             const v4u hd = *(const v4u*)row;
             v4u qs[4];
@@ -2108,7 +2148,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
             int Mn[NA];
 #pragma unroll
             for (int m = 0; m < NA; m++) Mn[m] = 0;
-            const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+            // min term: sub-blocks 2 s + h of this lane half
+            if constexpr (kSumsLds) {
+                v4f Sa = *(const v4f*)(sums + abase_s + 8 * b);
+                if (!act) Sa = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int s4 = 0; s4 < 4; s4++) {
+                    const uint32_t sm = kq_pair(hd.y, hd.z, hd.w, s4);
+                    const float bm = dmin * (float)((sm >> (16 + 8 * h)) & 0xFFu);
+                    Mf = __builtin_amdgcn_mfma_f32_32x32x2f32(Sa[s4], bm, Mf, 0, 0, 0);
+                }
+            }
 #pragma unroll
             for (int t = 0; t < 8; t++) {
                 const int j = 8 * b + t;
@@ -2124,27 +2174,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
                     B.z = (int)(w4.z & 0x0F0F0F0Fu); B.w = (int)(w4.w & 0x0F0F0F0Fu);
                 }
                 const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, Z, 0, 0, 0);
-                const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, ones, Z, 0, 0, 0);
-                // scale / min of sub-block t (kquant.h:56-64): bytes of pair t / 2
+                // scale / min of sub-block t (kquant.h:56-64): bytes t % 2 of pair t / 2
                 const uint32_t sm = kq_pair(hd.y, hd.z, hd.w, t >> 1);
-                const int sc = (int)((sm >> (8 * (t & 1))) & 0xFFu), mn = (int)((sm >> (16 + 8 * (t & 1))) & 0xFFu);
+                const int sc = (int)((sm >> (8 * (t & 1))) & 0xFFu);
 #pragma unroll
-                for (int m = 0; m < NA; m++) {
-                    I[m] += __mul24(sc, C[m]);
-                    Mn[m] += __mul24(mn, S[m]);
+                for (int m = 0; m < NA; m++) I[m] += __mul24(sc, C[m]);
+                if constexpr (!kSumsLds) {
+                    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+                    const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, ones, Z, 0, 0, 0);
+                    const int mn = (int)((sm >> (16 + 8 * (t & 1))) & 0xFFu);
+#pragma unroll
+                    for (int m = 0; m < NA; m++) Mn[m] += __mul24(mn, S[m]);
+#pragma unroll
+                    for (int m = 0; m < NA; m += 4)
+                        asm volatile("" : "+v"(Mn[m]), "+v"(Mn[m + 1]), "+v"(Mn[m + 2]), "+v"(Mn[m + 3]));
                 }
 #pragma unroll
-                for (int m = 0; m < NA; m += 4) {
+                for (int m = 0; m < NA; m += 4)
                     asm volatile("" : "+v"(I[m]), "+v"(I[m + 1]), "+v"(I[m + 2]), "+v"(I[m + 3]));
-                    asm volatile("" : "+v"(Mn[m]), "+v"(Mn[m + 1]), "+v"(Mn[m + 2]), "+v"(Mn[m + 3]));
-                }
             }
 #pragma unroll
-            for (int m = 0; m < NA; m++) acc[m] = fmaf(d, (float)I[m], fmaf(-dmin, (float)Mn[m], acc[m]));
+            for (int m = 0; m < NA; m++) acc[m] = fmaf(d, (float)I[m], kSumsLds ? acc[m] : fmaf(-dmin, (float)Mn[m], acc[m]));
         }
     };
     auto finish = [&]() __attribute__((always_inline)) {
-        // (Q6_K: the two halves' groups added), then the row's scale
+        // the row's scale
         const int n = tile * kTileRows + w * 32 + col;
         const bool second = n - col >= a.n1;  // (uniform: the wavefront's rows are in one matrix)
         float* Y = second ? a.C2 : a.C;
@@ -2152,8 +2206,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
 #pragma unroll
         for (int i = 0; i < NA; i++) {
             const int m = arow(i);
-            const float v = kFull ? acc[i] : acc[i] + __shfl_xor(acc[i], 32, 64);
-            if (m < mc && (kFull || h == 0) && n < a.N) Y[(int64_t)(r0 + m) * a.ldc + nn] = v * lsc[m];
+            const float v = kSumsLds ? acc[i] - Mf[i] : acc[i];
+            if (m < mc && n < a.N) Y[(int64_t)(r0 + m) * a.ldc + nn] = v * lsc[m];
         }
     };
     int q = 0;
@@ -2162,6 +2216,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
         const int b = q % NB;                                                      \
         if (b == 0) {                                                              \
             _Pragma("unroll") for (int m = 0; m < NA; m++) acc[m] = 0.0f;     \
+            if (kSumsLds) Mf = v16f{};                                             \
         }                                                                          \
         block(R, b);                                                               \
         R = fetch();                                                               \
@@ -2220,6 +2275,7 @@ hipError_t launch_i8_tile_grouped(uint32_t type, const void* W, int64_t w_stride
 
 bool i8_tile_codes_eligible(uint32_t type, const MoeGemm& g) {
     if (type != T_Q6_K && type != T_Q4_K) return false;
+    if (type == T_Q4_K && !g.QS) return false;  // the min term's code sums
     const int G = g.E + (g.Wsh ? 1 : 0);
     if (g.K % 256 != 0 || g.K <= 0 || g.K > kCodeMaxK || g.N <= 0 || g.E < 1 || G > 1023) return false;
     if (g.W2 ? (g.n1 % 32 != 0 || g.n1 <= 0 || g.n1 >= g.N || !g.C2) : g.n1 != g.N) return false;
@@ -2228,26 +2284,34 @@ bool i8_tile_codes_eligible(uint32_t type, const MoeGemm& g) {
     return g.w_stride >= (int64_t)g.n1 * rb && (int64_t)g.E * g.w_stride < (int64_t)kOOB;
 }
 
-hipError_t launch_i8_tile_codes(uint32_t type, const MoeGemm& g, hipStream_t s) {
+namespace {
+template <int T, int MR> hipError_t launch_codes_mr(const MoeGemm& g, int G, hipStream_t s) {
+    const int lds = code_lds_bytes(G, MR, g.K, CodeFmt<T>::STAGE_ROW, T == T_Q4_K && MR > 16);
+    // resident grid: up to 3 workgroups per CU for 16 rows a pass, 2 above
+    // (the kernel's register budget), as many as fit in its 160 KB of LDS
+    const int max_cu = MR > 16 ? 2 : 3;
+    int per_cu = (160 * 1024) / lds;
+    per_cu = per_cu > max_cu ? max_cu : per_cu < 1 ? 1 : per_cu;
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)i8_tile_codes_kernel<T, MR>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    i8_tile_codes_kernel<T, MR><<<dim3((unsigned)(per_cu * cu_count())), 256, lds, s>>>(g);
+    return hipGetLastError();
+}
+template <int T> hipError_t launch_codes(const MoeGemm& g, int G, int rows_per_group, hipStream_t s) {
+    // 16 rows per pass for small groups; otherwise the most rows that leave
+    // two workgroups per CU
+    if (rows_per_group <= 12) return launch_codes_mr<T, 16>(g, G, s);
+    if (2 * code_lds_bytes(G, 32, g.K, CodeFmt<T>::STAGE_ROW, T == T_Q4_K) <= 160 * 1024) return launch_codes_mr<T, 32>(g, G, s);
+    if (2 * code_lds_bytes(G, 24, g.K, CodeFmt<T>::STAGE_ROW, T == T_Q4_K) <= 160 * 1024) return launch_codes_mr<T, 24>(g, G, s);
+    return launch_codes_mr<T, 16>(g, G, s);
+}
+}  // namespace
+
+hipError_t launch_i8_tile_codes(uint32_t type, const MoeGemm& g, int rows_per_group, hipStream_t s) {
     if (!i8_tile_codes_eligible(type, g)) return hipErrorInvalidValue;
     const int G = g.E + (g.Wsh ? 1 : 0);
-    const int stage_row = type == T_Q6_K ? CodeFmt<T_Q6_K>::STAGE_ROW : CodeFmt<T_Q4_K>::STAGE_ROW;
-    const int lds = (((G + 1) * 4 + 15) & ~15) + kCodeMR * g.K + 4 * kCodeMR + 16 + 4 * 32 * stage_row;
-    int per_cu = (160 * 1024) / lds;
-    per_cu = per_cu > 3 ? 3 : per_cu < 1 ? 1 : per_cu;
-    const dim3 grid((unsigned)(per_cu * cu_count()));
-    if (type == T_Q6_K) {
-        static const hipError_t attr = hipFuncSetAttribute((const void*)i8_tile_codes_kernel<T_Q6_K, kCodeMR>,
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
-        if (attr != hipSuccess) return attr;
-        i8_tile_codes_kernel<T_Q6_K, kCodeMR><<<grid, 256, lds, s>>>(g);
-    } else {
-        static const hipError_t attr = hipFuncSetAttribute((const void*)i8_tile_codes_kernel<T_Q4_K, kCodeMR>,
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
-        if (attr != hipSuccess) return attr;
-        i8_tile_codes_kernel<T_Q4_K, kCodeMR><<<grid, 256, lds, s>>>(g);
-    }
-    return hipGetLastError();
+    return type == T_Q6_K ? launch_codes<T_Q6_K>(g, G, rows_per_group, s) : launch_codes<T_Q4_K>(g, G, rows_per_group, s);
 }
 
 }  // namespace ggq

@@ -213,9 +213,10 @@ hipError_t launch_moe_tiles(int32_t* grp, int32_t* x_idx, int E, int T_sh, int2*
 hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s);
 // The same grouped launch (int8 codes QA / sa, groups from grp with the
 // shared expert as group E when Wsh is set, grp[E + 1] written) on int8 row
-// tiles: Q4_K / Q6_K, K <= 2048, 16 rows of a group per pass.
+// tiles: Q4_K / Q6_K, K <= 2048, 16 to 32 rows of a group per pass (by
+// the average rows per group).
 bool i8_tile_codes_eligible(uint32_t type, const MoeGemm& g);
-hipError_t launch_i8_tile_codes(uint32_t type, const MoeGemm& g, hipStream_t s);
+hipError_t launch_i8_tile_codes(uint32_t type, const MoeGemm& g, int rows_per_group, hipStream_t s);
 // The same layer's grouped launches on the int8 GEMV in its given-codes
 // mode (per-row int8 codes g.QA / g.sa): a group's rows in chunks of up to 8
 // (4 for Q6_K / IQ4) from a chunk list built on the device over the E groups
