@@ -1060,14 +1060,14 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     int nl = 0;
     if (gu_i8) lists[nl++] = ggq::i8_moe_q8_list(p->gate_type, gu, (int)rows, base + o_it);
     if (dn_i8) lists[nl++] = ggq::i8_moe_q8_list(p->down_type, gd, (int)rows, base + o_it2);
-    bool built = false;
-    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, nl > 0 ? (int)ts : 0, lists, nl, &built)) !=
+    bool built = false, sh_built = false;
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, (int)ts, lists, nl, &built, &sh_built)) !=
         hipSuccess)
         return hip_status(c, e, "moe_group");
-    // The GEMM's tile list (and, when the grouping built no chunk lists, the
-    // shared expert's group end and token rows that the row tiles read too).
+    // The GEMM's tile list (and the shared expert's group end and token rows
+    // when the grouping launch did not write them).
     const bool any_gemm = (paired ? !gu_i8 && !gu_tc : true) || (!dn_i8 && !dn_tc);
-    if ((any_gemm || !built) &&
+    if ((any_gemm || !sh_built) &&
         (e = ggq::launch_moe_tiles(grp, tok, E, (int)ts, (int2*)tiles, ntiles, s)) != hipSuccess)
         return hip_status(c, e, "moe_tiles");
     // the token rows' codes, and their sums per 32 values for the K-quant

@@ -4372,9 +4372,11 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
             pos_of[f] = pos;
         }
     }
-    // The grouped int8 launches' chunk lists (and the shared expert's group
-    // end and token rows) from the offsets just written, saving their own
-    // launch.
+    // The shared expert's group end and token rows, and the grouped int8
+    // launches' chunk lists from the offsets just written, saving their own
+    // launches.
+    if (tid == 0) grp_off[E + 1] = n + t_sh;
+    for (int t = tid; t < t_sh; t += 1024) tok_idx[n + t] = t;
     if (n_lists > 0) {
         __shared__ ChunkList lists[2];
         if (tid == 0) { lists[0] = l0; lists[1] = l1; }
@@ -4386,9 +4388,7 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
         } else if (tid == E && t_sh > 0) {  // the shared expert: every token after the routed rows
             r0 = n;
             rows = t_sh;
-            grp_off[E + 1] = n + t_sh;
         }
-        for (int t = tid; t < t_sh; t += 1024) tok_idx[n + t] = t;
         __syncthreads();
         chunk_lists_from_rows(r0, rows, lists, n_lists, &hist[0][0]);
     }
@@ -4396,8 +4396,9 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
 
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s, int t_sh, const ChunkList* lists,
-                            int n_lists, bool* lists_built) {
+                            int n_lists, bool* lists_built, bool* shared_built) {
     if (lists_built) *lists_built = false;
+    if (shared_built) *shared_built = false;
     if (E > 1024 || n_lists < 0 || n_lists > 2) return hipErrorInvalidValue;
     if (E <= kGroupFastE) {
         const ChunkList none{0, nullptr, nullptr};
@@ -4405,6 +4406,7 @@ hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t*
                                                   n_lists > 0 ? lists[0] : none, n_lists > 1 ? lists[1] : none,
                                                   n_lists);
         if (lists_built) *lists_built = n_lists > 0;
+        if (shared_built) *shared_built = true;
         return hipGetLastError();
     }
     moe_group_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of);

@@ -175,9 +175,14 @@ hipError_t scratch_device_ptr(int device, void** out);
 // MoE helpers.
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel,
                             float* wsel, hipStream_t s);
+// Pairs grouped by expert (grp_off, tok_idx, pos_of).  On the small-E path
+// the same launch also writes the chunk lists asked for (*lists_built) and
+// the shared expert's group end grp_off[E + 1] and token rows, t_sh of them
+// (*shared_built).
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s, int t_sh = 0,
-                            const ChunkList* lists = nullptr, int n_lists = 0, bool* lists_built = nullptr);
+                            const ChunkList* lists = nullptr, int n_lists = 0, bool* lists_built = nullptr,
+                            bool* shared_built = nullptr);
 // Expert-grouped int8 GEMM over a device-built tile list (see
 // moe_gemm_kernel): C[p] = sa[row(p)] * codes(p) . W_e^T for every pair row
 // p of group e; rows [n1, N) of the output come from W2 into C2.
