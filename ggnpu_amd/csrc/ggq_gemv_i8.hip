@@ -2041,8 +2041,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR > 16 ? 2
     };
     const int m_l = lane & 31;  // activation row of this lane's A entries
     auto arow = [&](int i) __attribute__((always_inline)) { return 8 * (i >> 2) + 4 * h + (i & 3); };
+    // blocks in flight: 2, or (2 wavefronts per SIMD leave the registers)
+    // 3 / 4 for more than 16 rows a pass
+    constexpr int NR = MR > 16 ? (T == T_Q4_K ? 4 : 3) : 2;
     Raw ra = fetch();
     Raw rb = fetch();
+    Raw rc, rd;
+    if constexpr (NR > 2) rc = fetch();
+    if constexpr (NR > 3) rd = fetch();
     int mc = 0, r0 = 0, tile = 0;
     bool act = false;
     uint32_t abase = 0;
@@ -2231,13 +2237,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR > 16 ? 2
         start_segment();
         const int seg_units = min(ntiles - tile, u1 - u0 - q / NB);
         const int seg_end = q + seg_units * NB;
-        if (q & 1) {
-            do GGQ_CODE_STEP(rb) while (false);
+        // position q is in register set q % NR
+        const int ph = q % NR;
+        if (ph != 0) {
+            do {
+                if (ph <= 1) GGQ_CODE_STEP(rb)
+                if (NR > 2 && ph <= 2) GGQ_CODE_STEP(rc)
+                if (NR > 3) GGQ_CODE_STEP(rd)
+            } while (false);
             if (q >= seg_end) continue;
         }
         while (true) {
             GGQ_CODE_STEP(ra)
             GGQ_CODE_STEP(rb)
+            if constexpr (NR > 2) GGQ_CODE_STEP(rc)
+            if constexpr (NR > 3) GGQ_CODE_STEP(rd)
         }
     }
 #undef GGQ_CODE_STEP
