@@ -292,12 +292,32 @@ def test_moe_stages_f32_down_row_tiles(ctx, orc, H, F, types):
                                        (1056, 512, (8, 8, Q6K))])
 def test_moe_stages_q8_row_tiles(ctx, orc, H, F, types):
     """Per-row int8 MoE between 3 and 12 pair rows per expert on average,
-    where Q4_K / Q6_K gate+up and down run on the int8 row tiles (16 rows
-    of an expert per pass): K = 256..2048, N a multiple of the 128-row tile
+    where Q4_K / Q6_K gate+up and down run on the int8 row tiles with 16
+    rows of an expert per pass: K = 256..2048, N a multiple of the 128-row tile
     or not (1056), routing skewed so that a few experts take several passes
     next to experts with none; every stage of every expert at the full bar."""
     T, E, k = 64, 48, 4
     L = run_layer(ctx, T, H, F, E, k, types, 1, seed=H + 3 * F + sum(types), hot=3)
     grp = d2h(L["tr"].grp, (E + 1,), np.int32)
     assert np.diff(grp).max() > 16 and (np.diff(grp) == 0).any()
+    check_stages(orc, L, T, H, F, E, k, types, 1)
+
+
+@pytest.mark.parametrize("H,F,types", [(2048, 512, (Q4K, Q4K, Q6K)), (1024, 512, (Q4K, Q4K, Q4K)),
+                                       (1024, 768, (Q6K, Q6K, Q6K)), (1056, 512, (8, 8, Q6K))])
+def test_moe_stages_q8_row_tiles_wide(ctx, orc, H, F, types):
+    """Per-row int8 MoE between 12 and 24 pair rows per expert on average
+    (T = 128, 32 experts, top-4 plus the shared expert: 19 rows per group),
+    where the int8 row tiles carry 24 or 32 rows of an expert per pass:
+    Q4_K gate+up at K = 2048 with 24 rows and at K = 1024 with 32 (the min
+    term on the f32 MFMA from the staged code sums), Q6_K gate+up at
+    K = 1024 and Q4_K / Q6_K down with 32; routing skewed so that a few
+    experts take several passes; every stage of every expert at the full
+    bar."""
+    T, E, k = 128, 32, 4
+    L = run_layer(ctx, T, H, F, E, k, types, 1, seed=H + 5 * F + sum(types), hot=3)
+    grp = d2h(L["tr"].grp, (E + 1,), np.int32)
+    rows = int(grp[-1]) + T
+    assert 12 * (E + 1) < rows <= 24 * (E + 1)
+    assert np.diff(grp).max() > 32
     check_stages(orc, L, T, H, F, E, k, types, 1)
