@@ -957,7 +957,13 @@ static int moe_ffn_f16(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     gd.W = p->down_exps; gd.Wsh = p->down_shexp;
     gd.w_stride = (int64_t)H * ggq::row_bytes(p->down_type, F);
     gd.N = H; gd.n1 = H; gd.C = D;
-    if ((e = ggq::launch_moe_gemm(p->down_type, gd, s)) != hipSuccess) return hip_status(c, e, "moe down");
+    // A Q6_K down projection (K <= 1024) on the row tiles with fp16 rows
+    // (each expert's weights read once per 16 to 32 of its rows).
+    if (ggq::i8_tile_codes_eligible(p->down_type, gd))
+        e = ggq::launch_i8_tile_codes(p->down_type, gd, (int)(rows / (size_t)(E + (shared ? 1 : 0))), s);
+    else
+        e = ggq::launch_moe_gemm(p->down_type, gd, s);
+    if (e != hipSuccess) return hip_status(c, e, "moe down");
     if ((e = ggq::launch_moe_combine(D, pos, wsel, T, k, H, shared ? D + nk * H : nullptr, p->shared_w, p->out, s)) !=
         hipSuccess)
         return hip_status(c, e, "moe combine");

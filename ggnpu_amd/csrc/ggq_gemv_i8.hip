@@ -1885,13 +1885,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
 // (whose LDS must leave room for 3 workgroups per CU) the code sums from a
 // second MFMA against ones, Mn += m * S, acc -= dmin * Mn per block.  Paired matrices (gate / up):
 // rows [0, n1) of a group from W, [n1, N) from W2.
+// F16 (Q6_K only): fp32 rows as fp16 hi + lo planes with a power-of-two row
+// scale (the fp16 GEMM's split), the codes q - 32 exact in fp16, one
+// v_mfma_f32_32x32x16_f16 per plane and 16-value group (products summed in
+// fp32 by the matrix core), acc += d * sc * C.
 constexpr int kCodeMaxK = 2048;
+constexpr int kCodeF16MaxK = 1024;
 // LDS bytes of one workgroup: unit prefix, code planes (rows padded by 16
 // bytes, so that the rows of a K-step fall in distinct banks), row scales,
 // scan totals, staging
-__host__ __device__ constexpr int code_lds_bytes(int G, int MR, int K, int stage_row, bool sums) {
-    return (((G + 1) * 4 + 15) & ~15) + MR * (K + 16) + (sums ? MR * (K / 32) * 4 : 0) + 4 * MR + 16 +
-           4 * 32 * stage_row;
+// (fp16 rows: hi and lo planes of 2 bytes a value)
+__host__ __device__ constexpr int code_lds_bytes(int G, int MR, int K, int stage_row, bool sums, bool f16 = false) {
+    return (((G + 1) * 4 + 15) & ~15) + (f16 ? 2 * MR * (2 * K + 16) : MR * (K + 16)) +
+           (sums ? MR * (K / 32) * 4 : 0) + 4 * MR + 16 + 4 * 32 * stage_row;
+}
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+// Four 6-bit Q6_K values u (bytes of w, 0..63) as the fp16 codes u - 32,
+// exactly: the half 0x6400 | u is 1024 + u.
+__device__ __forceinline__ uint2 q6u_f16x4(uint32_t w) {
+    const h2v off = {(_Float16)1056.0f, (_Float16)1056.0f};
+    const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - off;
+    const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)) - off;
+    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
 }
 
 template <int T> struct CodeFmt;
@@ -1902,11 +1918,12 @@ template <> struct CodeFmt<T_Q4_K> {
     static constexpr int BB = 144, PIECES = 9, LOADS = 5, STAGE_ROW = 144;
 };
 
-template <int T, int MR>
 // (3 wavefronts per SIMD for 16 rows a pass, 2 above: the accumulators)
+template <int T, int MR, bool F16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR > 16 ? 2 : 3))) void i8_tile_codes_kernel(
     MoeGemm a) {
     typedef CodeFmt<T> CF;
+    static_assert(!F16 || T == T_Q6_K, "fp16 rows: Q6_K");
     static_assert(MR % 8 == 0 && MR <= 32, "rows per pass");
     constexpr int NA = MR / 2;  // output registers per lane
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -1921,12 +1938,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR > 16 ? 2
     // (16 B entries), row scales [16], wavefront totals of the scan,
     // staging (32 rows of one block per wavefront)
     const int pre_bytes = ((G + 1) * 4 + 15) & ~15;
-    const int PS = a.K + 16;  // plane row stride
+    const int PS = F16 ? 2 * a.K + 16 : a.K + 16;  // plane row stride (bytes)
     int* pre = (int*)lds;
     uint8_t* planes = lds + pre_bytes;
     // Q4_K: code sums [m][block][h][s] of sub-block 2 s + h (one 16-byte read
     // per lane and block)
-    float* sums = (float*)(planes + MR * PS);
+    float* sums = (float*)(planes + (F16 ? 2 : 1) * MR * PS);
     constexpr bool kSumsLds = T == T_Q4_K && MR > 16;
     float* lsc = sums + (kSumsLds ? MR * NJ : 0);
     int* wsum = (int*)(lsc + MR);
@@ -2067,17 +2084,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR > 16 ? 2
         mc = rows - MR * pass < MR ? rows - MR * pass : MR;
         __syncthreads();  // the previous segment's planes are read
         // codes of the pass's rows: 16-byte chunks, entry (m, j, half)
-        const int per_row = a.K >> 4;
-        for (int i = tid; i < mc * per_row; i += 256) {
-            const int m = i / per_row, k0 = 16 * (i - m * per_row);
-            const int r = r0 + m;
-            const int ar = a.x_idx ? a.x_idx[r] : r;
-            const uint4 v = *(const uint4*)(a.QA + (int64_t)ar * a.K + k0);
-            *(uint4*)(planes + m * PS + k0) = v;
-        }
-        if (tid < MR) {
-            const int r = r0 + (tid < mc ? tid : 0);
-            lsc[tid] = a.sa[a.x_idx ? a.x_idx[r] : r];
+        if constexpr (F16) {
+            // hi and lo planes: 8 values a 16-byte chunk
+            const int per_row = a.K >> 3;
+            for (int i = tid; i < mc * per_row; i += 256) {
+                const int m = i / per_row, k0 = 8 * (i - m * per_row);
+                const int r = r0 + m;
+                const int64_t src = (int64_t)(a.x_idx ? a.x_idx[r] : r) * a.K + k0;
+                *(uint4*)(planes + m * PS + 2 * k0) = *(const uint4*)((const _Float16*)a.XH + src);
+                *(uint4*)(planes + (MR + m) * PS + 2 * k0) = *(const uint4*)((const _Float16*)a.XL + src);
+            }
+            if (tid < MR) {
+                const int r = r0 + (tid < mc ? tid : 0);
+                lsc[tid] = a.xs[a.x_idx ? a.x_idx[r] : r];
+            }
+        } else {
+            const int per_row = a.K >> 4;
+            for (int i = tid; i < mc * per_row; i += 256) {
+                const int m = i / per_row, k0 = 16 * (i - m * per_row);
+                const int r = r0 + m;
+                const int ar = a.x_idx ? a.x_idx[r] : r;
+                const uint4 v = *(const uint4*)(a.QA + (int64_t)ar * a.K + k0);
+                *(uint4*)(planes + m * PS + k0) = v;
+            }
+            if (tid < MR) {
+                const int r = r0 + (tid < mc ? tid : 0);
+                lsc[tid] = a.sa[a.x_idx ? a.x_idx[r] : r];
+            }
         }
         if constexpr (kSumsLds) {
             for (int i = tid; i < mc * NJ; i += 256) {
@@ -2090,7 +2123,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR > 16 ? 2
         __syncthreads();
         act = m_l < mc;
         // lane half h: bytes 8 h.. of a 16-value K-step (Q6_K), 16 h.. of a 32-value one (Q4_K)
-        abase = (uint32_t)(m_l * PS + (T == T_Q6_K ? 8 : 16) * h);
+        abase = (uint32_t)(m_l * PS + (T == T_Q6_K && !F16 ? 8 : 16) * h);
         abase_s = (uint32_t)(m_l * NJ + 4 * h);
     };
     // One block: K-steps on the staged rows.
@@ -2104,7 +2137,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR > 16 ? 2
         int I[NA];
 #pragma unroll
         for (int m = 0; m < NA; m++) I[m] = 0;
-        if constexpr (T == T_Q6_K) {
+        if constexpr (F16) {
+            // lane half h: values 8 h .. 8 h + 7 of each 16-value group (u in
+            // 0..63: low 4 bits from ql, the top two from qh)
+            TileQ6 q;
+            auto ld2 = [&](const uint8_t* p) __attribute__((always_inline)) {
+                const uint2 u0 = *(const uint2*)p, u1 = *(const uint2*)(p + 16);
+                return v4u{u0.x, u0.y, u1.x, u1.y};
+            };
+#pragma unroll
+            for (int nh = 0; nh < 2; nh++) {
+                q.ql0[nh] = ld2(row + 64 * nh + 8 * h);
+                q.ql1[nh] = ld2(row + 64 * nh + 32 + 8 * h);
+                q.qh[nh] = ld2(row + 128 + 32 * nh + 8 * h);
+            }
+            q.sc = *(const v4u*)(row + 192);
+            const float dd = h2f(raw.d & 0xFFFFu);
+            typedef float v16f_ __attribute__((ext_vector_type(16)));
+            const v16f_ Zf = {};
+            const v8h Z8 = {};
+#pragma unroll
+            for (int nh = 0; nh < 2; nh++)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int g = 0; g < 2; g++) {
+                        const int j = 8 * b + 4 * nh + t;
+                        const uint32_t ko = (uint32_t)(2 * (32 * j + 16 * g));
+                        v8h Ah = *(const v8h*)(planes + abase + ko);
+                        v8h Al = *(const v8h*)(planes + MR * PS + abase + ko);
+                        if (!act) { Ah = Z8; Al = Z8; }
+                        const v4u ql = (t & 1) ? q.ql1[nh] : q.ql0[nh];
+                        const v4u qh = q.qh[nh];
+                        auto u6 = [&](uint32_t l, uint32_t hb) __attribute__((always_inline)) {
+                            const uint32_t lo = (t >> 1) ? (l >> 4) & 0x0F0F0F0Fu : l & 0x0F0F0F0Fu;
+                            return lo | (((hb >> (2 * t)) & 0x03030303u) << 4);
+                        };
+                        const uint2 b0 = q6u_f16x4(u6(g ? ql.z : ql.x, g ? qh.z : qh.x));
+                        const uint2 b1 = q6u_f16x4(u6(g ? ql.w : ql.y, g ? qh.w : qh.y));
+                        const v8h B = __builtin_bit_cast(v8h, make_uint4(b0.x, b0.y, b1.x, b1.y));
+                        v16f_ C = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ah, B, Zf, 0, 0, 0);
+                        C = __builtin_amdgcn_mfma_f32_32x32x16_f16(Al, B, C, 0, 0, 0);
+                        const float ds = dd * (float)tile_q6_scale(q, nh, t, g);
+#pragma unroll
+                        for (int m = 0; m < NA; m++) acc[m] = fmaf(ds, C[m], acc[m]);
+#pragma unroll
+                        for (int m = 0; m < NA; m += 4)
+                            asm volatile("" : "+v"(acc[m]), "+v"(acc[m + 1]), "+v"(acc[m + 2]), "+v"(acc[m + 3]));
+                    }
+        } else if constexpr (T == T_Q6_K) {
             // lane half h: codes 8 h .. 8 h + 7 of each 16-value group, the
             // two groups of a 32-value step in (x, y) and (z, w)
             TileQ6 q;
@@ -2289,7 +2370,11 @@ hipError_t launch_i8_tile_grouped(uint32_t type, const void* W, int64_t w_stride
 
 bool i8_tile_codes_eligible(uint32_t type, const MoeGemm& g) {
     if (type != T_Q6_K && type != T_Q4_K) return false;
-    if (type == T_Q4_K && !g.QS) return false;  // the min term's code sums
+    if (g.XH) {  // fp16 rows: Q6_K, hi / lo planes and row scales
+        if (type != T_Q6_K || !g.XL || !g.xs || g.K > kCodeF16MaxK || g.W2) return false;
+    } else if (!g.QA || !g.sa || (type == T_Q4_K && !g.QS)) {  // (the min term's code sums)
+        return false;
+    }
     const int G = g.E + (g.Wsh ? 1 : 0);
     if (g.K % 256 != 0 || g.K <= 0 || g.K > kCodeMaxK || g.N <= 0 || g.E < 1 || G > 1023) return false;
     if (g.W2 ? (g.n1 % 32 != 0 || g.n1 <= 0 || g.n1 >= g.N || !g.C2) : g.n1 != g.N) return false;
@@ -2299,33 +2384,38 @@ bool i8_tile_codes_eligible(uint32_t type, const MoeGemm& g) {
 }
 
 namespace {
-template <int T, int MR> hipError_t launch_codes_mr(const MoeGemm& g, int G, hipStream_t s) {
-    const int lds = code_lds_bytes(G, MR, g.K, CodeFmt<T>::STAGE_ROW, T == T_Q4_K && MR > 16);
+template <int T, int MR, bool F16> hipError_t launch_codes_mr(const MoeGemm& g, int G, hipStream_t s) {
+    const int lds = code_lds_bytes(G, MR, g.K, CodeFmt<T>::STAGE_ROW, T == T_Q4_K && MR > 16, F16);
     // resident grid: up to 3 workgroups per CU for 16 rows a pass, 2 above
     // (the kernel's register budget), as many as fit in its 160 KB of LDS
     const int max_cu = MR > 16 ? 2 : 3;
     int per_cu = (160 * 1024) / lds;
     per_cu = per_cu > max_cu ? max_cu : per_cu < 1 ? 1 : per_cu;
-    static const hipError_t attr =
-        hipFuncSetAttribute((const void*)i8_tile_codes_kernel<T, MR>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static const hipError_t attr = hipFuncSetAttribute((const void*)i8_tile_codes_kernel<T, MR, F16>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (attr != hipSuccess) return attr;
-    i8_tile_codes_kernel<T, MR><<<dim3((unsigned)(per_cu * cu_count())), 256, lds, s>>>(g);
+    i8_tile_codes_kernel<T, MR, F16><<<dim3((unsigned)(per_cu * cu_count())), 256, lds, s>>>(g);
     return hipGetLastError();
 }
-template <int T> hipError_t launch_codes(const MoeGemm& g, int G, int rows_per_group, hipStream_t s) {
+template <int T, bool F16> hipError_t launch_codes(const MoeGemm& g, int G, int rows_per_group, hipStream_t s) {
     // 16 rows per pass for small groups; otherwise the most rows that leave
     // two workgroups per CU
-    if (rows_per_group <= 12) return launch_codes_mr<T, 16>(g, G, s);
-    if (2 * code_lds_bytes(G, 32, g.K, CodeFmt<T>::STAGE_ROW, T == T_Q4_K) <= 160 * 1024) return launch_codes_mr<T, 32>(g, G, s);
-    if (2 * code_lds_bytes(G, 24, g.K, CodeFmt<T>::STAGE_ROW, T == T_Q4_K) <= 160 * 1024) return launch_codes_mr<T, 24>(g, G, s);
-    return launch_codes_mr<T, 16>(g, G, s);
+    const bool sums = T == T_Q4_K;
+    if (rows_per_group <= 12) return launch_codes_mr<T, 16, F16>(g, G, s);
+    if (2 * code_lds_bytes(G, 32, g.K, CodeFmt<T>::STAGE_ROW, sums, F16) <= 160 * 1024)
+        return launch_codes_mr<T, 32, F16>(g, G, s);
+    if (2 * code_lds_bytes(G, 24, g.K, CodeFmt<T>::STAGE_ROW, sums, F16) <= 160 * 1024)
+        return launch_codes_mr<T, 24, F16>(g, G, s);
+    return launch_codes_mr<T, 16, F16>(g, G, s);
 }
 }  // namespace
 
 hipError_t launch_i8_tile_codes(uint32_t type, const MoeGemm& g, int rows_per_group, hipStream_t s) {
     if (!i8_tile_codes_eligible(type, g)) return hipErrorInvalidValue;
     const int G = g.E + (g.Wsh ? 1 : 0);
-    return type == T_Q6_K ? launch_codes<T_Q6_K>(g, G, rows_per_group, s) : launch_codes<T_Q4_K>(g, G, rows_per_group, s);
+    if (g.XH) return launch_codes<T_Q6_K, true>(g, G, rows_per_group, s);
+    return type == T_Q6_K ? launch_codes<T_Q6_K, false>(g, G, rows_per_group, s)
+                          : launch_codes<T_Q4_K, false>(g, G, rows_per_group, s);
 }
 
 }  // namespace ggq

@@ -219,7 +219,8 @@ hipError_t launch_moe_gemm(uint32_t type, const MoeGemm& g, hipStream_t s);
 // The same grouped launch (int8 codes QA / sa, groups from grp with the
 // shared expert as group E when Wsh is set, grp[E + 1] written) on int8 row
 // tiles: Q4_K / Q6_K, K <= 2048, 16 to 32 rows of a group per pass (by
-// the average rows per group).
+// the average rows per group).  With XH set (fp32 rows as fp16 hi / lo
+// planes, XL, xs): Q6_K, K <= 1024, unpaired.
 bool i8_tile_codes_eligible(uint32_t type, const MoeGemm& g);
 hipError_t launch_i8_tile_codes(uint32_t type, const MoeGemm& g, int rows_per_group, hipStream_t s);
 // The same layer's grouped launches on the int8 GEMV in its given-codes

@@ -248,6 +248,23 @@ def test_moe_stages_f32_gemm_formats(ctx, orc, monkeypatch, types):
         check_stages(orc, L, T, H, F, E, k, types, 0)
 
 
+@pytest.mark.parametrize("H,F,T,E,types", [(1024, 256, 128, 16, (Q4K, Q4K, Q6K)), (1024, 768, 128, 16, (Q4K, Q4K, Q6K)),
+                                           (1024, 512, 64, 32, (Q4K, Q4K, Q6K)), (1056, 1024, 64, 32, (8, 8, Q6K))])
+def test_moe_stages_f32_down_f16_row_tiles(ctx, orc, monkeypatch, H, F, T, E, types):
+    """fp32-activation MoE at prefill-sized batches (the fp16 GEMM path,
+    GGQ_MOE_GEMV_MAX_AVG=0), where a Q6_K down projection runs on the row
+    tiles with the SwiGLU rows as fp16 hi + lo planes: 32 rows a pass at
+    K = 256, 16 at K = 512, 768 and 1024 (N = 1056: a partial 128-row
+    tile); routing skewed so that a few experts take several passes; every
+    stage of every expert."""
+    monkeypatch.setenv("GGQ_MOE_GEMV_MAX_AVG", "0")
+    k = 4
+    L = run_layer(ctx, T, H, F, E, k, types, 0, seed=F + T + E, hot=3)
+    grp = d2h(L["tr"].grp, (E + 1,), np.int32)
+    assert np.diff(grp).max() > 32
+    check_stages(orc, L, T, H, F, E, k, types, 0)
+
+
 @pytest.mark.parametrize("E", [300, 1023])
 @pytest.mark.parametrize("act_mode", [0, 1])
 def test_moe_stages_many_experts_shared(ctx, orc, monkeypatch, E, act_mode):
