@@ -68,7 +68,7 @@ struct ggq_ctx {
     uint32_t done_seq = 0;
     std::vector<void*> retired;  // outgrown device buffers, freed by ggq_destroy
     ggq_moe_trace trace{};       // intermediates of the last MoE call
-    bool trace_rows = false;     // Q8_ROW MoE calls keep their fp32 SwiGLU rows
+    bool trace_rows = false;     // MoE calls keep their fp32 SwiGLU rows
 };
 
 namespace {

@@ -383,17 +383,18 @@ typedef struct {
     const int32_t* pos;     /* [T][top_k] pair row of each (token, slot) */
     const float* gate;      /* [rows][F] gate projection outputs */
     const float* up;        /* [rows][F] up projection outputs */
-    const float* h;         /* [rows][F] SwiGLU rows silu(gate) * up: always
-                               with GGQ_ACT_F32; with GGQ_ACT_Q8_ROW only after
-                               ggq_moe_trace_rows(ctx, 1) (else NULL) */
+    const float* h;         /* [rows][F] SwiGLU rows silu(gate) * up: with
+                               GGQ_ACT_F32 at decode-sized batches always, else
+                               only after ggq_moe_trace_rows(ctx, 1) (else NULL) */
     const int8_t* h_codes;  /* [rows][F] GGQ_ACT_Q8_ROW: int8 codes of h */
     const float* h_scales;  /* [rows] their row scales */
     const float* down;      /* [T*top_k][H] down projection of each routed pair row */
     const float* down_shared; /* [T][H] the shared expert's, or NULL */
 } ggq_moe_trace;
 int ggq_moe_trace_get(const ggq_ctx* ctx, ggq_moe_trace* out);
-/* on != 0: later GGQ_ACT_Q8_ROW MoE calls also write the fp32 SwiGLU rows
- * they quantize (trace.h), from the same registers the codes come from. */
+/* on != 0: later MoE calls also write the fp32 SwiGLU rows (trace.h) that
+ * they quantize or split into fp16 planes, from the same registers the
+ * codes / planes come from. */
 int ggq_moe_trace_rows(ggq_ctx* ctx, int on);
 
 /* ------------------------------------------------------- synthetic data */
