@@ -434,12 +434,24 @@ def bench_host_api(torch, ctx, stream, steps=5, warmup=2):
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
-    sec = (time.perf_counter() - t0) / steps
+    sec_py = (time.perf_counter() - t0) / steps
+    # The same calls from a C++ loop (the reference's caller is C++): the
+    # driver gets the entry point of the library already loaded here.
+    drv = ctypes.CDLL(os.path.join(os.path.dirname(gl.LIB_PATH), "libggq_host_bench.so"))
+    drv.ggq_host_bench_run.restype = ctypes.c_int
+    drv.ggq_host_bench_run.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    arr = (gl.MulMatParams * len(params))(*params)
+    sec = ctypes.c_double(0.0)
+    ctx.check(drv.ggq_host_bench_run(ctypes.cast(ctx.lib.ggq_mul_mat_q, ctypes.c_void_p), ctx.h, arr, len(params), 0,
+                                     warmup, steps, ctypes.byref(sec)), "host bench")
+    sec = sec.value
     nbytes = sum(gl.row_bytes(t, K) * N + 4 * (K + N) for t, N, K, _ in host)
     return {"workload": "configs[1] decode step as 113 synchronous ggq_mul_mat_q calls (host A/B/C, weights "
-                        "resident after the first call)",
+                        "resident after the first call), issued from a C++ loop",
             "ms_per_step": round(sec * 1e3, 3), "GBps": round(nbytes / sec / 1e9, 1),
-            "us_per_call": round(sec * 1e6 / len(params), 2)}
+            "us_per_call": round(sec * 1e6 / len(params), 2),
+            "us_per_call_from_python": round(sec_py * 1e6 / len(params), 2)}
 
 
 def bench_prefill(torch, ctx, stream, steps=3, fused=False):

@@ -15,6 +15,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libggq_hip.so")
+# the benchmark's C++ driver of the synchronous entry point (no link to LIB:
+# it calls the entry point through a pointer the caller passes)
+HOST_BENCH = os.path.join(LIB_DIR, "libggq_host_bench.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 SOURCES = ["ggq_kernels.hip", "ggq_gemv_i8.hip", "ggq_api.cpp", "ggq_encode.cpp", "ggq_gguf.cpp"]
 CXX = os.environ.get("CXX", "g++")
 # Host-only sources go through the host compiler against the HIP runtime API.
@@ -60,6 +64,12 @@ def build(verbose: bool = False) -> str:
     subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
                     "-lpthread"], check=True)
     os.replace(tmp, LIB)
+    cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-shared", f"-I{INCLUDE}",
+           os.path.join(CSRC, "ggq_host_bench.cpp"), "-o", HOST_BENCH + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(HOST_BENCH + ".tmp", HOST_BENCH)
     return LIB
 
 
