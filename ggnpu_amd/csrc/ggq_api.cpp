@@ -1045,17 +1045,16 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         gu.W = p->gate_exps; gu.W2 = p->up_exps; gu.Wsh = p->gate_shexp; gu.W2sh = p->up_shexp;
         gu.N = 2 * F; gu.n1 = F; gu.C = G; gu.C2 = U;
     }
-    // Between 3 and 24 rows per group on average the int8 row tiles (16 rows
-    // of a group per pass) take Q4_K / Q6_K launches; above, gate / up go to
-    // the 32-row GEMM tiles (qwen35moe: 128 / 256 / 384 / 512 tokens 264 →
-    // 194, 289 → 214, 271 → 248, 328 → 292 µs; 1024 tokens 445 on the GEMM
-    // vs 456 µs on the tiles).
-    const bool mid = !small && rows <= 24 * (size_t)(E + (shared ? 1 : 0));
+    // Above 3 rows per group on average, Q4_K / Q6_K launches (K <= 2048)
+    // run on the int8 row tiles (16 to 32 rows of a group per pass, several
+    // passes for larger groups), other formats on the 32-row GEMM tiles
+    // (qwen35moe, tiles vs GEMM: 768 / 1024 / 2048 / 4096 / 6144 tokens
+    // 303 vs 315, 374 vs 392, 593 vs 636, 1036 vs 1108, 1478 vs 1576 us).
     const int rpg = (int)(rows / (size_t)(E + (shared ? 1 : 0)));
     // A Q6_K down projection takes the row tiles at every size (64 tokens:
     // 68 -> 61 us against the grouped GEMV's 4-row chunks).
     auto tc_ok = [&](uint32_t type, const ggq::MoeGemm& d, bool down) {
-        return ((!small && mid) || (down && type == ggq::T_Q6_K)) && ggq::i8_tile_codes_eligible(type, d);
+        return (!small || (down && type == ggq::T_Q6_K)) && ggq::i8_tile_codes_eligible(type, d);
     };
     const bool gu_tc = paired && tc_ok(p->gate_type, gu, false), dn_tc = tc_ok(p->down_type, gd, true);
     const bool gu_i8 = paired && !gu_tc && i8_ok(p->gate_type, gu), dn_i8 = !dn_tc && i8_ok(p->down_type, gd);

@@ -248,6 +248,21 @@ def test_moe_stages_f32_gemm_formats(ctx, orc, monkeypatch, types):
         check_stages(orc, L, T, H, F, E, k, types, 0)
 
 
+@pytest.mark.parametrize("H,F,types", [(2048, 512, (Q4K, Q4K, Q6K)), (1024, 512, (Q6K, Q6K, Q6K))])
+def test_moe_stages_q8_row_tiles_many_passes(ctx, orc, H, F, types):
+    """Per-row int8 MoE with ~113 pair rows per expert on average (T = 384,
+    16 experts, top-4 plus the shared expert), where the int8 row tiles run
+    each group in several passes of 24 or 32 rows (no 32-row GEMM above a
+    size bound); routing skewed so that a few experts take most rows; every
+    stage of every expert at the full bar."""
+    T, E, k = 384, 16, 4
+    L = run_layer(ctx, T, H, F, E, k, types, 1, seed=H + 7 * F + sum(types), hot=3)
+    grp = d2h(L["tr"].grp, (E + 1,), np.int32)
+    assert int(grp[-1]) + T > 100 * (E + 1)
+    assert np.diff(grp).max() > 4 * 32
+    check_stages(orc, L, T, H, F, E, k, types, 1)
+
+
 @pytest.mark.parametrize("H,F,T,E,types", [(1024, 256, 128, 16, (Q4K, Q4K, Q6K)), (1024, 768, 128, 16, (Q4K, Q4K, Q6K)),
                                            (1024, 512, 64, 32, (Q4K, Q4K, Q6K)), (1056, 1024, 64, 32, (8, 8, Q6K))])
 def test_moe_stages_f32_down_f16_row_tiles(ctx, orc, monkeypatch, H, F, T, E, types):
