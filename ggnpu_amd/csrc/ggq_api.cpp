@@ -1017,11 +1017,17 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
     ggq::MoeGemm g{};
     g.E = E; g.grp = grp; g.tiles = tiles; g.n_tiles = ntiles; g.max_tiles = max_tiles;
-    // Few rows per expert (decode-sized batches): the grouped int8 GEMV in
-    // its given-codes mode (chunks of 8 rows, 4 for Q6_K / IQ4), whose
-    // lanes carry the rows; more rows per expert: the int8 row tiles or the
-    // expert-grouped GEMM's 32-row tiles (moe_small_groups, below).
+    // Few rows per expert (decode-sized batches: up to 3 rows per group on
+    // average, up to 1 for Q4_K / Q6_K): the grouped int8 GEMV in its
+    // given-codes mode (chunks of 8 rows, 4 for Q6_K / IQ4), whose lanes
+    // carry the rows; more rows per expert: the int8 row tiles or the
+    // expert-grouped GEMM's 32-row tiles.
     const bool small = moe_small_groups(rows, E + (shared ? 1 : 0), 3);
+    // Q4_K / Q6_K launches leave the grouped GEMV for the int8 row tiles
+    // from 1 row per group on average (qwen35moe 32 / 64 / 128 tokens 142 ->
+    // 117, 164 -> 157, 189 -> 179 us; at 16 tokens the two tie, at 4 the
+    // GEMV is 5 us faster).
+    const bool tiny = moe_small_groups(rows, E + (shared ? 1 : 0), 1);
     auto i8_ok = [&](uint32_t type, const ggq::MoeGemm& d) {
         return small && ggq::i8_moe_q8_eligible(type, d, (int)rows) &&
                ggq::i8_moe_q8_ws_bytes(type, d, (int)rows) <= it_bytes;
@@ -1046,7 +1052,7 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         gu.N = 2 * F; gu.n1 = F; gu.C = G; gu.C2 = U;
     }
     // Above 3 rows per group on average, Q4_K / Q6_K launches (K <= 2048)
-    // run on the int8 row tiles (16 to 32 rows of a group per pass, several
+    // run on the int8 row tiles (8 to 32 rows of a group per pass, several
     // passes for larger groups), other formats on the 32-row GEMM tiles
     // (qwen35moe, tiles vs GEMM: 768 / 1024 / 2048 / 4096 / 6144 tokens
     // 303 vs 315, 374 vs 392, 593 vs 636, 1036 vs 1108, 1478 vs 1576 us).
@@ -1054,7 +1060,7 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     // A Q6_K down projection takes the row tiles at every size (64 tokens:
     // 68 -> 61 us against the grouped GEMV's 4-row chunks).
     auto tc_ok = [&](uint32_t type, const ggq::MoeGemm& d, bool down) {
-        return (!small || (down && type == ggq::T_Q6_K)) && ggq::i8_tile_codes_eligible(type, d);
+        return (!tiny || (down && type == ggq::T_Q6_K)) && ggq::i8_tile_codes_eligible(type, d);
     };
     const bool gu_tc = paired && tc_ok(p->gate_type, gu, false), dn_tc = tc_ok(p->down_type, gd, true);
     const bool gu_i8 = paired && !gu_tc && i8_ok(p->gate_type, gu), dn_i8 = !dn_tc && i8_ok(p->down_type, gd);

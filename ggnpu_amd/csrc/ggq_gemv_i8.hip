@@ -1871,9 +1871,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void i
 // The same units (group, pass, 128-row tile) for per-row int8 activation
 // codes (the XDNA semantics: codes and a scale per row, as the quantizer
 // wrote them): one digit per row, A row m holding the codes of row m of the
-// pass (MR of 16, 24 or 32 rows), so that a K-step is one scale group for
+// pass (MR of 8, 16, 24 or 32 rows), so that a K-step is one scale group for
 // both lane halves and output register i of lane (c, h) is the complete
-// dot product of row 8 (i / 4) + 4 h + i % 4 with weight row c.  Q6_K:
+// dot product of row 8 (i / 4) + 4 h + i % 4 with weight row c (MR of 8:
+// registers 0..3).  Q6_K:
 // signed codes (q - 32), K-steps of 16 (v_mfma_i32_32x32x16_i8: a scale
 // group), I += sc * C, acc += d * I per block.  Q4_K: unsigned nibbles,
 // K-steps of 32 (v_mfma_i32_32x32x32_i8: a sub-block); the min term takes
@@ -2398,9 +2399,11 @@ template <int T, int MR, bool F16> hipError_t launch_codes_mr(const MoeGemm& g, 
     return hipGetLastError();
 }
 template <int T, bool F16> hipError_t launch_codes(const MoeGemm& g, int G, int rows_per_group, hipStream_t s) {
-    // 16 rows per pass for small groups; otherwise the most rows that leave
-    // two workgroups per CU
+    // 8 rows per pass for up to 4 rows a group on average (half the
+    // products of 16-row passes), 16 up to 12; otherwise the most rows that
+    // leave two workgroups per CU
     const bool sums = T == T_Q4_K;
+    if (rows_per_group <= 4) return launch_codes_mr<T, 8, F16>(g, G, s);
     if (rows_per_group <= 12) return launch_codes_mr<T, 16, F16>(g, G, s);
     if (2 * code_lds_bytes(G, 32, g.K, CodeFmt<T>::STAGE_ROW, sums, F16) <= 160 * 1024)
         return launch_codes_mr<T, 32, F16>(g, G, s);

@@ -335,6 +335,24 @@ def test_moe_stages_q8_row_tiles(ctx, orc, H, F, types):
     check_stages(orc, L, T, H, F, E, k, types, 1)
 
 
+@pytest.mark.parametrize("H,F,types", [(1024, 512, (Q4K, Q4K, Q6K)), (2048, 768, (Q6K, Q6K, Q4K)),
+                                       (1056, 512, (8, 8, Q6K))])
+def test_moe_stages_q8_row_tiles_narrow(ctx, orc, H, F, types):
+    """Per-row int8 MoE between 1 and 4 pair rows per expert on average
+    (T = 36, 64 experts, top-4 plus the shared expert: 2.8 rows per group),
+    where Q4_K / Q6_K launches run on the int8 row tiles with 8 rows of an
+    expert per pass (the Q8_0 gate / up of the last case on the grouped
+    GEMV); routing skewed so that a few experts take several passes next
+    to experts with none; every stage of every expert at the full bar."""
+    T, E, k = 36, 64, 4
+    L = run_layer(ctx, T, H, F, E, k, types, 1, seed=H + 11 * F + sum(types), hot=3)
+    grp = d2h(L["tr"].grp, (E + 1,), np.int32)
+    rows = int(grp[-1]) + T
+    assert (E + 1) < rows <= 3 * (E + 1)
+    assert np.diff(grp).max() > 8 and (np.diff(grp) == 0).any()
+    check_stages(orc, L, T, H, F, E, k, types, 1)
+
+
 @pytest.mark.parametrize("H,F,types", [(2048, 512, (Q4K, Q4K, Q6K)), (1024, 512, (Q4K, Q4K, Q4K)),
                                        (1024, 768, (Q6K, Q6K, Q6K)), (1056, 512, (8, 8, Q6K))])
 def test_moe_stages_q8_row_tiles_wide(ctx, orc, H, F, types):
