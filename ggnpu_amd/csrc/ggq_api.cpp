@@ -924,8 +924,14 @@ static int moe_ffn_f16(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     void* tiles = base + o_tl;
     int32_t* ntiles = (int32_t*)(base + o_nt);
 
-    if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
-    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s)) != hipSuccess) return hip_status(c, e, "moe_group");
+    // (decode-sized batches: the grouping launch routes the tokens itself)
+    const bool route_in_group = ggq::moe_group_routes(T, k, E);
+    const float* const rlog = route_in_group ? p->router_logits : nullptr;
+    if (!route_in_group && (e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess)
+        return hip_status(c, e, "moe_route");
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, 0, nullptr, 0, nullptr, nullptr, rlog, sel, wsel)) !=
+        hipSuccess)
+        return hip_status(c, e, "moe_group");
     if ((e = ggq::launch_moe_tiles(grp, tok, E, (int)ts, (int2*)tiles, ntiles, s)) != hipSuccess)
         return hip_status(c, e, "moe_tiles");
     if ((e = ggq::launch_split_rows(0, p->x, nullptr, H, T, H, base + o_xh, base + o_xl, (float*)(base + o_xs),
@@ -1014,7 +1020,11 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     void* tiles = base + o_tl;
     int32_t* ntiles = (int32_t*)(base + o_nt);
 
-    if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
+    // (decode-sized batches: the grouping launch routes the tokens itself)
+    const bool route_in_group = ggq::moe_group_routes(T, k, E);
+    const float* const rlog = route_in_group ? p->router_logits : nullptr;
+    if (!route_in_group && (e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess)
+        return hip_status(c, e, "moe_route");
     ggq::MoeGemm g{};
     g.E = E; g.grp = grp; g.tiles = tiles; g.n_tiles = ntiles; g.max_tiles = max_tiles;
     // Few rows per expert (decode-sized batches: up to 3 rows per group on
@@ -1072,7 +1082,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if (gu_i8) lists[nl++] = ggq::i8_moe_q8_list(p->gate_type, gu, (int)rows, base + o_it);
     if (dn_i8) lists[nl++] = ggq::i8_moe_q8_list(p->down_type, gd, (int)rows, base + o_it2);
     bool built = false, sh_built = false;
-    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, (int)ts, lists, nl, &built, &sh_built)) !=
+    if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, (int)ts, lists, nl, &built, &sh_built, rlog, sel,
+                                   wsel)) !=
         hipSuccess)
         return hip_status(c, e, "moe_group");
     // The GEMM's tile list (and the shared expert's group end and token rows
@@ -1194,7 +1205,11 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     int32_t* pos = (int32_t*)(base + o_pos);
     float *G = (float*)(base + o_g), *U = (float*)(base + o_u), *Hh = (float*)(base + o_h), *D = (float*)(base + o_d);
 
-    if ((e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess) return hip_status(c, e, "moe_route");
+    // (decode-sized batches: the grouping launch routes the tokens itself)
+    const bool route_in_group = ggq::moe_group_routes(T, k, E);
+    const float* const rlog = route_in_group ? p->router_logits : nullptr;
+    if (!route_in_group && (e = ggq::launch_moe_route(p->router_logits, T, E, k, sel, wsel, s)) != hipSuccess)
+        return hip_status(c, e, "moe_route");
 
     bool shared_done = false;  // the shared expert's gate / up ran in the routed launch
     ggq::GemvProblem g{};
@@ -1217,7 +1232,7 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     const ggq::ChunkList cl = pre ? ggq::i8_gemv_grouped_list(gp, base + o_it, t_list) : ggq::ChunkList{0, nullptr, nullptr};
     bool built = false;
     if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, pre ? t_list : 0, pre ? &cl : nullptr, pre ? 1 : 0,
-                                   &built)) != hipSuccess)
+                                   &built, nullptr, rlog, sel, wsel)) != hipSuccess)
         return hip_status(c, e, "moe_group");
     if (paired) {
         // gate and up of each expert in one launch: each workgroup loads a

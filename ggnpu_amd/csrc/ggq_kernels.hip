@@ -4133,10 +4133,13 @@ template <int CTRL> __device__ __forceinline__ void route_step(float& best, int&
 
 // PL: logits per lane (E <= 64 * PL), so the per-step scan covers only the
 // experts that exist.
+// One wavefront routes token t (lane = its lane): selections and weights of
+// the token to sel / wsel (and, when sel_l is given, the selections to
+// sel_l too).
 template <int PL>
-__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int E, int topk,
-                                                       int32_t* __restrict__ sel, float* __restrict__ wsel) {
-    const int t = blockIdx.x, lane = threadIdx.x;
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, int E, int topk, int t, int lane,
+                                            int32_t* __restrict__ sel, float* __restrict__ wsel,
+                                            int32_t* sel_l) {
     const float* l = logits + (int64_t)t * E;
     float v[PL];
     uint32_t taken = 0;
@@ -4193,7 +4196,14 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
     if (lane < topk) {
         sel[t * topk + lane] = my_sel;
         wsel[t * topk + lane] = ex / sum;
+        if (sel_l) sel_l[t * topk + lane] = my_sel;
     }
+}
+
+template <int PL>
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int E, int topk,
+                                                       int32_t* __restrict__ sel, float* __restrict__ wsel) {
+    route_token<PL>(logits, E, topk, blockIdx.x, threadIdx.x, sel, wsel, nullptr);
 }
 
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t* sel, float* wsel,
@@ -4299,16 +4309,28 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t* __restri
 // the round, from per-wavefront histograms) + (pairs of e in earlier lanes
 // of its wavefront).
 constexpr int kGroupFastE = 256;
-__global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __restrict__ sel, int n, int E,
+// With logits given (moe_group_routes: up to 16 tokens), the launch first
+// routes the tokens itself, a wavefront per token (route_token: the same selections
+// and weights as moe_route_kernel), keeping the selections in LDS.
+constexpr int kGroupRouteMax = 1024;
+__global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __restrict__ sel_in, int n, int E,
                                                                int topk, int32_t* __restrict__ grp_off,
                                                                int32_t* __restrict__ tok_idx,
                                                                int32_t* __restrict__ pos_of, int t_sh,
-                                                               ChunkList l0, ChunkList l1, int n_lists) {
+                                                               ChunkList l0, ChunkList l1, int n_lists,
+                                                               const float* __restrict__ logits,
+                                                               int32_t* __restrict__ sel_out,
+                                                               float* __restrict__ wsel_out) {
     __shared__ int32_t hist[16][kGroupFastE];  // per wavefront: pairs of each expert in its slice
     __shared__ int32_t start[kGroupFastE];     // first position of each expert (then its end)
     __shared__ int32_t wsum[4];
+    __shared__ int32_t sel_l[kGroupRouteMax];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int i = tid; i < 16 * kGroupFastE; i += 1024) (&hist[0][0])[i] = 0;
+    if (logits)
+        for (int t = wave; t < n / topk; t += 16)
+            route_token<kGroupFastE / 64>(logits, E, topk, t, lane, sel_out, wsel_out, sel_l);
+    const int32_t* sel = logits ? sel_l : sel_in;
     __syncthreads();
     // Wavefront w ranks the pairs of its slice [w * S, (w + 1) * S), 64 at
     // a time: lanes holding the same expert are found with one ballot per
@@ -4394,17 +4416,25 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
     }
 }
 
+// (one token per wavefront: more tokens per wavefront run their routing
+// serially, slower than the separate launch: 64 tokens 165 -> 191 us)
+bool moe_group_routes(int T, int topk, int E) {
+    return E <= kGroupFastE && topk <= 64 && T <= 16 && (int64_t)T * topk <= kGroupRouteMax;
+}
+
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s, int t_sh, const ChunkList* lists,
-                            int n_lists, bool* lists_built, bool* shared_built) {
+                            int n_lists, bool* lists_built, bool* shared_built, const float* logits,
+                            int32_t* sel_out, float* wsel_out) {
     if (lists_built) *lists_built = false;
     if (shared_built) *shared_built = false;
     if (E > 1024 || n_lists < 0 || n_lists > 2) return hipErrorInvalidValue;
+    if (logits && (!moe_group_routes(T, topk, E) || !sel_out || !wsel_out)) return hipErrorInvalidValue;
     if (E <= kGroupFastE) {
         const ChunkList none{0, nullptr, nullptr};
         moe_group_small_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of, t_sh,
                                                   n_lists > 0 ? lists[0] : none, n_lists > 1 ? lists[1] : none,
-                                                  n_lists);
+                                                  n_lists, logits, sel_out, wsel_out);
         if (lists_built) *lists_built = n_lists > 0;
         if (shared_built) *shared_built = true;
         return hipGetLastError();

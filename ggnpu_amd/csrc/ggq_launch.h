@@ -178,11 +178,15 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t
 // Pairs grouped by expert (grp_off, tok_idx, pos_of).  On the small-E path
 // the same launch also writes the chunk lists asked for (*lists_built) and
 // the shared expert's group end grp_off[E + 1] and token rows, t_sh of them
-// (*shared_built).
+// (*shared_built).  With logits given (moe_group_routes(T, topk, E) must
+// hold) it first routes the tokens itself, writing sel_out / wsel_out as
+// launch_moe_route does, and sel is not read.
+bool moe_group_routes(int T, int topk, int E);
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s, int t_sh = 0,
                             const ChunkList* lists = nullptr, int n_lists = 0, bool* lists_built = nullptr,
-                            bool* shared_built = nullptr);
+                            bool* shared_built = nullptr, const float* logits = nullptr, int32_t* sel_out = nullptr,
+                            float* wsel_out = nullptr);
 // Expert-grouped int8 GEMM over a device-built tile list (see
 // moe_gemm_kernel): C[p] = sa[row(p)] * codes(p) . W_e^T for every pair row
 // p of group e; rows [n1, N) of the output come from W2 into C2.

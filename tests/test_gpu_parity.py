@@ -461,12 +461,14 @@ def test_moe_routing_expert_counts(ctx, orc, E, k):
     assert np.allclose(wsel, rw, rtol=1e-6)
     assert orc.rel_l2(out, ref) < TOL
 
-def test_moe_nan_router_logits(ctx, orc):
+@pytest.mark.parametrize("T,E", [(12, 64), (12, 256), (40, 64), (40, 256)])
+def test_moe_nan_router_logits(ctx, orc, T, E):
     """Router rows holding NaN: a NaN logit ranks with -inf, so every
     selection is a valid expert id (an all-NaN row selects experts 0..k-1);
     tokens with finite logits are unaffected.  Rows with tied logits select
-    the lower expert id first."""
-    T, H, F, E, k = 12, 256, 256, 64, 8
+    the lower expert id first.  Up to 16 tokens the grouping launch routes
+    them itself; 40 tokens take the separate routing launch."""
+    H, F, k = 256, 256, 8
 
     def edit(lg):
         lg[1, :] = np.nan                 # all NaN
