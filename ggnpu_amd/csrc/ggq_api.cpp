@@ -1082,8 +1082,14 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     if (gu_i8) lists[nl++] = ggq::i8_moe_q8_list(p->gate_type, gu, (int)rows, base + o_it);
     if (dn_i8) lists[nl++] = ggq::i8_moe_q8_list(p->down_type, gd, (int)rows, base + o_it2);
     bool built = false, sh_built = false;
+    // (up to 16 tokens the grouping launch also quantizes the token rows)
+    ggq::RowQuant rq;
+    const bool quant_in_group = route_in_group && H <= 2048 && H % 8 == 0;
+    if (quant_in_group) {
+        rq.A = p->x; rq.lda = H; rq.M = T; rq.K = H; rq.q = qx; rq.scales = sx; rq.gsum = qsx;
+    }
     if ((e = ggq::launch_moe_group(sel, T, k, E, grp, tok, pos, s, (int)ts, lists, nl, &built, &sh_built, rlog, sel,
-                                   wsel)) !=
+                                   wsel, quant_in_group ? &rq : nullptr)) !=
         hipSuccess)
         return hip_status(c, e, "moe_group");
     // The GEMM's tile list (and the shared expert's group end and token rows
@@ -1094,7 +1100,8 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
         return hip_status(c, e, "moe_tiles");
     // the token rows' codes, and their sums per 32 values for the K-quant
     // min term of the grouped GEMM
-    if ((e = ggq::launch_produce_quant(0, p->x, nullptr, H, T, H, 0.0f, qx, sx, s, nullptr, qsx)) != hipSuccess)
+    if (!quant_in_group &&
+        (e = ggq::launch_produce_quant(0, p->x, nullptr, H, T, H, 0.0f, qx, sx, s, nullptr, qsx)) != hipSuccess)
         return hip_status(c, e, "quant x");
     auto grouped = [&](uint32_t type, const ggq::MoeGemm& d) -> hipError_t {
         if (i8_ok(type, d)) return ggq::launch_i8_moe_q8(type, d, (int)rows, base + o_it, s);

@@ -355,6 +355,11 @@ hipError_t launch_quant_act(const float* A, int lda, int M, int K, int mode, int
 // (no barrier).  Same arithmetic per value as quant_row_regs, so the codes
 // and scales are identical; code sums per 32 values from 4 lanes.
 template <int P>
+__device__ __forceinline__ void quant_row_wave(const float* __restrict__ A, const float* __restrict__ aux,
+                                               int lda, int m, int K, int8_t* __restrict__ q,
+                                               float* __restrict__ scales, float* __restrict__ prod_out,
+                                               float* __restrict__ gsum, int lane);
+template <int P>
 __global__ __launch_bounds__(256) void produce_quant_wave_kernel(const float* __restrict__ A,
                                                                  const float* __restrict__ aux, int lda, int M,
                                                                  int K, int8_t* __restrict__ q,
@@ -364,6 +369,15 @@ __global__ __launch_bounds__(256) void produce_quant_wave_kernel(const float* __
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (m >= M) return;
+    quant_row_wave<P>(A, aux, lda, m, K, q, scales, prod_out, gsum, lane);
+}
+
+// Row m by one wavefront (lane = its lane), K <= 2048.
+template <int P>
+__device__ __forceinline__ void quant_row_wave(const float* __restrict__ A, const float* __restrict__ aux,
+                                               int lda, int m, int K, int8_t* __restrict__ q,
+                                               float* __restrict__ scales, float* __restrict__ prod_out,
+                                               float* __restrict__ gsum, int lane) {
     constexpr int R = 4;  // chunks per lane (K <= 2048)
     const float* a = A + (int64_t)m * lda;
     const float* u = P == PROD_SWIGLU ? aux + (int64_t)m * lda : nullptr;
@@ -4320,7 +4334,7 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
                                                                ChunkList l0, ChunkList l1, int n_lists,
                                                                const float* __restrict__ logits,
                                                                int32_t* __restrict__ sel_out,
-                                                               float* __restrict__ wsel_out) {
+                                                               float* __restrict__ wsel_out, RowQuant rq) {
     __shared__ int32_t hist[16][kGroupFastE];  // per wavefront: pairs of each expert in its slice
     __shared__ int32_t start[kGroupFastE];     // first position of each expert (then its end)
     __shared__ int32_t wsum[4];
@@ -4330,6 +4344,9 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
     if (logits)
         for (int t = wave; t < n / topk; t += 16)
             route_token<kGroupFastE / 64>(logits, E, topk, t, lane, sel_out, wsel_out, sel_l);
+    if (rq.A)
+        for (int m = wave; m < rq.M; m += 16)
+            quant_row_wave<PROD_NONE>(rq.A, nullptr, rq.lda, m, rq.K, rq.q, rq.scales, nullptr, rq.gsum, lane);
     const int32_t* sel = logits ? sel_l : sel_in;
     __syncthreads();
     // Wavefront w ranks the pairs of its slice [w * S, (w + 1) * S), 64 at
@@ -4425,16 +4442,21 @@ bool moe_group_routes(int T, int topk, int E) {
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s, int t_sh, const ChunkList* lists,
                             int n_lists, bool* lists_built, bool* shared_built, const float* logits,
-                            int32_t* sel_out, float* wsel_out) {
+                            int32_t* sel_out, float* wsel_out, const RowQuant* rq) {
     if (lists_built) *lists_built = false;
     if (shared_built) *shared_built = false;
     if (E > 1024 || n_lists < 0 || n_lists > 2) return hipErrorInvalidValue;
     if (logits && (!moe_group_routes(T, topk, E) || !sel_out || !wsel_out)) return hipErrorInvalidValue;
+    const RowQuant rq0{};
+    if (rq && rq->A &&
+        (!logits || rq->M > 16 || rq->K <= 0 || rq->K > 2048 || rq->K % 8 || (uintptr_t)rq->A % 16 || rq->lda % 4 ||
+         (uintptr_t)rq->q % 8 || (rq->gsum && rq->K % 32)))
+        return hipErrorInvalidValue;
     if (E <= kGroupFastE) {
         const ChunkList none{0, nullptr, nullptr};
         moe_group_small_kernel<<<1, 1024, 0, s>>>(sel, T * topk, E, topk, grp_off, tok_idx, pos_of, t_sh,
                                                   n_lists > 0 ? lists[0] : none, n_lists > 1 ? lists[1] : none,
-                                                  n_lists, logits, sel_out, wsel_out);
+                                                  n_lists, logits, sel_out, wsel_out, rq ? *rq : rq0);
         if (lists_built) *lists_built = n_lists > 0;
         if (shared_built) *shared_built = true;
         return hipGetLastError();

@@ -182,11 +182,22 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int32_t
 // hold) it first routes the tokens itself, writing sel_out / wsel_out as
 // launch_moe_route does, and sel is not read.
 bool moe_group_routes(int T, int topk, int E);
+// Rows the grouping launch also quantizes per row when it routes (M <= 16,
+// K <= 2048 and a multiple of 8, A 16-byte aligned with lda % 4 == 0, q
+// 8-byte aligned): the codes, scales and code sums per 32 values of
+// launch_produce_quant(PROD_NONE), bit for bit.
+struct RowQuant {
+    const float* A = nullptr;
+    int lda = 0, M = 0, K = 0;
+    int8_t* q = nullptr;
+    float* scales = nullptr;
+    float* gsum = nullptr;
+};
 hipError_t launch_moe_group(const int32_t* sel, int T, int topk, int E, int32_t* grp_off,
                             int32_t* tok_idx, int32_t* pos_of, hipStream_t s, int t_sh = 0,
                             const ChunkList* lists = nullptr, int n_lists = 0, bool* lists_built = nullptr,
                             bool* shared_built = nullptr, const float* logits = nullptr, int32_t* sel_out = nullptr,
-                            float* wsel_out = nullptr);
+                            float* wsel_out = nullptr, const RowQuant* rq = nullptr);
 // Expert-grouped int8 GEMM over a device-built tile list (see
 // moe_gemm_kernel): C[p] = sa[row(p)] * codes(p) . W_e^T for every pair row
 // p of group e; rows [n1, N) of the output come from W2 into C2.

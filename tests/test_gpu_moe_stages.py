@@ -248,6 +248,24 @@ def test_moe_stages_f32_gemm_formats(ctx, orc, monkeypatch, types):
         check_stages(orc, L, T, H, F, E, k, types, 0)
 
 
+@pytest.mark.parametrize("T", [1, 8, 16])
+@pytest.mark.parametrize("act_mode", [0, 1])
+def test_moe_stages_decode_batch(ctx, orc, T, act_mode):
+    """Decode-sized batches (up to 16 tokens), where the grouping launch
+    also routes the tokens and, with per-row int8 activations, quantizes
+    their rows: selections, every stage of every expert and the layer
+    output at the full bar."""
+    H, F, E, k = 1024, 512, 32, 4
+    types = (Q4K, Q4K, Q6K)
+    L = run_layer(ctx, T, H, F, E, k, types, act_mode, seed=T + 100 * act_mode)
+    check_stages(orc, L, T, H, F, E, k, types, act_mode)
+    ref, rsel, _ = orc.moe_ffn_f64(L["x"], L["logits"], H, F, E, k, *types[:1], L["Wg"], types[1], L["Wu"],
+                                   types[2], L["Wd"], *L["S"], L["sw"], act_mode=act_mode)
+    assert np.array_equal(L["sel"], rsel)
+    if act_mode == 0:
+        assert orc.rel_l2(L["out"], ref) < TOL
+
+
 @pytest.mark.parametrize("H,F,types", [(2048, 512, (Q4K, Q4K, Q6K)), (1024, 512, (Q6K, Q6K, Q6K))])
 def test_moe_stages_q8_row_tiles_many_passes(ctx, orc, H, F, types):
     """Per-row int8 MoE with ~113 pair rows per expert on average (T = 384,
