@@ -893,9 +893,10 @@ static bool moe_small_groups(size_t rows, int groups, int dflt = 5) {
 // (tile list over the experts and the shared expert as group E), the token
 // rows split once into fp16 hi + lo planes, one expert-grouped fp16 GEMM
 // for every expert's gate and up (paired when their types match), SwiGLU
-// fused into the split of the pair rows, one grouped GEMM for down,
-// combine.  Requires H and F multiples of 64 (at most 16384), E <= 1023,
-// x 16-byte aligned (checked by the caller).
+// fused into the split of the pair rows, one grouped launch for down (the
+// row tiles on the fp16 planes for Q6_K, else the GEMM), combine.  Requires
+// H and F multiples of 64 (at most 16384), E <= 1023, x 16-byte aligned
+// (checked by the caller).
 static int moe_ffn_f16(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     const int T = p->T, H = p->H, F = p->F, E = p->E, k = p->top_k;
     const bool shared = p->gate_shexp != nullptr;
@@ -983,10 +984,12 @@ static int moe_ffn_f16(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
 }
 
 // MoE layer with per-row int8 activations (GGQ_ACT_Q8_ROW): route, group,
-// quantize the token rows once, one grouped int8 launch for every expert's
-// gate and up (and the shared expert's, as group E: the expert-grouped GEMM,
-// or the grouped int8 GEMV when the groups are small), SwiGLU fused into the
-// row quantization of the pair rows, one grouped launch for down, combine.
+// quantize the token rows once (up to 16 tokens the grouping launch routes
+// and quantizes too), one grouped int8 launch for every expert's gate and
+// up (and the shared expert's, as group E: the int8 row tiles for Q4_K /
+// Q6_K, else the expert-grouped GEMM, or the grouped int8 GEMV when the
+// groups are small), SwiGLU fused into the row quantization of the pair
+// rows, one grouped launch for down, combine.
 static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     const int T = p->T, H = p->H, F = p->F, E = p->E, k = p->top_k;
     const bool shared = p->gate_shexp != nullptr;
