@@ -1070,10 +1070,12 @@ static int moe_ffn_q8(ggq_ctx* c, const ggq_moe_params* p, hipStream_t s) {
     // (qwen35moe, tiles vs GEMM: 768 / 1024 / 2048 / 4096 / 6144 tokens
     // 303 vs 315, 374 vs 392, 593 vs 636, 1036 vs 1108, 1478 vs 1576 us).
     const int rpg = (int)(rows / (size_t)(E + (shared ? 1 : 0)));
-    // A Q6_K down projection takes the row tiles at every size (64 tokens:
-    // 68 -> 61 us against the grouped GEMV's 4-row chunks).
+    // A Q6_K down projection takes the row tiles from 32 routed pair rows
+    // (64 tokens: 68 -> 61 us against the grouped GEMV's 4-row chunks; with
+    // fewer, the few groups leave most of the tiles' resident grid idle: one
+    // token of qwen35moe 41.1 vs 51.6 us on the GEMV, four 58.5 vs 54.7).
     auto tc_ok = [&](uint32_t type, const ggq::MoeGemm& d, bool down) {
-        return (!tiny || (down && type == ggq::T_Q6_K)) && ggq::i8_tile_codes_eligible(type, d);
+        return (!tiny || (down && type == ggq::T_Q6_K && nk >= 32)) && ggq::i8_tile_codes_eligible(type, d);
     };
     const bool gu_tc = paired && tc_ok(p->gate_type, gu, false), dn_tc = tc_ok(p->down_type, gd, true);
     const bool gu_i8 = paired && !gu_tc && i8_ok(p->gate_type, gu), dn_i8 = !dn_tc && i8_ok(p->down_type, gd);
@@ -1287,7 +1289,11 @@ int ggq_moe_ffn_dev(ggq_ctx* c, const ggq_moe_params* p, void* stream) {
     // Q6_K down: expert-grouped row tiles on the int8 matrix cores (each
     // expert's weights decoded once per 4 of its rows), the shared expert as
     // one more group of the same launch.
-    const bool tiles = ggq::i8_tile_grouped_eligible(p->down_type, H, F, E, g.w_group_stride, shared) && F % 4 == 0;
+    // (from 16 routed pair rows: below, the few groups leave most of the
+    // tiles' resident grid idle and the grouped GEMV is faster, one token of
+    // qwen35moe 43.4 vs 50.0 us; two tokens 55.4 vs 51.1 us)
+    const bool tiles =
+        ggq::i8_tile_grouped_eligible(p->down_type, H, F, E, g.w_group_stride, shared) && F % 4 == 0 && nk >= 16;
     if (tiles) {
         if ((e = ggq::launch_i8_tile_grouped(p->down_type, p->down_exps, g.w_group_stride, shared ? p->down_shexp : nullptr,
                                              Hh, F, grp, E, shared ? T : 0, D, Dsh, H, H, F, s)) != hipSuccess)
