@@ -4344,8 +4344,8 @@ __global__ __launch_bounds__(1024) void moe_group_small_kernel(const int32_t* __
     if (logits)
         for (int t = wave; t < n / topk; t += 16)
             route_token<kGroupFastE / 64>(logits, E, topk, t, lane, sel_out, wsel_out, sel_l);
-    if (rq.A)
-        for (int m = wave; m < rq.M; m += 16)
+    if (rq.A)  // row m on wavefront (m + 8) % 16, beside the routing of token m on wavefront m
+        for (int m = (wave + 8) & 15; m < rq.M; m += 16)
             quant_row_wave<PROD_NONE>(rq.A, nullptr, rq.lda, m, rq.K, rq.q, rq.scales, nullptr, rq.gsum, lane);
     const int32_t* sel = logits ? sel_l : sel_in;
     __syncthreads();
