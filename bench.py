@@ -613,13 +613,13 @@ def bench_config4(torch, ctx, stream, steps=40):
     return res
 
 
-def bench_config5(torch, ctx, stream, steps=20, T=64, act_mode=0):
+def bench_config5(torch, ctx, stream, steps=50, T=64, act_mode=0):
     """one qwen35moe-A3B MoE FFN layer, 64 tokens (T), top-8 of
     256 experts (FFN 512, Q4_K gate/up, Q6_K down) + 1 shared expert, as one
     expert-grouped ggq_moe_ffn_act_dev call (act_mode 0: fp32 activations,
-    1: per-row int8 activations).  Up to 5 pair rows per expert on average
-    (64 tokens) the grouped GEMVs run, above it (512 tokens) the
-    expert-grouped GEMMs (fp16 hi + lo for fp32, int8 for per-row int8)."""
+    1: per-row int8 activations), 50 calls timed after 5.  The launches the
+    layer takes depend on the pair rows per expert: grouped GEMVs, int8 row
+    tiles, expert-grouped GEMMs (fp16 hi + lo for fp32)."""
     H, F, E, k = 2048, 512, 256, 8
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
@@ -645,7 +645,7 @@ def bench_config5(torch, ctx, stream, steps=20, T=64, act_mode=0):
     def run():
         ctx.check(ctx.lib.ggq_moe_ffn_act_dev(ctx.h, ctypes.byref(p), act_mode, stream), "moe_ffn")
 
-    sec = time_steps(torch, run, steps, 2)
+    sec = time_steps(torch, run, steps, 5)
     hit = int(torch.unique(sel).numel())
     per_expert = 2 * gl.row_bytes(Q4K, H) * F + gl.row_bytes(Q6K, F) * H
     b = (hit + 1) * per_expert + 4 * T * H * 2 + 4 * T * E
